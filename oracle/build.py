@@ -1,0 +1,31 @@
+"""Build recipe for the oracle's C part (test infrastructure only).
+
+Compiles oracle/hba_oracle.c with gcc into oracle/_build/libhba_oracle.so.
+No reference sources are compiled: the reference is pure Python and ships no
+C/C++, so there is no oracle/_ref build.
+"""
+import os
+import subprocess
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+SRC = os.path.join(HERE, "hba_oracle.c")
+OUT_DIR = os.path.join(HERE, "_build")
+LIB = os.path.join(OUT_DIR, "libhba_oracle.so")
+
+
+def build(force=False):
+    """Compile the oracle library; returns its path."""
+    os.makedirs(OUT_DIR, exist_ok=True)
+    if (not force and os.path.exists(LIB)
+            and os.path.getmtime(LIB) >= os.path.getmtime(SRC)):
+        return LIB
+    tmp = LIB + ".tmp%d" % os.getpid()
+    cmd = ["gcc", "-O2", "-fPIC", "-shared", "-std=c99", "-ffp-contract=off",
+           "-fno-fast-math", "-o", tmp, SRC, "-lm"]
+    subprocess.run(cmd, check=True)
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(force=True))
