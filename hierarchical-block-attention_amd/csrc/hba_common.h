@@ -1,0 +1,113 @@
+// Shared device helpers for the HBA kernels (gfx950 only).
+//
+// Storage types: fp32 and bf16.  bf16 rounding is round-to-nearest-even,
+// identical to the rounding the reference applies when it casts fp32 results
+// back to bf16 tensors (e.g. _HeadRMSNorm's `.to(x.dtype)`,
+// src/hba/attention.py:94).
+//
+// All code is compiled with -ffp-contract=off: every a*b+c below is two
+// roundings unless written as fmaf().  The declared-order routines
+// (qknorm_row, dot_decl, slot max) reproduce the oracle's operation order
+// exactly so that block selection is bit-exact.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/hba_amd.h"
+
+namespace hba {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint16_t bf16_t;  // raw bf16 bits in memory
+
+__device__ __forceinline__ float bf2f(bf16_t b) { return __uint_as_float((uint32_t)b << 16); }
+
+__device__ __forceinline__ bf16_t f2bf(float x) {
+    uint32_t u = __float_as_uint(x);
+    if ((u & 0x7f800000u) == 0x7f800000u) {
+        if (u & 0x007fffffu) u |= 0x00400000u;
+        return (bf16_t)(u >> 16);
+    }
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (bf16_t)(u >> 16);
+}
+
+__device__ __forceinline__ float rnd_bf16(float x) { return bf2f(f2bf(x)); }
+
+// Storage-type traits: DT 0 = fp32, 1 = bf16.
+template <int DT> struct St;
+template <> struct St<0> {
+    typedef float T;
+    static __device__ __forceinline__ float ld(const T *p, int64_t i) { return p[i]; }
+    static __device__ __forceinline__ void st(T *p, int64_t i, float v) { p[i] = v; }
+    static __device__ __forceinline__ float rnd(float v) { return v; }
+};
+template <> struct St<1> {
+    typedef bf16_t T;
+    static __device__ __forceinline__ float ld(const T *p, int64_t i) { return bf2f(p[i]); }
+    static __device__ __forceinline__ void st(T *p, int64_t i, float v) { p[i] = f2bf(v); }
+    static __device__ __forceinline__ float rnd(float v) { return rnd_bf16(v); }
+};
+
+// Largest candidate block of query position i (0 = none):
+// candidate(i, b) <=> b >= 1 and (b + 1) * Bk <= i - W + 1   (attention.py:250-256)
+__device__ __host__ __forceinline__ int64_t cand_bmax(int64_t i, int64_t Bk, int64_t W) {
+    int64_t lim = i - W + 1;
+    if (lim < 2 * Bk) return 0;
+    return lim / Bk - 1;
+}
+
+// QKNorm of one row held in registers, declared order (see oracle):
+// ss = fma(x,x,ss) sequential, ms = ss/d, ms = max(ms, eps), r = sqrt(ms),
+// y = (x / r) * gain, rounded to the storage dtype.
+template <int DT, int D>
+__device__ __forceinline__ void qknorm_row(float (&x)[D], float gain, float eps) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int t = 0; t < D; ++t) ss = fmaf(x[t], x[t], ss);
+    float ms = ss / (float)D;
+    if (ms < eps) ms = eps;
+    float r = sqrtf(ms);
+#pragma unroll
+    for (int t = 0; t < D; ++t) x[t] = St<DT>::rnd((x[t] / r) * gain);
+}
+
+// RoPE of one row (rotate-half; cos/sin rounded to the storage dtype and each
+// elementwise op rounded, as apply_rope does on x.dtype tensors).
+template <int DT, int D>
+__device__ __forceinline__ void rope_row(const float (&x)[D], float (&y)[D], const float *cs,
+                                         const float *sn) {
+    constexpr int H = D / 2;
+#pragma unroll
+    for (int t = 0; t < D; ++t) {
+        float rot = (t < H) ? -x[t + H] : x[t - H];
+        float c = St<DT>::rnd(cs[t]);
+        float s = St<DT>::rnd(sn[t]);
+        float t1 = St<DT>::rnd(x[t] * c);
+        float t2 = St<DT>::rnd(rot * s);
+        y[t] = St<DT>::rnd(t1 + t2);
+    }
+}
+
+// ----------------------------------------------------------- wave helpers --
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+}  // namespace hba
+
+// Host-side launch check.
+#define HBA_LAUNCH_CHECK()                                      \
+    do {                                                        \
+        if (hipGetLastError() != hipSuccess) return HBA_ERR_LAUNCH; \
+    } while (0)

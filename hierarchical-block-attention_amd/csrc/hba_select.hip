@@ -1,0 +1,380 @@
+// Block selection: flat top-k (route_topk, src/hba/attention.py:272-303; eval
+// :695-698) and two-level beam descent (hier_select, src/hba/attention.py:217-246).
+//
+// One thread per (query, KV head); 64 queries per workgroup.  The routing
+// query (QKNorm of the G heads, summed) is built in registers in the declared
+// order, the block summaries are staged through LDS as fp32 and read as
+// broadcasts, and every slot dot product is a sequential fp32 FMA chain over
+// d -- the same operation order as the oracle, so scores and the selected
+// indices are bit-exact.  The top-k list is a register-resident sorted array
+// (score descending, block index ascending).
+#include "hba_common.h"
+#include "hba_abi.h"
+
+namespace hba {
+
+constexpr int SEL_WG = 64;
+constexpr int SEL_LDS_FLOATS = 4096;  // 16 KiB of staged summaries
+
+__device__ __forceinline__ bool better(float v, int id, float w, int iw) {
+    return (v > w) || (v == w && id < iw);
+}
+
+// Insert (v, id) into a list sorted by (value desc, id asc).  Entries arrive
+// in increasing id order, so an equal value never displaces an earlier one.
+template <int K>
+__device__ __forceinline__ void insert_inorder(float (&vals)[K], int (&ids)[K], float v, int id) {
+    if (v > vals[K - 1]) {
+#pragma unroll
+        for (int j = 0; j < K; ++j) {
+            bool sw = v > vals[j];
+            float tv = sw ? vals[j] : v;
+            int ti = sw ? ids[j] : id;
+            vals[j] = sw ? v : vals[j];
+            ids[j] = sw ? id : ids[j];
+            v = tv;
+            id = ti;
+        }
+    }
+}
+
+// Same with the full (value desc, id asc) comparator, for out-of-order ids.
+template <int K>
+__device__ __forceinline__ void insert_any(float (&vals)[K], int (&ids)[K], float v, int id) {
+    if (better(v, id, vals[K - 1], ids[K - 1])) {
+#pragma unroll
+        for (int j = 0; j < K; ++j) {
+            bool sw = better(v, id, vals[j], ids[j]);
+            float tv = sw ? vals[j] : v;
+            int ti = sw ? ids[j] : id;
+            vals[j] = sw ? v : vals[j];
+            ids[j] = sw ? id : ids[j];
+            v = tv;
+            id = ti;
+        }
+    }
+}
+
+// Routing query of (b, i, g): QKNorm each of the G heads (declared order),
+// sequential fp32 head sum, rounded to the storage dtype (summarizer.py:50-54).
+template <int DT, int D>
+__device__ __forceinline__ void routing_query(const typename St<DT>::T *q, int64_t qsb, int64_t qsn,
+                                              int64_t qsh, const float *qgain, float eps, int64_t b,
+                                              int64_t i, int g, int G, float (&qg)[D]) {
+    for (int h = 0; h < G; ++h) {
+        float x[D];
+        const typename St<DT>::T *row = q + b * qsb + i * qsn + (int64_t)(g * G + h) * qsh;
+        if constexpr (DT == 1) {
+            const uint4 *p = reinterpret_cast<const uint4 *>(row);
+#pragma unroll
+            for (int c = 0; c < D / 8; ++c) {
+                uint4 u = p[c];
+                uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    x[8 * c + 2 * e] = __uint_as_float(w[e] << 16);
+                    x[8 * c + 2 * e + 1] = __uint_as_float(w[e] & 0xffff0000u);
+                }
+            }
+        } else {
+            const float4 *p = reinterpret_cast<const float4 *>(row);
+#pragma unroll
+            for (int c = 0; c < D / 4; ++c) {
+                float4 u = p[c];
+                x[4 * c] = u.x;
+                x[4 * c + 1] = u.y;
+                x[4 * c + 2] = u.z;
+                x[4 * c + 3] = u.w;
+            }
+        }
+        if (qgain) qknorm_row<DT, D>(x, qgain[g * G + h], eps);
+        if (h == 0) {
+#pragma unroll
+            for (int t = 0; t < D; ++t) qg[t] = x[t];
+        } else {
+#pragma unroll
+            for (int t = 0; t < D; ++t) qg[t] = qg[t] + x[t];
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < D; ++t) qg[t] = St<DT>::rnd(qg[t]);
+}
+
+// max over slots of the sequential-FMA dot products, times scale.
+template <int D, int M>
+__device__ __forceinline__ float slot_score_lds(const float (&qg)[D], const float *S, float scale) {
+    float acc[M];
+#pragma unroll
+    for (int s = 0; s < M; ++s) acc[s] = 0.0f;
+#pragma unroll
+    for (int t = 0; t < D; t += 4) {
+#pragma unroll
+        for (int s = 0; s < M; ++s) {
+            float4 sv = *reinterpret_cast<const float4 *>(S + s * D + t);
+            acc[s] = fmaf(qg[t], sv.x, acc[s]);
+            acc[s] = fmaf(qg[t + 1], sv.y, acc[s]);
+            acc[s] = fmaf(qg[t + 2], sv.z, acc[s]);
+            acc[s] = fmaf(qg[t + 3], sv.w, acc[s]);
+        }
+    }
+    float best = acc[0];
+#pragma unroll
+    for (int s = 1; s < M; ++s) best = (acc[s] > best) ? acc[s] : best;
+    return best * scale;
+}
+
+template <int DT, int D, int M>
+__device__ __forceinline__ float slot_score_gmem(const float (&qg)[D], const typename St<DT>::T *S,
+                                                 float scale) {
+    float acc[M];
+#pragma unroll
+    for (int s = 0; s < M; ++s) acc[s] = 0.0f;
+#pragma unroll
+    for (int s = 0; s < M; ++s) {
+#pragma unroll 4
+        for (int t = 0; t < D; ++t) acc[s] = fmaf(qg[t], St<DT>::ld(S, s * D + t), acc[s]);
+    }
+    float best = acc[0];
+#pragma unroll
+    for (int s = 1; s < M; ++s) best = (acc[s] > best) ? acc[s] : best;
+    return best * scale;
+}
+
+// Stage summaries [first, first+cnt) of one (b, g) into LDS as fp32.
+template <int DT, int D, int M>
+__device__ __forceinline__ void stage_blocks(float *lds, const typename St<DT>::T *S, int64_t first,
+                                             int cnt) {
+    const int total = cnt * M * D;
+    const typename St<DT>::T *src = S + first * M * D;
+    for (int e = threadIdx.x; e < total; e += SEL_WG) lds[e] = St<DT>::ld(src, e);
+}
+
+template <int DT, int D, int M, int KMAX>
+__global__ __launch_bounds__(SEL_WG) void score_select_kernel(
+    const typename St<DT>::T *__restrict__ q, int64_t qsb, int64_t qsn, int64_t qsh,
+    const float *__restrict__ qgain, float eps, const typename St<DT>::T *__restrict__ S0, int64_t n,
+    int Hq, int Hkv, int64_t nb, int64_t W, int kk, float scale, int32_t *__restrict__ idx,
+    float *__restrict__ val, int32_t *__restrict__ cnt) {
+    constexpr int CB = SEL_LDS_FLOATS / (M * D);
+    __shared__ __align__(16) float lds[SEL_LDS_FLOATS];
+    const int lane = threadIdx.x;
+    const int g = blockIdx.y;
+    const int64_t b = blockIdx.z;
+    const int G = Hq / Hkv;
+    const int64_t i0 = (int64_t)blockIdx.x * SEL_WG;
+    const int64_t i = i0 + lane;
+    const bool active = i < n;
+    float qg[D];
+    if (active) routing_query<DT, D>(q, qsb, qsn, qsh, qgain, eps, b, i, g, G, qg);
+    const int64_t bmax = active ? cand_bmax(i, 64, W) : 0;
+    const int64_t last = (i0 + SEL_WG - 1 < n) ? i0 + SEL_WG - 1 : n - 1;
+    const int64_t tile_bmax = cand_bmax(last, 64, W);
+    float vals[KMAX];
+    int ids[KMAX];
+#pragma unroll
+    for (int j = 0; j < KMAX; ++j) {
+        vals[j] = -INFINITY;
+        ids[j] = -1;
+    }
+    const typename St<DT>::T *Sg = S0 + (b * Hkv + g) * nb * M * D;
+    for (int64_t b0 = 1; b0 <= tile_bmax; b0 += CB) {
+        int cb = (int)((tile_bmax - b0 + 1 < CB) ? tile_bmax - b0 + 1 : CB);
+        __syncthreads();
+        stage_blocks<DT, D, M>(lds, Sg, b0, cb);
+        __syncthreads();
+        for (int c = 0; c < cb; ++c) {
+            int64_t blk = b0 + c;
+            if (blk <= bmax) {
+                float v = slot_score_lds<D, M>(qg, lds + c * M * D, scale);
+                insert_inorder<KMAX>(vals, ids, v, (int)blk);
+            }
+        }
+    }
+    if (!active) return;
+    int64_t o = ((b * Hkv + g) * n + i) * kk;
+    int c = 0;
+    for (int j = 0; j < kk; ++j) {
+        idx[o + j] = ids[j];
+        val[o + j] = vals[j];
+        c += (vals[j] != -INFINITY) ? 1 : 0;
+    }
+    cnt[(b * Hkv + g) * n + i] = c;
+}
+
+template <int DT, int D, int M, int KMAX>
+__global__ __launch_bounds__(SEL_WG) void hier_select_kernel(
+    const typename St<DT>::T *__restrict__ q, int64_t qsb, int64_t qsn, int64_t qsh,
+    const float *__restrict__ qgain, float eps, const typename St<DT>::T *__restrict__ S0,
+    const typename St<DT>::T *__restrict__ S1, int64_t n, int Hq, int Hkv, int64_t nb, int64_t W,
+    int kk, int F, int beam, float scale, int32_t *__restrict__ idx, float *__restrict__ val,
+    int32_t *__restrict__ cnt) {
+    constexpr int CB = SEL_LDS_FLOATS / (M * D);
+    constexpr int BEAMMAX = 16;
+    __shared__ __align__(16) float lds[SEL_LDS_FLOATS];
+    const int lane = threadIdx.x;
+    const int g = blockIdx.y;
+    const int64_t b = blockIdx.z;
+    const int G = Hq / Hkv;
+    const int64_t i = (int64_t)blockIdx.x * SEL_WG + lane;
+    const bool active = i < n;
+    const int64_t ns = (nb + F - 1) / F;
+    const int beff = (int)((beam < ns) ? beam : ns);
+    float qg[D];
+    if (active) routing_query<DT, D>(q, qsb, qsn, qsh, qgain, eps, b, i, g, G, qg);
+    const int64_t bmax = active ? cand_bmax(i, 64, W) : 0;
+    // level 1: supers holding at least one candidate child
+    float pv[BEAMMAX];
+    int pid[BEAMMAX];
+#pragma unroll
+    for (int j = 0; j < BEAMMAX; ++j) {
+        pv[j] = -INFINITY;
+        pid[j] = -1;
+    }
+    const typename St<DT>::T *S1g = S1 + (b * Hkv + g) * ns * M * D;
+    for (int64_t p0 = 0; p0 < ns; p0 += CB) {
+        int cb = (int)((ns - p0 < CB) ? ns - p0 : CB);
+        __syncthreads();
+        stage_blocks<DT, D, M>(lds, S1g, p0, cb);
+        __syncthreads();
+        for (int c = 0; c < cb; ++c) {
+            int64_t p = p0 + c;
+            int64_t lo = p * F, hi = lo + F - 1;
+            if (hi > nb - 1) hi = nb - 1;
+            bool has = (bmax >= 1) && (lo <= bmax) && (hi >= 1);
+            if (has) {
+                float v = slot_score_lds<D, M>(qg, lds + c * M * D, scale);
+                insert_inorder<BEAMMAX>(pv, pid, v, (int)p);
+            }
+        }
+    }
+    if (!active) return;
+    // level 2: children of the kept parents, in parent-rank order
+    float vals[KMAX];
+    int ids[KMAX];
+#pragma unroll
+    for (int j = 0; j < KMAX; ++j) {
+        vals[j] = -INFINITY;
+        ids[j] = -1;
+    }
+    const typename St<DT>::T *S0g = S0 + (b * Hkv + g) * nb * M * D;
+    for (int a = 0; a < beff; ++a) {
+        if (pv[a] == -INFINITY) break;
+        int64_t base = (int64_t)pid[a] * F;
+        for (int c = 0; c < F; ++c) {
+            int64_t blk = base + c;
+            if (blk >= nb) break;
+            if (blk < 1 || blk > bmax) continue;
+            float v = slot_score_gmem<DT, D, M>(qg, S0g + blk * M * D, scale);
+            insert_any<KMAX>(vals, ids, v, (int)blk);
+        }
+    }
+    int kke = (kk < beff * F) ? kk : beff * F;
+    int64_t o = ((b * Hkv + g) * n + i) * kk;
+    int c = 0;
+    for (int j = 0; j < kk; ++j) {
+        bool ok = j < kke && vals[j] != -INFINITY;
+        idx[o + j] = ok ? ids[j] : -1;
+        val[o + j] = ok ? vals[j] : -INFINITY;
+        c += ok ? 1 : 0;
+    }
+    cnt[(b * Hkv + g) * n + i] = c;
+}
+
+}  // namespace hba
+
+using namespace hba;
+
+namespace {
+
+int select_checks(int dtype, const void *q, const int64_t *qs, const void *S0, int64_t B, int64_t n,
+                  int64_t Hq, int64_t Hkv, int64_t d, int64_t m, int64_t Bk, int64_t W, int64_t k,
+                  const int32_t *idx, const float *val, const int32_t *cnt) {
+    int st = abi::check_dtype_dim(dtype, d);
+    if (st) return st;
+    if (!q || !qs || !S0 || !idx || !val || !cnt) return HBA_ERR_INVALID_ARG;
+    if (B <= 0 || n <= 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv != 0 || W < 1 || k < 1)
+        return HBA_ERR_INVALID_ARG;
+    if (Bk != 64) return HBA_ERR_UNSUPPORTED;
+    if (n % Bk != 0) return HBA_ERR_INVALID_ARG;
+    if (k > 64 || !(m == 1 || m == 2 || m == 4 || m == 8)) return HBA_ERR_UNSUPPORTED;
+    if (m * d > SEL_LDS_FLOATS) return HBA_ERR_UNSUPPORTED;
+    if (!abi::rows_aligned(dtype, q, qs)) return HBA_ERR_UNSUPPORTED;
+    if (B > 65535 || Hkv > 65535 || (n + SEL_WG - 1) / SEL_WG > 0x7fffffff) return HBA_ERR_UNSUPPORTED;
+    return HBA_OK;
+}
+
+template <int DT, int D, int M, int KMAX>
+void launch_flat(const void *q, const int64_t *qs, const float *qgain, float eps, const void *S0,
+                 int64_t B, int64_t n, int64_t Hq, int64_t Hkv, int64_t W, int64_t k, float scale,
+                 int32_t *idx, float *val, int32_t *cnt, hipStream_t s) {
+    dim3 grid((unsigned)((n + SEL_WG - 1) / SEL_WG), (unsigned)Hkv, (unsigned)B);
+    hipLaunchKernelGGL((score_select_kernel<DT, D, M, KMAX>), grid, dim3(SEL_WG), 0, s,
+                       (const typename St<DT>::T *)q, qs[0], qs[1], qs[2], qgain, eps,
+                       (const typename St<DT>::T *)S0, n, (int)Hq, (int)Hkv, n / 64, W, (int)k,
+                       scale, idx, val, cnt);
+}
+
+template <int DT, int D, int M, int KMAX>
+void launch_hier(const void *q, const int64_t *qs, const float *qgain, float eps, const void *S0,
+                 const void *S1, int64_t B, int64_t n, int64_t Hq, int64_t Hkv, int64_t W, int64_t k,
+                 int64_t F, int64_t beam, float scale, int32_t *idx, float *val, int32_t *cnt,
+                 hipStream_t s) {
+    dim3 grid((unsigned)((n + SEL_WG - 1) / SEL_WG), (unsigned)Hkv, (unsigned)B);
+    hipLaunchKernelGGL((hier_select_kernel<DT, D, M, KMAX>), grid, dim3(SEL_WG), 0, s,
+                       (const typename St<DT>::T *)q, qs[0], qs[1], qs[2], qgain, eps,
+                       (const typename St<DT>::T *)S0, (const typename St<DT>::T *)S1, n, (int)Hq,
+                       (int)Hkv, n / 64, W, (int)k, (int)F, (int)beam, scale, idx, val, cnt);
+}
+
+#define HBA_SEL_DISPATCH_K(FN, DT, D, M, ...)                   \
+    do {                                                        \
+        if (k <= 16) FN<DT, D, M, 16>(__VA_ARGS__);             \
+        else if (k <= 32) FN<DT, D, M, 32>(__VA_ARGS__);        \
+        else FN<DT, D, M, 64>(__VA_ARGS__);                     \
+    } while (0)
+
+#define HBA_SEL_DISPATCH_M(FN, DT, D, ...)                               \
+    do {                                                                 \
+        if (m == 1) HBA_SEL_DISPATCH_K(FN, DT, D, 1, __VA_ARGS__);       \
+        else if (m == 2) HBA_SEL_DISPATCH_K(FN, DT, D, 2, __VA_ARGS__);  \
+        else if (m == 4) HBA_SEL_DISPATCH_K(FN, DT, D, 4, __VA_ARGS__);  \
+        else HBA_SEL_DISPATCH_K(FN, DT, D, 8, __VA_ARGS__);              \
+    } while (0)
+
+}  // namespace
+
+extern "C" int hba_score_select(int dtype, const void *q, const int64_t q_strides[3],
+                                const float *q_gain, float eps, const void *S0, int64_t B, int64_t n,
+                                int64_t Hq, int64_t Hkv, int64_t d, int64_t m, int64_t Bk, int64_t W,
+                                int64_t k, float scale, int32_t *idx, float *val, int32_t *cnt,
+                                void *stream) {
+    int st = select_checks(dtype, q, q_strides, S0, B, n, Hq, Hkv, d, m, Bk, W, k, idx, val, cnt);
+    if (st) return st;
+    hipStream_t s = (hipStream_t)stream;
+#define HBA_FLAT(DT, D)                                                                            \
+    HBA_SEL_DISPATCH_M(launch_flat, DT, D, q, q_strides, q_gain, eps, S0, B, n, Hq, Hkv, W, k, scale, \
+                       idx, val, cnt, s)
+    HBA_DISPATCH_DT_D(dtype, d, HBA_FLAT);
+#undef HBA_FLAT
+    HBA_LAUNCH_CHECK();
+    return HBA_OK;
+}
+
+extern "C" int hba_hier_select(int dtype, const void *q, const int64_t q_strides[3],
+                               const float *q_gain, float eps, const void *S0, const void *S1,
+                               int64_t B, int64_t n, int64_t Hq, int64_t Hkv, int64_t d, int64_t m,
+                               int64_t Bk, int64_t W, int64_t k, int64_t fanout, int64_t beam,
+                               float scale, int32_t *idx, float *val, int32_t *cnt, void *stream) {
+    int st = select_checks(dtype, q, q_strides, S0, B, n, Hq, Hkv, d, m, Bk, W, k, idx, val, cnt);
+    if (st) return st;
+    if (!S1 || fanout < 1 || beam < 1) return HBA_ERR_INVALID_ARG;
+    if (beam > 16 || fanout > 64) return HBA_ERR_UNSUPPORTED;
+    hipStream_t s = (hipStream_t)stream;
+#define HBA_HIER(DT, D)                                                                            \
+    HBA_SEL_DISPATCH_M(launch_hier, DT, D, q, q_strides, q_gain, eps, S0, S1, B, n, Hq, Hkv, W, k,   \
+                       fanout, beam, scale, idx, val, cnt, s)
+    HBA_DISPATCH_DT_D(dtype, d, HBA_HIER);
+#undef HBA_HIER
+    HBA_LAUNCH_CHECK();
+    return HBA_OK;
+}

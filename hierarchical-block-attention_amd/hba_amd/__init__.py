@@ -1,0 +1,22 @@
+"""MI355X (gfx950) Hierarchical Block Attention operator.
+
+The forward path of the reference's attention module -- block-summary
+scoring, top-k / hierarchical block selection, the union-softmax attention
+over sinks, the RoPE window and the selected blocks, and a paged-KV decode
+step -- as hand-written HIP kernels behind a C-ABI (include/hba_amd.h), bound
+here through ctypes and registered as torch.library ops (namespace `hba`).
+"""
+from . import ops
+from .attention import (build_super, forward_stages, hba_attention_dense, hba_attention_eval,
+                        hba_attention_fused, selected_mask)
+from .config import (HBAConfig, content_scale, log_len_tau, resolve_backend, rope_tables,
+                     route_scale, union_scale)
+from .decode import PagedKVCache, hba_decode_step
+from .modules import QKNorm, SlotSummarizer
+
+__all__ = [
+    "ops", "HBAConfig", "resolve_backend", "content_scale", "log_len_tau", "union_scale",
+    "route_scale", "rope_tables", "QKNorm", "SlotSummarizer", "hba_attention_eval",
+    "hba_attention_dense", "hba_attention_fused", "build_super", "forward_stages",
+    "selected_mask", "PagedKVCache", "hba_decode_step",
+]

@@ -1,0 +1,95 @@
+"""Drop-in attention functions with the reference's signatures, backed by the
+HIP kernels (forward only).
+
+  hba_attention_eval(q, k, v, cos, sin, cfg, summ, qkn, cap, hier=False)
+      src/hba/attention.py:610-713
+  hba_attention_dense(q, k, v, cos, sin, cfg, summ, qkn) -> (out, aux=0)
+      src/hba/attention.py:306-356 (forward; the aux-KL teacher is training-only)
+  hba_attention_fused(q, k, v, cos, sin, cfg, summ, qkn) -> (out, aux=0)
+      src/hba/attention.py:552-607 (forward: same math as dense)
+
+Tensors: q [B, n, Hq, d], k, v [B, n, Hkv, d] (token-major views, last dim
+contiguous), cos/sin fp32 [n, d] from rope_tables.  `cfg` is read duck-typed
+(a reference HBAConfig works), `summ` must expose .probes [Hkv, m, d] and
+.proj [Hkv, d, d], `qkn` .q.gain/.k.gain/.q.eps/.k.eps.  The output is a new
+tensor of q's shape and dtype; inputs are not modified.  Errors follow the
+reference: AssertionError for n % block != 0, ValueError for an unknown
+content_scale_mode.
+"""
+import torch
+
+from . import ops
+from .config import route_scale, union_scale
+
+
+def _qk(cfg, qkn):
+    if getattr(cfg, "qknorm", False):
+        return qkn.q.gain, qkn.k.gain, float(qkn.q.eps), float(qkn.k.eps)
+    return None, None, 1e-6, 1e-6
+
+
+def forward_stages(q, k, v, cos, sin, cfg, summ, qkn, hier=False, dense_route=False):
+    """The forward path stage by stage; returns a dict with every intermediate
+    (kc, kr, vt, S0, [S1], idx, val, cnt, out) and the scales used."""
+    B, n, Hq, dh = q.shape
+    assert n % cfg.block == 0, (n, cfg.block)
+    if cfg.block != ops.BLOCK:
+        raise ValueError(f"block {cfg.block} unsupported: the kernels use {ops.BLOCK}-key blocks")
+    qg, kg, qeps, keps = _qk(cfg, qkn)
+    scale = union_scale(cfg, dh, n)
+    sel_scale = route_scale(cfg, dh) if dense_route else scale
+    r = {"scale": scale, "sel_scale": sel_scale}
+    r["kc"], r["kr"], r["vt"] = ops.prep_keys(k, v, kg, keps, cos, sin)
+    r["S0"] = ops.summarize(r["kc"], summ.probes, summ.proj)
+    kk = min(cfg.k_blocks, n // cfg.block)
+    if hier:
+        r["S1"] = ops.build_super(r["S0"], cfg.fanout)
+        r["idx"], r["val"], r["cnt"] = ops.hier_select(q, qg, qeps, r["S0"], r["S1"], cfg.window, kk,
+                                                       cfg.fanout, cfg.beam, sel_scale)
+    else:
+        r["idx"], r["val"], r["cnt"] = ops.score_select(q, qg, qeps, r["S0"], cfg.window, kk, sel_scale)
+    r["out"] = ops.attn_fwd(q, qg, qeps, r["kc"], r["kr"], r["vt"], cos, sin, r["idx"], r["cnt"],
+                            cfg.sinks, cfg.window, scale)
+    return r
+
+
+def hba_attention_eval(q, k, v, cos, sin, cfg, summ, qkn, cap=None, hier=False, equiv=False):
+    """Gathered union attention with flat or hierarchical selection; `cap`
+    (the reference's memory cap for its chunk loop) is accepted and unused."""
+    if equiv:
+        raise NotImplementedError("equiv=True (dense uniform-RoPE attention) is not part of the "
+                                  "HBA operator")
+    return forward_stages(q, k, v, cos, sin, cfg, summ, qkn, hier=hier)["out"]
+
+
+def hba_attention_dense(q, k, v, cos, sin, cfg, summ, qkn, equiv=False):
+    """Forward of the reference's naive path: selection with route_topk's
+    scale (no temperature), attention with the union scale.  aux = 0."""
+    if equiv:
+        raise NotImplementedError("equiv=True (dense uniform-RoPE attention) is not part of the "
+                                  "HBA operator")
+    out = forward_stages(q, k, v, cos, sin, cfg, summ, qkn, dense_route=True)["out"]
+    return out, q.new_zeros(())
+
+
+def hba_attention_fused(q, k, v, cos, sin, cfg, summ, qkn):
+    """Forward of the reference's fused path (identical math to dense)."""
+    return hba_attention_dense(q, k, v, cos, sin, cfg, summ, qkn)
+
+
+def build_super(S0, fanout):
+    """attention.py:202-214 for summaries [B, Hkv, nb, m, d] (or [B, nb, m, d]):
+    returns (S1, ns) like the reference."""
+    squeeze = S0.dim() == 4
+    S = S0.unsqueeze(1) if squeeze else S0
+    S1 = ops.build_super(S, fanout)
+    return (S1.squeeze(1) if squeeze else S1), S1.shape[2]
+
+
+def selected_mask(idx, cnt, nb):
+    """Boolean selection mask [B, Hkv, n, nb] (route_topk's `sel`) from idx/cnt."""
+    B, Hkv, n, kk = idx.shape
+    valid = torch.arange(kk, device=idx.device)[None, None, None, :] < cnt[..., None]
+    sel = torch.zeros(B, Hkv, n, nb + 1, dtype=torch.bool, device=idx.device)
+    sel.scatter_(-1, torch.where(valid, idx.long(), nb), True)
+    return sel[..., :nb]

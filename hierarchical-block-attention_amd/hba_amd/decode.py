@@ -1,0 +1,113 @@
+"""Paged KV cache and the decode step.
+
+The reference has no decode path or KV cache.  The decode step here is row
+L-1 of hba_attention_eval (src/hba/attention.py:610-713) for a sequence of
+length L, served from a cache laid out for the operator:
+
+  kc_pages   [P, Hkv, 64, d]  QKNorm'd NoPE keys (normalised once, on append)
+  v_pages    [P, Hkv, 64, d]
+  summ_pages [P, Hkv, m, d]   slot summaries of full pages
+  page_table int32 [batch, max_pages]  logical page -> physical page
+  seq_lens   int32 [batch]    tokens in the cache (the current one included)
+
+Window keys are rotated in the kernel from kc with the caller's cos/sin
+tables, so the cache holds one key representation only.  A page's summary is
+written when the page fills; it is read only once the page has left the
+window.
+"""
+import torch
+
+from . import ops
+from .config import union_scale
+
+PAGE = ops.BLOCK
+
+
+class PagedKVCache:
+    def __init__(self, cfg, batch, max_len, dtype, device, num_pages=None):
+        self.cfg = cfg
+        self.batch = batch
+        self.max_len = max_len
+        self.max_pages = (max_len + PAGE - 1) // PAGE
+        P = num_pages if num_pages is not None else batch * self.max_pages
+        Hkv, d, m = cfg.n_kv, cfg.head_dim, cfg.slots
+        self.kc_pages = torch.zeros(P, Hkv, PAGE, d, dtype=dtype, device=device)
+        self.v_pages = torch.zeros(P, Hkv, PAGE, d, dtype=dtype, device=device)
+        self.summ_pages = torch.zeros(P, Hkv, m, d, dtype=dtype, device=device)
+        self.page_table = torch.zeros(batch, self.max_pages, dtype=torch.int32, device=device)
+        self.seq_lens = torch.zeros(batch, dtype=torch.int32, device=device)
+        self.lens = [0] * batch
+        self._table = [[] for _ in range(batch)]
+        self._free = list(range(P - 1, -1, -1))
+
+    def _ensure_pages(self, s, length):
+        need = (length + PAGE - 1) // PAGE
+        if need > self.max_pages:
+            raise ValueError(f"sequence {s}: length {length} exceeds max_len {self.max_len}")
+        new = []
+        while len(self._table[s]) < need:
+            if not self._free:
+                raise RuntimeError("paged KV cache is out of pages")
+            p = self._free.pop()
+            self._table[s].append(p)
+            new.append(p)
+        return new
+
+    def _sync_table(self):
+        rows = [t + [0] * (self.max_pages - len(t)) for t in self._table]
+        self.page_table.copy_(torch.tensor(rows, dtype=torch.int32))
+        self.seq_lens.copy_(torch.tensor(self.lens, dtype=torch.int32))
+
+    def load(self, s, kc_seq, v_seq, summ):
+        """Fill sequence s with already-QKNorm'd keys kc_seq [L, Hkv, d] and
+        values v_seq [L, Hkv, d] (a prefill's outputs), and summarise its full
+        pages.  Setup path: plain tensor copies."""
+        L = kc_seq.shape[0]
+        self._ensure_pages(s, L)
+        pages = torch.tensor(self._table[s], dtype=torch.long, device=self.kc_pages.device)
+        npg = (L + PAGE - 1) // PAGE
+        pad = npg * PAGE - L
+        kpad = torch.nn.functional.pad(kc_seq, (0, 0, 0, 0, 0, pad))
+        vpad = torch.nn.functional.pad(v_seq, (0, 0, 0, 0, 0, pad))
+        Hkv, d = kc_seq.shape[1], kc_seq.shape[2]
+        self.kc_pages[pages[:npg]] = kpad.view(npg, PAGE, Hkv, d).transpose(1, 2).to(self.kc_pages.dtype)
+        self.v_pages[pages[:npg]] = vpad.view(npg, PAGE, Hkv, d).transpose(1, 2).to(self.v_pages.dtype)
+        self.lens[s] = L
+        self._sync_table()
+        full = pages[: L // PAGE]
+        if full.numel():
+            ops.summarize_pages(self.kc_pages, full, summ.probes, summ.proj, self.summ_pages)
+
+    def append(self, k_new, v_new, qkn, summ):
+        """Append one token per sequence (raw k_new, v_new [batch, Hkv, d]):
+        QKNorm + write in the kernel; summarise the pages that just filled."""
+        for s in range(self.batch):
+            self._ensure_pages(s, self.lens[s] + 1)
+            self.lens[s] += 1
+        self._sync_table()
+        cfg = self.cfg
+        kg = qkn.k.gain if getattr(cfg, "qknorm", False) else None
+        keps = float(qkn.k.eps) if kg is not None else 1e-6
+        ops.kv_append(k_new, v_new, kg, keps, self.page_table, self.seq_lens, self.kc_pages, self.v_pages)
+        done = [self._table[s][self.lens[s] // PAGE - 1] for s in range(self.batch)
+                if self.lens[s] % PAGE == 0]
+        if done:
+            ops.summarize_pages(self.kc_pages, torch.tensor(done, dtype=torch.int32), summ.probes,
+                                summ.proj, self.summ_pages)
+
+    def scales(self, cfg=None):
+        cfg = cfg or self.cfg
+        return torch.tensor([union_scale(cfg, cfg.head_dim, max(L, 1)) for L in self.lens],
+                            dtype=torch.float32, device=self.kc_pages.device)
+
+
+def hba_decode_step(q, cache, cfg, qkn, cos, sin, scales=None):
+    """Union attention of each sequence's new query q [batch, Hq, d] (raw;
+    QKNorm and RoPE at position L-1 in the kernel) over the cache.  Returns
+    (out [batch, Hq, d], selected page ids [batch, Hkv, k], counts [batch, Hkv])."""
+    qg = qkn.q.gain if getattr(cfg, "qknorm", False) else None
+    qeps = float(qkn.q.eps) if qg is not None else 1e-6
+    sc = cache.scales(cfg) if scales is None else scales
+    max_len = max(cache.lens)
+    return ops.decode_fwd(q, qg, qeps, cache.kc_pages, cache.v_pages, cache.summ_pages, cache.page_table,
+                          cache.seq_lens, cos, sin, sc, cfg.sinks, cfg.window, cfg.k_blocks, max_len)

@@ -1,0 +1,314 @@
+"""torch.library custom ops over the C-ABI (namespace `hba`).
+
+Every op is registered for the CUDA (ROCm/HIP) dispatch key only and has a
+fake (meta) implementation for tracing; CPU tensors raise -- there is no CPU
+path.  Kernels run asynchronously on the current HIP stream of the tensors'
+device.
+
+    hba::prep_keys        QKNorm(k), RoPE(kc), V^T
+    hba::summarize        slot summaries of every 64-key block
+    hba::build_super      super-summaries (fanout mean)
+    hba::score_select     flat top-k block selection
+    hba::hier_select      two-level beam selection
+    hba::attn_fwd         union attention forward (prefill)
+    hba::kv_append        paged-cache append (mutates the pages)
+    hba::summarize_pages  summaries of listed pages (mutates summ_pages)
+    hba::decode_fwd       decode step over the paged cache
+"""
+import ctypes
+from typing import Optional, Tuple
+
+import torch
+from torch import Tensor
+
+from ._lib import BF16, F32, check, lib, strides3
+
+BLOCK = 64
+_DT = {torch.float32: F32, torch.bfloat16: BF16}
+_CHECKED = set()
+
+
+def _code(t):
+    if t.dtype not in _DT:
+        raise TypeError(f"unsupported dtype {t.dtype}: HBA kernels take float32 or bfloat16")
+    return _DT[t.dtype]
+
+
+def _p(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(dev):
+    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
+def _dev(t):
+    if t.device.type != "cuda":
+        raise RuntimeError("hba ops run on a gfx950 GPU only; got a tensor on " + str(t.device))
+    idx = t.device.index if t.device.index is not None else torch.cuda.current_device()
+    if idx not in _CHECKED:
+        with torch.cuda.device(idx):
+            check(lib().hba_device_check(), "hba_device_check")
+        _CHECKED.add(idx)
+    return t.device
+
+
+def _f32c(t, dev, n=None, what="tensor"):
+    """fp32 contiguous copy/view on `dev` (gains, probes, proj, tables)."""
+    if t is None:
+        return None
+    t = t.detach().to(device=dev, dtype=torch.float32).contiguous()
+    if n is not None and t.numel() != n:
+        raise ValueError(f"{what}: expected {n} elements, got {t.numel()}")
+    return t
+
+
+def _rows(t, what):
+    if t.dim() != 4 or t.stride(3) != 1:
+        raise ValueError(f"{what}: expected a [B, n, H, d] view with a contiguous last dim")
+    return t
+
+
+def _tables(cos, sin, n, d, dev):
+    if cos.shape[-1] != d or cos.shape[0] < n or sin.shape != cos.shape:
+        raise ValueError(f"cos/sin: expected [>= {n}, {d}] tables, got {tuple(cos.shape)}")
+    return _f32c(cos, dev), _f32c(sin, dev)
+
+
+# ------------------------------------------------------------------ prep ----
+@torch.library.custom_op("hba::prep_keys", mutates_args=(), device_types="cuda")
+def prep_keys(k: Tensor, v: Tensor, k_gain: Optional[Tensor], eps: float, cos: Tensor,
+              sin: Tensor) -> Tuple[Tensor, Tensor, Tensor]:
+    dev = _dev(k)
+    _rows(k, "k")
+    _rows(v, "v")
+    B, n, Hkv, d = k.shape
+    if v.shape != k.shape or v.dtype != k.dtype:
+        raise ValueError("v must match k in shape and dtype")
+    cos, sin = _tables(cos, sin, n, d, dev)
+    kg = _f32c(k_gain, dev, Hkv, "k_gain")
+    kc = torch.empty(B, Hkv, n, d, dtype=k.dtype, device=dev)
+    kr = torch.empty_like(kc)
+    vt = torch.empty(B, Hkv, d, n, dtype=k.dtype, device=dev)
+    with torch.cuda.device(dev):
+        st = lib().hba_prep_keys(_code(k), _p(k), strides3(k), _p(v), strides3(v), _p(kg), eps,
+                                 _p(cos), _p(sin), B, n, Hkv, d, _p(kc), _p(kr), _p(vt), _stream(dev))
+    check(st, "hba_prep_keys")
+    return kc, kr, vt
+
+
+@prep_keys.register_fake
+def _(k, v, k_gain, eps, cos, sin):
+    B, n, Hkv, d = k.shape
+    kc = k.new_empty(B, Hkv, n, d)
+    return kc, k.new_empty(B, Hkv, n, d), k.new_empty(B, Hkv, d, n)
+
+
+@torch.library.custom_op("hba::summarize", mutates_args=(), device_types="cuda")
+def summarize(kc: Tensor, probes: Tensor, proj: Tensor) -> Tensor:
+    dev = _dev(kc)
+    B, Hkv, n, d = kc.shape
+    if not kc.is_contiguous():
+        raise ValueError("kc must be contiguous [B, Hkv, n, d]")
+    m = probes.shape[1]
+    pr = _f32c(probes, dev, Hkv * m * d, "probes")
+    pj = _f32c(proj, dev, Hkv * d * d, "proj")
+    out = torch.empty(B, Hkv, n // BLOCK, m, d, dtype=kc.dtype, device=dev)
+    with torch.cuda.device(dev):
+        st = lib().hba_summarize(_code(kc), _p(kc), B, Hkv, n, d, BLOCK, _p(pr), _p(pj), m, _p(out),
+                                 _stream(dev))
+    check(st, "hba_summarize")
+    return out
+
+
+@summarize.register_fake
+def _(kc, probes, proj):
+    B, Hkv, n, d = kc.shape
+    return kc.new_empty(B, Hkv, n // BLOCK, probes.shape[1], d)
+
+
+@torch.library.custom_op("hba::build_super", mutates_args=(), device_types="cuda")
+def build_super(S0: Tensor, fanout: int) -> Tensor:
+    dev = _dev(S0)
+    S0 = S0.contiguous()
+    B, Hkv, nb, m, d = S0.shape
+    ns = (nb + fanout - 1) // fanout
+    out = torch.empty(B, Hkv, ns, m, d, dtype=S0.dtype, device=dev)
+    with torch.cuda.device(dev):
+        st = lib().hba_build_super(_code(S0), _p(S0), B, Hkv, nb, m, d, fanout, _p(out), _stream(dev))
+    check(st, "hba_build_super")
+    return out
+
+
+@build_super.register_fake
+def _(S0, fanout):
+    B, Hkv, nb, m, d = S0.shape
+    return S0.new_empty(B, Hkv, (nb + fanout - 1) // fanout, m, d)
+
+
+# ------------------------------------------------------------- selection ----
+def _sel_out(q, Hkv, k):
+    B, n = q.shape[0], q.shape[1]
+    return (torch.empty(B, Hkv, n, k, dtype=torch.int32, device=q.device),
+            torch.empty(B, Hkv, n, k, dtype=torch.float32, device=q.device),
+            torch.empty(B, Hkv, n, dtype=torch.int32, device=q.device))
+
+
+@torch.library.custom_op("hba::score_select", mutates_args=(), device_types="cuda")
+def score_select(q: Tensor, q_gain: Optional[Tensor], eps: float, S0: Tensor, window: int, k: int,
+                 scale: float) -> Tuple[Tensor, Tensor, Tensor]:
+    dev = _dev(q)
+    _rows(q, "q")
+    B, n, Hq, d = q.shape
+    S0 = S0.contiguous()
+    Hkv, nb, m = S0.shape[1], S0.shape[2], S0.shape[3]
+    if S0.shape[0] != B or S0.shape[4] != d or S0.dtype != q.dtype or nb != n // BLOCK:
+        raise ValueError(f"S0 {tuple(S0.shape)} does not match q {tuple(q.shape)}")
+    qg = _f32c(q_gain, dev, Hq, "q_gain")
+    idx, val, cnt = _sel_out(q, Hkv, k)
+    with torch.cuda.device(dev):
+        st = lib().hba_score_select(_code(q), _p(q), strides3(q), _p(qg), eps, _p(S0), B, n, Hq, Hkv, d,
+                                    m, BLOCK, window, k, scale, _p(idx), _p(val), _p(cnt), _stream(dev))
+    check(st, "hba_score_select")
+    return idx, val, cnt
+
+
+@score_select.register_fake
+def _(q, q_gain, eps, S0, window, k, scale):
+    B, n = q.shape[0], q.shape[1]
+    Hkv = S0.shape[1]
+    return (q.new_empty(B, Hkv, n, k, dtype=torch.int32), q.new_empty(B, Hkv, n, k, dtype=torch.float32),
+            q.new_empty(B, Hkv, n, dtype=torch.int32))
+
+
+@torch.library.custom_op("hba::hier_select", mutates_args=(), device_types="cuda")
+def hier_select(q: Tensor, q_gain: Optional[Tensor], eps: float, S0: Tensor, S1: Tensor, window: int,
+                k: int, fanout: int, beam: int, scale: float) -> Tuple[Tensor, Tensor, Tensor]:
+    dev = _dev(q)
+    _rows(q, "q")
+    B, n, Hq, d = q.shape
+    S0 = S0.contiguous()
+    S1 = S1.contiguous()
+    Hkv, nb, m = S0.shape[1], S0.shape[2], S0.shape[3]
+    if nb != n // BLOCK or S1.shape[2] != (nb + fanout - 1) // fanout:
+        raise ValueError("S0/S1 do not match q and fanout")
+    qg = _f32c(q_gain, dev, Hq, "q_gain")
+    idx, val, cnt = _sel_out(q, Hkv, k)
+    with torch.cuda.device(dev):
+        st = lib().hba_hier_select(_code(q), _p(q), strides3(q), _p(qg), eps, _p(S0), _p(S1), B, n, Hq,
+                                   Hkv, d, m, BLOCK, window, k, fanout, beam, scale, _p(idx), _p(val),
+                                   _p(cnt), _stream(dev))
+    check(st, "hba_hier_select")
+    return idx, val, cnt
+
+
+@hier_select.register_fake
+def _(q, q_gain, eps, S0, S1, window, k, fanout, beam, scale):
+    B, n = q.shape[0], q.shape[1]
+    Hkv = S0.shape[1]
+    return (q.new_empty(B, Hkv, n, k, dtype=torch.int32), q.new_empty(B, Hkv, n, k, dtype=torch.float32),
+            q.new_empty(B, Hkv, n, dtype=torch.int32))
+
+
+# ------------------------------------------------------------- attention ----
+@torch.library.custom_op("hba::attn_fwd", mutates_args=(), device_types="cuda")
+def attn_fwd(q: Tensor, q_gain: Optional[Tensor], eps: float, kc: Tensor, kr: Tensor, vt: Tensor,
+             cos: Tensor, sin: Tensor, idx: Tensor, cnt: Tensor, sinks: int, window: int,
+             scale: float) -> Tensor:
+    dev = _dev(q)
+    _rows(q, "q")
+    B, n, Hq, d = q.shape
+    Hkv = kc.shape[1]
+    if kc.shape != (B, Hkv, n, d) or kr.shape != kc.shape or vt.shape != (B, Hkv, d, n):
+        raise ValueError("kc/kr/vt do not match q")
+    if idx.shape[:3] != (B, Hkv, n) or cnt.shape != (B, Hkv, n):
+        raise ValueError("idx/cnt do not match q")
+    if idx.dtype != torch.int32 or cnt.dtype != torch.int32:
+        raise TypeError("idx/cnt must be int32")
+    cos, sin = _tables(cos, sin, n, d, dev)
+    qg = _f32c(q_gain, dev, Hq, "q_gain")
+    idx = idx.contiguous()
+    cnt = cnt.contiguous()
+    out = torch.empty(B, n, Hq, d, dtype=q.dtype, device=dev)
+    with torch.cuda.device(dev):
+        st = lib().hba_attn_fwd(_code(q), _p(q), strides3(q), _p(qg), eps, _p(kc.contiguous()),
+                                _p(kr.contiguous()), _p(vt.contiguous()), _p(cos), _p(sin), _p(idx),
+                                _p(cnt), B, n, Hq, Hkv, d, sinks, window, BLOCK, idx.shape[3], scale,
+                                _p(out), strides3(out), _stream(dev))
+    check(st, "hba_attn_fwd")
+    return out
+
+
+@attn_fwd.register_fake
+def _(q, q_gain, eps, kc, kr, vt, cos, sin, idx, cnt, sinks, window, scale):
+    return q.new_empty(q.shape)
+
+
+# ---------------------------------------------------------------- decode ----
+@torch.library.custom_op("hba::kv_append", mutates_args=("kc_pages", "v_pages"), device_types="cuda")
+def kv_append(k_new: Tensor, v_new: Tensor, k_gain: Optional[Tensor], eps: float, page_table: Tensor,
+              seq_lens: Tensor, kc_pages: Tensor, v_pages: Tensor) -> None:
+    dev = _dev(k_new)
+    Bd, Hkv, d = k_new.shape
+    kg = _f32c(k_gain, dev, Hkv, "k_gain")
+    with torch.cuda.device(dev):
+        st = lib().hba_kv_append(_code(k_new), _p(k_new.contiguous()), _p(v_new.contiguous()), _p(kg), eps,
+                                 _p(page_table), page_table.shape[1], _p(seq_lens), Bd, Hkv, d, BLOCK,
+                                 _p(kc_pages), _p(v_pages), _stream(dev))
+    check(st, "hba_kv_append")
+
+
+@torch.library.custom_op("hba::summarize_pages", mutates_args=("summ_pages",), device_types="cuda")
+def summarize_pages(kc_pages: Tensor, pages: Tensor, probes: Tensor, proj: Tensor,
+                    summ_pages: Tensor) -> None:
+    dev = _dev(kc_pages)
+    P, Hkv, Bk, d = kc_pages.shape
+    m = probes.shape[1]
+    pr = _f32c(probes, dev, Hkv * m * d, "probes")
+    pj = _f32c(proj, dev, Hkv * d * d, "proj")
+    pages = pages.to(device=dev, dtype=torch.int32).contiguous()
+    with torch.cuda.device(dev):
+        st = lib().hba_summarize_pages(_code(kc_pages), _p(kc_pages), _p(pages), pages.numel(), Hkv, d, Bk,
+                                       _p(pr), _p(pj), m, _p(summ_pages), _stream(dev))
+    check(st, "hba_summarize_pages")
+
+
+def decode_workspace_bytes(Bd, Hq, Hkv, d, k, window, max_len):
+    n = ctypes.c_size_t(0)
+    check(lib().hba_decode_workspace_size(Bd, Hq, Hkv, d, k, BLOCK, window, max_len, ctypes.byref(n)),
+          "hba_decode_workspace_size")
+    return int(n.value)
+
+
+@torch.library.custom_op("hba::decode_fwd", mutates_args=(), device_types="cuda")
+def decode_fwd(q: Tensor, q_gain: Optional[Tensor], eps: float, kc_pages: Tensor, v_pages: Tensor,
+               summ_pages: Tensor, page_table: Tensor, seq_lens: Tensor, cos: Tensor, sin: Tensor,
+               scales: Tensor, sinks: int, window: int, k: int,
+               max_len: int) -> Tuple[Tensor, Tensor, Tensor]:
+    dev = _dev(q)
+    Bd, Hq, d = q.shape
+    Hkv, m = summ_pages.shape[1], summ_pages.shape[2]
+    cos, sin = _tables(cos, sin, max_len, d, dev)
+    qg = _f32c(q_gain, dev, Hq, "q_gain")
+    sc = _f32c(scales, dev, Bd, "scales")
+    q = q.contiguous()
+    out = torch.empty_like(q)
+    sel_idx = torch.empty(Bd, Hkv, k, dtype=torch.int32, device=dev)
+    sel_cnt = torch.empty(Bd, Hkv, dtype=torch.int32, device=dev)
+    nbytes = decode_workspace_bytes(Bd, Hq, Hkv, d, k, window, max_len)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev):
+        st = lib().hba_decode_fwd(_code(q), _p(q), _p(qg), eps, _p(kc_pages), _p(v_pages), _p(summ_pages),
+                                  _p(page_table), page_table.shape[1], _p(seq_lens), _p(cos), _p(sin),
+                                  _p(sc), Bd, Hq, Hkv, d, m, sinks, window, BLOCK, k, max_len, _p(ws),
+                                  nbytes, _p(out), _p(sel_idx), _p(sel_cnt), _stream(dev))
+    check(st, "hba_decode_fwd")
+    return out, sel_idx, sel_cnt
+
+
+@decode_fwd.register_fake
+def _(q, q_gain, eps, kc_pages, v_pages, summ_pages, page_table, seq_lens, cos, sin, scales, sinks,
+      window, k, max_len):
+    Bd, Hkv = q.shape[0], summ_pages.shape[1]
+    return (q.new_empty(q.shape), q.new_empty(Bd, Hkv, k, dtype=torch.int32),
+            q.new_empty(Bd, Hkv, dtype=torch.int32))

@@ -1,0 +1,203 @@
+/*
+ * hba_amd.h -- C-ABI of the MI355X (gfx950) Hierarchical Block Attention
+ * forward path.
+ *
+ * Conventions
+ *   - Every pointer argument named as a tensor is a DEVICE pointer; stride and
+ *     size arguments are host values in ELEMENTS.  No C++ types cross the
+ *     boundary.
+ *   - `dtype` is HBA_DTYPE_F32 or HBA_DTYPE_BF16 and applies to the q/k/v and
+ *     summary tensors; gains, probes, proj, RoPE tables, scores and scales are
+ *     always fp32; indices are int32.
+ *   - All calls are asynchronous on `stream` (a hipStream_t; NULL = the null
+ *     stream).  No call allocates memory, keeps global mutable state or
+ *     synchronises; calls on distinct streams are independent.  Scratch space
+ *     (decode only) is passed in by the caller, sized by the *_workspace_size
+ *     query.
+ *   - Return value: HBA_OK (0) or a negative status (invalid argument,
+ *     unsupported shape/dtype/architecture, launch failure);
+ *     hba_status_string() names it.  Nothing is launched when a status other
+ *     than HBA_OK or HBA_ERR_LAUNCH is returned.
+ *   - Layouts: q [B, n, Hq, d] and k, v [B, n, Hkv, d] are the reference's
+ *     token-major views (model.py:121-123) with arbitrary strides for the
+ *     first three dims and a contiguous last dim; prepared keys are
+ *     head-major: kc, kr [B, Hkv, n, d], vt [B, Hkv, d, n]; summaries
+ *     S0 [B, Hkv, nb, m, d], supers S1 [B, Hkv, ns, m, d]; selections
+ *     idx, val [B, Hkv, n, k] and cnt [B, Hkv, n].
+ *   - Head h uses KV head h / (Hq / Hkv) (heads group-contiguous,
+ *     summarizer.py:50-54).
+ */
+#ifndef HBA_AMD_H
+#define HBA_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HBA_ABI_VERSION 1
+
+enum {
+    HBA_OK = 0,
+    HBA_ERR_INVALID_ARG = -1,   /* null pointer, bad size, n % block != 0, ... */
+    HBA_ERR_UNSUPPORTED = -2,   /* shape/dtype outside what the kernels implement */
+    HBA_ERR_DEVICE = -3,        /* no device, or the current device is not gfx950 */
+    HBA_ERR_LAUNCH = -4         /* the kernel launch itself failed */
+};
+
+enum { HBA_DTYPE_F32 = 0, HBA_DTYPE_BF16 = 1 };
+
+/* Version of this ABI (HBA_ABI_VERSION). */
+int hba_abi_version(void);
+
+/* Static description of a status code. */
+const char *hba_status_string(int status);
+
+/* HBA_OK when the current HIP device is a gfx950 (MI355X-class) GPU. */
+int hba_device_check(void);
+
+/*
+ * Key preparation: QKNorm of k (per-head RMS normalisation, scalar gain; the
+ * key half of _content_qk), its RoPE rotation for the window branch, and V
+ * transposed for the attention kernel.
+ *   replaces: _HeadRMSNorm.forward  src/hba/attention.py:88-94 (via _content_qk :185)
+ *             apply_rope            src/hba/attention.py:40-44 (k_rope, :633)
+ * k_gain == NULL means qknorm=False (kc = k unchanged).  cos_tab/sin_tab are
+ * fp32 [>= n, d] tables (rope_tables, attention.py:27-32).  kr or vt may be
+ * NULL when not needed.
+ */
+int hba_prep_keys(int dtype, const void *k, const int64_t k_strides[3],
+                  const void *v, const int64_t v_strides[3],
+                  const float *k_gain, float eps,
+                  const float *cos_tab, const float *sin_tab,
+                  int64_t B, int64_t n, int64_t Hkv, int64_t d,
+                  void *kc, void *kr, void *vt, void *stream);
+
+/*
+ * Slot summaries of every full block of kc.
+ *   replaces: SlotSummarizer.summarize  src/hba/summarizer.py:34-42
+ * probes fp32 [Hkv, m, d]; proj fp32 [Hkv, d, d]; S0 [B, Hkv, n/Bk, m, d].
+ */
+int hba_summarize(int dtype, const void *kc, int64_t B, int64_t Hkv, int64_t n,
+                  int64_t d, int64_t Bk, const float *probes, const float *proj,
+                  int64_t m, void *S0, void *stream);
+
+/*
+ * Super-summaries: per-slot mean of `fanout` consecutive block summaries.
+ *   replaces: build_super  src/hba/attention.py:202-214
+ * S1 [B, Hkv, ceil(nb/fanout), m, d].
+ */
+int hba_build_super(int dtype, const void *S0, int64_t B, int64_t Hkv, int64_t nb,
+                    int64_t m, int64_t d, int64_t fanout, void *S1, void *stream);
+
+/*
+ * Flat block selection: QKNorm of q, grouped routing query, slot scores
+ * (max over slots, times `scale`), candidate mask, top-k per (query, KV head)
+ * with ties broken by lowest block index.
+ *   replaces: route_topk            src/hba/attention.py:272-303
+ *             eval flat selection   src/hba/attention.py:695-698
+ *             grouped_query / slot_block_scores  src/hba/summarizer.py:45-54
+ * q_gain == NULL means qknorm=False.  Invalid picks (fewer than k
+ * candidates) get idx -1 / val -inf; cnt holds the number of valid picks.
+ * 1 <= k <= 64.
+ */
+int hba_score_select(int dtype, const void *q, const int64_t q_strides[3],
+                     const float *q_gain, float eps, const void *S0,
+                     int64_t B, int64_t n, int64_t Hq, int64_t Hkv, int64_t d,
+                     int64_t m, int64_t Bk, int64_t W, int64_t k, float scale,
+                     int32_t *idx, float *val, int32_t *cnt, void *stream);
+
+/*
+ * Two-level selection: score the super-summaries, keep the top
+ * min(beam, ns) supers that hold a candidate, score their children, keep the
+ * top min(k, beam*fanout).  Same outputs and tie rule as hba_score_select.
+ *   replaces: hier_select  src/hba/attention.py:217-246 (eval :690-693)
+ * 1 <= beam <= 16, fanout <= 64.
+ */
+int hba_hier_select(int dtype, const void *q, const int64_t q_strides[3],
+                    const float *q_gain, float eps, const void *S0, const void *S1,
+                    int64_t B, int64_t n, int64_t Hq, int64_t Hkv, int64_t d,
+                    int64_t m, int64_t Bk, int64_t W, int64_t k, int64_t fanout,
+                    int64_t beam, float scale, int32_t *idx, float *val, int32_t *cnt,
+                    void *stream);
+
+/*
+ * Union attention forward: one softmax per (query, head) over the NoPE sinks
+ * j < min(S, i+1), the RoPE window max(S, i-W+1) <= j <= i, and the NoPE keys
+ * of the valid selected blocks idx[b, h/G, i, 0..cnt).
+ *   replaces: hba_attention_dense forward  src/hba/attention.py:306-356
+ *             hba_attention_eval           src/hba/attention.py:610-713
+ *             hba_attention_fused forward  src/hba/attention.py:552-603
+ * q is the raw query (QKNorm and RoPE are applied in the kernel); kc, kr, vt
+ * come from hba_prep_keys.  `scale` is the union scale (content scale times
+ * the log-length temperature).  out [B, n, Hq, d] with out_strides.
+ * Requires S <= Bk and n % Bk == 0; Bk == 64 and d in {64, 128}.
+ */
+int hba_attn_fwd(int dtype, const void *q, const int64_t q_strides[3],
+                 const float *q_gain, float eps,
+                 const void *kc, const void *kr, const void *vt,
+                 const float *cos_tab, const float *sin_tab,
+                 const int32_t *idx, const int32_t *cnt,
+                 int64_t B, int64_t n, int64_t Hq, int64_t Hkv, int64_t d,
+                 int64_t S, int64_t W, int64_t Bk, int64_t k, float scale,
+                 void *out, const int64_t out_strides[3], void *stream);
+
+/*
+ * Paged KV cache (decode).  Page = Bk tokens of one sequence; all tensors
+ * page-major:  kc_pages, v_pages [P, Hkv, Bk, d] (kc = QKNorm'd NoPE keys),
+ * summ_pages [P, Hkv, m, d] (slot summaries of full pages);
+ * page_table int32 [Bd, max_pages] (logical page -> physical page);
+ * seq_lens int32 [Bd] (tokens already in the cache, including the current one).
+ * There is no reference function for these: the decode step is defined as row
+ * L-1 of hba_attention_eval (src/hba/attention.py:610-713) for a sequence of
+ * length L.
+ */
+
+/*
+ * Append one token per sequence at position seq_lens[s]-1: QKNorm of k_new
+ * (as hba_prep_keys) into kc_pages, v_new into v_pages.  k_new, v_new
+ * [Bd, Hkv, d] contiguous.  k_gain == NULL means qknorm=False.
+ */
+int hba_kv_append(int dtype, const void *k_new, const void *v_new, const float *k_gain,
+                  float eps, const int32_t *page_table, int64_t max_pages,
+                  const int32_t *seq_lens, int64_t Bd, int64_t Hkv, int64_t d, int64_t Bk,
+                  void *kc_pages, void *v_pages, void *stream);
+
+/*
+ * Slot summaries of the listed physical pages (SlotSummarizer.summarize on
+ * one block each): pages int32 [npages]; writes summ_pages[pages[i]].
+ */
+int hba_summarize_pages(int dtype, const void *kc_pages, const int32_t *pages,
+                        int64_t npages, int64_t Hkv, int64_t d, int64_t Bk,
+                        const float *probes, const float *proj, int64_t m,
+                        void *summ_pages, void *stream);
+
+/* Scratch bytes hba_decode_fwd needs for these sizes (max_len = max seq_len). */
+int hba_decode_workspace_size(int64_t Bd, int64_t Hq, int64_t Hkv, int64_t d, int64_t k,
+                              int64_t Bk, int64_t W, int64_t max_len, size_t *bytes);
+
+/*
+ * Decode step: for each sequence s of length L = seq_lens[s], the union
+ * attention of its new query q[s] (raw; QKNorm and RoPE at position L-1 are
+ * applied in the kernel) over the cached keys, with flat top-k selection
+ * over the full pages that lie before the window.  scales fp32 [Bd] holds
+ * each sequence's union scale (content scale times the temperature at n=L).
+ * out [Bd, Hq, d].  Optional sel_idx int32 [Bd, Hkv, k] / sel_cnt
+ * int32 [Bd, Hkv] receive the selection (NULL to skip).
+ */
+int hba_decode_fwd(int dtype, const void *q, const float *q_gain, float eps,
+                   const void *kc_pages, const void *v_pages, const void *summ_pages,
+                   const int32_t *page_table, int64_t max_pages, const int32_t *seq_lens,
+                   const float *cos_tab, const float *sin_tab, const float *scales,
+                   int64_t Bd, int64_t Hq, int64_t Hkv, int64_t d, int64_t m,
+                   int64_t S, int64_t W, int64_t Bk, int64_t k, int64_t max_len,
+                   void *workspace, size_t ws_bytes, void *out,
+                   int32_t *sel_idx, int32_t *sel_cnt, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HBA_AMD_H */

@@ -1,0 +1,60 @@
+"""The C-ABI library loads and exports every entry point include/hba_amd.h
+declares (no compute calls: this runs without a GPU)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+import hba_amd
+from hba_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_symbols():
+    src = open(os.path.join(ROOT, "include", "hba_amd.h")).read()
+    return sorted(set(re.findall(r"^(?:int|const char \*)\s*(hba_\w+)\(", src, flags=re.M)))
+
+
+def test_every_declared_symbol_is_exported():
+    names = declared_symbols()
+    assert len(names) >= 13
+    L = ctypes.CDLL(_lib.LIB_PATH)
+    missing = [n for n in names if not hasattr(L, n)]
+    assert not missing, missing
+
+
+def test_binding_table_covers_the_header():
+    assert sorted(_lib.SIGNATURES) == declared_symbols()
+
+
+def test_static_queries_without_a_gpu():
+    L = _lib.lib()
+    assert L.hba_abi_version() == 1
+    assert L.hba_status_string(0) == b"ok"
+    assert L.hba_status_string(-1) == b"invalid argument"
+    n = ctypes.c_size_t(0)
+    assert L.hba_decode_workspace_size(32, 14, 2, 64, 16, 64, 1024, 32768, ctypes.byref(n)) == 0
+    assert n.value > 0
+    assert L.hba_decode_workspace_size(32, 14, 2, 64, 16, 32, 1024, 32768, ctypes.byref(n)) == -2
+
+
+def test_ops_refuse_cpu_tensors():
+    import torch
+    q = torch.zeros(1, 64, 2, 64)
+    with pytest.raises(NotImplementedError):
+        hba_amd.ops.score_select(q, None, 1e-6, torch.zeros(1, 1, 1, 4, 64), 16, 4, 0.1)
+
+
+def test_argument_checks_run_before_any_launch():
+    """Invalid sizes are rejected on the host with no device pointer touched."""
+    L = _lib.lib()
+    s3 = (ctypes.c_int64 * 3)(0, 0, 0)
+    fake = ctypes.c_void_p(16)
+    st = L.hba_attn_fwd(1, fake, s3, None, 1e-6, fake, fake, fake, fake, fake, fake, fake, 1, 100, 14,
+                        2, 64, 4, 1024, 64, 16, 0.1, fake, s3, None)
+    assert st == -1                                    # n % 64 != 0
+    st = L.hba_score_select(1, fake, s3, None, 1e-6, fake, 1, 128, 14, 2, 96, 4, 64, 1024, 16, 0.1,
+                            fake, fake, fake, None)
+    assert st == -2                                    # d = 96 unsupported
