@@ -1,0 +1,288 @@
+"""HBA layer forward benchmark on one MI355X.
+
+Step = one HBA attention layer forward at 32K context (B=1, n=32768, 14 query
+/ 2 KV heads, d=64, 4 sinks, RoPE window 1024, 64-token blocks, 4 slots,
+top-16, bf16, 16 needle blocks per KV head): key preparation, slot summaries,
+flat block selection and the union attention, all HIP kernels, inputs resident
+in HBM.  `value` = tokens/s of that forward.  The JSON line also carries the
+roofline of the dominant kernel (the union attention, MFMA-bound), the
+per-stage times, the 32K decode step (B=32 sequences, paged bf16 cache) as
+µs/step against the HBM roofline, and the oracle's CPU restatement timed on a
+bounded sample of the same workload.
+
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-decode]
+"""
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "hierarchical-block-attention_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+PEAK_BF16_TFLOPS = 2500.0     # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
+
+WORKLOAD = dict(workload="hba_layer_fwd_32k", batch=1, seq_len=32768, q_heads=14, kv_heads=2,
+                head_dim=64, sinks=4, window=1024, block=64, slots=4, top_k=16, needles=16,
+                qknorm="sharp gains d**0.25", selection="flat")
+DECODE = dict(batch=32, len_lo=16384, len_hi=32768, seed=0)
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor()
+
+
+def layer_setup(dev):
+    import torch
+    import hba_amd
+    from hba_amd import synth
+    w = WORKLOAD
+    cfg = hba_amd.HBAConfig(n_heads=w["q_heads"], n_kv=w["kv_heads"], head_dim=w["head_dim"],
+                            sinks=w["sinks"], window=w["window"], block=w["block"], slots=w["slots"],
+                            k_blocks=w["top_k"])
+    x = synth.layer_inputs(w["batch"], w["seq_len"], w["q_heads"], w["kv_heads"], w["head_dim"],
+                           m=w["slots"], dtype=torch.bfloat16, device=dev, seed=0, sharp=True,
+                           needles=True, window=w["window"])
+    prm = synth.Params(x["q_gain"], x["k_gain"], x["probes"], x["proj"])
+    cos, sin = hba_amd.rope_tables(w["seq_len"], w["head_dim"], cfg.rope_theta, dev)
+    return cfg, x, prm, cos, sin
+
+
+def run_layer(cfg, x, prm, cos, sin, ev=None):
+    """One layer forward; with `ev` (dict of event pairs) each stage is bracketed."""
+    from hba_amd import ops
+    qeps = keps = 1e-6
+
+    def mark(name, i):
+        if ev is not None:
+            ev[name][i].record()
+    n = x["q"].shape[1]
+    d = x["q"].shape[3]
+    from hba_amd.config import union_scale
+    scale = union_scale(cfg, d, n)
+    mark("prep", 0)
+    kc, kr, vt = ops.prep_keys(x["k"], x["v"], prm.k.gain, keps, cos, sin)
+    mark("prep", 1)
+    mark("summ", 0)
+    S0 = ops.summarize(kc, prm.probes, prm.proj)
+    mark("summ", 1)
+    mark("select", 0)
+    idx, val, cnt = ops.score_select(x["q"], prm.q.gain, qeps, S0, cfg.window, cfg.k_blocks, scale)
+    mark("select", 1)
+    mark("attn", 0)
+    out = ops.attn_fwd(x["q"], prm.q.gain, qeps, kc, kr, vt, cos, sin, idx, cnt, cfg.sinks, cfg.window,
+                       scale)
+    mark("attn", 1)
+    return out
+
+
+def bench_layer(dev, steps, warmup):
+    import torch
+    from hba_amd import synth
+    cfg, x, prm, cos, sin = layer_setup(dev)
+    for _ in range(warmup):
+        run_layer(cfg, x, prm, cos, sin)
+    torch.cuda.synchronize()
+    names = ("prep", "summ", "select", "attn")
+    evs = [{k: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for k in names}
+           for _ in range(steps)]
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    wall0 = time.perf_counter()
+    t0.record()
+    for s in range(steps):
+        run_layer(cfg, x, prm, cos, sin, evs[s])
+    t1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    ms = t0.elapsed_time(t1) / steps
+    stage = {k: sum(e[k][0].elapsed_time(e[k][1]) for e in evs) / steps for k in names}
+    w = WORKLOAD
+    n = w["seq_len"]
+    attn_flop = synth.attention_flops(w["batch"], n, w["q_heads"], w["head_dim"], w["sinks"],
+                                      w["window"], w["block"], w["top_k"])
+    score_flop = synth.scoring_flops(w["batch"], n, w["kv_heads"], w["head_dim"], w["slots"],
+                                     w["block"], w["window"])
+    summ_flop = synth.summarizer_flops(w["batch"], n, w["kv_heads"], w["head_dim"], w["slots"],
+                                       w["block"])
+    return dict(ms=ms, wall_s=wall, stage_ms=stage, attn_flop=attn_flop, score_flop=score_flop,
+                summ_flop=summ_flop, tokens=w["batch"] * n,
+                mean_keys=synth.mean_keys(n, w["sinks"], w["window"], w["block"], w["top_k"]),
+                cfg=cfg, x=x, prm=prm, cos=cos, sin=sin)
+
+
+def decode_bytes(lens, Hkv, d, m, S, W, k, Hq, esize=2):
+    """Algorithmic HBM bytes of one decode step: per (sequence, KV head) the K
+    and V rows of the attended union plus the candidate summaries; plus q and o."""
+    from hba_amd.synth import ncand
+    tot = 0
+    for L in lens:
+        i = L - 1
+        nc = ncand(i, 64, W)
+        keys = min(S, i + 1) + max(0, i - max(S, i - W + 1) + 1) + min(k, nc) * 64
+        tot += Hkv * (keys * 2 * d * esize + nc * m * d * esize)
+    tot += 2 * len(lens) * Hq * d * esize
+    return tot
+
+
+def bench_decode(dev, iters=200):
+    import torch
+    import hba_amd
+    from hba_amd import ops, synth
+    Bd = DECODE["batch"]
+    Hq, Hkv, d, m, S, W, k = 14, 2, 64, 4, 4, 1024, 16
+    cfg = hba_amd.HBAConfig(n_heads=Hq, n_kv=Hkv, head_dim=d, slots=m, sinks=S, window=W, k_blocks=k)
+    lens = synth.decode_lengths(Bd, DECODE["len_lo"], DECODE["len_hi"], seed=DECODE["seed"])
+    Lmax = max(lens)
+    cache = hba_amd.PagedKVCache(cfg, Bd, Lmax, torch.bfloat16, dev)
+    cache._free = synth.shuffled_pages(len(cache._free), seed=1)
+    g = torch.Generator().manual_seed(0)
+    probes = torch.randn(Hkv, m, d, generator=g) * d ** -0.5
+    proj = torch.eye(d).unsqueeze(0).repeat(Hkv, 1, 1) + torch.randn(Hkv, d, d, generator=g) * 0.02
+    gq = torch.full((Hq,), d ** 0.25, device=dev)
+    gk = torch.full((Hkv,), d ** 0.25, device=dev)
+    prm = synth.Params(gq, gk, probes.to(dev), proj.to(dev))
+    cos, sin = hba_amd.rope_tables(Lmax, d, cfg.rope_theta, dev)
+    for s, L in enumerate(lens):
+        kraw = torch.randn(1, L, Hkv, d, generator=g).to(torch.bfloat16).to(dev)
+        vraw = torch.randn(1, L, Hkv, d, generator=g).to(torch.bfloat16).to(dev)
+        kc = ops.prep_keys(kraw, vraw, gk, 1e-6, cos, sin)[0][0].transpose(0, 1)
+        cache.load(s, kc, vraw[0], prm)
+        del kraw, vraw, kc
+    q = torch.randn(Bd, Hq, d, generator=g).to(torch.bfloat16).to(dev)
+    scales = cache.scales()
+    eager = hba_amd.hba_decode_step(q, cache, cfg, prm, cos, sin, scales=scales)[0]
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        for _ in range(2):
+            hba_amd.hba_decode_step(q, cache, cfg, prm, cos, sin, scales=scales)
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph):
+        gout = hba_amd.hba_decode_step(q, cache, cfg, prm, cos, sin, scales=scales)[0]
+    for _ in range(10):
+        graph.replay()
+    torch.cuda.synchronize()
+    ok = bool(torch.equal(gout, eager))
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(iters):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1000.0 / iters
+    ok = ok and bool(torch.equal(gout, eager))
+    nbytes = decode_bytes(lens, Hkv, d, m, S, W, k, Hq)
+    gbs = nbytes / (us * 1e-6) / 1e9
+    return dict(us_per_step=round(us, 3), algorithmic_bytes=nbytes, achieved_GBs=round(gbs, 1),
+                hbm_frac=round(gbs / PEAK_HBM_GBS, 4), graph_replay_matches_eager=ok,
+                batch=Bd, context="L ~ U[16384, 32768], paged bf16, shuffled page table",
+                kernels="decode_d1 (scores + window partials), decode_d2 (routed partials), "
+                        "decode_d3 (merge), one HIP graph")
+
+
+def cpu_baseline(res, budget_s=20.0):
+    """The oracle's restatement of hba_attention_eval (gathered union softmax,
+    attention.py:610-713) on the host: the whole-sequence prologue (QKNorm,
+    RoPE, summaries, routing queries) plus per-row selection + attention on a
+    sample of query rows, extrapolated to all rows."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+    import oracle.hba_oracle as O
+    cfg, x, prm = res["cfg"], res["x"], res["prm"]
+    f = lambda t: t.detach().float().cpu().numpy()
+    q, k, v = f(x["q"])[0], f(x["k"])[0], f(x["v"])[0]
+    cos, sin = f(res["cos"]), f(res["sin"])
+    n = q.shape[0]
+    with threadpool_limits(limits=1):
+        t0 = time.perf_counter()
+        P = O.prepare(q, k, v, cos, sin, cfg, f(prm.probes), f(prm.proj), f(prm.q.gain), f(prm.k.gain),
+                      1e-6, "bf16")
+        t_pro = time.perf_counter() - t0
+        rng = np.random.RandomState(0)
+        done, t_rows = 0, 0.0
+        while t_rows < budget_s and done < n:
+            rows = np.sort(rng.choice(n, 256, replace=False))
+            t0 = time.perf_counter()
+            idx, val, cnt = O.flat_select(P.qg, P.S0, P.scale, cfg.k_blocks, 64, cfg.window, rows)
+            I, C = O._scatter_rows(idx, cnt, rows, n)
+            O.attn_rows(P.qc, P.qr, P.kc, P.kr, P.v, I, C, P.scale, cfg.sinks, cfg.window, 64, rows)
+            t_rows += time.perf_counter() - t0
+            done += rows.size
+    total = t_pro + t_rows * n / done
+    return {"value": round(n / total, 1), "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": f"oracle gathered path (hba_attention_eval restated, numpy/C, 1 thread) on the "
+                      f"same 32K workload: full prologue {t_pro:.1f}s + {done} sampled query rows in "
+                      f"{t_rows:.1f}s, extrapolated to {n} rows; host {cpu_model()}"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=20.0)
+    a = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", a.gpus))
+    if a.gpus != 1 or world != 1:
+        print(json.dumps({"error": "this benchmark runs on exactly one GPU: the HBA operator is "
+                                   "measured on one MI355X (multi-GPU sharding is design-only)",
+                          "n_gpus": a.gpus}))
+        sys.exit(2)
+    import torch
+    dev = torch.device("cuda:0")
+    res = bench_layer(dev, a.steps, a.warmup)
+    ms = res["ms"]
+    attn_ms = res["stage_ms"]["attn"]
+    achieved = res["attn_flop"] / (attn_ms * 1e-3) / 1e12
+    dec = None if a.no_decode else bench_decode(dev)
+    cpu = None if a.no_cpu else cpu_baseline(res, a.cpu_budget)
+    total_flop = res["attn_flop"] + res["score_flop"] + res["summ_flop"]
+    line = {
+        "metric": "HBA layer fwd tokens/s at 32K (% MFMA roofline); decode µs/step (% HBM BW)",
+        "value": round(res["tokens"] / (ms * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": dict(WORKLOAD),
+        "roofline": {"bound": "mfma", "kernel": "attn_bf16_kernel<64>",
+                     "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "algorithmic_flop_per_launch": res["attn_flop"],
+                     "mean_keys_per_query": round(res["mean_keys"], 1)},
+        "layer_frac_of_mfma_roofline": round(total_flop / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+        "stage_ms": {k: round(v, 4) for k, v in res["stage_ms"].items()},
+        "decode": dec,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()
