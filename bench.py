@@ -82,7 +82,7 @@ def run_layer(cfg, x, prm, cos, sin, ev=None):
     idx, val, cnt = ops.score_select(x["q"], prm.q.gain, qeps, S0, cfg.window, cfg.k_blocks, scale)
     mark("select", 1)
     mark("attn", 0)
-    out = ops.attn_fwd(x["q"], prm.q.gain, qeps, kc, kr, vt, cos, sin, idx, cnt, cfg.sinks, cfg.window,
+    out = ops.attn_fwd(x["q"], prm.q.gain, prm.k.gain, qeps, kc, kr, vt, cos, sin, idx, cnt, cfg.sinks, cfg.window,
                        scale)
     mark("attn", 1)
     return out

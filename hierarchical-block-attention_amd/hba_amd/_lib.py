@@ -30,7 +30,7 @@ SIGNATURES = {
                          _i64, _i64, _f, _vp, _vp, _vp, _vp],
     "hba_hier_select": [_i, _vp, _c_i64p, _vp, _f, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
                         _i64, _i64, _i64, _i64, _i64, _f, _vp, _vp, _vp, _vp],
-    "hba_attn_fwd": [_i, _vp, _c_i64p, _vp, _f, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64,
+    "hba_attn_fwd": [_i, _vp, _c_i64p, _vp, _vp, _f, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64,
                      _i64, _i64, _i64, _i64, _i64, _i64, _f, _vp, _c_i64p, _vp],
     "hba_kv_append": [_i, _vp, _vp, _vp, _f, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp],
     "hba_summarize_pages": [_i, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _vp],

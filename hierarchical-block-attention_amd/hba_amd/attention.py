@@ -48,7 +48,7 @@ def forward_stages(q, k, v, cos, sin, cfg, summ, qkn, hier=False, dense_route=Fa
                                                        cfg.fanout, cfg.beam, sel_scale)
     else:
         r["idx"], r["val"], r["cnt"] = ops.score_select(q, qg, qeps, r["S0"], cfg.window, kk, sel_scale)
-    r["out"] = ops.attn_fwd(q, qg, qeps, r["kc"], r["kr"], r["vt"], cos, sin, r["idx"], r["cnt"],
+    r["out"] = ops.attn_fwd(q, qg, kg, qeps, r["kc"], r["kr"], r["vt"], cos, sin, r["idx"], r["cnt"],
                             cfg.sinks, cfg.window, scale)
     return r
 

@@ -212,9 +212,9 @@ def _(q, q_gain, eps, S0, S1, window, k, fanout, beam, scale):
 
 # ------------------------------------------------------------- attention ----
 @torch.library.custom_op("hba::attn_fwd", mutates_args=(), device_types="cuda")
-def attn_fwd(q: Tensor, q_gain: Optional[Tensor], eps: float, kc: Tensor, kr: Tensor, vt: Tensor,
-             cos: Tensor, sin: Tensor, idx: Tensor, cnt: Tensor, sinks: int, window: int,
-             scale: float) -> Tensor:
+def attn_fwd(q: Tensor, q_gain: Optional[Tensor], k_gain: Optional[Tensor], eps: float, kc: Tensor,
+             kr: Tensor, vt: Tensor, cos: Tensor, sin: Tensor, idx: Tensor, cnt: Tensor, sinks: int,
+             window: int, scale: float) -> Tensor:
     dev = _dev(q)
     _rows(q, "q")
     B, n, Hq, d = q.shape
@@ -227,11 +227,12 @@ def attn_fwd(q: Tensor, q_gain: Optional[Tensor], eps: float, kc: Tensor, kr: Te
         raise TypeError("idx/cnt must be int32")
     cos, sin = _tables(cos, sin, n, d, dev)
     qg = _f32c(q_gain, dev, Hq, "q_gain")
+    kg = _f32c(k_gain, dev, Hkv, "k_gain")
     idx = idx.contiguous()
     cnt = cnt.contiguous()
     out = torch.empty(B, n, Hq, d, dtype=q.dtype, device=dev)
     with torch.cuda.device(dev):
-        st = lib().hba_attn_fwd(_code(q), _p(q), strides3(q), _p(qg), eps, _p(kc.contiguous()),
+        st = lib().hba_attn_fwd(_code(q), _p(q), strides3(q), _p(qg), _p(kg), eps, _p(kc.contiguous()),
                                 _p(kr.contiguous()), _p(vt.contiguous()), _p(cos), _p(sin), _p(idx),
                                 _p(cnt), B, n, Hq, Hkv, d, sinks, window, BLOCK, idx.shape[3], scale,
                                 _p(out), strides3(out), _stream(dev))
@@ -240,7 +241,7 @@ def attn_fwd(q: Tensor, q_gain: Optional[Tensor], eps: float, kc: Tensor, kr: Te
 
 
 @attn_fwd.register_fake
-def _(q, q_gain, eps, kc, kr, vt, cos, sin, idx, cnt, sinks, window, scale):
+def _(q, q_gain, k_gain, eps, kc, kr, vt, cos, sin, idx, cnt, sinks, window, scale):
     return q.new_empty(q.shape)
 
 

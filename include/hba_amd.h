@@ -132,11 +132,13 @@ int hba_hier_select(int dtype, const void *q, const int64_t q_strides[3],
  *             hba_attention_fused forward  src/hba/attention.py:552-603
  * q is the raw query (QKNorm and RoPE are applied in the kernel); kc, kr, vt
  * come from hba_prep_keys.  `scale` is the union scale (content scale times
- * the log-length temperature).  out [B, n, Hq, d] with out_strides.
- * Requires S <= Bk and n % Bk == 0; Bk == 64 and d in {64, 128}.
+ * the log-length temperature).  k_gain (the gains hba_prep_keys applied; NULL
+ * if none) lets the kernel bound the logits by d*max(q_gain)*k_gain*scale
+ * and use that bound as the softmax shift.  out [B, n, Hq, d] with
+ * out_strides.  Requires S <= Bk and n % Bk == 0; Bk == 64 and d in {64, 128}.
  */
 int hba_attn_fwd(int dtype, const void *q, const int64_t q_strides[3],
-                 const float *q_gain, float eps,
+                 const float *q_gain, const float *k_gain, float eps,
                  const void *kc, const void *kr, const void *vt,
                  const float *cos_tab, const float *sin_tab,
                  const int32_t *idx, const int32_t *cnt,

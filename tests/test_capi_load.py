@@ -52,7 +52,7 @@ def test_argument_checks_run_before_any_launch():
     L = _lib.lib()
     s3 = (ctypes.c_int64 * 3)(0, 0, 0)
     fake = ctypes.c_void_p(16)
-    st = L.hba_attn_fwd(1, fake, s3, None, 1e-6, fake, fake, fake, fake, fake, fake, fake, 1, 100, 14,
+    st = L.hba_attn_fwd(1, fake, s3, None, None, 1e-6, fake, fake, fake, fake, fake, fake, fake, 1, 100, 14,
                         2, 64, 4, 1024, 64, 16, 0.1, fake, s3, None)
     assert st == -1                                    # n % 64 != 0
     st = L.hba_score_select(1, fake, s3, None, 1e-6, fake, 1, 128, 14, 2, 96, 4, 64, 1024, 16, 0.1,
