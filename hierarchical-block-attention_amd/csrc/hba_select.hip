@@ -154,7 +154,7 @@ __global__ __launch_bounds__(SEL_WG) void score_select_kernel(
     const typename St<DT>::T *__restrict__ q, int64_t qsb, int64_t qsn, int64_t qsh,
     const float *__restrict__ qgain, float eps, const typename St<DT>::T *__restrict__ S0, int64_t n,
     int Hq, int Hkv, int64_t nb, int64_t W, int kk, float scale, int32_t *__restrict__ idx,
-    float *__restrict__ val, int32_t *__restrict__ cnt) {
+    float *__restrict__ val, int32_t *__restrict__ cnt, float *__restrict__ scores) {
     constexpr int CB = SEL_LDS_FLOATS / (M * D);
     __shared__ __align__(16) float lds[SEL_LDS_FLOATS];
     const int lane = threadIdx.x;
@@ -186,6 +186,7 @@ __global__ __launch_bounds__(SEL_WG) void score_select_kernel(
             int64_t blk = b0 + c;
             if (blk <= bmax) {
                 float v = slot_score_lds<D, M>(qg, lds + c * M * D, scale);
+                if (scores) scores[((b * Hkv + g) * n + i) * nb + blk] = v;
                 insert_inorder<KMAX>(vals, ids, v, (int)blk);
             }
         }
@@ -199,6 +200,136 @@ __global__ __launch_bounds__(SEL_WG) void score_select_kernel(
         c += (vals[j] != -INFINITY) ? 1 : 0;
     }
     cnt[(b * Hkv + g) * n + i] = c;
+}
+
+
+// ----------------------------------------------------- bf16 MFMA scoring ----
+// Block scores as one bf16 MFMA GEMM per (batch, KV head, 64 queries):
+// C^T[summary rows x queries] = S0 . qg^T with v_mfma_f32_16x16x32_bf16
+// (fp32 accumulation).  A 16-row M-tile is 4 blocks x 4 slots, so lane
+// (l16, lg) receives the 4 slot scores of block 4*mt + lg for query l16 and
+// takes their max in registers; each lane keeps a top-k of the blocks it sees
+// (ascending ids: in-order insertion), and the four lane groups of a query
+// are merged under (score desc, block asc).  The routing query is built in
+// the declared fp32 order and is exactly representable in bf16.  Summary
+// rows are staged in LDS, shared by the four waves (16 queries each).
+typedef unsigned int u32x4s __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ bf16x8 ldb8(const bf16_t *p) {
+    return __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4s *>(p));
+}
+
+template <int D, int KMAX>
+__global__ __launch_bounds__(256) void score_select_mfma_kernel(
+    const bf16_t *__restrict__ q, int64_t qsb, int64_t qsn, int64_t qsh, const float *__restrict__ qgain,
+    float eps, const bf16_t *__restrict__ S0, int64_t n, int Hq, int Hkv, int64_t nb, int64_t W, int kk,
+    float scale, int32_t *__restrict__ idx, float *__restrict__ val, int32_t *__restrict__ cnt,
+    float *__restrict__ scores) {
+    constexpr int NKS = D / 32;
+    constexpr int ROW = D + 8;            // padded LDS row (bf16)
+    constexpr int CB = 16;                // blocks per stage (4 M-tiles)
+    __shared__ __align__(16) bf16_t qgs[64 * ROW];
+    __shared__ __align__(16) bf16_t sst[CB * 4 * ROW];
+    __shared__ float mv[64][4][KMAX];
+    __shared__ int mi[64][4][KMAX];
+    const int tid = threadIdx.x;
+    const int w = tid >> 6, lane = tid & 63, l16 = lane & 15, lg = lane >> 4;
+    const int g = blockIdx.y;
+    const int64_t b = blockIdx.z;
+    const int G = Hq / Hkv;
+    const int64_t i0 = (int64_t)blockIdx.x * 64;
+    if (tid < 64) {
+        const int64_t i = (i0 + tid < n) ? i0 + tid : n - 1;
+        float qg[D];
+        routing_query<1, D>(q, qsb, qsn, qsh, qgain, eps, b, i, g, G, qg);
+#pragma unroll
+        for (int t = 0; t < D; ++t) qgs[tid * ROW + t] = f2bf(qg[t]);
+    }
+    __syncthreads();
+    const int qcol = 16 * w + l16;
+    const int64_t iq = i0 + qcol;
+    bf16x8 qb[NKS];
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) qb[ks] = ldb8(qgs + qcol * ROW + 32 * ks + 8 * lg);
+    const int64_t bmax = (iq < n) ? cand_bmax(iq, 64, W) : 0;
+    const int64_t last = (i0 + 63 < n) ? i0 + 63 : n - 1;
+    const int64_t tile_bmax = cand_bmax(last, 64, W);
+    float vals[KMAX];
+    int ids[KMAX];
+#pragma unroll
+    for (int j = 0; j < KMAX; ++j) {
+        vals[j] = -INFINITY;
+        ids[j] = -1;
+    }
+    const bf16_t *Sg = S0 + (b * Hkv + g) * nb * 4 * D;
+    for (int64_t b0 = 1; b0 <= tile_bmax; b0 += CB) {
+        const int cb = (int)((tile_bmax - b0 + 1 < CB) ? tile_bmax - b0 + 1 : CB);
+        __syncthreads();
+        for (int c = tid; c < cb * 4 * (D / 8); c += 256) {
+            const int row = c / (D / 8), ch = c % (D / 8);
+            *reinterpret_cast<u32x4s *>(sst + row * ROW + 8 * ch) =
+                *reinterpret_cast<const u32x4s *>(Sg + (b0 * 4 + row) * D + 8 * ch);
+        }
+        __syncthreads();
+        const int nmt = (cb + 3) / 4;
+        for (int mt = 0; mt < nmt; ++mt) {
+            f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+            const bf16_t *ar = sst + (mt * 16 + l16) * ROW + 8 * lg;
+#pragma unroll
+            for (int ks = 0; ks < NKS; ++ks)
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ldb8(ar + 32 * ks), qb[ks], acc, 0, 0, 0);
+            const int64_t blk = b0 + 4 * mt + lg;
+            float best = acc[0];
+            best = (acc[1] > best) ? acc[1] : best;
+            best = (acc[2] > best) ? acc[2] : best;
+            best = (acc[3] > best) ? acc[3] : best;
+            const float v = best * scale;
+            const bool ok = (4 * mt + lg < cb) && blk <= bmax;
+            if (ok) {
+                if (scores) scores[((b * Hkv + g) * n + iq) * nb + blk] = v;
+                insert_inorder<KMAX>(vals, ids, v, (int)blk);
+            }
+        }
+    }
+    // merge the four lane groups of each query
+#pragma unroll
+    for (int j = 0; j < KMAX; ++j) {
+        mv[qcol][lg][j] = vals[j];
+        mi[qcol][lg][j] = ids[j];
+    }
+    __syncthreads();
+    if (tid < 64 && i0 + tid < n) {
+        const int64_t i = i0 + tid;
+        int hp[4] = {0, 0, 0, 0};
+        const int64_t o = ((b * Hkv + g) * n + i) * kk;
+        int c = 0;
+        for (int j = 0; j < kk; ++j) {
+            int bestl = -1;
+            float bv = -INFINITY;
+            int bi = 0x7fffffff;
+            for (int l = 0; l < 4; ++l) {
+                if (hp[l] >= KMAX) continue;
+                const float v = mv[tid][l][hp[l]];
+                const int id = mi[tid][l][hp[l]];
+                if (v == -INFINITY) continue;
+                if (bestl < 0 || better(v, id, bv, bi)) {
+                    bestl = l;
+                    bv = v;
+                    bi = id;
+                }
+            }
+            if (bestl < 0) {
+                idx[o + j] = -1;
+                val[o + j] = -INFINITY;
+            } else {
+                idx[o + j] = bi;
+                val[o + j] = bv;
+                ++hp[bestl];
+                ++c;
+            }
+        }
+        cnt[(b * Hkv + g) * n + i] = c;
+    }
 }
 
 template <int DT, int D, int M, int KMAX>
@@ -306,12 +437,18 @@ int select_checks(int dtype, const void *q, const int64_t *qs, const void *S0, i
 template <int DT, int D, int M, int KMAX>
 void launch_flat(const void *q, const int64_t *qs, const float *qgain, float eps, const void *S0,
                  int64_t B, int64_t n, int64_t Hq, int64_t Hkv, int64_t W, int64_t k, float scale,
-                 int32_t *idx, float *val, int32_t *cnt, hipStream_t s) {
+                 int32_t *idx, float *val, int32_t *cnt, float *scores, hipStream_t s) {
     dim3 grid((unsigned)((n + SEL_WG - 1) / SEL_WG), (unsigned)Hkv, (unsigned)B);
-    hipLaunchKernelGGL((score_select_kernel<DT, D, M, KMAX>), grid, dim3(SEL_WG), 0, s,
-                       (const typename St<DT>::T *)q, qs[0], qs[1], qs[2], qgain, eps,
-                       (const typename St<DT>::T *)S0, n, (int)Hq, (int)Hkv, n / 64, W, (int)k,
-                       scale, idx, val, cnt);
+    if constexpr (DT == 1 && M == 4 && KMAX <= 32) {
+        hipLaunchKernelGGL((score_select_mfma_kernel<D, KMAX>), grid, dim3(256), 0, s, (const bf16_t *)q,
+                           qs[0], qs[1], qs[2], qgain, eps, (const bf16_t *)S0, n, (int)Hq, (int)Hkv,
+                           n / 64, W, (int)k, scale, idx, val, cnt, scores);
+    } else {
+        hipLaunchKernelGGL((score_select_kernel<DT, D, M, KMAX>), grid, dim3(SEL_WG), 0, s,
+                           (const typename St<DT>::T *)q, qs[0], qs[1], qs[2], qgain, eps,
+                           (const typename St<DT>::T *)S0, n, (int)Hq, (int)Hkv, n / 64, W, (int)k,
+                           scale, idx, val, cnt, scores);
+    }
 }
 
 template <int DT, int D, int M, int KMAX>
@@ -347,13 +484,13 @@ extern "C" int hba_score_select(int dtype, const void *q, const int64_t q_stride
                                 const float *q_gain, float eps, const void *S0, int64_t B, int64_t n,
                                 int64_t Hq, int64_t Hkv, int64_t d, int64_t m, int64_t Bk, int64_t W,
                                 int64_t k, float scale, int32_t *idx, float *val, int32_t *cnt,
-                                void *stream) {
+                                float *scores, void *stream) {
     int st = select_checks(dtype, q, q_strides, S0, B, n, Hq, Hkv, d, m, Bk, W, k, idx, val, cnt);
     if (st) return st;
     hipStream_t s = (hipStream_t)stream;
 #define HBA_FLAT(DT, D)                                                                            \
     HBA_SEL_DISPATCH_M(launch_flat, DT, D, q, q_strides, q_gain, eps, S0, B, n, Hq, Hkv, W, k, scale, \
-                       idx, val, cnt, s)
+                       idx, val, cnt, scores, s)
     HBA_DISPATCH_DT_D(dtype, d, HBA_FLAT);
 #undef HBA_FLAT
     HBA_LAUNCH_CHECK();

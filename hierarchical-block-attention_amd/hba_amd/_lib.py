@@ -27,7 +27,7 @@ SIGNATURES = {
     "hba_summarize": [_i, _vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _vp],
     "hba_build_super": [_i, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp],
     "hba_score_select": [_i, _vp, _c_i64p, _vp, _f, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
-                         _i64, _i64, _f, _vp, _vp, _vp, _vp],
+                         _i64, _i64, _f, _vp, _vp, _vp, _vp, _vp],
     "hba_hier_select": [_i, _vp, _c_i64p, _vp, _f, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
                         _i64, _i64, _i64, _i64, _i64, _f, _vp, _vp, _vp, _vp],
     "hba_attn_fwd": [_i, _vp, _c_i64p, _vp, _vp, _f, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64,

@@ -157,6 +157,19 @@ def _sel_out(q, Hkv, k):
 @torch.library.custom_op("hba::score_select", mutates_args=(), device_types="cuda")
 def score_select(q: Tensor, q_gain: Optional[Tensor], eps: float, S0: Tensor, window: int, k: int,
                  scale: float) -> Tuple[Tensor, Tensor, Tensor]:
+    return _score_select(q, q_gain, eps, S0, window, k, scale, None)
+
+
+def score_select_with_scores(q, q_gain, eps, S0, window, k, scale):
+    """score_select that also returns every ranked candidate's fp32 score
+    [B, Hkv, n, nb] (-inf elsewhere): the verification form, not a torch op."""
+    B, n = q.shape[0], q.shape[1]
+    scores = torch.full((B, S0.shape[1], n, S0.shape[2]), float("-inf"), dtype=torch.float32,
+                        device=q.device)
+    return (*_score_select(q, q_gain, eps, S0, window, k, scale, scores), scores)
+
+
+def _score_select(q, q_gain, eps, S0, window, k, scale, scores):
     dev = _dev(q)
     _rows(q, "q")
     B, n, Hq, d = q.shape
@@ -168,7 +181,8 @@ def score_select(q: Tensor, q_gain: Optional[Tensor], eps: float, S0: Tensor, wi
     idx, val, cnt = _sel_out(q, Hkv, k)
     with torch.cuda.device(dev):
         st = lib().hba_score_select(_code(q), _p(q), strides3(q), _p(qg), eps, _p(S0), B, n, Hq, Hkv, d,
-                                    m, BLOCK, window, k, scale, _p(idx), _p(val), _p(cnt), _stream(dev))
+                                    m, BLOCK, window, k, scale, _p(idx), _p(val), _p(cnt), _p(scores),
+                                    _stream(dev))
     check(st, "hba_score_select")
     return idx, val, cnt
 

@@ -101,13 +101,18 @@ int hba_build_super(int dtype, const void *S0, int64_t B, int64_t Hkv, int64_t n
  *             grouped_query / slot_block_scores  src/hba/summarizer.py:45-54
  * q_gain == NULL means qknorm=False.  Invalid picks (fewer than k
  * candidates) get idx -1 / val -inf; cnt holds the number of valid picks.
- * 1 <= k <= 64.
+ * 1 <= k <= 64.  fp32 inputs are scored with sequential fp32 FMAs over d (the
+ * oracle's declared order: bit-exact); bf16 inputs with m == 4 and k <= 32 as
+ * a bf16 MFMA GEMM with fp32 accumulation.  scores (optional, NULL to skip):
+ * fp32 [B, Hkv, n, n/Bk] receiving the score of every candidate the kernel
+ * ranked (other entries are left untouched), so the top-k can be checked on
+ * identical score arrays.
  */
 int hba_score_select(int dtype, const void *q, const int64_t q_strides[3],
                      const float *q_gain, float eps, const void *S0,
                      int64_t B, int64_t n, int64_t Hq, int64_t Hkv, int64_t d,
                      int64_t m, int64_t Bk, int64_t W, int64_t k, float scale,
-                     int32_t *idx, float *val, int32_t *cnt, void *stream);
+                     int32_t *idx, float *val, int32_t *cnt, float *scores, void *stream);
 
 /*
  * Two-level selection: score the super-summaries, keep the top

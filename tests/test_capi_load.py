@@ -56,5 +56,5 @@ def test_argument_checks_run_before_any_launch():
                         2, 64, 4, 1024, 64, 16, 0.1, fake, s3, None)
     assert st == -1                                    # n % 64 != 0
     st = L.hba_score_select(1, fake, s3, None, 1e-6, fake, 1, 128, 14, 2, 96, 4, 64, 1024, 16, 0.1,
-                            fake, fake, fake, None)
+                            fake, fake, fake, None, None)
     assert st == -2                                    # d = 96 unsupported

@@ -103,22 +103,69 @@ SEL_CASES = [
 ]
 
 
+def margin_equal(k_idx, k_cnt, o_scores, kk, rel=1e-5):
+    """Kernel selection vs the oracle's declared-order scores o_scores [r, nb]:
+    identical sets, except that blocks whose oracle score is within `rel` of
+    the k-th score (a near-tie at the top-k boundary) may be swapped."""
+    bad = 0
+    for r in range(o_scores.shape[0]):
+        row = o_scores[r]
+        fin = np.isfinite(row)
+        c = min(kk, int(fin.sum()))
+        assert int(k_cnt[r]) == c
+        if c == 0:
+            continue
+        order = np.lexsort((np.arange(row.size), -np.where(fin, row, -np.inf)))
+        ref = set(order[:c].tolist())
+        got = set(k_idx[r, :c].tolist())
+        if got != ref:
+            kth = row[order[c - 1]]
+            for blk in got ^ ref:
+                assert abs(row[blk] - kth) <= rel * max(1.0, abs(kth)), (r, blk, row[blk], kth)
+            bad += 1
+    return bad
+
+
+def uses_mfma(dt, m, k):
+    return dt == "bf16" and m == 4 and k <= 32
+
+
 @pytest.mark.parametrize("case", SEL_CASES, ids=lambda c: "-".join(f"{k}{v}" for k, v in c.items()))
-def test_flat_select_bit_exact(dev, case):
+def test_flat_select(dev, case):
+    """fp32 (and bf16 with m != 4): bit-exact against the oracle's declared
+    order.  bf16 MFMA path: top-k bit-exact on the kernel's own score array,
+    scores within fp32 accumulation noise of the oracle's, and the same sets
+    up to near-ties at the k boundary."""
     c = dict(case)
     dt = c.pop("dt")
     cfg, x, prm, cos, sin = make(dev, dt, **c)
-    r = hba_amd.forward_stages(x["q"], x["k"], x["v"], cos, sin, cfg, prm, prm)
-    torch.cuda.synchronize()
-    S0 = f(r["S0"])
     n = x["q"].shape[1]
+    kk = min(cfg.k_blocks, n // 64)
+    r = hba_amd.forward_stages(x["q"], x["k"], x["v"], cos, sin, cfg, prm, prm)
+    idx, val, cnt, scores = ops.score_select_with_scores(x["q"], x["q_gain"], 1e-6, r["S0"], cfg.window,
+                                                         kk, r["sel_scale"])
+    torch.cuda.synchronize()
+    assert torch.equal(idx, r["idx"]) and torch.equal(cnt, r["cnt"])
+    S0 = f(r["S0"])
+    sc = scores.cpu().numpy()
     for b in range(x["q"].shape[0]):
         P = oracle_prep(cfg, x, cos, sin, dt, b, S0[b])
-        idx, val, cnt = O.flat_select(P.qg, P.S0, r["sel_scale"], min(cfg.k_blocks, n // 64), 64,
-                                      cfg.window)
-        assert np.array_equal(r["cnt"][b].cpu().numpy(), cnt)
-        assert np.array_equal(r["idx"][b].cpu().numpy(), idx)
-        assert np.array_equal(r["val"][b].cpu().numpy(), val)
+        o_idx, o_val, o_cnt = O.flat_select(P.qg, P.S0, r["sel_scale"], kk, 64, cfg.window)
+        ki, kv, kc_ = idx[b].cpu().numpy(), val[b].cpu().numpy(), cnt[b].cpu().numpy()
+        # top-k of the kernel's own scores, by the oracle: bit-exact
+        for g in range(cfg.n_kv):
+            ti, tv, tc = O.topk(sc[b, g], kk)
+            assert np.array_equal(ti, ki[g]) and np.array_equal(tv, kv[g]) and np.array_equal(tc, kc_[g])
+        if not uses_mfma(dt, cfg.slots, kk):
+            assert np.array_equal(ki, o_idx) and np.array_equal(kv, o_val) and np.array_equal(kc_, o_cnt)
+            continue
+        for g in range(cfg.n_kv):
+            osc = O.block_scores(P.qg[g], P.S0[g], np.arange(n), r["sel_scale"], 64, cfg.window)
+            fin = np.isfinite(osc)
+            assert np.array_equal(np.isfinite(sc[b, g]), fin)
+            assert np.abs(sc[b, g][fin] - osc[fin]).max() <= 2e-6 * max(1.0, np.abs(osc[fin]).max())
+            flips = margin_equal(ki[g], kc_[g], osc, kk)
+            assert flips <= max(2, n // 1000), flips
 
 
 HIER_CASES = [
@@ -317,7 +364,7 @@ def test_decode_equals_prefill_last_row(dev):
     cfg, x, prm, cos, sin, cache, kcs, qn = build_cache(dev, "bf16", [L], W=1024, k=16, seed=4)
     out, sidx, scnt = hba_amd.hba_decode_step(qn, cache, cfg, prm, cos, sin)
     r = hba_amd.forward_stages(x["q"][:, :L], x["k"][:, :L], x["v"][:, :L], cos[:L], sin[:L], cfg, prm, prm)
-    assert torch.equal(sidx[0], r["idx"][0, :, L - 1])
+    assert torch.equal(sidx[0].sort().values, r["idx"][0, :, L - 1].sort().values)
     assert (out[0].float() - r["out"][0, L - 1].float()).abs().max().item() <= 2e-2
 
 
