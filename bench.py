@@ -159,9 +159,9 @@ def bench_decode(dev, iters=200):
     for s, L in enumerate(lens):
         kraw = torch.randn(1, L, Hkv, d, generator=g).to(torch.bfloat16).to(dev)
         vraw = torch.randn(1, L, Hkv, d, generator=g).to(torch.bfloat16).to(dev)
-        kc = ops.prep_keys(kraw, vraw, gk, 1e-6, cos, sin)[0][0].transpose(0, 1)
-        cache.load(s, kc, vraw[0], prm)
-        del kraw, vraw, kc
+        kc, kr, _ = ops.prep_keys(kraw, vraw, gk, 1e-6, cos, sin)
+        cache.load(s, kc[0].transpose(0, 1), kr[0].transpose(0, 1), vraw[0], prm)
+        del kraw, vraw, kc, kr
     q = torch.randn(Bd, Hq, d, generator=g).to(torch.bfloat16).to(dev)
     scales = cache.scales()
     eager = hba_amd.hba_decode_step(q, cache, cfg, prm, cos, sin, scales=scales)[0]

@@ -181,23 +181,31 @@ __global__ __launch_bounds__(256) void build_super_kernel(const typename St<DT>:
 template <int DT, int D>
 __global__ __launch_bounds__(256) void kv_append_kernel(
     const typename St<DT>::T *__restrict__ knew, const typename St<DT>::T *__restrict__ vnew,
-    const float *__restrict__ kgain, float eps, const int32_t *__restrict__ ptab, int64_t maxp,
-    const int32_t *__restrict__ lens, int64_t Bd, int64_t Hkv, typename St<DT>::T *__restrict__ kcp,
+    const float *__restrict__ kgain, float eps, const float *__restrict__ cosT,
+    const float *__restrict__ sinT, const int32_t *__restrict__ ptab, int64_t maxp,
+    const int32_t *__restrict__ lens, int64_t lmax, int64_t Bd, int64_t Hkv,
+    typename St<DT>::T *__restrict__ kcp, typename St<DT>::T *__restrict__ krp,
     typename St<DT>::T *__restrict__ vp) {
     constexpr int BK = 64;
     int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (gid >= Bd * Hkv) return;
     int64_t s = gid / Hkv, g = gid % Hkv;
     int64_t pos = (int64_t)lens[s] - 1;
-    if (pos < 0 || pos / BK >= maxp) return;  // nothing to append / outside the table
+    // nothing to append, outside the page table or past the RoPE tables
+    if (pos < 0 || pos / BK >= maxp || pos >= lmax) return;
     int64_t page = ptab[s * maxp + pos / BK];
     int64_t dst = ((page * Hkv + g) * BK + pos % BK) * D;
-    float x[D];
+    float x[D], y[D];
     load_row<DT, D>(knew + gid * D, x);
     if (kgain) qknorm_row<DT, D>(x, kgain[g], eps);
     store_row<DT, D>(kcp + dst, x);
+    rope_row<DT, D>(x, y, cosT + pos * D, sinT + pos * D);
+    store_row<DT, D>(krp + dst, y);
     load_row<DT, D>(vnew + gid * D, x);
-    store_row<DT, D>(vp + dst, x);
+    // values are d-major within a page: element t of token pos at [t][pos % 64]
+    typename St<DT>::T *vcol = vp + (page * Hkv + g) * D * BK + pos % BK;
+#pragma unroll
+    for (int t = 0; t < D; ++t) St<DT>::st(vcol, (int64_t)t * BK, x[t]);
 }
 
 }  // namespace hba
@@ -314,24 +322,26 @@ extern "C" int hba_build_super(int dtype, const void *S0, int64_t B, int64_t Hkv
 }
 
 extern "C" int hba_kv_append(int dtype, const void *k_new, const void *v_new, const float *k_gain,
-                             float eps, const int32_t *page_table, int64_t max_pages,
-                             const int32_t *seq_lens, int64_t Bd, int64_t Hkv, int64_t d, int64_t Bk,
-                             void *kc_pages, void *v_pages, void *stream) {
+                             float eps, const float *cos_tab, const float *sin_tab, int64_t n_tab,
+                             const int32_t *page_table, int64_t max_pages, const int32_t *seq_lens,
+                             int64_t Bd, int64_t Hkv, int64_t d, int64_t Bk, void *kc_pages,
+                             void *kr_pages, void *v_pages, void *stream) {
     int st = abi::check_dtype_dim(dtype, d);
     if (st) return st;
-    if (!k_new || !v_new || !page_table || !seq_lens || !kc_pages || !v_pages || Bd <= 0 ||
-        Hkv <= 0 || max_pages <= 0)
+    if (!k_new || !v_new || !cos_tab || !sin_tab || !page_table || !seq_lens || !kc_pages ||
+        !kr_pages || !v_pages || Bd <= 0 || Hkv <= 0 || max_pages <= 0 || n_tab <= 0)
         return HBA_ERR_INVALID_ARG;
     if (Bk != 64) return HBA_ERR_UNSUPPORTED;
     if (!abi::aligned16(k_new) || !abi::aligned16(v_new) || !abi::aligned16(kc_pages) ||
-        !abi::aligned16(v_pages))
+        !abi::aligned16(kr_pages) || !abi::aligned16(v_pages))
         return HBA_ERR_UNSUPPORTED;
     hipStream_t s = (hipStream_t)stream;
     dim3 grid((unsigned)((Bd * Hkv + 255) / 256));
 #define HBA_APP(DT, D)                                                                             \
     hipLaunchKernelGGL((kv_append_kernel<DT, D>), grid, dim3(256), 0, s, (const St<DT>::T *)k_new,   \
-                       (const St<DT>::T *)v_new, k_gain, eps, page_table, max_pages, seq_lens, Bd,  \
-                       Hkv, (St<DT>::T *)kc_pages, (St<DT>::T *)v_pages)
+                       (const St<DT>::T *)v_new, k_gain, eps, cos_tab, sin_tab, page_table,        \
+                       max_pages, seq_lens, n_tab, Bd, Hkv, (St<DT>::T *)kc_pages,                  \
+                       (St<DT>::T *)kr_pages, (St<DT>::T *)v_pages)
     HBA_DISPATCH_DT_D(dtype, d, HBA_APP);
 #undef HBA_APP
     HBA_LAUNCH_CHECK();

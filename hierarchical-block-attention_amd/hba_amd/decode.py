@@ -5,15 +5,17 @@ L-1 of hba_attention_eval (src/hba/attention.py:610-713) for a sequence of
 length L, served from a cache laid out for the operator:
 
   kc_pages   [P, Hkv, 64, d]  QKNorm'd NoPE keys (normalised once, on append)
-  v_pages    [P, Hkv, 64, d]
+  kr_pages   [P, Hkv, 64, d]  the same keys rotated at their own positions
+  v_pages    [P, Hkv, d, 64]  values, d-major within a page (the P.V operand)
   summ_pages [P, Hkv, m, d]   slot summaries of full pages
   page_table int32 [batch, max_pages]  logical page -> physical page
   seq_lens   int32 [batch]    tokens in the cache (the current one included)
 
-Window keys are rotated in the kernel from kc with the caller's cos/sin
-tables, so the cache holds one key representation only.  A page's summary is
-written when the page fills; it is read only once the page has left the
-window.
+A key's rotation depends only on its own position, so it is applied once, on
+append, and the window reads kr directly (the query is rotated in the kernel
+with the caller's cos/sin tables).  The second key copy costs 2*d bytes per
+token and KV head (bf16).  A page's summary is written when the page fills;
+it is read only once the page has left the window.
 """
 import torch
 
@@ -32,7 +34,8 @@ class PagedKVCache:
         P = num_pages if num_pages is not None else batch * self.max_pages
         Hkv, d, m = cfg.n_kv, cfg.head_dim, cfg.slots
         self.kc_pages = torch.zeros(P, Hkv, PAGE, d, dtype=dtype, device=device)
-        self.v_pages = torch.zeros(P, Hkv, PAGE, d, dtype=dtype, device=device)
+        self.kr_pages = torch.zeros(P, Hkv, PAGE, d, dtype=dtype, device=device)
+        self.v_pages = torch.zeros(P, Hkv, d, PAGE, dtype=dtype, device=device)
         self.summ_pages = torch.zeros(P, Hkv, m, d, dtype=dtype, device=device)
         self.page_table = torch.zeros(batch, self.max_pages, dtype=torch.int32, device=device)
         self.seq_lens = torch.zeros(batch, dtype=torch.int32, device=device)
@@ -58,29 +61,34 @@ class PagedKVCache:
         self.page_table.copy_(torch.tensor(rows, dtype=torch.int32))
         self.seq_lens.copy_(torch.tensor(self.lens, dtype=torch.int32))
 
-    def load(self, s, kc_seq, v_seq, summ):
-        """Fill sequence s with already-QKNorm'd keys kc_seq [L, Hkv, d] and
-        values v_seq [L, Hkv, d] (a prefill's outputs), and summarise its full
-        pages.  Setup path: plain tensor copies."""
+    def load(self, s, kc_seq, kr_seq, v_seq, summ):
+        """Fill sequence s with already-QKNorm'd keys kc_seq [L, Hkv, d], their
+        rotations kr_seq [L, Hkv, d] and values v_seq [L, Hkv, d] (a prefill's
+        outputs: hba_prep_keys' kc and kr), and summarise its full pages.
+        Setup path: plain tensor copies."""
         L = kc_seq.shape[0]
         self._ensure_pages(s, L)
         pages = torch.tensor(self._table[s], dtype=torch.long, device=self.kc_pages.device)
         npg = (L + PAGE - 1) // PAGE
         pad = npg * PAGE - L
-        kpad = torch.nn.functional.pad(kc_seq, (0, 0, 0, 0, 0, pad))
-        vpad = torch.nn.functional.pad(v_seq, (0, 0, 0, 0, 0, pad))
         Hkv, d = kc_seq.shape[1], kc_seq.shape[2]
-        self.kc_pages[pages[:npg]] = kpad.view(npg, PAGE, Hkv, d).transpose(1, 2).to(self.kc_pages.dtype)
-        self.v_pages[pages[:npg]] = vpad.view(npg, PAGE, Hkv, d).transpose(1, 2).to(self.v_pages.dtype)
+
+        def paged(x):
+            return torch.nn.functional.pad(x, (0, 0, 0, 0, 0, pad)).view(npg, PAGE, Hkv, d)
+
+        self.kc_pages[pages[:npg]] = paged(kc_seq).transpose(1, 2).to(self.kc_pages.dtype)
+        self.kr_pages[pages[:npg]] = paged(kr_seq).transpose(1, 2).to(self.kr_pages.dtype)
+        self.v_pages[pages[:npg]] = paged(v_seq).permute(0, 2, 3, 1).to(self.v_pages.dtype)
         self.lens[s] = L
         self._sync_table()
         full = pages[: L // PAGE]
         if full.numel():
             ops.summarize_pages(self.kc_pages, full, summ.probes, summ.proj, self.summ_pages)
 
-    def append(self, k_new, v_new, qkn, summ):
+    def append(self, k_new, v_new, qkn, summ, cos, sin):
         """Append one token per sequence (raw k_new, v_new [batch, Hkv, d]):
-        QKNorm + write in the kernel; summarise the pages that just filled."""
+        QKNorm, rotation at the token's position and the writes in one kernel;
+        summarise the pages that just filled.  cos/sin: fp32 [>= max_len, d]."""
         for s in range(self.batch):
             self._ensure_pages(s, self.lens[s] + 1)
             self.lens[s] += 1
@@ -88,7 +96,10 @@ class PagedKVCache:
         cfg = self.cfg
         kg = qkn.k.gain if getattr(cfg, "qknorm", False) else None
         keps = float(qkn.k.eps) if kg is not None else 1e-6
-        ops.kv_append(k_new, v_new, kg, keps, self.page_table, self.seq_lens, self.kc_pages, self.v_pages)
+        if cos.shape[0] < max(self.lens):
+            raise ValueError(f"cos/sin tables cover {cos.shape[0]} positions, need {max(self.lens)}")
+        ops.kv_append(k_new, v_new, kg, keps, cos, sin, self.page_table, self.seq_lens, self.kc_pages,
+                      self.kr_pages, self.v_pages)
         done = [self._table[s][self.lens[s] // PAGE - 1] for s in range(self.batch)
                 if self.lens[s] % PAGE == 0]
         if done:
@@ -109,5 +120,6 @@ def hba_decode_step(q, cache, cfg, qkn, cos, sin, scales=None):
     qeps = float(qkn.q.eps) if qg is not None else 1e-6
     sc = cache.scales(cfg) if scales is None else scales
     max_len = max(cache.lens)
-    return ops.decode_fwd(q, qg, qeps, cache.kc_pages, cache.v_pages, cache.summ_pages, cache.page_table,
-                          cache.seq_lens, cos, sin, sc, cfg.sinks, cfg.window, cfg.k_blocks, max_len)
+    return ops.decode_fwd(q, qg, qeps, cache.kc_pages, cache.kr_pages, cache.v_pages, cache.summ_pages,
+                          cache.page_table, cache.seq_lens, cos, sin, sc, cfg.sinks, cfg.window, cfg.k_blocks,
+                          max_len)

@@ -260,16 +260,20 @@ def _(q, q_gain, k_gain, eps, kc, kr, vt, cos, sin, idx, cnt, sinks, window, sca
 
 
 # ---------------------------------------------------------------- decode ----
-@torch.library.custom_op("hba::kv_append", mutates_args=("kc_pages", "v_pages"), device_types="cuda")
-def kv_append(k_new: Tensor, v_new: Tensor, k_gain: Optional[Tensor], eps: float, page_table: Tensor,
-              seq_lens: Tensor, kc_pages: Tensor, v_pages: Tensor) -> None:
+@torch.library.custom_op("hba::kv_append", mutates_args=("kc_pages", "kr_pages", "v_pages"),
+                         device_types="cuda")
+def kv_append(k_new: Tensor, v_new: Tensor, k_gain: Optional[Tensor], eps: float, cos: Tensor, sin: Tensor,
+              page_table: Tensor, seq_lens: Tensor, kc_pages: Tensor, kr_pages: Tensor,
+              v_pages: Tensor) -> None:
     dev = _dev(k_new)
     Bd, Hkv, d = k_new.shape
     kg = _f32c(k_gain, dev, Hkv, "k_gain")
+    cos, sin = _tables(cos, sin, 1, d, dev)
     with torch.cuda.device(dev):
         st = lib().hba_kv_append(_code(k_new), _p(k_new.contiguous()), _p(v_new.contiguous()), _p(kg), eps,
-                                 _p(page_table), page_table.shape[1], _p(seq_lens), Bd, Hkv, d, BLOCK,
-                                 _p(kc_pages), _p(v_pages), _stream(dev))
+                                 _p(cos), _p(sin), cos.shape[0], _p(page_table), page_table.shape[1],
+                                 _p(seq_lens), Bd, Hkv, d, BLOCK, _p(kc_pages), _p(kr_pages), _p(v_pages),
+                                 _stream(dev))
     check(st, "hba_kv_append")
 
 
@@ -296,9 +300,9 @@ def decode_workspace_bytes(Bd, Hq, Hkv, d, k, window, max_len):
 
 
 @torch.library.custom_op("hba::decode_fwd", mutates_args=(), device_types="cuda")
-def decode_fwd(q: Tensor, q_gain: Optional[Tensor], eps: float, kc_pages: Tensor, v_pages: Tensor,
-               summ_pages: Tensor, page_table: Tensor, seq_lens: Tensor, cos: Tensor, sin: Tensor,
-               scales: Tensor, sinks: int, window: int, k: int,
+def decode_fwd(q: Tensor, q_gain: Optional[Tensor], eps: float, kc_pages: Tensor, kr_pages: Tensor,
+               v_pages: Tensor, summ_pages: Tensor, page_table: Tensor, seq_lens: Tensor, cos: Tensor,
+               sin: Tensor, scales: Tensor, sinks: int, window: int, k: int,
                max_len: int) -> Tuple[Tensor, Tensor, Tensor]:
     dev = _dev(q)
     Bd, Hq, d = q.shape
@@ -313,17 +317,17 @@ def decode_fwd(q: Tensor, q_gain: Optional[Tensor], eps: float, kc_pages: Tensor
     nbytes = decode_workspace_bytes(Bd, Hq, Hkv, d, k, window, max_len)
     ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
     with torch.cuda.device(dev):
-        st = lib().hba_decode_fwd(_code(q), _p(q), _p(qg), eps, _p(kc_pages), _p(v_pages), _p(summ_pages),
-                                  _p(page_table), page_table.shape[1], _p(seq_lens), _p(cos), _p(sin),
-                                  _p(sc), Bd, Hq, Hkv, d, m, sinks, window, BLOCK, k, max_len, _p(ws),
+        st = lib().hba_decode_fwd(_code(q), _p(q), _p(qg), eps, _p(kc_pages), _p(kr_pages), _p(v_pages),
+                                  _p(summ_pages), _p(page_table), page_table.shape[1], _p(seq_lens), _p(cos),
+                                  _p(sin), _p(sc), Bd, Hq, Hkv, d, m, sinks, window, BLOCK, k, max_len, _p(ws),
                                   nbytes, _p(out), _p(sel_idx), _p(sel_cnt), _stream(dev))
     check(st, "hba_decode_fwd")
     return out, sel_idx, sel_cnt
 
 
 @decode_fwd.register_fake
-def _(q, q_gain, eps, kc_pages, v_pages, summ_pages, page_table, seq_lens, cos, sin, scales, sinks,
-      window, k, max_len):
+def _(q, q_gain, eps, kc_pages, kr_pages, v_pages, summ_pages, page_table, seq_lens, cos, sin, scales,
+      sinks, window, k, max_len):
     Bd, Hkv = q.shape[0], summ_pages.shape[1]
     return (q.new_empty(q.shape), q.new_empty(Bd, Hkv, k, dtype=torch.int32),
             q.new_empty(Bd, Hkv, dtype=torch.int32))

@@ -153,8 +153,10 @@ int hba_attn_fwd(int dtype, const void *q, const int64_t q_strides[3],
 
 /*
  * Paged KV cache (decode).  Page = Bk tokens of one sequence; all tensors
- * page-major:  kc_pages, v_pages [P, Hkv, Bk, d] (kc = QKNorm'd NoPE keys),
- * summ_pages [P, Hkv, m, d] (slot summaries of full pages);
+ * page-major:  kc_pages [P, Hkv, Bk, d] (QKNorm'd NoPE keys), kr_pages
+ * [P, Hkv, Bk, d] (the same keys rotated at their own positions: hba_prep_keys'
+ * kr), v_pages [P, Hkv, d, Bk] (values, d-major within a page), summ_pages
+ * [P, Hkv, m, d] (slot summaries of full pages);
  * page_table int32 [Bd, max_pages] (logical page -> physical page);
  * seq_lens int32 [Bd] (tokens already in the cache, including the current one).
  * There is no reference function for these: the decode step is defined as row
@@ -163,14 +165,17 @@ int hba_attn_fwd(int dtype, const void *q, const int64_t q_strides[3],
  */
 
 /*
- * Append one token per sequence at position seq_lens[s]-1: QKNorm of k_new
- * (as hba_prep_keys) into kc_pages, v_new into v_pages.  k_new, v_new
- * [Bd, Hkv, d] contiguous.  k_gain == NULL means qknorm=False.
+ * Append one token per sequence at position pos = seq_lens[s]-1: QKNorm of
+ * k_new into kc_pages and its rotation at pos (as hba_prep_keys) into
+ * kr_pages, v_new into v_pages.  k_new, v_new [Bd, Hkv, d] contiguous;
+ * cos_tab/sin_tab fp32 [n_tab, d] (a position >= n_tab is not appended).
+ * k_gain == NULL means qknorm=False.
  */
 int hba_kv_append(int dtype, const void *k_new, const void *v_new, const float *k_gain,
-                  float eps, const int32_t *page_table, int64_t max_pages,
-                  const int32_t *seq_lens, int64_t Bd, int64_t Hkv, int64_t d, int64_t Bk,
-                  void *kc_pages, void *v_pages, void *stream);
+                  float eps, const float *cos_tab, const float *sin_tab, int64_t n_tab,
+                  const int32_t *page_table, int64_t max_pages, const int32_t *seq_lens,
+                  int64_t Bd, int64_t Hkv, int64_t d, int64_t Bk, void *kc_pages,
+                  void *kr_pages, void *v_pages, void *stream);
 
 /*
  * Slot summaries of the listed physical pages (SlotSummarizer.summarize on
@@ -192,14 +197,16 @@ int hba_decode_workspace_size(int64_t Bd, int64_t Hq, int64_t Hkv, int64_t d, in
  * over the full pages that lie before the window.  scales fp32 [Bd] holds
  * each sequence's union scale (content scale times the temperature at n=L).
  * out [Bd, Hq, d].  Optional sel_idx int32 [Bd, Hkv, k] / sel_cnt
- * int32 [Bd, Hkv] receive the selection (NULL to skip).
+ * int32 [Bd, Hkv] receive the selection (NULL to skip).  max_len bounds
+ * every seq_lens[s] (a longer length is read as max_len); cos_tab/sin_tab
+ * fp32 [>= max_len, d].
  */
 int hba_decode_fwd(int dtype, const void *q, const float *q_gain, float eps,
-                   const void *kc_pages, const void *v_pages, const void *summ_pages,
-                   const int32_t *page_table, int64_t max_pages, const int32_t *seq_lens,
-                   const float *cos_tab, const float *sin_tab, const float *scales,
-                   int64_t Bd, int64_t Hq, int64_t Hkv, int64_t d, int64_t m,
-                   int64_t S, int64_t W, int64_t Bk, int64_t k, int64_t max_len,
+                   const void *kc_pages, const void *kr_pages, const void *v_pages,
+                   const void *summ_pages, const int32_t *page_table, int64_t max_pages,
+                   const int32_t *seq_lens, const float *cos_tab, const float *sin_tab,
+                   const float *scales, int64_t Bd, int64_t Hq, int64_t Hkv, int64_t d,
+                   int64_t m, int64_t S, int64_t W, int64_t Bk, int64_t k, int64_t max_len,
                    void *workspace, size_t ws_bytes, void *out,
                    int32_t *sel_idx, int32_t *sel_cnt, void *stream);
 

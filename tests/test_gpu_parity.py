@@ -327,9 +327,10 @@ def build_cache(dev, dt, lens, Hq=14, Hkv=2, d=64, m=4, W=1024, S=4, k=16, seed=
     cache._free = synth.shuffled_pages(len(cache._free), seed=seed)    # shuffled physical pages
     kcs = []
     for s, Ls in enumerate(lens):
-        kc = ops.prep_keys(x["k"][s:s + 1, :Ls], x["v"][s:s + 1, :Ls], x["k_gain"] if qknorm else None,
-                           1e-6, cos, sin)[0][0].transpose(0, 1)
-        cache.load(s, kc, x["v"][s, :Ls], prm)
+        kc, kr, _ = ops.prep_keys(x["k"][s:s + 1, :Ls], x["v"][s:s + 1, :Ls], x["k_gain"] if qknorm else None,
+                                  1e-6, cos, sin)
+        kc, kr = kc[0].transpose(0, 1), kr[0].transpose(0, 1)
+        cache.load(s, kc, kr, x["v"][s, :Ls], prm)
         kcs.append(kc)
     qn = x["q"][torch.arange(Bd), torch.tensor(lens) - 1]                  # [Bd, Hq, d]
     return cfg, x, prm, cos, sin, cache, kcs, qn
@@ -374,15 +375,27 @@ def test_kv_append_and_page_summaries(dev):
     g = torch.Generator().manual_seed(3)
     kn = torch.randn(2, 2, 64, generator=g).to(torch.bfloat16).to(dev)
     vn = torch.randn(2, 2, 64, generator=g).to(torch.bfloat16).to(dev)
-    cache.append(kn, vn, prm, prm)
+    cache.append(kn, vn, prm, prm, cos, sin)
     torch.cuda.synchronize()
     assert cache.lens == [128, 61]
-    s, pos = 0, 127
-    page = cache._table[s][pos // 64]
-    want = O.qknorm(f(kn)[s], f(x["k_gain"]), 1e-6, "bf16")
-    assert np.array_equal(f(cache.kc_pages[page, :, pos % 64]), want)
-    assert np.array_equal(f(cache.v_pages[page, :, pos % 64]), f(vn)[s])
-    # the page that just filled got its summary
-    kpage = f(cache.kc_pages[page]).transpose(1, 0, 2)                    # [64, Hkv, d]
-    ref = O.summarize(kpage, f(x["probes"]), f(x["proj"]), 64)[:, 0]
-    assert np.abs(f(cache.summ_pages[page]) - ref).max() <= 2 ** -7 * max(1, np.abs(ref).max())
+    for s, pos in enumerate([127, 60]):
+        page = cache._table[s][pos // 64]
+        want = O.qknorm(f(kn)[s], f(x["k_gain"]), 1e-6, "bf16")
+        assert np.array_equal(f(cache.kc_pages[page, :, pos % 64]), want)
+        rot = O.apply_rope(want[None], f(cos), f(sin), "bf16", positions=np.array([pos]))[0]
+        assert np.array_equal(f(cache.kr_pages[page, :, pos % 64]), rot)
+        assert np.array_equal(f(cache.v_pages[page, :, :, pos % 64]), f(vn)[s])
+        kcs[s] = torch.cat([kcs[s], torch.from_numpy(want)[None].to(kcs[s])], 0)
+    # a decode step after the append sees the appended token (keys, rotation, value)
+    qd = torch.randn(2, 14, 64, generator=g).to(torch.bfloat16).to(dev)
+    out, sidx, scnt = hba_amd.hba_decode_step(qd, cache, cfg, prm, cos, sin)
+    for s, L in enumerate(cache.lens):
+        vseq = np.concatenate([f(x["v"][s, :L - 1]), f(vn)[s][None]], 0)
+        ref, _ = O.decode_row(f(qd[s]), f(kcs[s]), vseq, f(cos), f(sin), cfg, cache_summaries(cache, s, L // 64),
+                              f(x["q_gain"]), 1e-6, "bf16", hba_amd.union_scale(cfg, 64, L))
+        assert np.abs(f(out[s]) - ref).max() <= TOL["bf16"], s
+    # the page that just filled (sequence 0, tokens 64..127) got its summary
+    full = cache._table[0][127 // 64]
+    kpage = f(cache.kc_pages[full]).transpose(1, 0, 2)                    # [64, Hkv, d]
+    sref = O.summarize(kpage, f(x["probes"]), f(x["proj"]), 64)[:, 0]
+    assert np.abs(f(cache.summ_pages[full]) - sref).max() <= 2 ** -7 * max(1, np.abs(sref).max())
