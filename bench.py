@@ -194,8 +194,8 @@ def bench_decode(dev, iters=200):
     return dict(us_per_step=round(us, 3), algorithmic_bytes=nbytes, achieved_GBs=round(gbs, 1),
                 hbm_frac=round(gbs / PEAK_HBM_GBS, 4), graph_replay_matches_eager=ok,
                 batch=Bd, context="L ~ U[16384, 32768], paged bf16, shuffled page table",
-                kernels="decode_d1 (scores + window partials), decode_d2 (routed partials), "
-                        "decode_d3 (merge), one HIP graph")
+                kernels="decode_d1 (page scores, chunk top-k, query operands), decode_d2 (window, "
+                        "sink and routed page units on MFMA), decode_d3 (LSE merge), one HIP graph")
 
 
 def cpu_baseline(res, budget_s=20.0):
