@@ -1,0 +1,17 @@
+// Launcher of the bf16 union attention (window kernel, then sinks + routed
+// kernel merging into the window's rows).  lse: fp32 [B, Hq, n] scratch.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace hba {
+
+template <int D>
+int launch_attn_bf16(const void *q, const int64_t *qs, const float *qgain, const float *kgain, float eps,
+                     const void *kc, const void *kr, const void *vt, const float *cosT, const float *sinT,
+                     const int32_t *idx, const int32_t *cnt, int64_t B, int64_t n, int64_t Hq, int64_t Hkv,
+                     int64_t S, int64_t W, int64_t k, float scale, void *out, const int64_t *os, float *lse,
+                     hipStream_t s);
+
+}  // namespace hba

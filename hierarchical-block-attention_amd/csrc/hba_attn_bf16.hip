@@ -1,0 +1,880 @@
+// Union attention forward for bf16 inputs on MFMA (gfx950).  Two launches
+// together compute one softmax per (query i, head h) over
+//   sinks   j < min(S, i+1)                 NoPE  (qc . kc)
+//   window  max(S, i-W+1) <= j <= i          RoPE  (qr . kr)
+//   routed  the 64 keys of each selected block    NoPE
+// (hba_attention_dense src/hba/attention.py:342-356, hba_attention_eval
+//  :676-711); the two partial softmaxes merge by LSE, as hba_attention_fused
+// merges its two regions (:592-603).
+//
+// attn_win_kernel -- the RoPE window.  Workgroup = (batch, KV head, QT
+//   consecutive queries); one wave per (head, 16*RT consecutive queries).  The
+//   MFMA rows of a 16-row tile are 16 consecutive queries of one head, so no
+//   row of a tile is idle.  64-key tiles of kr and vt go through an LDS double
+//   buffer (register prefetch of the next tile), shared by every wave, and
+//   each K / V^T fragment read from LDS feeds the wave's RT row tiles.  Only
+//   tiles on a window's edges are masked.  Output: the window's normalised
+//   rows (bf16, into out) and their LSE (fp32 workspace).
+// attn_routed_kernel -- sinks and routed blocks.  Workgroup = (batch, KV head,
+//   QT queries); the rows of a 16-row tile are the G heads of 16/G queries
+//   (the rows that share a routed block).  The sorted union of the tile's
+//   selections, preceded by block 0 for the sinks, streams through an LDS
+//   ring by direct-to-LDS DMA several blocks ahead, one barrier per block;
+//   a wave updates a tile only if one of its queries picked the block.  The
+//   partial then merges with the window's (out, LSE) and the row is stored.
+//
+// Scores are S^T = K . Q^T with v_mfma_f32_16x16x32_bf16: key rows of the A
+// operand are permuted (permk) so that the probabilities leave the
+// accumulators in the B-operand layout of O^T = V^T . P^T.  Softmax: when
+// QKNorm bounds every logit of a KV-head group by d*max|gq|*|gk|*scale
+// (attention.py:74-81) and bound*log2(e) <= 60 (so exp2 of the lowest
+// possible logit, 2*bound below the shift, is >= 2^-120, a normal fp32),
+// the bound is the shift: no running max, no rescaling (the same softmax).
+// Otherwise a running max per row is kept.  Each kernel decides per group.
+#include "hba_common.h"
+#include "hba_abi.h"
+#include "hba_attn_bf16.h"
+
+namespace hba {
+namespace ab {
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+constexpr float LOG2E = 1.4426950408889634f;
+constexpr int16_t SENT = 0x7fff;     // list terminator (block ids are < 0x7fff)
+
+__device__ __forceinline__ bf16x8 ldb8(const bf16_t *p) {
+    return __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(p));
+}
+__device__ __forceinline__ f32x4 mma(bf16x8 a, bf16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ float ex2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Byte offset of an LDS object within the workgroup's LDS (for M0).
+__device__ __forceinline__ uint32_t lds_offset(const void *p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+
+// Logit bound of KV-head group g in log2 units, and whether it can serve as
+// the softmax shift.
+__device__ __forceinline__ bool group_bound(const float *qgain, const float *kgain, int g, int G, float scale_l2,
+                                            int D, float &bl2) {
+    bl2 = 0.0f;
+    if (!qgain || !kgain) return false;
+    float gq = 0.0f;
+    for (int hh = 0; hh < G; ++hh) gq = fmaxf(gq, fabsf(qgain[g * G + hh]));
+    bl2 = (float)D * gq * fabsf(kgain[g]) * scale_l2;
+    return bl2 <= 60.0f;
+}
+
+// Key held by row r of M-tile mt of S^T: lane (l16, lg) then receives keys
+// 32*(mt>>1) + 8*lg + 4*(mt&1) + e -- keys 8*lg..8*lg+7 of each 32-key half
+// over the two M-tiles of a half, which is the B layout of the P.V MFMA.
+__device__ __forceinline__ int permk(int mt, int r) {
+    return 32 * (mt >> 1) + 8 * (r >> 2) + 4 * (mt & 1) + (r & 3);
+}
+
+__device__ __forceinline__ bf16x8 pack8(const float (&x)[8]) {
+    bf16x8 r;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) r[e] = (__bf16)x[e];   // v_cvt_pk_bf16_f32, round to nearest even
+    return r;
+}
+
+// acc + the sum of 8 bf16 values (v_dot2 against ones: the products are exact)
+__device__ __forceinline__ float sum8(bf16x8 v, float acc) {
+    const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const bf16x2 pr = {v[2 * k], v[2 * k + 1]};
+        acc = __builtin_amdgcn_fdot2_f32_bf16(pr, one, acc, false);
+    }
+    return acc;
+}
+
+// Query operand of one lane's column (query i, head h) for S^T = K . Q^T:
+// d = 32*ks + 8*lg + 0..7.  QKNorm in fp32 rounded to bf16 (attention.py:
+// 88-94; the sum of squares is reduced across the column's four lanes); with
+// rope, apply_rope's rotation and bf16 roundings (:40-44) at position i.  The
+// rotation partner d +- D/2 sits in the same lane at ks +- NKS/2.  Invalid
+// columns read row 0 and are zeroed (no divergence around the shuffles).
+template <int D>
+__device__ __forceinline__ void qoperand(const bf16_t *q, int64_t qsb, int64_t qsn, int64_t qsh,
+                                         const float *qgain, float eps, const float *cosT,
+                                         const float *sinT, int64_t b, int64_t i, int h, bool valid,
+                                         bool rope, int lg, bf16x8 (&qop)[D / 32]) {
+    constexpr int NKS = D / 32;
+    const int64_t ii = valid ? i : 0;
+    const bf16_t *row = q + b * qsb + ii * qsn + (int64_t)h * qsh;
+    float x[NKS][8];
+    float ss = 0.0f;
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+        const u32x4 u = *reinterpret_cast<const u32x4 *>(row + 32 * ks + 8 * lg);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            x[ks][2 * e] = __uint_as_float(u[e] << 16);
+            x[ks][2 * e + 1] = __uint_as_float(u[e] & 0xffff0000u);
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss = fmaf(x[ks][e], x[ks][e], ss);
+    }
+    ss += __shfl_xor(ss, 16, 64);
+    ss += __shfl_xor(ss, 32, 64);
+    if (qgain) {
+        float ms = ss / (float)D;
+        if (ms < eps) ms = eps;
+        const float r = sqrtf(ms);
+        const float gn = qgain[h];
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) x[ks][e] = rnd_bf16((x[ks][e] / r) * gn);
+    }
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+        float y[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            float v = x[ks][e];
+            if (rope) {
+                const int d = 32 * ks + 8 * lg + e;
+                const float rot = (ks < NKS / 2) ? -x[ks + NKS / 2][e] : x[ks - NKS / 2][e];
+                const float t1 = rnd_bf16(v * rnd_bf16(cosT[ii * D + d]));
+                const float t2 = rnd_bf16(rot * rnd_bf16(sinT[ii * D + d]));
+                v = rnd_bf16(t1 + t2);
+            }
+            y[e] = valid ? v : 0.0f;
+        }
+        qop[ks] = pack8(y);
+    }
+}
+
+// Workgroup -> (batch*KV head combo, query tile).  Workgroup i runs on XCD
+// i % 8; xmap 1 (8 % Cn == 0) and 2 (Cn % 8 == 0) give each XCD one combo's
+// keys at a time, so the blocks it gathers share that XCD's L2.
+__device__ __forceinline__ void xcd_map(int i, int Cn, int ntiles, int xmap, int &combo, int &tile) {
+    if (xmap == 1) {
+        combo = (i & 7) % Cn;
+        tile = (i >> 3) * (8 / Cn) + (i & 7) / Cn;
+    } else if (xmap == 2) {
+        combo = (i / (8 * ntiles)) * 8 + (i & 7);
+        tile = (i >> 3) % ntiles;
+    } else {
+        combo = i / ntiles;
+        tile = i % ntiles;
+    }
+}
+
+// ======================================================== tile staging ====
+// LDS ring slot: K tile [64 keys][D] then V^T tile [D][64 keys], rows
+// unpadded; 16-byte chunk c of row r is stored at chunk c ^ f(r) (f < 8) so
+// that the MFMA fragment reads hit distinct banks: the K rows one read
+// instruction touches are permk(mt, 0..15), the V^T rows 16*dt + 0..15.
+__device__ __forceinline__ int swzK(int r) { return (r & 3) | ((r >> 1) & 4); }
+__device__ __forceinline__ int swzV(int r) { return r & 7; }
+
+template <int D>
+struct RtCfg {
+    static constexpr int NKS = D / 32;
+    static constexpr int NDT = D / 16;
+    static constexpr int WAVES = 8;
+    static constexpr int NTHR = WAVES * 64;
+    static constexpr int PTW = (D == 64) ? 4 : 2;      // max 16-row tiles per wave
+    static constexpr int SLOT = 2 * 64 * D;            // bf16 per ring slot (K + V^T)
+    static constexpr int NS = 4;                       // ring depth (blocks)
+    static constexpr int DPW = 2 * D / 64;             // 1 KB DMA instructions per wave per block
+};
+
+// One 1 KB direct-to-LDS copy: lane l's 16 bytes land at lds + 16*l.  Written
+// as inline asm so that the compiler does not serialise the ring on it (it
+// would wait for every outstanding LDS DMA before each LDS read); the ring
+// orders it by hand: s_waitcnt vmcnt + barrier before a slot is read, a
+// barrier before a slot is refilled.
+__device__ __forceinline__ void dma16(const bf16_t *src, uint32_t lds_addr) {
+    const uint32_t a = __builtin_amdgcn_readfirstlane(lds_addr);   // wave-uniform by construction
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+                 :
+                 : "s"(a), "v"(src)
+                 : "memory");
+}
+
+// vmcnt(N) with the other counters left alone (gfx9 s_waitcnt encoding)
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// vmcnt(c) for a runtime c in [0, 8] (larger values wait for everything)
+__device__ __forceinline__ void wait_vm_n(int c) {
+    switch (c) {
+        case 1: wait_vm<1>(); break;
+        case 2: wait_vm<2>(); break;
+        case 3: wait_vm<3>(); break;
+        case 4: wait_vm<4>(); break;
+        case 5: wait_vm<5>(); break;
+        case 6: wait_vm<6>(); break;
+        case 7: wait_vm<7>(); break;
+        case 8: wait_vm<8>(); break;
+        default: wait_vm<0>(); break;
+    }
+}
+
+// The wave's share of one block into ring slot `slot`: the block's K tile
+// (kc rows blk*64..+63) and V^T tile (vt columns blk*64..+63), swizzled.
+template <int D>
+__device__ __forceinline__ void ring_fill(const bf16_t *KC, const bf16_t *VT, int64_t n, int blk,
+                                          uint32_t slot_lds, int w, int lane) {
+    constexpr int CPR = D / 8;                          // 16-byte chunks per K row
+    constexpr int KPARTS = 64 * D * 2 / 1024;           // 1 KB parts of a K tile
+#pragma unroll
+    for (int pp = 0; pp < KPARTS / 8; ++pp) {
+        const int part = w + 8 * pp;
+        const int p = part * 64 + lane;                 // physical chunk index
+        const int r = p / CPR, pc = p % CPR;
+        const int c = pc ^ swzK(r);
+        dma16(KC + ((int64_t)blk * 64 + r) * D + 8 * c, slot_lds + (uint32_t)part * 1024u);
+    }
+#pragma unroll
+    for (int pp = 0; pp < KPARTS / 8; ++pp) {
+        const int part = w + 8 * pp;
+        const int p = part * 64 + lane;
+        const int r = p >> 3, pc = p & 7;
+        const int c = pc ^ swzV(r);
+        dma16(VT + (int64_t)r * n + (int64_t)blk * 64 + 8 * c,
+              slot_lds + (uint32_t)(64 * D * 2) + (uint32_t)part * 1024u);
+    }
+}
+
+
+// ======================================================= window kernel ====
+template <int D, int RT>
+struct WinCfg {
+    static constexpr int NKS = D / 32;                 // 32-wide d steps of S^T
+    static constexpr int NDT = D / 16;                 // 16-row d tiles of O^T
+    static constexpr int SLOT = 2 * 64 * D;            // bf16 per staged tile (K + V^T)
+    static constexpr int NS = 3;                       // tiles in flight
+};
+
+// DMA of one 64-key tile (kr rows, vt columns) into a ring slot by the
+// workgroup's waves: 2*D/64 KB split over nw waves (parts w, w + nw, ...).
+template <int D>
+__device__ __forceinline__ void win_fill(const bf16_t *KR, const bf16_t *VT, int n, int kb, uint32_t slot_lds,
+                                         int w, int nw, int lane) {
+    constexpr int CPR = D / 8;
+    constexpr int KPARTS = 64 * D * 2 / 1024;
+    for (int part = w; part < 2 * KPARTS; part += nw) {
+        const int p = (part % KPARTS) * 64 + lane;
+        if (part < KPARTS) {
+            const int r = p / CPR, c = (p % CPR) ^ swzK(p / CPR);
+            dma16(KR + (int64_t)(kb + r) * D + 8 * c, slot_lds + (uint32_t)part * 1024u);
+        } else {
+            const int r = p >> 3, c = (p & 7) ^ swzV(p >> 3);
+            dma16(VT + (int64_t)r * n + kb + 8 * c, slot_lds + (uint32_t)part * 1024u);
+        }
+    }
+}
+
+template <int D, int RT, bool FIXED>
+__device__ __forceinline__ void win_body(
+    const bf16_t *__restrict__ q, int64_t qsb, int64_t qsn, int64_t qsh, const float *__restrict__ qgain,
+    float eps, const bf16_t *__restrict__ kr, const bf16_t *__restrict__ vt,
+    const float *__restrict__ cosT, const float *__restrict__ sinT, int n, int Hq, int Hkv, int S,
+    int W, float sl2, float bl2, int gw, int wsplit, int combo, int hs, int tile, bf16_t *__restrict__ out,
+    int64_t osb, int64_t osn, int64_t osh, float *__restrict__ lse, bf16_t *ring) {
+    using C = WinCfg<D, RT>;
+    const int G = Hq / Hkv;
+    const int nw = blockDim.x >> 6;
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, lg = lane >> 4;
+    const int hh = hs * gw + w % gw, rg = w / gw;     // head within the group, query range
+    const bool hv = hh < G;                            // waves past the group's last head only stage
+    constexpr int QW = 16 * RT;                        // queries per wave
+    const int QT = QW * wsplit;                        // queries per workgroup
+    const int b = combo / Hkv, g = combo % Hkv;
+    const int64_t bh = (int64_t)b * Hkv + g;
+    const int h = g * G + (hv ? hh : 0);
+    const int i0 = tile * QT;
+    const int q0 = i0 + QW * rg;
+    const bf16_t *KR = kr + bh * n * D;
+    const bf16_t *VT = vt + bh * D * n;
+    const uint32_t ring_lds = lds_offset(ring);
+
+    bf16x8 qop[RT][C::NKS];
+    f32x4 O[RT][C::NDT];
+    float ls[RT], mr[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+        const int i = q0 + 16 * rt + l16;
+        qoperand<D>(q, qsb, qsn, qsh, qgain, eps, cosT, sinT, b, i, h, i < n, true, lg, qop[rt]);
+#pragma unroll
+        for (int dt = 0; dt < C::NDT; ++dt) O[rt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        ls[rt] = 0.0f;
+        mr[rt] = -INFINITY;
+    }
+    // this lane's key offset within a tile for accumulator element (mt, e)
+    const int kl = 8 * lg;
+
+    // the 64-key tiles covering every window of the workgroup's queries
+    const int ilast = ((i0 + QT < n) ? i0 + QT : n) - 1;
+    const int kfirst = (S > i0 - W + 1) ? S : i0 - W + 1;
+    if (kfirst <= ilast) {
+        const int t0 = kfirst / 64, t1 = ilast / 64, nt = t1 - t0 + 1;
+        for (int e = 0; e < C::NS - 1 && e < nt; ++e)
+            win_fill<D>(KR, VT, n, 64 * (t0 + e), ring_lds + (uint32_t)(e * C::SLOT * 2), w, nw, lane);
+        for (int e = 0; e < nt; ++e) {
+            // this wave's parts of tile e have landed once at most those of the
+            // next tile are still in flight
+            {
+                constexpr int PARTS = 2 * (64 * D * 2 / 1024);   // 1 KB parts of a tile
+                const int mine = (PARTS - w + nw - 1) / nw;       // this wave's parts per tile
+                const int ahead = (nt - 1 - e < C::NS - 2) ? nt - 1 - e : C::NS - 2;
+                wait_vm_n(ahead * mine);
+            }
+            __syncthreads();   // all parts of tile e landed; tile e-1 is consumed
+            if (e + C::NS - 1 < nt)
+                win_fill<D>(KR, VT, n, 64 * (t0 + e + C::NS - 1),
+                            ring_lds + (uint32_t)(((e + C::NS - 1) % C::NS) * C::SLOT * 2), w, nw, lane);
+            const bf16_t *Ks = ring + (e % C::NS) * C::SLOT;
+            const bf16_t *Vs = Ks + 64 * D;
+            const int kb = 64 * (t0 + e);
+            bool act[RT], full[RT];
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) {
+                const int qa = q0 + 16 * rt;
+                const int qb = (qa + 15 < n) ? qa + 15 : n - 1;
+                const int lo = (S > qa - W + 1) ? S : qa - W + 1;
+                const int lob = (S > qb - W + 1) ? S : qb - W + 1;
+                act[rt] = hv && qa < n && kb <= qb && kb + 63 >= lo;
+                full[rt] = kb >= lob && kb + 63 <= qa;
+            }
+            // the tile's K fragments, read from LDS once for all row tiles
+            bf16x8 kf[4][C::NKS];
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) {
+                const int r = permk(mt, l16);
+                const bf16_t *kp = Ks + r * D;
+                const int sw = swzK(r);
+#pragma unroll
+                for (int ks = 0; ks < C::NKS; ++ks) kf[mt][ks] = ldb8(kp + 8 * ((4 * ks + lg) ^ sw));
+            }
+            // per row tile: S^T, probabilities, packed P^T
+            bf16x8 pb[RT][2];
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) {
+                if (!act[rt]) continue;
+                f32x4 Sa[4];
+#pragma unroll
+                for (int mt = 0; mt < 4; ++mt) {
+                    Sa[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int ks = 0; ks < C::NKS; ++ks) Sa[mt] = mma(kf[mt][ks], qop[rt][ks], Sa[mt]);
+                }
+                const int i = q0 + 16 * rt + l16;      // this lane's column
+                const int jlo = ((S > i - W + 1) ? S : i - W + 1) - kb;   // valid key offsets [jlo, jhi]
+                const int jhi = i - kb;
+                const bool fullt = full[rt];           // wave-uniform: no mask at all
+                float p[2][8];
+                float shift = bl2;
+                if constexpr (!FIXED) {
+                    float tmax = -INFINITY;
+#pragma unroll
+                    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const int j = kl + 32 * (mt >> 1) + 4 * (mt & 1) + e;
+                            const bool ok = fullt | ((j >= jlo) & (j <= jhi));
+                            tmax = fmaxf(tmax, ok ? Sa[mt][e] : -INFINITY);
+                        }
+                    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+                    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+                    const float mnew = fmaxf(mr[rt], tmax * sl2);
+                    shift = (mnew == -INFINITY) ? 0.0f : mnew;
+                    const float alpha = ex2(mr[rt] - shift);
+                    mr[rt] = mnew;
+                    ls[rt] *= alpha;
+#pragma unroll
+                    for (int dt = 0; dt < C::NDT; ++dt) O[rt][dt] *= alpha;
+                }
+                if (fullt) {
+#pragma unroll
+                    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) p[mt >> 1][(mt & 1) * 4 + e] = ex2(fmaf(Sa[mt][e], sl2, -shift));
+                } else {
+                    // masked keys: the exp2 argument is selected to -inf (no branch per element)
+#pragma unroll
+                    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const int j = kl + 32 * (mt >> 1) + 4 * (mt & 1) + e;
+                            const bool ok = (j >= jlo) & (j <= jhi);
+                            const float a = fmaf(Sa[mt][e], sl2, -shift);
+                            p[mt >> 1][(mt & 1) * 4 + e] = ex2(ok ? a : -INFINITY);
+                        }
+                }
+                pb[rt][0] = pack8(p[0]);
+                pb[rt][1] = pack8(p[1]);
+                ls[rt] = sum8(pb[rt][1], sum8(pb[rt][0], ls[rt]));
+            }
+            // O^T += V^T . P^T; each V^T fragment read once
+#pragma unroll
+            for (int dt = 0; dt < C::NDT; ++dt) {
+                const int r = 16 * dt + l16;
+                const bf16_t *vp = Vs + r * 64;
+                const int sw = swzV(r);
+                const bf16x8 v0 = ldb8(vp + 8 * (lg ^ sw)), v1 = ldb8(vp + 8 * ((lg + 4) ^ sw));
+#pragma unroll
+                for (int rt = 0; rt < RT; ++rt) {
+                    if (!act[rt]) continue;
+                    O[rt][dt] = mma(v0, pb[rt][0], O[rt][dt]);
+                    O[rt][dt] = mma(v1, pb[rt][1], O[rt][dt]);
+                }
+            }
+        }
+    }
+
+    // normalise and store the window's rows and their LSE
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+        float l = ls[rt];
+        l += __shfl_xor(l, 16, 64);
+        l += __shfl_xor(l, 32, 64);
+        const int i = q0 + 16 * rt + l16;
+        if (i >= n || !hv) continue;
+        const float inv = (l > 0.0f) ? 1.0f / l : 0.0f;
+        bf16_t *orow = out + (int64_t)b * osb + (int64_t)i * osn + (int64_t)h * osh;
+#pragma unroll
+        for (int dt = 0; dt < C::NDT; ++dt) {
+            u32x2 u;
+            u[0] = (uint32_t)f2bf(O[rt][dt][0] * inv) | ((uint32_t)f2bf(O[rt][dt][1] * inv) << 16);
+            u[1] = (uint32_t)f2bf(O[rt][dt][2] * inv) | ((uint32_t)f2bf(O[rt][dt][3] * inv) << 16);
+            *reinterpret_cast<u32x2 *>(orow + 16 * dt + 4 * lg) = u;
+        }
+        if (lg == 0) {
+            const float sh = FIXED ? bl2 : mr[rt];
+            lse[((int64_t)b * Hq + h) * n + i] = (l > 0.0f) ? (__log2f(l) + sh) / LOG2E : -INFINITY;
+        }
+    }
+}
+
+// Grid: Cn = B*Hkv*hsplit combos (the heads of a group split over hsplit
+// workgroups of gw heads when G > 8) times the query tiles.
+template <int D, int RT>
+__global__ __launch_bounds__(512) void attn_win_kernel(
+    const bf16_t *__restrict__ q, int64_t qsb, int64_t qsn, int64_t qsh, const float *__restrict__ qgain,
+    const float *__restrict__ kgain, float eps, const bf16_t *__restrict__ kr, const bf16_t *__restrict__ vt,
+    const float *__restrict__ cosT, const float *__restrict__ sinT, int n, int Hq, int Hkv, int S,
+    int W, float scale, int gw, int hsplit, int wsplit, int ntiles, int Cn, int xmap,
+    bf16_t *__restrict__ out, int64_t osb, int64_t osn, int64_t osh, float *__restrict__ lse) {
+    extern __shared__ __align__(16) char smem[];
+    int cx, tile;
+    xcd_map(blockIdx.x, Cn, ntiles, xmap, cx, tile);
+    if (tile >= ntiles || cx >= Cn) return;
+    const int combo = cx / hsplit, hs = cx % hsplit;
+    const int G = Hq / Hkv;
+    const float sl2 = scale * LOG2E;
+    float bl2;
+    if (group_bound(qgain, kgain, combo % Hkv, G, sl2, D, bl2))
+        win_body<D, RT, true>(q, qsb, qsn, qsh, qgain, eps, kr, vt, cosT, sinT, n, Hq, Hkv, S, W, sl2, bl2, gw,
+                              wsplit, combo, hs, tile, out, osb, osn, osh, lse, reinterpret_cast<bf16_t *>(smem));
+    else
+        win_body<D, RT, false>(q, qsb, qsn, qsh, qgain, eps, kr, vt, cosT, sinT, n, Hq, Hkv, S, W, sl2, bl2, gw,
+                               wsplit, combo, hs, tile, out, osb, osn, osh, lse, reinterpret_cast<bf16_t *>(smem));
+}
+
+// ======================================================= routed kernel ====
+enum { RM_SINK = 0, RM_COL = 1 };
+
+// One staged block against one 16-row tile.  mode RM_SINK: keys j < S and
+// j <= i are valid (nmt M-tiles can hold them); RM_COL: the whole block is
+// valid for the columns whose query picked it (colok).
+template <int D, bool FIXED>
+__device__ __forceinline__ void rt_update(const bf16_t *Ks, const bf16_t *Vs, const bf16x8 (&qop)[D / 32],
+                                          f32x4 (&O)[D / 16], float &mrun, float &lsum, int mode,
+                                          int64_t icol, bool colok, int S, int nmt, float sl2, float bl2,
+                                          int l16, int lg) {
+    constexpr int NKS = D / 32, NDT = D / 16;
+    f32x4 Sa[4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+        Sa[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (mt < nmt) {
+            const int r = permk(mt, l16);
+            const bf16_t *kp = Ks + r * D;
+            const int sw = swzK(r);
+#pragma unroll
+            for (int ks = 0; ks < NKS; ++ks) Sa[mt] = mma(ldb8(kp + 8 * ((4 * ks + lg) ^ sw)), qop[ks], Sa[mt]);
+        }
+    }
+    float p[2][8];
+    float shift = bl2;
+    if constexpr (!FIXED) {
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int j = 32 * (mt >> 1) + 8 * lg + 4 * (mt & 1) + e;
+                const bool ok = (mode == RM_SINK) ? ((mt < nmt) & (j < S) & ((int64_t)j <= icol)) : colok;
+                tmax = fmaxf(tmax, ok ? Sa[mt][e] : -INFINITY);
+            }
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        const float mnew = fmaxf(mrun, tmax * sl2);
+        shift = (mnew == -INFINITY) ? 0.0f : mnew;
+        const float alpha = ex2(mrun - shift);
+        mrun = mnew;
+        lsum *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) O[dt] *= alpha;
+    }
+    if (mode == RM_COL) {
+        // a column whose query did not pick the block: shift +inf, so every
+        // exp2 argument is -inf (no select per element)
+        const float sh = colok ? shift : INFINITY;
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) p[mt >> 1][(mt & 1) * 4 + e] = ex2(fmaf(Sa[mt][e], sl2, -sh));
+    } else {
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int j = 32 * (mt >> 1) + 8 * lg + 4 * (mt & 1) + e;
+                const bool ok = (mt < nmt) & (j < S) & ((int64_t)j <= icol);
+                const float a = fmaf(Sa[mt][e], sl2, -shift);
+                p[mt >> 1][(mt & 1) * 4 + e] = ex2(ok ? a : -INFINITY);
+            }
+    }
+    const bf16x8 pb0 = pack8(p[0]), pb1 = pack8(p[1]);
+    lsum = sum8(pb1, sum8(pb0, lsum));
+    const bool two = mode != RM_SINK || nmt > 2;        // keys 32..63 can be valid
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+        const int r = 16 * dt + l16;
+        const bf16_t *vp = Vs + r * 64;
+        const int sw = swzV(r);
+        O[dt] = mma(ldb8(vp + 8 * (lg ^ sw)), pb0, O[dt]);
+        if (two) O[dt] = mma(ldb8(vp + 8 * ((lg + 4) ^ sw)), pb1, O[dt]);
+    }
+}
+
+template <int D, bool FIXED>
+__device__ __forceinline__ void routed_body(
+    const bf16_t *__restrict__ q, int64_t qsb, int64_t qsn, int64_t qsh, const float *__restrict__ qgain,
+    float eps, const bf16_t *__restrict__ kc, const bf16_t *__restrict__ vt,
+    const int32_t *__restrict__ idx, const int32_t *__restrict__ cnt, int64_t n, int Hq, int Hkv, int S,
+    int kk, float sl2, float bl2, int ptw, int combo, int tile, bf16_t *__restrict__ out,
+    int64_t osb, int64_t osn, int64_t osh, const float *__restrict__ lse, char *smem, int &nlist) {
+    using C = RtCfg<D>;
+    const int G = Hq / Hkv;
+    const int QPT = 16 / G;
+    const int QT = C::WAVES * ptw * QPT;
+    const int tid = threadIdx.x;
+    const int w = tid >> 6, lane = tid & 63, l16 = lane & 15, lg = lane >> 4;
+    const int b = combo / Hkv, g = combo % Hkv;
+    const int64_t i0 = (int64_t)tile * QT;
+    const int64_t bh = (int64_t)b * Hkv + g;
+    const int64_t nb = n / 64;
+    const int nbw = (int)((nb + 31) / 32);
+    const bf16_t *KC = kc + bh * n * D;
+    const bf16_t *VT = vt + bh * D * n;
+
+    bf16_t *ring = reinterpret_cast<bf16_t *>(smem);
+    const uint32_t ring_lds = lds_offset(ring);            // LDS byte address of the ring
+    int16_t *sel = reinterpret_cast<int16_t *>(smem + (size_t)C::NS * C::SLOT * 2);
+    uint32_t *bitmap = reinterpret_cast<uint32_t *>(sel + ((QT * kk + 1) & ~1));
+    int16_t *list = reinterpret_cast<int16_t *>(bitmap + nbw);   // [0 if sinks] + union
+
+    // ------------------------------------- selection lists and their union
+    for (int e = tid; e < nbw; e += C::NTHR) bitmap[e] = 0u;
+    __syncthreads();
+    for (int qq = tid; qq < QT; qq += C::NTHR) {
+        int16_t *sl = sel + qq * kk;
+        const int64_t i = i0 + qq;
+        int m2 = 0;
+        if (i < n) {
+            const int c = min(max(cnt[bh * n + i], 0), kk);
+            const int32_t *ix = idx + (bh * n + i) * kk;
+            for (int r = 0; r < c; ++r) {
+                const int v = ix[r];
+                if (v < 1 || v >= nb) continue;          // block 0 is never routed
+                int p = m2++;
+                while (p > 0 && sl[p - 1] > v) {
+                    sl[p] = sl[p - 1];
+                    --p;
+                }
+                sl[p] = (int16_t)v;
+                atomicOr(&bitmap[v >> 5], 1u << (v & 31));
+            }
+        }
+        for (int r = m2; r < kk; ++r) sl[r] = SENT;
+    }
+    __syncthreads();
+    if (w == 0) {
+        const int first = (S > 0) ? 1 : 0;
+        if (lane == 0 && first) list[0] = 0;
+        int base = first;
+        for (int w0 = 0; w0 < nbw; w0 += 64) {
+            uint32_t word = (w0 + lane < nbw) ? bitmap[w0 + lane] : 0u;
+            const int pc = __popc(word);
+            int incl = pc;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const int t = __shfl_up(incl, o, 64);
+                if (lane >= o) incl += t;
+            }
+            int off = base + incl - pc;
+            while (word) {
+                const int bit = __ffs(word) - 1;
+                list[off++] = (int16_t)((w0 + lane) * 32 + bit);
+                word &= word - 1u;
+            }
+            base += __shfl(incl, 63, 64);
+        }
+        if (lane == 0) nlist = base;
+    }
+
+    // ----------------------------------------------------- per-row state --
+    const int qs = l16 / G;
+    const int hh = l16 % G;
+    const bool colv = l16 < QPT * G;
+    bf16x8 qop[C::PTW][C::NKS];
+    f32x4 O[C::PTW][C::NDT];
+    float mrun[C::PTW], lsum[C::PTW];
+    int64_t icol[C::PTW];
+    bool cok[C::PTW];
+#pragma unroll
+    for (int t = 0; t < C::PTW; ++t) {
+        icol[t] = i0 + (int64_t)(w * ptw + t) * QPT + qs;
+        cok[t] = colv && t < ptw && icol[t] < n;
+        mrun[t] = -INFINITY;
+        lsum[t] = 0.0f;
+#pragma unroll
+        for (int dt = 0; dt < C::NDT; ++dt) O[t][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (t < ptw)
+            qoperand<D>(q, qsb, qsn, qsh, qgain, eps, nullptr, nullptr, b, icol[t], g * G + hh, cok[t], false, lg,
+                        qop[t]);
+    }
+    __syncthreads();
+    const int ne = nlist;
+
+    // ------------------------------------------ sinks + routed, DMA ring --
+    int cur[C::PTW], nxt[C::PTW];
+#pragma unroll
+    for (int t = 0; t < C::PTW; ++t) {
+        cur[t] = 0;
+        const int ql = (w * ptw + t) * QPT + qs;
+        nxt[t] = cok[t] ? (int)sel[ql * kk] : (int)SENT;
+    }
+    const int nmt_s = (S <= 4) ? 1 : (S <= 32 ? 2 : 4);
+    for (int e = 0; e < C::NS - 1 && e < ne; ++e)
+        ring_fill<D>(KC, VT, n, list[e], ring_lds + (uint32_t)(e * C::SLOT * 2), w, lane);
+    for (int e = 0; e < ne; ++e) {
+        // this wave's share of entry e has landed once at most the shares of
+        // the entries after it (up to NS-2 of them) are still in flight
+        const int ahead = (ne - 1 - e < C::NS - 2) ? ne - 1 - e : C::NS - 2;
+        if (ahead >= 2) wait_vm<2 * C::DPW>();
+        else if (ahead == 1) wait_vm<C::DPW>();
+        else wait_vm<0>();
+        __syncthreads();   // every share of entry e landed; entry e-1 is consumed
+        if (e + C::NS - 1 < ne)
+            ring_fill<D>(KC, VT, n, list[e + C::NS - 1],
+                         ring_lds + (uint32_t)(((e + C::NS - 1) % C::NS) * C::SLOT * 2), w, lane);
+        const bf16_t *Ks = ring + (e % C::NS) * C::SLOT;
+        const bf16_t *Vs = Ks + 64 * D;
+        const int blk = list[e];
+        const bool sink = S > 0 && e == 0;
+#pragma unroll
+        for (int tt = 0; tt < C::PTW; ++tt) {
+            if (tt >= ptw) break;
+            if (sink) {
+                if (i0 + (int64_t)(w * ptw + tt) * QPT >= n) break;
+                rt_update<D, FIXED>(Ks, Vs, qop[tt], O[tt], mrun[tt], lsum[tt], RM_SINK, icol[tt], cok[tt], S,
+                                    nmt_s, sl2, bl2, l16, lg);
+            } else {
+                const bool hit = nxt[tt] == blk;
+                if (__ballot(hit) == 0) continue;
+                rt_update<D, FIXED>(Ks, Vs, qop[tt], O[tt], mrun[tt], lsum[tt], RM_COL, icol[tt], hit, S, 4,
+                                    sl2, bl2, l16, lg);
+                if (hit) {
+                    ++cur[tt];
+                    const int ql = (w * ptw + tt) * QPT + qs;
+                    nxt[tt] = (cur[tt] < kk) ? (int)sel[ql * kk + cur[tt]] : (int)SENT;
+                }
+            }
+        }
+    }
+
+    // ------------------- merge with the window's (out, LSE), normalise, store
+#pragma unroll
+    for (int t = 0; t < C::PTW; ++t) {
+        if (t >= ptw) break;
+        float l = lsum[t];
+        l += __shfl_xor(l, 16, 64);
+        l += __shfl_xor(l, 32, 64);
+        if (!cok[t]) continue;
+        const int h = g * G + hh;
+        const int64_t i = icol[t];
+        const float lw = lse[((int64_t)b * Hq + h) * n + i];           // natural log
+        const float sh = FIXED ? bl2 : mrun[t];
+        const float lr = (l > 0.0f) ? (__log2f(l) + sh) / LOG2E : -INFINITY;
+        const float m = fmaxf(lw, lr);
+        const float ww = (lw == -INFINITY) ? 0.0f : __expf(lw - m);
+        const float wr = (lr == -INFINITY) ? 0.0f : __expf(lr - m);
+        const float den = ww + wr;
+        const float fw = den > 0.0f ? ww / den : 0.0f;
+        const float fr = (den > 0.0f && l > 0.0f) ? wr / (den * l) : 0.0f;
+        bf16_t *orow = out + (int64_t)b * osb + i * osn + (int64_t)h * osh;
+#pragma unroll
+        for (int dt = 0; dt < C::NDT; ++dt) {
+            u32x2 u = *reinterpret_cast<const u32x2 *>(orow + 16 * dt + 4 * lg);
+            float o[4];
+            o[0] = __uint_as_float(u[0] << 16) * fw + O[t][dt][0] * fr;
+            o[1] = __uint_as_float(u[0] & 0xffff0000u) * fw + O[t][dt][1] * fr;
+            o[2] = __uint_as_float(u[1] << 16) * fw + O[t][dt][2] * fr;
+            o[3] = __uint_as_float(u[1] & 0xffff0000u) * fw + O[t][dt][3] * fr;
+            u[0] = (uint32_t)f2bf(o[0]) | ((uint32_t)f2bf(o[1]) << 16);
+            u[1] = (uint32_t)f2bf(o[2]) | ((uint32_t)f2bf(o[3]) << 16);
+            *reinterpret_cast<u32x2 *>(orow + 16 * dt + 4 * lg) = u;
+        }
+    }
+}
+
+template <int D>
+__global__ __launch_bounds__(512) void attn_routed_kernel(
+    const bf16_t *__restrict__ q, int64_t qsb, int64_t qsn, int64_t qsh, const float *__restrict__ qgain,
+    const float *__restrict__ kgain, float eps, const bf16_t *__restrict__ kc, const bf16_t *__restrict__ vt,
+    const int32_t *__restrict__ idx, const int32_t *__restrict__ cnt, int64_t n, int Hq, int Hkv, int S,
+    int kk, float scale, int ptw, int ntiles, int Cn, int xmap, bf16_t *__restrict__ out,
+    int64_t osb, int64_t osn, int64_t osh, const float *__restrict__ lse) {
+    extern __shared__ __align__(16) char smem[];
+    __shared__ int nlist;
+    int combo, tile;
+    xcd_map(blockIdx.x, Cn, ntiles, xmap, combo, tile);
+    if (tile >= ntiles || combo >= Cn) return;
+    const int G = Hq / Hkv;
+    const float sl2 = scale * LOG2E;
+    float bl2;
+    if (group_bound(qgain, kgain, combo % Hkv, G, sl2, D, bl2))
+        routed_body<D, true>(q, qsb, qsn, qsh, qgain, eps, kc, vt, idx, cnt, n, Hq, Hkv, S, kk, sl2, bl2, ptw,
+                             combo, tile, out, osb, osn, osh, lse, smem, nlist);
+    else
+        routed_body<D, false>(q, qsb, qsn, qsh, qgain, eps, kc, vt, idx, cnt, n, Hq, Hkv, S, kk, sl2, bl2, ptw,
+                              combo, tile, out, osb, osn, osh, lse, smem, nlist);
+}
+
+// ============================================================ launchers ====
+static void grid_map(int64_t Cn, int64_t ntiles, int &xmap, int64_t &grid) {
+    if (8 % Cn == 0) {
+        xmap = 1;   // 8 workgroups per round, 8/Cn tiles of each combo per round
+        grid = 8 * ((ntiles + (8 / Cn) - 1) / (8 / Cn));
+    } else if (Cn % 8 == 0) {
+        xmap = 2;
+        grid = Cn * ntiles;
+    } else {
+        xmap = 0;
+        grid = Cn * ntiles;
+    }
+}
+
+template <int D, int RT>
+static int launch_win(const void *q, const int64_t *qs, const float *qgain, const float *kgain, float eps,
+                      const void *kr, const void *vt, const float *cosT, const float *sinT, int64_t B, int64_t n,
+                      int64_t Hq, int64_t Hkv, int64_t S, int64_t W, float scale, void *out, const int64_t *os,
+                      float *lse, hipStream_t s) {
+    using C = WinCfg<D, RT>;
+    const int G = (int)(Hq / Hkv);
+    const int hsplit = (G + 7) / 8;                    // at most 8 heads (waves) per workgroup
+    const int gw = (G + hsplit - 1) / hsplit;
+    const int wsplit = (gw >= 4) ? 1 : (4 + gw - 1) / gw;   // at least 4 waves (256 threads)
+    const int nthr = 64 * gw * wsplit;
+    if (nthr > 512 || nthr < 256) return HBA_ERR_UNSUPPORTED;
+    const int64_t QT = 16 * RT * wsplit;
+    const int64_t ntiles = (n + QT - 1) / QT;
+    const int64_t Cn = B * Hkv * hsplit;
+    int xmap;
+    int64_t grid;
+    grid_map(Cn, ntiles, xmap, grid);
+    if (grid > 0x7fffffff) return HBA_ERR_UNSUPPORTED;
+    const size_t lds = (size_t)C::NS * C::SLOT * 2;
+    if (hipFuncSetAttribute(reinterpret_cast<const void *>(&attn_win_kernel<D, RT>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+        return HBA_ERR_LAUNCH;
+    const int Wc = (int)((W < n + 1) ? W : n + 1);     // a window longer than the sequence is the sequence
+    hipLaunchKernelGGL((attn_win_kernel<D, RT>), dim3((unsigned)grid), dim3(nthr), lds, s, (const bf16_t *)q, qs[0],
+                       qs[1], qs[2], qgain, kgain, eps, (const bf16_t *)kr, (const bf16_t *)vt, cosT, sinT, (int)n,
+                       (int)Hq, (int)Hkv, (int)S, Wc, scale, gw, hsplit, wsplit, (int)ntiles, (int)Cn, xmap,
+                       (bf16_t *)out, os[0], os[1], os[2], lse);
+    return HBA_OK;
+}
+
+template <int D>
+static int launch_routed(const void *q, const int64_t *qs, const float *qgain, const float *kgain, float eps,
+                         const void *kc, const void *vt, const int32_t *idx, const int32_t *cnt, int64_t B,
+                         int64_t n, int64_t Hq, int64_t Hkv, int64_t S, int64_t k, float scale, void *out,
+                         const int64_t *os, const float *lse, hipStream_t s) {
+    using C = RtCfg<D>;
+    const int G = (int)(Hq / Hkv);
+    const int QPT = 16 / G;
+    const int64_t nb = n / 64;
+    const int64_t nbw = (nb + 31) / 32;
+    int ptw = C::PTW;
+    size_t lds = 0;
+    for (; ptw >= 1; --ptw) {
+        const int64_t QT = (int64_t)C::WAVES * ptw * QPT;
+        lds = (size_t)C::NS * C::SLOT * 2 + (size_t)((QT * k + 1) & ~1LL) * 2 + (size_t)nbw * 4 +
+              (size_t)(nb + 1) * 2 + 16;
+        if (lds <= 160 * 1024 - 64) break;
+    }
+    if (ptw < 1) return HBA_ERR_UNSUPPORTED;
+    const int64_t QT = (int64_t)C::WAVES * ptw * QPT;
+    const int64_t ntiles = (n + QT - 1) / QT;
+    int xmap;
+    int64_t grid;
+    grid_map(B * Hkv, ntiles, xmap, grid);
+    if (grid > 0x7fffffff) return HBA_ERR_UNSUPPORTED;
+    if (hipFuncSetAttribute(reinterpret_cast<const void *>(&attn_routed_kernel<D>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+        return HBA_ERR_LAUNCH;
+    hipLaunchKernelGGL((attn_routed_kernel<D>), dim3((unsigned)grid), dim3(C::NTHR), lds, s, (const bf16_t *)q,
+                       qs[0], qs[1], qs[2], qgain, kgain, eps, (const bf16_t *)kc, (const bf16_t *)vt, idx, cnt, n,
+                       (int)Hq, (int)Hkv, (int)S, (int)k, scale, ptw, (int)ntiles, (int)(B * Hkv), xmap,
+                       (bf16_t *)out, os[0], os[1], os[2], lse);
+    return HBA_OK;
+}
+
+}  // namespace ab
+
+template <int D>
+int launch_attn_bf16(const void *q, const int64_t *qs, const float *qgain, const float *kgain, float eps,
+                     const void *kc, const void *kr, const void *vt, const float *cosT, const float *sinT,
+                     const int32_t *idx, const int32_t *cnt, int64_t B, int64_t n, int64_t Hq, int64_t Hkv,
+                     int64_t S, int64_t W, int64_t k, float scale, void *out, const int64_t *os, float *lse,
+                     hipStream_t s) {
+    using namespace ab;
+    const int G = (int)(Hq / Hkv);
+    if (G > 16 || n / 64 >= SENT) return HBA_ERR_UNSUPPORTED;
+    constexpr int RT = (D == 64) ? 3 : 1;      // row tiles per wave: the most that fit 256 VGPRs
+    int st = launch_win<D, RT>(q, qs, qgain, kgain, eps, kr, vt, cosT, sinT, B, n, Hq, Hkv, S, W, scale, out, os,
+                               lse, s);
+    if (st) return st;
+    return launch_routed<D>(q, qs, qgain, kgain, eps, kc, vt, idx, cnt, B, n, Hq, Hkv, S, k, scale, out, os, lse,
+                            s);
+}
+
+template int launch_attn_bf16<64>(const void *, const int64_t *, const float *, const float *, float,
+                                     const void *, const void *, const void *, const float *, const float *,
+                                     const int32_t *, const int32_t *, int64_t, int64_t, int64_t, int64_t,
+                                     int64_t, int64_t, int64_t, float, void *, const int64_t *, float *,
+                                     hipStream_t);
+template int launch_attn_bf16<128>(const void *, const int64_t *, const float *, const float *, float,
+                                      const void *, const void *, const void *, const float *, const float *,
+                                      const int32_t *, const int32_t *, int64_t, int64_t, int64_t, int64_t,
+                                      int64_t, int64_t, int64_t, float, void *, const int64_t *, float *,
+                                      hipStream_t);
+
+}  // namespace hba

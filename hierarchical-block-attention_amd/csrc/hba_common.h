@@ -25,14 +25,14 @@ typedef uint16_t bf16_t;  // raw bf16 bits in memory
 
 __device__ __forceinline__ float bf2f(bf16_t b) { return __uint_as_float((uint32_t)b << 16); }
 
+// fp32 -> bf16, round to nearest even; a NaN stays a (quiet) NaN.  Branch
+// free: infinities pass through the rounding unchanged, finite values that
+// round past the largest bf16 become infinities, as RNE requires.
 __device__ __forceinline__ bf16_t f2bf(float x) {
-    uint32_t u = __float_as_uint(x);
-    if ((u & 0x7f800000u) == 0x7f800000u) {
-        if (u & 0x007fffffu) u |= 0x00400000u;
-        return (bf16_t)(u >> 16);
-    }
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return (bf16_t)(u >> 16);
+    const uint32_t u = __float_as_uint(x);
+    const uint32_t r = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+    const uint32_t qnan = (u >> 16) | 0x40u;
+    return (bf16_t)(((u & 0x7fffffffu) > 0x7f800000u) ? qnan : r);
 }
 
 __device__ __forceinline__ float rnd_bf16(float x) { return bf2f(f2bf(x)); }

@@ -245,11 +245,14 @@ def attn_fwd(q: Tensor, q_gain: Optional[Tensor], k_gain: Optional[Tensor], eps:
     idx = idx.contiguous()
     cnt = cnt.contiguous()
     out = torch.empty(B, n, Hq, d, dtype=q.dtype, device=dev)
+    nbytes = ctypes.c_size_t(0)
+    check(lib().hba_attn_workspace_size(_code(q), B, n, Hq, ctypes.byref(nbytes)), "hba_attn_workspace_size")
+    ws = torch.empty(max(int(nbytes.value), 16), dtype=torch.uint8, device=dev)
     with torch.cuda.device(dev):
         st = lib().hba_attn_fwd(_code(q), _p(q), strides3(q), _p(qg), _p(kg), eps, _p(kc.contiguous()),
                                 _p(kr.contiguous()), _p(vt.contiguous()), _p(cos), _p(sin), _p(idx),
                                 _p(cnt), B, n, Hq, Hkv, d, sinks, window, BLOCK, idx.shape[3], scale,
-                                _p(out), strides3(out), _stream(dev))
+                                _p(ws), int(nbytes.value), _p(out), strides3(out), _stream(dev))
     check(st, "hba_attn_fwd")
     return out
 

@@ -12,7 +12,7 @@
  *   - All calls are asynchronous on `stream` (a hipStream_t; NULL = the null
  *     stream).  No call allocates memory, keeps global mutable state or
  *     synchronises; calls on distinct streams are independent.  Scratch space
- *     (decode only) is passed in by the caller, sized by the *_workspace_size
+ *     (bf16 attention, decode) is passed in by the caller, sized by the *_workspace_size
  *     query.
  *   - Return value: HBA_OK (0) or a negative status (invalid argument,
  *     unsupported shape/dtype/architecture, launch failure);
@@ -149,7 +149,12 @@ int hba_attn_fwd(int dtype, const void *q, const int64_t q_strides[3],
                  const int32_t *idx, const int32_t *cnt,
                  int64_t B, int64_t n, int64_t Hq, int64_t Hkv, int64_t d,
                  int64_t S, int64_t W, int64_t Bk, int64_t k, float scale,
+                 void *workspace, size_t ws_bytes,
                  void *out, const int64_t out_strides[3], void *stream);
+
+/* Scratch bytes hba_attn_fwd needs (bf16: the window's LSE, B*Hq*n fp32;
+ * fp32: none).  workspace must be 16-byte aligned. */
+int hba_attn_workspace_size(int dtype, int64_t B, int64_t n, int64_t Hq, size_t *bytes);
 
 /*
  * Paged KV cache (decode).  Page = Bk tokens of one sequence; all tensors
