@@ -180,12 +180,14 @@ template <int D>
 struct RtCfg {
     static constexpr int NKS = D / 32;
     static constexpr int NDT = D / 16;
-    static constexpr int WAVES = 8;
+    static constexpr int WAVES = 16;                   // 4 per SIMD: latency hiding
     static constexpr int NTHR = WAVES * 64;
-    static constexpr int PTW = (D == 64) ? 4 : 2;      // max 16-row tiles per wave
+    static constexpr int PTW = (D == 64) ? 2 : 1;      // max 16-row tiles per wave (<= 128 VGPRs)
     static constexpr int SLOT = 2 * 64 * D;            // bf16 per ring slot (K + V^T)
-    static constexpr int NS = 4;                       // ring depth (blocks)
-    static constexpr int DPW = 2 * D / 64;             // 1 KB DMA instructions per wave per block
+    static constexpr int NS = (D == 64) ? 8 : 4;       // ring depth (blocks, 128 KB)
+    static constexpr int KPARTS = 64 * D * 2 / 1024;   // 1 KB parts of a K (and of a V^T) tile
+    static constexpr int DPW = 2 * KPARTS / WAVES;     // DMA instructions per wave per block
+    static_assert(DPW * WAVES == 2 * KPARTS, "parts split evenly over the waves");
 };
 
 // One 1 KB direct-to-LDS copy: lane l's 16 bytes land at lds + 16*l.  Written
@@ -207,17 +209,16 @@ __device__ __forceinline__ void wait_vm() {
     __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
-// vmcnt(c) for a runtime c in [0, 8] (larger values wait for everything)
+// vmcnt(c) for a wave-uniform runtime c in [0, 24] (larger values wait for
+// everything: always safe, only slower)
 __device__ __forceinline__ void wait_vm_n(int c) {
     switch (c) {
-        case 1: wait_vm<1>(); break;
-        case 2: wait_vm<2>(); break;
-        case 3: wait_vm<3>(); break;
-        case 4: wait_vm<4>(); break;
-        case 5: wait_vm<5>(); break;
-        case 6: wait_vm<6>(); break;
-        case 7: wait_vm<7>(); break;
-        case 8: wait_vm<8>(); break;
+#define HBA_VMW(N) \
+    case N: wait_vm<N>(); break;
+        HBA_VMW(1) HBA_VMW(2) HBA_VMW(3) HBA_VMW(4) HBA_VMW(5) HBA_VMW(6) HBA_VMW(7) HBA_VMW(8)
+        HBA_VMW(9) HBA_VMW(10) HBA_VMW(11) HBA_VMW(12) HBA_VMW(13) HBA_VMW(14) HBA_VMW(15) HBA_VMW(16)
+        HBA_VMW(17) HBA_VMW(18) HBA_VMW(19) HBA_VMW(20) HBA_VMW(21) HBA_VMW(22) HBA_VMW(23) HBA_VMW(24)
+#undef HBA_VMW
         default: wait_vm<0>(); break;
     }
 }
@@ -227,24 +228,19 @@ __device__ __forceinline__ void wait_vm_n(int c) {
 template <int D>
 __device__ __forceinline__ void ring_fill(const bf16_t *KC, const bf16_t *VT, int64_t n, int blk,
                                           uint32_t slot_lds, int w, int lane) {
+    using C = RtCfg<D>;
     constexpr int CPR = D / 8;                          // 16-byte chunks per K row
-    constexpr int KPARTS = 64 * D * 2 / 1024;           // 1 KB parts of a K tile
 #pragma unroll
-    for (int pp = 0; pp < KPARTS / 8; ++pp) {
-        const int part = w + 8 * pp;
-        const int p = part * 64 + lane;                 // physical chunk index
-        const int r = p / CPR, pc = p % CPR;
-        const int c = pc ^ swzK(r);
-        dma16(KC + ((int64_t)blk * 64 + r) * D + 8 * c, slot_lds + (uint32_t)part * 1024u);
-    }
-#pragma unroll
-    for (int pp = 0; pp < KPARTS / 8; ++pp) {
-        const int part = w + 8 * pp;
-        const int p = part * 64 + lane;
-        const int r = p >> 3, pc = p & 7;
-        const int c = pc ^ swzV(r);
-        dma16(VT + (int64_t)r * n + (int64_t)blk * 64 + 8 * c,
-              slot_lds + (uint32_t)(64 * D * 2) + (uint32_t)part * 1024u);
+    for (int pp = 0; pp < C::DPW; ++pp) {
+        const int part = w + C::WAVES * pp;
+        const int p = (part % C::KPARTS) * 64 + lane;   // physical chunk index in its tile
+        if (part < C::KPARTS) {
+            const int r = p / CPR, c = (p % CPR) ^ swzK(p / CPR);
+            dma16(KC + ((int64_t)blk * 64 + r) * D + 8 * c, slot_lds + (uint32_t)part * 1024u);
+        } else {
+            const int r = p >> 3, c = (p & 7) ^ swzV(p >> 3);
+            dma16(VT + (int64_t)r * n + (int64_t)blk * 64 + 8 * c, slot_lds + (uint32_t)part * 1024u);
+        }
     }
 }
 
@@ -255,7 +251,7 @@ struct WinCfg {
     static constexpr int NKS = D / 32;                 // 32-wide d steps of S^T
     static constexpr int NDT = D / 16;                 // 16-row d tiles of O^T
     static constexpr int SLOT = 2 * 64 * D;            // bf16 per staged tile (K + V^T)
-    static constexpr int NS = 3;                       // tiles in flight
+    static constexpr int NS = (D == 64) ? 8 : 4;       // ring slots (128 KB): NS-1 tiles in flight
 };
 
 // DMA of one 64-key tile (kr rows, vt columns) into a ring slot by the
@@ -287,7 +283,8 @@ __device__ __forceinline__ void win_body(
     using C = WinCfg<D, RT>;
     const int G = Hq / Hkv;
     const int nw = blockDim.x >> 6;
-    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, lg = lane >> 4;
+    const int tid = threadIdx.x, lane = tid & 63, l16 = lane & 15, lg = lane >> 4;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave index: uniform, kept in SGPRs
     const int hh = hs * gw + w % gw, rg = w / gw;     // head within the group, query range
     const bool hv = hh < G;                            // waves past the group's last head only stage
     constexpr int QW = 16 * RT;                        // queries per wave
@@ -574,7 +571,8 @@ __device__ __forceinline__ void routed_body(
     const int QPT = 16 / G;
     const int QT = C::WAVES * ptw * QPT;
     const int tid = threadIdx.x;
-    const int w = tid >> 6, lane = tid & 63, l16 = lane & 15, lg = lane >> 4;
+    const int lane = tid & 63, l16 = lane & 15, lg = lane >> 4;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave index: uniform, kept in SGPRs
     const int b = combo / Hkv, g = combo % Hkv;
     const int64_t i0 = (int64_t)tile * QT;
     const int64_t bh = (int64_t)b * Hkv + g;
@@ -677,9 +675,7 @@ __device__ __forceinline__ void routed_body(
         // this wave's share of entry e has landed once at most the shares of
         // the entries after it (up to NS-2 of them) are still in flight
         const int ahead = (ne - 1 - e < C::NS - 2) ? ne - 1 - e : C::NS - 2;
-        if (ahead >= 2) wait_vm<2 * C::DPW>();
-        else if (ahead == 1) wait_vm<C::DPW>();
-        else wait_vm<0>();
+        wait_vm_n(ahead * C::DPW);
         __syncthreads();   // every share of entry e landed; entry e-1 is consumed
         if (e + C::NS - 1 < ne)
             ring_fill<D>(KC, VT, n, list[e + C::NS - 1],
@@ -745,7 +741,7 @@ __device__ __forceinline__ void routed_body(
 }
 
 template <int D>
-__global__ __launch_bounds__(512) void attn_routed_kernel(
+__global__ __launch_bounds__(1024) void attn_routed_kernel(
     const bf16_t *__restrict__ q, int64_t qsb, int64_t qsn, int64_t qsh, const float *__restrict__ qgain,
     const float *__restrict__ kgain, float eps, const bf16_t *__restrict__ kc, const bf16_t *__restrict__ vt,
     const int32_t *__restrict__ idx, const int32_t *__restrict__ cnt, int64_t n, int Hq, int Hkv, int S,
