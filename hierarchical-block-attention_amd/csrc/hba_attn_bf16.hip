@@ -185,6 +185,8 @@ struct RtCfg {
     static constexpr int PTW = (D == 64) ? 2 : 1;      // max 16-row tiles per wave (<= 128 VGPRs)
     static constexpr int SLOT = 2 * 64 * D;            // bf16 per ring slot (K + V^T)
     static constexpr int NS = (D == 64) ? 8 : 4;       // ring depth (blocks, 128 KB)
+    static constexpr int PH = NS / 2;                  // blocks per barrier phase
+    static_assert(NS % PH == 0, "the ring holds whole phases");
     static constexpr int KPARTS = 64 * D * 2 / 1024;   // 1 KB parts of a K (and of a V^T) tile
     static constexpr int DPW = 2 * KPARTS / WAVES;     // DMA instructions per wave per block
     static_assert(DPW * WAVES == 2 * KPARTS, "parts split evenly over the waves");
@@ -559,17 +561,17 @@ __device__ __forceinline__ void rt_update(const bf16_t *Ks, const bf16_t *Vs, co
     }
 }
 
-template <int D, bool FIXED>
+template <int D, int PTW, bool FIXED>
 __device__ __forceinline__ void routed_body(
     const bf16_t *__restrict__ q, int64_t qsb, int64_t qsn, int64_t qsh, const float *__restrict__ qgain,
     float eps, const bf16_t *__restrict__ kc, const bf16_t *__restrict__ vt,
     const int32_t *__restrict__ idx, const int32_t *__restrict__ cnt, int64_t n, int Hq, int Hkv, int S,
-    int kk, float sl2, float bl2, int ptw, int combo, int tile, bf16_t *__restrict__ out,
+    int kk, float sl2, float bl2, int combo, int tile, bf16_t *__restrict__ out,
     int64_t osb, int64_t osn, int64_t osh, const float *__restrict__ lse, char *smem, int &nlist) {
     using C = RtCfg<D>;
     const int G = Hq / Hkv;
     const int QPT = 16 / G;
-    const int QT = C::WAVES * ptw * QPT;
+    const int QT = C::WAVES * PTW * QPT;
     const int tid = threadIdx.x;
     const int lane = tid & 63, l16 = lane & 15, lg = lane >> 4;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave index: uniform, kept in SGPRs
@@ -585,7 +587,7 @@ __device__ __forceinline__ void routed_body(
     const uint32_t ring_lds = lds_offset(ring);            // LDS byte address of the ring
     int16_t *sel = reinterpret_cast<int16_t *>(smem + (size_t)C::NS * C::SLOT * 2);
     uint32_t *bitmap = reinterpret_cast<uint32_t *>(sel + ((QT * kk + 1) & ~1));
-    int16_t *list = reinterpret_cast<int16_t *>(bitmap + nbw);   // [0 if sinks] + union
+    int16_t *list = reinterpret_cast<int16_t *>(bitmap + nbw);   // union of the routed blocks, ascending
 
     // ------------------------------------- selection lists and their union
     for (int e = tid; e < nbw; e += C::NTHR) bitmap[e] = 0u;
@@ -613,9 +615,7 @@ __device__ __forceinline__ void routed_body(
     }
     __syncthreads();
     if (w == 0) {
-        const int first = (S > 0) ? 1 : 0;
-        if (lane == 0 && first) list[0] = 0;
-        int base = first;
+        int base = 0;
         for (int w0 = 0; w0 < nbw; w0 += 64) {
             uint32_t word = (w0 + lane < nbw) ? bitmap[w0 + lane] : 0u;
             const int pc = __popc(word);
@@ -640,65 +640,75 @@ __device__ __forceinline__ void routed_body(
     const int qs = l16 / G;
     const int hh = l16 % G;
     const bool colv = l16 < QPT * G;
-    bf16x8 qop[C::PTW][C::NKS];
-    f32x4 O[C::PTW][C::NDT];
-    float mrun[C::PTW], lsum[C::PTW];
-    int64_t icol[C::PTW];
-    bool cok[C::PTW];
+    bf16x8 qop[PTW][C::NKS];
+    f32x4 O[PTW][C::NDT];
+    float mrun[PTW], lsum[PTW];
+    int64_t icol[PTW];
+    bool cok[PTW];
 #pragma unroll
-    for (int t = 0; t < C::PTW; ++t) {
-        icol[t] = i0 + (int64_t)(w * ptw + t) * QPT + qs;
-        cok[t] = colv && t < ptw && icol[t] < n;
+    for (int t = 0; t < PTW; ++t) {
+        icol[t] = i0 + (int64_t)(w * PTW + t) * QPT + qs;
+        cok[t] = colv && icol[t] < n;
         mrun[t] = -INFINITY;
         lsum[t] = 0.0f;
 #pragma unroll
         for (int dt = 0; dt < C::NDT; ++dt) O[t][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-        if (t < ptw)
-            qoperand<D>(q, qsb, qsn, qsh, qgain, eps, nullptr, nullptr, b, icol[t], g * G + hh, cok[t], false, lg,
-                        qop[t]);
+        qoperand<D>(q, qsb, qsn, qsh, qgain, eps, nullptr, nullptr, b, icol[t], g * G + hh, cok[t], false, lg,
+                    qop[t]);
     }
     __syncthreads();
     const int ne = nlist;
 
-    // ------------------------------------------ sinks + routed, DMA ring --
-    int cur[C::PTW], nxt[C::PTW];
+    // The ring holds NPH phases of PH blocks, with one barrier per phase: a
+    // block's hits fall on few of the 16 waves, and a phase of several blocks
+    // evens the waves' work out before they meet again.
+    constexpr int P = C::PH, NPH = C::NS / C::PH;
+    const int npro = min(ne, (NPH - 1) * P);
+    // sinks: block 0 into the last slot (free until the first refill), ahead of the prologue
+    if (S > 0) ring_fill<D>(KC, VT, n, 0, ring_lds + (uint32_t)((C::NS - 1) * C::SLOT * 2), w, lane);
+    for (int e = 0; e < npro; ++e)
+        ring_fill<D>(KC, VT, n, list[e], ring_lds + (uint32_t)(e * C::SLOT * 2), w, lane);
+    if (S > 0) {
+        wait_vm_n(npro * C::DPW);
+        __syncthreads();   // every share of block 0 landed
+        const bf16_t *Ks = ring + (C::NS - 1) * C::SLOT;
+        const int nmt = (S <= 4) ? 1 : (S <= 32 ? 2 : 4);   // M-tiles holding keys 0..S-1
 #pragma unroll
-    for (int t = 0; t < C::PTW; ++t) {
+        for (int tt = 0; tt < PTW; ++tt) {
+            if (i0 + (int64_t)(w * PTW + tt) * QPT >= n) break;
+            rt_update<D, FIXED>(Ks, Ks + 64 * D, qop[tt], O[tt], mrun[tt], lsum[tt], RM_SINK, icol[tt], cok[tt], S,
+                                nmt, sl2, bl2, l16, lg);
+        }
+    }
+    int cur[PTW], nxt[PTW];
+#pragma unroll
+    for (int t = 0; t < PTW; ++t) {
         cur[t] = 0;
-        const int ql = (w * ptw + t) * QPT + qs;
+        const int ql = (w * PTW + t) * QPT + qs;
         nxt[t] = cok[t] ? (int)sel[ql * kk] : (int)SENT;
     }
-    const int nmt_s = (S <= 4) ? 1 : (S <= 32 ? 2 : 4);
-    for (int e = 0; e < C::NS - 1 && e < ne; ++e)
-        ring_fill<D>(KC, VT, n, list[e], ring_lds + (uint32_t)(e * C::SLOT * 2), w, lane);
-    for (int e = 0; e < ne; ++e) {
-        // this wave's share of entry e has landed once at most the shares of
-        // the entries after it (up to NS-2 of them) are still in flight
-        const int ahead = (ne - 1 - e < C::NS - 2) ? ne - 1 - e : C::NS - 2;
-        wait_vm_n(ahead * C::DPW);
-        __syncthreads();   // every share of entry e landed; entry e-1 is consumed
-        if (e + C::NS - 1 < ne)
-            ring_fill<D>(KC, VT, n, list[e + C::NS - 1],
-                         ring_lds + (uint32_t)(((e + C::NS - 1) % C::NS) * C::SLOT * 2), w, lane);
-        const bf16_t *Ks = ring + (e % C::NS) * C::SLOT;
-        const bf16_t *Vs = Ks + 64 * D;
-        const int blk = list[e];
-        const bool sink = S > 0 && e == 0;
+    for (int e0 = 0; e0 < ne; e0 += P) {
+        // this wave's shares of entries e0..e0+P-1 have landed once at most
+        // the shares of the entries issued after them are in flight
+        const int issued = min(ne, e0 + (NPH - 1) * P);
+        wait_vm_n(max(0, issued - (e0 + P)) * C::DPW);
+        __syncthreads();   // every share of this phase landed; the previous phase (and the sinks) consumed
+        const int nf = min(ne, e0 + NPH * P);
+        for (int e = issued; e < nf; ++e)
+            ring_fill<D>(KC, VT, n, list[e], ring_lds + (uint32_t)((e % C::NS) * C::SLOT * 2), w, lane);
+        const int e1 = min(ne, e0 + P);
+        for (int e = e0; e < e1; ++e) {
+            const bf16_t *Ks = ring + (e % C::NS) * C::SLOT;
+            const int blk = list[e];
 #pragma unroll
-        for (int tt = 0; tt < C::PTW; ++tt) {
-            if (tt >= ptw) break;
-            if (sink) {
-                if (i0 + (int64_t)(w * ptw + tt) * QPT >= n) break;
-                rt_update<D, FIXED>(Ks, Vs, qop[tt], O[tt], mrun[tt], lsum[tt], RM_SINK, icol[tt], cok[tt], S,
-                                    nmt_s, sl2, bl2, l16, lg);
-            } else {
+            for (int tt = 0; tt < PTW; ++tt) {
                 const bool hit = nxt[tt] == blk;
                 if (__ballot(hit) == 0) continue;
-                rt_update<D, FIXED>(Ks, Vs, qop[tt], O[tt], mrun[tt], lsum[tt], RM_COL, icol[tt], hit, S, 4,
-                                    sl2, bl2, l16, lg);
+                rt_update<D, FIXED>(Ks, Ks + 64 * D, qop[tt], O[tt], mrun[tt], lsum[tt], RM_COL, icol[tt], hit, S,
+                                    4, sl2, bl2, l16, lg);
                 if (hit) {
                     ++cur[tt];
-                    const int ql = (w * ptw + tt) * QPT + qs;
+                    const int ql = (w * PTW + tt) * QPT + qs;
                     nxt[tt] = (cur[tt] < kk) ? (int)sel[ql * kk + cur[tt]] : (int)SENT;
                 }
             }
@@ -707,8 +717,7 @@ __device__ __forceinline__ void routed_body(
 
     // ------------------- merge with the window's (out, LSE), normalise, store
 #pragma unroll
-    for (int t = 0; t < C::PTW; ++t) {
-        if (t >= ptw) break;
+    for (int t = 0; t < PTW; ++t) {
         float l = lsum[t];
         l += __shfl_xor(l, 16, 64);
         l += __shfl_xor(l, 32, 64);
@@ -740,12 +749,12 @@ __device__ __forceinline__ void routed_body(
     }
 }
 
-template <int D>
+template <int D, int PTW>
 __global__ __launch_bounds__(1024) void attn_routed_kernel(
     const bf16_t *__restrict__ q, int64_t qsb, int64_t qsn, int64_t qsh, const float *__restrict__ qgain,
     const float *__restrict__ kgain, float eps, const bf16_t *__restrict__ kc, const bf16_t *__restrict__ vt,
     const int32_t *__restrict__ idx, const int32_t *__restrict__ cnt, int64_t n, int Hq, int Hkv, int S,
-    int kk, float scale, int ptw, int ntiles, int Cn, int xmap, bf16_t *__restrict__ out,
+    int kk, float scale, int ntiles, int Cn, int xmap, bf16_t *__restrict__ out,
     int64_t osb, int64_t osn, int64_t osh, const float *__restrict__ lse) {
     extern __shared__ __align__(16) char smem[];
     __shared__ int nlist;
@@ -756,12 +765,13 @@ __global__ __launch_bounds__(1024) void attn_routed_kernel(
     const float sl2 = scale * LOG2E;
     float bl2;
     if (group_bound(qgain, kgain, combo % Hkv, G, sl2, D, bl2))
-        routed_body<D, true>(q, qsb, qsn, qsh, qgain, eps, kc, vt, idx, cnt, n, Hq, Hkv, S, kk, sl2, bl2, ptw,
-                             combo, tile, out, osb, osn, osh, lse, smem, nlist);
+        routed_body<D, PTW, true>(q, qsb, qsn, qsh, qgain, eps, kc, vt, idx, cnt, n, Hq, Hkv, S, kk, sl2, bl2,
+                                  combo, tile, out, osb, osn, osh, lse, smem, nlist);
     else
-        routed_body<D, false>(q, qsb, qsn, qsh, qgain, eps, kc, vt, idx, cnt, n, Hq, Hkv, S, kk, sl2, bl2, ptw,
-                              combo, tile, out, osb, osn, osh, lse, smem, nlist);
+        routed_body<D, PTW, false>(q, qsb, qsn, qsh, qgain, eps, kc, vt, idx, cnt, n, Hq, Hkv, S, kk, sl2, bl2,
+                                   combo, tile, out, osb, osn, osh, lse, smem, nlist);
 }
+
 
 // ============================================================ launchers ====
 static void grid_map(int64_t Cn, int64_t ntiles, int &xmap, int64_t &grid) {
@@ -808,39 +818,54 @@ static int launch_win(const void *q, const int64_t *qs, const float *qgain, cons
     return HBA_OK;
 }
 
-template <int D>
-static int launch_routed(const void *q, const int64_t *qs, const float *qgain, const float *kgain, float eps,
-                         const void *kc, const void *vt, const int32_t *idx, const int32_t *cnt, int64_t B,
-                         int64_t n, int64_t Hq, int64_t Hkv, int64_t S, int64_t k, float scale, void *out,
-                         const int64_t *os, const float *lse, hipStream_t s) {
+template <int D, int PTW>
+static size_t routed_lds(int64_t n, int64_t G, int64_t k) {
+    using C = RtCfg<D>;
+    const int64_t QT = (int64_t)C::WAVES * PTW * (16 / G);
+    const int64_t nb = n / 64;
+    return (size_t)C::NS * C::SLOT * 2 + (size_t)((QT * k + 1) & ~1LL) * 2 + (size_t)((nb + 31) / 32) * 4 +
+           (size_t)nb * 2 + 16;
+}
+
+template <int D, int PTW>
+static int launch_routed_t(const void *q, const int64_t *qs, const float *qgain, const float *kgain, float eps,
+                           const void *kc, const void *vt, const int32_t *idx, const int32_t *cnt, int64_t B,
+                           int64_t n, int64_t Hq, int64_t Hkv, int64_t S, int64_t k, float scale, void *out,
+                           const int64_t *os, const float *lse, hipStream_t s) {
     using C = RtCfg<D>;
     const int G = (int)(Hq / Hkv);
-    const int QPT = 16 / G;
-    const int64_t nb = n / 64;
-    const int64_t nbw = (nb + 31) / 32;
-    int ptw = C::PTW;
-    size_t lds = 0;
-    for (; ptw >= 1; --ptw) {
-        const int64_t QT = (int64_t)C::WAVES * ptw * QPT;
-        lds = (size_t)C::NS * C::SLOT * 2 + (size_t)((QT * k + 1) & ~1LL) * 2 + (size_t)nbw * 4 +
-              (size_t)(nb + 1) * 2 + 16;
-        if (lds <= 160 * 1024 - 64) break;
-    }
-    if (ptw < 1) return HBA_ERR_UNSUPPORTED;
-    const int64_t QT = (int64_t)C::WAVES * ptw * QPT;
+    const size_t lds = routed_lds<D, PTW>(n, G, k);
+    const int64_t QT = (int64_t)C::WAVES * PTW * (16 / G);
     const int64_t ntiles = (n + QT - 1) / QT;
     int xmap;
     int64_t grid;
     grid_map(B * Hkv, ntiles, xmap, grid);
     if (grid > 0x7fffffff) return HBA_ERR_UNSUPPORTED;
-    if (hipFuncSetAttribute(reinterpret_cast<const void *>(&attn_routed_kernel<D>),
+    if (hipFuncSetAttribute(reinterpret_cast<const void *>(&attn_routed_kernel<D, PTW>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
         return HBA_ERR_LAUNCH;
-    hipLaunchKernelGGL((attn_routed_kernel<D>), dim3((unsigned)grid), dim3(C::NTHR), lds, s, (const bf16_t *)q,
-                       qs[0], qs[1], qs[2], qgain, kgain, eps, (const bf16_t *)kc, (const bf16_t *)vt, idx, cnt, n,
-                       (int)Hq, (int)Hkv, (int)S, (int)k, scale, ptw, (int)ntiles, (int)(B * Hkv), xmap,
-                       (bf16_t *)out, os[0], os[1], os[2], lse);
+    hipLaunchKernelGGL((attn_routed_kernel<D, PTW>), dim3((unsigned)grid), dim3(C::NTHR), lds, s,
+                       (const bf16_t *)q, qs[0], qs[1], qs[2], qgain, kgain, eps, (const bf16_t *)kc,
+                       (const bf16_t *)vt, idx, cnt, n, (int)Hq, (int)Hkv, (int)S, (int)k, scale, (int)ntiles,
+                       (int)(B * Hkv), xmap, (bf16_t *)out, os[0], os[1], os[2], lse);
     return HBA_OK;
+}
+
+// PTW row tiles per wave when the selection lists fit LDS beside the ring, else one
+template <int D>
+static int launch_routed(const void *q, const int64_t *qs, const float *qgain, const float *kgain, float eps,
+                         const void *kc, const void *vt, const int32_t *idx, const int32_t *cnt, int64_t B,
+                         int64_t n, int64_t Hq, int64_t Hkv, int64_t S, int64_t k, float scale, void *out,
+                         const int64_t *os, const float *lse, hipStream_t s) {
+    constexpr size_t LDS_MAX = 160 * 1024 - 64;   // 64 bytes for the static nlist
+    const int64_t G = Hq / Hkv;
+    if (routed_lds<D, RtCfg<D>::PTW>(n, G, k) <= LDS_MAX)
+        return launch_routed_t<D, RtCfg<D>::PTW>(q, qs, qgain, kgain, eps, kc, vt, idx, cnt, B, n, Hq, Hkv, S, k,
+                                                  scale, out, os, lse, s);
+    if (RtCfg<D>::PTW > 1 && routed_lds<D, 1>(n, G, k) <= LDS_MAX)
+        return launch_routed_t<D, 1>(q, qs, qgain, kgain, eps, kc, vt, idx, cnt, B, n, Hq, Hkv, S, k, scale, out,
+                                     os, lse, s);
+    return HBA_ERR_UNSUPPORTED;
 }
 
 }  // namespace ab
