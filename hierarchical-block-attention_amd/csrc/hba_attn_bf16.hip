@@ -583,14 +583,20 @@ __device__ __forceinline__ void routed_body(
     const bf16_t *KC = kc + bh * n * D;
     const bf16_t *VT = vt + bh * D * n;
 
+    // LDS: ring | sel [QT][kk] | bitmap [nbw] | pre [nbw] | list [nb] |
+    //      qbits [QT][nbw] | wbits [WAVES*PTW][nbw]
     bf16_t *ring = reinterpret_cast<bf16_t *>(smem);
     const uint32_t ring_lds = lds_offset(ring);            // LDS byte address of the ring
     int16_t *sel = reinterpret_cast<int16_t *>(smem + (size_t)C::NS * C::SLOT * 2);
-    uint32_t *bitmap = reinterpret_cast<uint32_t *>(sel + ((QT * kk + 1) & ~1));
-    int16_t *list = reinterpret_cast<int16_t *>(bitmap + nbw);   // union of the routed blocks, ascending
+    uint32_t *bitmap = reinterpret_cast<uint32_t *>(sel + ((QT * kk + 1) & ~1));   // union over blocks
+    int *pre = reinterpret_cast<int *>(bitmap + nbw);        // union entries before each bitmap word
+    int16_t *list = reinterpret_cast<int16_t *>(pre + nbw);   // union of the routed blocks, ascending
+    uint32_t *qbits = reinterpret_cast<uint32_t *>(list + ((nb + 1) & ~1LL));   // per query, over entries
+    uint32_t *wbits = qbits + QT * nbw;                      // per row tile: OR of its queries' qbits
 
     // ------------------------------------- selection lists and their union
     for (int e = tid; e < nbw; e += C::NTHR) bitmap[e] = 0u;
+    for (int e = tid; e < (QT + C::WAVES * PTW) * nbw; e += C::NTHR) qbits[e] = 0u;
     __syncthreads();
     for (int qq = tid; qq < QT; qq += C::NTHR) {
         int16_t *sl = sel + qq * kk;
@@ -602,12 +608,7 @@ __device__ __forceinline__ void routed_body(
             for (int r = 0; r < c; ++r) {
                 const int v = ix[r];
                 if (v < 1 || v >= nb) continue;          // block 0 is never routed
-                int p = m2++;
-                while (p > 0 && sl[p - 1] > v) {
-                    sl[p] = sl[p - 1];
-                    --p;
-                }
-                sl[p] = (int16_t)v;
+                sl[m2++] = (int16_t)v;
                 atomicOr(&bitmap[v >> 5], 1u << (v & 31));
             }
         }
@@ -626,6 +627,7 @@ __device__ __forceinline__ void routed_body(
                 if (lane >= o) incl += t;
             }
             int off = base + incl - pc;
+            if (w0 + lane < nbw) pre[w0 + lane] = off;
             while (word) {
                 const int bit = __ffs(word) - 1;
                 list[off++] = (int16_t)((w0 + lane) * 32 + bit);
@@ -634,6 +636,20 @@ __device__ __forceinline__ void routed_body(
             base += __shfl(incl, 63, 64);
         }
         if (lane == 0) nlist = base;
+    }
+    __syncthreads();
+    // each query's picks as union entry indices: its own bits, and its row tile's
+    for (int qq = tid; qq < QT; qq += C::NTHR) {
+        const int16_t *sl = sel + qq * kk;
+        uint32_t *qb = qbits + qq * nbw;
+        uint32_t *wb = wbits + (qq / QPT) * nbw;              // row tile qq / QPT = w * PTW + tt
+        for (int r = 0; r < kk; ++r) {
+            const int v = sl[r];
+            if (v == SENT) break;
+            const int e = pre[v >> 5] + __popc(bitmap[v >> 5] & ((1u << (v & 31)) - 1u));
+            qb[e >> 5] |= 1u << (e & 31);
+            atomicOr(&wb[e >> 5], 1u << (e & 31));
+        }
     }
 
     // ----------------------------------------------------- per-row state --
@@ -663,6 +679,7 @@ __device__ __forceinline__ void routed_body(
     // block's hits fall on few of the 16 waves, and a phase of several blocks
     // evens the waves' work out before they meet again.
     constexpr int P = C::PH, NPH = C::NS / C::PH;
+    static_assert(32 % P == 0, "a phase's entries lie in one bitmap word");
     const int npro = min(ne, (NPH - 1) * P);
     // sinks: block 0 into the last slot (free until the first refill), ahead of the prologue
     if (S > 0) ring_fill<D>(KC, VT, n, 0, ring_lds + (uint32_t)((C::NS - 1) * C::SLOT * 2), w, lane);
@@ -680,13 +697,7 @@ __device__ __forceinline__ void routed_body(
                                 nmt, sl2, bl2, l16, lg);
         }
     }
-    int cur[PTW], nxt[PTW];
-#pragma unroll
-    for (int t = 0; t < PTW; ++t) {
-        cur[t] = 0;
-        const int ql = (w * PTW + t) * QPT + qs;
-        nxt[t] = cok[t] ? (int)sel[ql * kk] : (int)SENT;
-    }
+    uint32_t qw[PTW], ww[PTW];   // this lane's query's / this row tile's bits of the current word
     for (int e0 = 0; e0 < ne; e0 += P) {
         // this wave's shares of entries e0..e0+P-1 have landed once at most
         // the shares of the entries issued after them are in flight
@@ -696,21 +707,26 @@ __device__ __forceinline__ void routed_body(
         const int nf = min(ne, e0 + NPH * P);
         for (int e = issued; e < nf; ++e)
             ring_fill<D>(KC, VT, n, list[e], ring_lds + (uint32_t)((e % C::NS) * C::SLOT * 2), w, lane);
-        const int e1 = min(ne, e0 + P);
-        for (int e = e0; e < e1; ++e) {
-            const bf16_t *Ks = ring + (e % C::NS) * C::SLOT;
-            const int blk = list[e];
+        const int sh = e0 & 31;
+        if (sh == 0) {
 #pragma unroll
             for (int tt = 0; tt < PTW; ++tt) {
-                const bool hit = nxt[tt] == blk;
-                if (__ballot(hit) == 0) continue;
+                const int rt = w * PTW + tt;
+                qw[tt] = cok[tt] ? qbits[(rt * QPT + qs) * nbw + (e0 >> 5)] : 0u;
+                ww[tt] = __builtin_amdgcn_readfirstlane(wbits[rt * nbw + (e0 >> 5)]);
+            }
+        }
+#pragma unroll
+        for (int tt = 0; tt < PTW; ++tt) {
+            uint32_t hits = (ww[tt] >> sh) & ((1u << P) - 1u);   // this phase's entries the row tile needs
+            while (hits) {
+                const int j = __builtin_ctz(hits);
+                hits &= hits - 1u;
+                const int e = e0 + j;
+                const bf16_t *Ks = ring + (e % C::NS) * C::SLOT;
+                const bool hit = (qw[tt] >> (sh + j)) & 1u;
                 rt_update<D, FIXED>(Ks, Ks + 64 * D, qop[tt], O[tt], mrun[tt], lsum[tt], RM_COL, icol[tt], hit, S,
                                     4, sl2, bl2, l16, lg);
-                if (hit) {
-                    ++cur[tt];
-                    const int ql = (w * PTW + tt) * QPT + qs;
-                    nxt[tt] = (cur[tt] < kk) ? (int)sel[ql * kk + cur[tt]] : (int)SENT;
-                }
             }
         }
     }
@@ -823,8 +839,9 @@ static size_t routed_lds(int64_t n, int64_t G, int64_t k) {
     using C = RtCfg<D>;
     const int64_t QT = (int64_t)C::WAVES * PTW * (16 / G);
     const int64_t nb = n / 64;
-    return (size_t)C::NS * C::SLOT * 2 + (size_t)((QT * k + 1) & ~1LL) * 2 + (size_t)((nb + 31) / 32) * 4 +
-           (size_t)nb * 2 + 16;
+    const int64_t nbw = (nb + 31) / 32;
+    return (size_t)C::NS * C::SLOT * 2 + (size_t)((QT * k + 1) & ~1LL) * 2 + (size_t)nbw * 8 +
+           (size_t)((nb + 1) & ~1LL) * 2 + (size_t)(QT + C::WAVES * PTW) * nbw * 4 + 16;
 }
 
 template <int D, int PTW>
