@@ -253,7 +253,8 @@ struct WinCfg {
     static constexpr int NKS = D / 32;                 // 32-wide d steps of S^T
     static constexpr int NDT = D / 16;                 // 16-row d tiles of O^T
     static constexpr int SLOT = 2 * 64 * D;            // bf16 per staged tile (K + V^T)
-    static constexpr int NS = (D == 64) ? 8 : 4;       // ring slots (128 KB): NS-1 tiles in flight
+    static constexpr int NS = (D == 64) ? 8 : 4;       // ring slots (128 KB)
+    static constexpr int PH = NS / 2;                  // tiles per barrier phase
 };
 
 // DMA of one 64-key tile (kr rows, vt columns) into a ring slot by the
@@ -320,115 +321,161 @@ __device__ __forceinline__ void win_body(
     const int kfirst = (S > i0 - W + 1) ? S : i0 - W + 1;
     if (kfirst <= ilast) {
         const int t0 = kfirst / 64, t1 = ilast / 64, nt = t1 - t0 + 1;
-        for (int e = 0; e < C::NS - 1 && e < nt; ++e)
+        // one barrier per phase of PH tiles; the ring holds NPH phases
+        constexpr int P = C::PH, NPH = C::NS / C::PH;
+        constexpr int PARTS = 2 * (64 * D * 2 / 1024);   // 1 KB parts of a tile
+        const int mine = (PARTS - w + nw - 1) / nw;       // this wave's parts per tile
+        for (int e = 0; e < (NPH - 1) * P && e < nt; ++e)
             win_fill<D>(KR, VT, n, 64 * (t0 + e), ring_lds + (uint32_t)(e * C::SLOT * 2), w, nw, lane);
-        for (int e = 0; e < nt; ++e) {
-            // this wave's parts of tile e have landed once at most those of the
-            // next tile are still in flight
-            {
-                constexpr int PARTS = 2 * (64 * D * 2 / 1024);   // 1 KB parts of a tile
-                const int mine = (PARTS - w + nw - 1) / nw;       // this wave's parts per tile
-                const int ahead = (nt - 1 - e < C::NS - 2) ? nt - 1 - e : C::NS - 2;
-                wait_vm_n(ahead * mine);
-            }
-            __syncthreads();   // all parts of tile e landed; tile e-1 is consumed
-            if (e + C::NS - 1 < nt)
-                win_fill<D>(KR, VT, n, 64 * (t0 + e + C::NS - 1),
-                            ring_lds + (uint32_t)(((e + C::NS - 1) % C::NS) * C::SLOT * 2), w, nw, lane);
-            const bf16_t *Ks = ring + (e % C::NS) * C::SLOT;
-            const bf16_t *Vs = Ks + 64 * D;
-            const int kb = 64 * (t0 + e);
-            bool act[RT], full[RT];
+        for (int e0 = 0; e0 < nt; e0 += P) {
+            // this wave's parts of the phase's tiles have landed once at most
+            // those of the tiles issued after them are in flight
+            const int issued = min(nt, e0 + (NPH - 1) * P);
+            wait_vm_n(max(0, issued - (e0 + P)) * mine);
+            __syncthreads();   // all parts of this phase landed; the previous phase is consumed
+            const int nf = min(nt, e0 + NPH * P);
+            for (int e = issued; e < nf; ++e)
+                win_fill<D>(KR, VT, n, 64 * (t0 + e), ring_lds + (uint32_t)((e % C::NS) * C::SLOT * 2), w, nw,
+                            lane);
+            const int e1 = min(nt, e0 + P);
+            for (int e = e0; e < e1; ++e) {
+                const bf16_t *Ks = ring + (e % C::NS) * C::SLOT;
+                const bf16_t *Vs = Ks + 64 * D;
+                const int kb = 64 * (t0 + e);
+                bool act[RT], full[RT];
 #pragma unroll
-            for (int rt = 0; rt < RT; ++rt) {
-                const int qa = q0 + 16 * rt;
-                const int qb = (qa + 15 < n) ? qa + 15 : n - 1;
-                const int lo = (S > qa - W + 1) ? S : qa - W + 1;
-                const int lob = (S > qb - W + 1) ? S : qb - W + 1;
-                act[rt] = hv && qa < n && kb <= qb && kb + 63 >= lo;
-                full[rt] = kb >= lob && kb + 63 <= qa;
-            }
-            // the tile's K fragments, read from LDS once for all row tiles
-            bf16x8 kf[4][C::NKS];
-#pragma unroll
-            for (int mt = 0; mt < 4; ++mt) {
-                const int r = permk(mt, l16);
-                const bf16_t *kp = Ks + r * D;
-                const int sw = swzK(r);
-#pragma unroll
-                for (int ks = 0; ks < C::NKS; ++ks) kf[mt][ks] = ldb8(kp + 8 * ((4 * ks + lg) ^ sw));
-            }
-            // per row tile: S^T, probabilities, packed P^T
-            bf16x8 pb[RT][2];
-#pragma unroll
-            for (int rt = 0; rt < RT; ++rt) {
-                if (!act[rt]) continue;
-                f32x4 Sa[4];
+                for (int rt = 0; rt < RT; ++rt) {
+                    const int qa = q0 + 16 * rt;
+                    const int qb = (qa + 15 < n) ? qa + 15 : n - 1;
+                    const int lo = (S > qa - W + 1) ? S : qa - W + 1;
+                    const int lob = (S > qb - W + 1) ? S : qb - W + 1;
+                    act[rt] = hv && qa < n && kb <= qb && kb + 63 >= lo;
+                    full[rt] = kb >= lob && kb + 63 <= qa;
+                }
+                // the tile's K fragments, read from LDS once for all row tiles
+                bf16x8 kf[4][C::NKS];
 #pragma unroll
                 for (int mt = 0; mt < 4; ++mt) {
-                    Sa[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+                    const int r = permk(mt, l16);
+                    const bf16_t *kp = Ks + r * D;
+                    const int sw = swzK(r);
 #pragma unroll
-                    for (int ks = 0; ks < C::NKS; ++ks) Sa[mt] = mma(kf[mt][ks], qop[rt][ks], Sa[mt]);
+                    for (int ks = 0; ks < C::NKS; ++ks) kf[mt][ks] = ldb8(kp + 8 * ((4 * ks + lg) ^ sw));
                 }
-                const int i = q0 + 16 * rt + l16;      // this lane's column
-                const int jlo = ((S > i - W + 1) ? S : i - W + 1) - kb;   // valid key offsets [jlo, jhi]
-                const int jhi = i - kb;
-                const bool fullt = full[rt];           // wave-uniform: no mask at all
-                float p[2][8];
-                float shift = bl2;
-                if constexpr (!FIXED) {
-                    float tmax = -INFINITY;
+                bool allfull = true;
 #pragma unroll
-                    for (int mt = 0; mt < 4; ++mt)
+                for (int rt = 0; rt < RT; ++rt) allfull = allfull && act[rt] && full[rt];
+                if (FIXED && RT > 1 && allfull) {
+                    // interior tile (every key valid for every row tile), fixed
+                    // shift: straight-line code over the row tiles, so that one
+                    // row tile's exponentials overlap another's MFMAs
+                    f32x4 Sa[RT][4];
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            const int j = kl + 32 * (mt >> 1) + 4 * (mt & 1) + e;
-                            const bool ok = fullt | ((j >= jlo) & (j <= jhi));
-                            tmax = fmaxf(tmax, ok ? Sa[mt][e] : -INFINITY);
+                    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+                        for (int mt = 0; mt < 4; ++mt) {
+                            Sa[rt][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                            for (int ks = 0; ks < C::NKS; ++ks) Sa[rt][mt] = mma(kf[mt][ks], qop[rt][ks], Sa[rt][mt]);
                         }
-                    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-                    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-                    const float mnew = fmaxf(mr[rt], tmax * sl2);
-                    shift = (mnew == -INFINITY) ? 0.0f : mnew;
-                    const float alpha = ex2(mr[rt] - shift);
-                    mr[rt] = mnew;
-                    ls[rt] *= alpha;
+                    bf16x8 pf[RT][2];
 #pragma unroll
-                    for (int dt = 0; dt < C::NDT; ++dt) O[rt][dt] *= alpha;
-                }
-                if (fullt) {
+                    for (int rt = 0; rt < RT; ++rt) {
+                        float p[2][8];
 #pragma unroll
-                    for (int mt = 0; mt < 4; ++mt)
+                        for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) p[mt >> 1][(mt & 1) * 4 + e] = ex2(fmaf(Sa[mt][e], sl2, -shift));
-                } else {
-                    // masked keys: the exp2 argument is selected to -inf (no branch per element)
+                            for (int e = 0; e < 4; ++e) p[mt >> 1][(mt & 1) * 4 + e] = ex2(fmaf(Sa[rt][mt][e], sl2, -bl2));
+                        pf[rt][0] = pack8(p[0]);
+                        pf[rt][1] = pack8(p[1]);
+                        ls[rt] = sum8(pf[rt][1], sum8(pf[rt][0], ls[rt]));
+                    }
 #pragma unroll
-                    for (int mt = 0; mt < 4; ++mt)
+                    for (int dt = 0; dt < C::NDT; ++dt) {
+                        const int r = 16 * dt + l16;
+                        const bf16_t *vp = Vs + r * 64;
+                        const int sw = swzV(r);
+                        const bf16x8 v0 = ldb8(vp + 8 * (lg ^ sw)), v1 = ldb8(vp + 8 * ((lg + 4) ^ sw));
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            const int j = kl + 32 * (mt >> 1) + 4 * (mt & 1) + e;
-                            const bool ok = (j >= jlo) & (j <= jhi);
-                            const float a = fmaf(Sa[mt][e], sl2, -shift);
-                            p[mt >> 1][(mt & 1) * 4 + e] = ex2(ok ? a : -INFINITY);
+                        for (int rt = 0; rt < RT; ++rt) {
+                            O[rt][dt] = mma(v0, pf[rt][0], O[rt][dt]);
+                            O[rt][dt] = mma(v1, pf[rt][1], O[rt][dt]);
                         }
+                    }
+                    continue;
                 }
-                pb[rt][0] = pack8(p[0]);
-                pb[rt][1] = pack8(p[1]);
-                ls[rt] = sum8(pb[rt][1], sum8(pb[rt][0], ls[rt]));
-            }
-            // O^T += V^T . P^T; each V^T fragment read once
-#pragma unroll
-            for (int dt = 0; dt < C::NDT; ++dt) {
-                const int r = 16 * dt + l16;
-                const bf16_t *vp = Vs + r * 64;
-                const int sw = swzV(r);
-                const bf16x8 v0 = ldb8(vp + 8 * (lg ^ sw)), v1 = ldb8(vp + 8 * ((lg + 4) ^ sw));
+                // per row tile: S^T, probabilities, packed P^T
+                bf16x8 pb[RT][2];
 #pragma unroll
                 for (int rt = 0; rt < RT; ++rt) {
                     if (!act[rt]) continue;
-                    O[rt][dt] = mma(v0, pb[rt][0], O[rt][dt]);
-                    O[rt][dt] = mma(v1, pb[rt][1], O[rt][dt]);
+                    f32x4 Sa[4];
+#pragma unroll
+                    for (int mt = 0; mt < 4; ++mt) {
+                        Sa[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                        for (int ks = 0; ks < C::NKS; ++ks) Sa[mt] = mma(kf[mt][ks], qop[rt][ks], Sa[mt]);
+                    }
+                    const int i = q0 + 16 * rt + l16;      // this lane's column
+                    const int jlo = ((S > i - W + 1) ? S : i - W + 1) - kb;   // valid key offsets [jlo, jhi]
+                    const int jhi = i - kb;
+                    const bool fullt = full[rt];           // wave-uniform: no mask at all
+                    float p[2][8];
+                    float shift = bl2;
+                    if constexpr (!FIXED) {
+                        float tmax = -INFINITY;
+#pragma unroll
+                        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) {
+                                const int j = kl + 32 * (mt >> 1) + 4 * (mt & 1) + e;
+                                const bool ok = fullt | ((j >= jlo) & (j <= jhi));
+                                tmax = fmaxf(tmax, ok ? Sa[mt][e] : -INFINITY);
+                            }
+                        tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+                        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+                        const float mnew = fmaxf(mr[rt], tmax * sl2);
+                        shift = (mnew == -INFINITY) ? 0.0f : mnew;
+                        const float alpha = ex2(mr[rt] - shift);
+                        mr[rt] = mnew;
+                        ls[rt] *= alpha;
+#pragma unroll
+                        for (int dt = 0; dt < C::NDT; ++dt) O[rt][dt] *= alpha;
+                    }
+                    if (fullt) {
+#pragma unroll
+                        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) p[mt >> 1][(mt & 1) * 4 + e] = ex2(fmaf(Sa[mt][e], sl2, -shift));
+                    } else {
+                        // masked keys: the exp2 argument is selected to -inf (no branch per element)
+#pragma unroll
+                        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) {
+                                const int j = kl + 32 * (mt >> 1) + 4 * (mt & 1) + e;
+                                const bool ok = (j >= jlo) & (j <= jhi);
+                                const float a = fmaf(Sa[mt][e], sl2, -shift);
+                                p[mt >> 1][(mt & 1) * 4 + e] = ex2(ok ? a : -INFINITY);
+                            }
+                    }
+                    pb[rt][0] = pack8(p[0]);
+                    pb[rt][1] = pack8(p[1]);
+                    ls[rt] = sum8(pb[rt][1], sum8(pb[rt][0], ls[rt]));
+                }
+                // O^T += V^T . P^T; each V^T fragment read once
+#pragma unroll
+                for (int dt = 0; dt < C::NDT; ++dt) {
+                    const int r = 16 * dt + l16;
+                    const bf16_t *vp = Vs + r * 64;
+                    const int sw = swzV(r);
+                    const bf16x8 v0 = ldb8(vp + 8 * (lg ^ sw)), v1 = ldb8(vp + 8 * ((lg + 4) ^ sw));
+#pragma unroll
+                    for (int rt = 0; rt < RT; ++rt) {
+                        if (!act[rt]) continue;
+                        O[rt][dt] = mma(v0, pb[rt][0], O[rt][dt]);
+                        O[rt][dt] = mma(v1, pb[rt][1], O[rt][dt]);
+                    }
                 }
             }
         }
