@@ -11,6 +11,7 @@ per-stage times, the 32K decode step (B=32 sequences, paged bf16 cache) as
 bounded sample of the same workload.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-decode]
+  python bench.py --copy-probe MIB      # plain device copy, for counter calibration
 """
 import argparse
 import json
@@ -31,6 +32,17 @@ WORKLOAD = dict(workload="hba_layer_fwd_32k", batch=1, seq_len=32768, q_heads=14
                 head_dim=64, sinks=4, window=1024, block=64, slots=4, top_k=16, needles=16,
                 qknorm="sharp gains d**0.25", selection="flat")
 DECODE = dict(batch=32, len_lo=16384, len_hi=32768, seed=0)
+
+# The union attention is one op (hba_attn_fwd) of two launches on one stream:
+# the window kernel writes the window's rows and their LSE, the routed kernel
+# adds the sinks and routed blocks and merges.  Its time is taken with HIP
+# events around the op.
+ATTN_KERNELS = "hba_attn_fwd = attn_win_kernel<64,3> + attn_routed_kernel<64,2>"
+# HBM (beyond-L2) bytes per hba_attn_fwd call on this workload: rocprofv3 --pmc
+# FETCH_SIZE and WRITE_SIZE summed over the two kernels, each divided by the
+# counter's reading per byte of a plain device copy (python bench.py
+# --copy-probe 1024); profiles/hba_attn_32k_traffic.md.
+ATTN_TRAFFIC_BYTES = 979184251
 
 
 def cpu_model():
@@ -241,7 +253,18 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="only run 3 plain device copies of MIB MiB (counter calibration) and exit")
     a = ap.parse_args()
+    if a.copy_probe:
+        import torch
+        src = torch.empty(a.copy_probe << 20, dtype=torch.uint8, device="cuda:0").fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_MiB": a.copy_probe, "copies": 3}))
+        return
     world = int(os.environ.get("WORLD_SIZE", a.gpus))
     if a.gpus != 1 or world != 1:
         print(json.dumps({"error": "this benchmark runs on exactly one GPU: the HBA operator is "
@@ -271,9 +294,9 @@ def main():
         "dtype": "bf16",
         "data": "synthetic",
         "config": dict(WORKLOAD),
-        "roofline": {"bound": "mfma", "kernel": "attn_bf16_kernel<64>",
+        "roofline": {"bound": "mfma", "kernel": ATTN_KERNELS,
                      "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": ATTN_TRAFFIC_BYTES,
                      "algorithmic_flop_per_launch": res["attn_flop"],
                      "mean_keys_per_query": round(res["mean_keys"], 1)},
         "layer_frac_of_mfma_roofline": round(total_flop / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
