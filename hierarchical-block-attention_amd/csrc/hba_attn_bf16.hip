@@ -253,7 +253,7 @@ struct WinCfg {
     static constexpr int NKS = D / 32;                 // 32-wide d steps of S^T
     static constexpr int NDT = D / 16;                 // 16-row d tiles of O^T
     static constexpr int SLOT = 2 * 64 * D;            // bf16 per staged tile (K + V^T)
-    static constexpr int NS = (D == 64) ? 8 : 4;       // ring slots (128 KB)
+    static constexpr int NS = 2;                       // ring slots: 2 or 3 workgroups share a CU
     static constexpr int PH = NS / 2;                  // tiles per barrier phase
 };
 
@@ -508,17 +508,24 @@ __device__ __forceinline__ void win_body(
 // Grid: Cn = B*Hkv*hsplit combos (the heads of a group split over hsplit
 // workgroups of gw heads when G > 8) times the query tiles.
 template <int D, int RT>
-__global__ __launch_bounds__(512) void attn_win_kernel(
+__global__ __launch_bounds__(256, 3) void attn_win_kernel(
     const bf16_t *__restrict__ q, int64_t qsb, int64_t qsn, int64_t qsh, const float *__restrict__ qgain,
     const float *__restrict__ kgain, float eps, const bf16_t *__restrict__ kr, const bf16_t *__restrict__ vt,
     const float *__restrict__ cosT, const float *__restrict__ sinT, int n, int Hq, int Hkv, int S,
-    int W, float scale, int gw, int hsplit, int wsplit, int ntiles, int Cn, int xmap,
+    int W, float scale, int gw, int hsplit, int wsplit, int ntiles, int Cn,
     bf16_t *__restrict__ out, int64_t osb, int64_t osn, int64_t osh, float *__restrict__ lse) {
     extern __shared__ __align__(16) char smem[];
-    int cx, tile;
-    xcd_map(blockIdx.x, Cn, ntiles, xmap, cx, tile);
-    if (tile >= ntiles || cx >= Cn) return;
-    const int combo = cx / hsplit, hs = cx % hsplit;
+    // Work unit u = ((combo * ntiles + tile) * hsplit + hs), hs fastest.  XCD
+    // x (workgroup i runs on XCD i % 8) takes the x-th contiguous eighth of
+    // the units, so the heads and neighbouring tiles that read the same
+    // keys share that XCD's L2.
+    const int U = Cn * ntiles;
+    const int chunk = (U + 7) / 8;
+    const int u = (int)(blockIdx.x & 7) * chunk + (int)(blockIdx.x >> 3);
+    if (u >= U) return;
+    const int hs = u % hsplit;
+    const int tile = (u / hsplit) % ntiles;
+    const int combo = u / (hsplit * ntiles);
     const int G = Hq / Hkv;
     const float sl2 = scale * LOG2E;
     float bl2;
@@ -857,17 +864,18 @@ static int launch_win(const void *q, const int64_t *qs, const float *qgain, cons
                       float *lse, hipStream_t s) {
     using C = WinCfg<D, RT>;
     const int G = (int)(Hq / Hkv);
-    const int hsplit = (G + 7) / 8;                    // at most 8 heads (waves) per workgroup
-    const int gw = (G + hsplit - 1) / hsplit;
-    const int wsplit = (gw >= 4) ? 1 : (4 + gw - 1) / gw;   // at least 4 waves (256 threads)
+    // one head per workgroup, 4 waves over consecutive 16*RT-query ranges:
+    // a small ring and <= 168 VGPRs let 2-3 workgroups share a CU, so one
+    // workgroup's set-up and tail overlap another's tiles
+    const int hsplit = G;
+    const int gw = 1;
+    const int wsplit = 4;
     const int nthr = 64 * gw * wsplit;
-    if (nthr > 512 || nthr < 256) return HBA_ERR_UNSUPPORTED;
     const int64_t QT = 16 * RT * wsplit;
     const int64_t ntiles = (n + QT - 1) / QT;
     const int64_t Cn = B * Hkv * hsplit;
-    int xmap;
-    int64_t grid;
-    grid_map(Cn, ntiles, xmap, grid);
+    const int64_t U = Cn * ntiles;
+    const int64_t grid = 8 * ((U + 7) / 8);
     if (grid > 0x7fffffff) return HBA_ERR_UNSUPPORTED;
     const size_t lds = (size_t)C::NS * C::SLOT * 2;
     if (hipFuncSetAttribute(reinterpret_cast<const void *>(&attn_win_kernel<D, RT>),
@@ -876,7 +884,7 @@ static int launch_win(const void *q, const int64_t *qs, const float *qgain, cons
     const int Wc = (int)((W < n + 1) ? W : n + 1);     // a window longer than the sequence is the sequence
     hipLaunchKernelGGL((attn_win_kernel<D, RT>), dim3((unsigned)grid), dim3(nthr), lds, s, (const bf16_t *)q, qs[0],
                        qs[1], qs[2], qgain, kgain, eps, (const bf16_t *)kr, (const bf16_t *)vt, cosT, sinT, (int)n,
-                       (int)Hq, (int)Hkv, (int)S, Wc, scale, gw, hsplit, wsplit, (int)ntiles, (int)Cn, xmap,
+                       (int)Hq, (int)Hkv, (int)S, Wc, scale, gw, hsplit, wsplit, (int)ntiles, (int)Cn,
                        (bf16_t *)out, os[0], os[1], os[2], lse);
     return HBA_OK;
 }
@@ -943,7 +951,7 @@ int launch_attn_bf16(const void *q, const int64_t *qs, const float *qgain, const
     using namespace ab;
     const int G = (int)(Hq / Hkv);
     if (G > 16 || n / 64 >= SENT) return HBA_ERR_UNSUPPORTED;
-    constexpr int RT = (D == 64) ? 3 : 1;      // row tiles per wave: the most that fit 256 VGPRs
+    constexpr int RT = (D == 64) ? 2 : 1;      // row tiles per wave within 168 VGPRs (3 waves per SIMD)
     int st = launch_win<D, RT>(q, qs, qgain, kgain, eps, kr, vt, cosT, sinT, B, n, Hq, Hkv, S, W, scale, out, os,
                                lse, s);
     if (st) return st;
