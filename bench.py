@@ -37,7 +37,7 @@ DECODE = dict(batch=32, len_lo=16384, len_hi=32768, seed=0)
 # the window kernel writes the window's rows and their LSE, the routed kernel
 # adds the sinks and routed blocks and merges.  Its time is taken with HIP
 # events around the op.
-ATTN_KERNELS = "hba_attn_fwd = attn_win_kernel<64,3> + attn_routed_kernel<64,2>"
+ATTN_KERNELS = "hba_attn_fwd = attn_win_kernel<64,2> + attn_routed_kernel<64,2>"
 # HBM (beyond-L2) bytes per hba_attn_fwd call on this workload: rocprofv3 --pmc
 # FETCH_SIZE and WRITE_SIZE summed over the two kernels, each divided by the
 # counter's reading per byte of a plain device copy (python bench.py

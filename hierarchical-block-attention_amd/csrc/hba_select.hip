@@ -10,6 +10,7 @@
 // (score descending, block index ascending).
 #include "hba_common.h"
 #include "hba_abi.h"
+#include "hba_dma.h"
 
 namespace hba {
 
@@ -22,12 +23,17 @@ __device__ __forceinline__ bool better(float v, int id, float w, int iw) {
 
 // Insert (v, id) into a list sorted by (value desc, id asc).  Entries arrive
 // in increasing id order, so an equal value never displaces an earlier one.
+// Once the new entry has taken a position, every later entry moves down one
+// place (an entry displaced from position j precedes, in the order, the
+// equal-valued entries after it).
 template <int K>
 __device__ __forceinline__ void insert_inorder(float (&vals)[K], int (&ids)[K], float v, int id) {
     if (v > vals[K - 1]) {
+        bool moving = false;
 #pragma unroll
         for (int j = 0; j < K; ++j) {
-            bool sw = v > vals[j];
+            const bool sw = moving || v > vals[j];
+            moving = sw;
             float tv = sw ? vals[j] : v;
             int ti = sw ? ids[j] : id;
             vals[j] = sw ? v : vals[j];
@@ -204,20 +210,31 @@ __global__ __launch_bounds__(SEL_WG) void score_select_kernel(
 
 
 // ----------------------------------------------------- bf16 MFMA scoring ----
-// Block scores as one bf16 MFMA GEMM per (batch, KV head, 64 queries):
-// C^T[summary rows x queries] = S0 . qg^T with v_mfma_f32_16x16x32_bf16
-// (fp32 accumulation).  A 16-row M-tile is 4 blocks x 4 slots, so lane
-// (l16, lg) receives the 4 slot scores of block 4*mt + lg for query l16 and
-// takes their max in registers; each lane keeps a top-k of the blocks it sees
-// (ascending ids: in-order insertion), and the four lane groups of a query
-// are merged under (score desc, block asc).  The routing query is built in
-// the declared fp32 order and is exactly representable in bf16.  Summary
-// rows are staged in LDS, shared by the four waves (16 queries each).
 typedef unsigned int u32x4s __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ bf16x8 ldb8(const bf16_t *p) {
     return __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4s *>(p));
 }
+
+// Scores as one bf16 GEMM per (batch, KV head, 64 queries):
+// C^T[summary rows x queries] = S0 . qg^T with v_mfma_f32_16x16x32_bf16 (fp32
+// accumulation).  A 16-row M tile is 4 blocks x 4 slots, so lane (l16, lg)
+// receives the 4 slot scores of block 4*mt + lg for query column l16 and takes
+// their max.  The summaries stream through a 3-stage direct-to-LDS ring of
+// 16 blocks per stage.  Each lane keeps a top-KMAX of the blocks it sees (in
+// ascending block order); the four lane lists of a query are then merged
+// under the same order.  The routing query is built in the declared fp32 order
+// and is exactly representable in bf16.
+namespace sel {
+constexpr int CB = 16;       // blocks per stage
+constexpr int NSS = 3;       // stages in the ring
+// chunk swizzle of stage row r: the 16 rows an A-fragment read touches land in
+// distinct 16-byte bank groups
+template <int D>
+__device__ __forceinline__ int sw(int r) {
+    return (D == 64) ? ((r >> 1) & 7) : (r & 15);
+}
+}  // namespace sel
 
 template <int D, int KMAX>
 __global__ __launch_bounds__(256) void score_select_mfma_kernel(
@@ -225,13 +242,21 @@ __global__ __launch_bounds__(256) void score_select_mfma_kernel(
     float eps, const bf16_t *__restrict__ S0, int64_t n, int Hq, int Hkv, int64_t nb, int64_t W, int kk,
     float scale, int32_t *__restrict__ idx, float *__restrict__ val, int32_t *__restrict__ cnt,
     float *__restrict__ scores) {
+    using namespace sel;
     constexpr int NKS = D / 32;
-    constexpr int ROW = D + 8;            // padded LDS row (bf16)
-    constexpr int CB = 16;                // blocks per stage (4 M-tiles)
-    __shared__ __align__(16) bf16_t qgs[64 * ROW];
-    __shared__ __align__(16) bf16_t sst[CB * 4 * ROW];
-    __shared__ float mv[64][4][KMAX];
-    __shared__ int mi[64][4][KMAX];
+    constexpr int CPR = D / 8;                         // 16-byte chunks per summary row
+    constexpr int ROWQ = D + 8;                        // padded LDS row of the routing queries
+    constexpr int SROWS = CB * 4;                      // rows per stage
+    constexpr int PPW = SROWS * D * 2 / 1024 / 4;      // 1 KB DMA parts per wave per stage
+    // LDS: the routing queries; the stage ring, reused for the lane lists
+    constexpr int RING_BYTES = NSS * SROWS * D * 2;
+    constexpr int LIST_BYTES = 64 * 4 * KMAX * 8;
+    __shared__ __align__(16) bf16_t qgs[64 * ROWQ];
+    __shared__ __align__(16) char pool[RING_BYTES > LIST_BYTES ? RING_BYTES : LIST_BYTES];
+    bf16_t *ring = reinterpret_cast<bf16_t *>(pool);
+    float (*mv)[4][KMAX] = reinterpret_cast<float (*)[4][KMAX]>(pool);
+    int (*mi)[4][KMAX] = reinterpret_cast<int (*)[4][KMAX]>(pool + 64 * 4 * KMAX * 4);
+
     const int tid = threadIdx.x;
     const int w = tid >> 6, lane = tid & 63, l16 = lane & 15, lg = lane >> 4;
     const int g = blockIdx.y;
@@ -243,17 +268,35 @@ __global__ __launch_bounds__(256) void score_select_mfma_kernel(
         float qg[D];
         routing_query<1, D>(q, qsb, qsn, qsh, qgain, eps, b, i, g, G, qg);
 #pragma unroll
-        for (int t = 0; t < D; ++t) qgs[tid * ROW + t] = f2bf(qg[t]);
+        for (int t = 0; t < D; ++t) qgs[tid * ROWQ + t] = f2bf(qg[t]);
     }
     __syncthreads();
     const int qcol = 16 * w + l16;
     const int64_t iq = i0 + qcol;
     bf16x8 qb[NKS];
 #pragma unroll
-    for (int ks = 0; ks < NKS; ++ks) qb[ks] = ldb8(qgs + qcol * ROW + 32 * ks + 8 * lg);
+    for (int ks = 0; ks < NKS; ++ks) qb[ks] = ldb8(qgs + qcol * ROWQ + 32 * ks + 8 * lg);
     const int64_t bmax = (iq < n) ? cand_bmax(iq, 64, W) : 0;
     const int64_t last = (i0 + 63 < n) ? i0 + 63 : n - 1;
     const int64_t tile_bmax = cand_bmax(last, 64, W);
+    const int nst = (tile_bmax >= 1) ? (int)((tile_bmax + CB - 1) / CB) : 0;   // stages: blocks 1..tile_bmax
+    const bf16_t *Sg = S0 + (b * Hkv + g) * nb * 4 * D;
+    const uint32_t ring_lds = lds_offset(ring);
+
+    // this wave's DMA parts of stage st into ring slot st % NSS (rows past
+    // tile_bmax read block tile_bmax: never scored)
+    auto fill = [&](int st) {
+        const uint32_t slot = ring_lds + (uint32_t)((st % NSS) * SROWS * D * 2);
+#pragma unroll
+        for (int pp = 0; pp < PPW; ++pp) {
+            const int part = w * PPW + pp;
+            const int p = part * 64 + lane;              // physical chunk index in the stage
+            const int r = p / CPR, c = (p % CPR) ^ sw<D>(r & 15);
+            int64_t blk = 1 + (int64_t)st * CB + r / 4;
+            blk = (blk <= tile_bmax) ? blk : tile_bmax;
+            dma16(Sg + (blk * 4 + (r & 3)) * D + 8 * c, slot + (uint32_t)part * 1024u);
+        }
+    };
     float vals[KMAX];
     int ids[KMAX];
 #pragma unroll
@@ -261,37 +304,37 @@ __global__ __launch_bounds__(256) void score_select_mfma_kernel(
         vals[j] = -INFINITY;
         ids[j] = -1;
     }
-    const bf16_t *Sg = S0 + (b * Hkv + g) * nb * 4 * D;
-    for (int64_t b0 = 1; b0 <= tile_bmax; b0 += CB) {
-        const int cb = (int)((tile_bmax - b0 + 1 < CB) ? tile_bmax - b0 + 1 : CB);
-        __syncthreads();
-        for (int c = tid; c < cb * 4 * (D / 8); c += 256) {
-            const int row = c / (D / 8), ch = c % (D / 8);
-            *reinterpret_cast<u32x4s *>(sst + row * ROW + 8 * ch) =
-                *reinterpret_cast<const u32x4s *>(Sg + (b0 * 4 + row) * D + 8 * ch);
-        }
-        __syncthreads();
-        const int nmt = (cb + 3) / 4;
-        for (int mt = 0; mt < nmt; ++mt) {
+    for (int st = 0; st < NSS - 1 && st < nst; ++st) fill(st);
+    for (int st = 0; st < nst; ++st) {
+        const int ahead = (nst - 1 - st < NSS - 2) ? nst - 1 - st : NSS - 2;
+        wait_vm_n(ahead * PPW);
+        __syncthreads();   // stage st landed everywhere; stage st-1 is consumed
+        if (st + NSS - 1 < nst) fill(st + NSS - 1);
+        const bf16_t *Ss = ring + (st % NSS) * SROWS * D;
+        const int64_t b0 = 1 + (int64_t)st * CB;
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+            const int r = mt * 16 + l16;
+            const bf16_t *ar = Ss + r * D;
             f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-            const bf16_t *ar = sst + (mt * 16 + l16) * ROW + 8 * lg;
 #pragma unroll
             for (int ks = 0; ks < NKS; ++ks)
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ldb8(ar + 32 * ks), qb[ks], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ldb8(ar + 8 * ((4 * ks + lg) ^ sw<D>(r & 15))), qb[ks],
+                                                             acc, 0, 0, 0);
             const int64_t blk = b0 + 4 * mt + lg;
             float best = acc[0];
             best = (acc[1] > best) ? acc[1] : best;
             best = (acc[2] > best) ? acc[2] : best;
             best = (acc[3] > best) ? acc[3] : best;
             const float v = best * scale;
-            const bool ok = (4 * mt + lg < cb) && blk <= bmax;
-            if (ok) {
+            if (blk <= bmax && blk <= tile_bmax) {
                 if (scores) scores[((b * Hkv + g) * n + iq) * nb + blk] = v;
                 insert_inorder<KMAX>(vals, ids, v, (int)blk);
             }
         }
     }
-    // merge the four lane groups of each query
+    // merge the four lane groups of each query (the lists reuse the ring)
+    __syncthreads();
 #pragma unroll
     for (int j = 0; j < KMAX; ++j) {
         mv[qcol][lg][j] = vals[j];
@@ -311,7 +354,7 @@ __global__ __launch_bounds__(256) void score_select_mfma_kernel(
                 if (hp[l] >= KMAX) continue;
                 const float v = mv[tid][l][hp[l]];
                 const int id = mi[tid][l][hp[l]];
-                if (v == -INFINITY) continue;
+                if (id < 0) continue;
                 if (bestl < 0 || better(v, id, bv, bi)) {
                     bestl = l;
                     bv = v;

@@ -168,6 +168,39 @@ def test_flat_select(dev, case):
             assert flips <= max(2, n // 1000), flips
 
 
+@pytest.mark.parametrize("dt", ["bf16", "f32"])
+@pytest.mark.parametrize("pattern", ["lane0", "ties", "zero_q"])
+def test_flat_select_adversarial(dev, pattern, dt):
+    """Selection on score layouts that stress the tie rule and the bf16 MFMA
+    path's first-pass threshold: the best blocks all fall to one of the four
+    lanes that scan a query's blocks (blocks 1, 5, 9, ...), massive ties, and
+    all-zero scores.  The top-k must equal the top-k (score desc, block asc)
+    of the kernel's own score array."""
+    torch.manual_seed(3)
+    n, Hkv, Hq, d, m, W, kk = 4096, 2, 14, 64, 4, 512, 16
+    nb = n // 64
+    tdt = torch.bfloat16 if dt == "bf16" else torch.float32
+    q = torch.randn(1, n, Hq, d, device=dev).to(tdt)
+    if pattern == "zero_q":
+        q.zero_()
+    gq = torch.full((Hq,), d ** 0.25, device=dev)
+    v = torch.randn(d)
+    a = torch.ones(nb)
+    if pattern == "lane0":
+        a[1::4] = 4.0 + torch.arange(a[1::4].numel()) / 64.0      # blocks 1, 5, 9, ... rank above the rest
+    elif pattern == "ties":
+        a = (torch.arange(nb) % 3).float() + 1.0                    # three values, a third of the blocks each
+    S0 = (a[:, None, None] * v[None, None, :]).expand(nb, m, d).contiguous()
+    S0 = S0[None, None].expand(1, Hkv, nb, m, d).contiguous().to(tdt).to(dev)
+    idx, val, cnt, scores = ops.score_select_with_scores(q, gq, 1e-6, S0, W, kk, 0.125)
+    torch.cuda.synchronize()
+    sc = scores[0].cpu().numpy()
+    ki, kv, kc_ = idx[0].cpu().numpy(), val[0].cpu().numpy(), cnt[0].cpu().numpy()
+    for g in range(Hkv):
+        ti, tv, tc = O.topk(sc[g], kk)
+        assert np.array_equal(ti, ki[g]) and np.array_equal(tv, kv[g]) and np.array_equal(tc, kc_[g])
+
+
 HIER_CASES = [
     dict(dt="f32", n=4096, W=512, k=8, fanout=4, beam=2),
     dict(dt="bf16", n=4096, W=1024, k=16, fanout=16, beam=2),
