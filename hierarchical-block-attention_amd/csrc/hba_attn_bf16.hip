@@ -96,11 +96,13 @@ __device__ __forceinline__ float sum8(bf16x8 v, float acc) {
 // rope, apply_rope's rotation and bf16 roundings (:40-44) at position i.  The
 // rotation partner d +- D/2 sits in the same lane at ks +- NKS/2.  Invalid
 // columns read row 0 and are zeroed (no divergence around the shuffles).
+// qscale multiplies the operand before its bf16 rounding: the fixed-shift
+// softmax passes scale*log2(e), so that S^T comes out in log2 units.
 template <int D>
 __device__ __forceinline__ void qoperand(const bf16_t *q, int64_t qsb, int64_t qsn, int64_t qsh,
                                          const float *qgain, float eps, const float *cosT,
                                          const float *sinT, int64_t b, int64_t i, int h, bool valid,
-                                         bool rope, int lg, bf16x8 (&qop)[D / 32]) {
+                                         bool rope, int lg, float qscale, bf16x8 (&qop)[D / 32]) {
     constexpr int NKS = D / 32;
     const int64_t ii = valid ? i : 0;
     const bf16_t *row = q + b * qsb + ii * qsn + (int64_t)h * qsh;
@@ -142,7 +144,7 @@ __device__ __forceinline__ void qoperand(const bf16_t *q, int64_t qsb, int64_t q
                 const float t2 = rnd_bf16(rot * rnd_bf16(sinT[ii * D + d]));
                 v = rnd_bf16(t1 + t2);
             }
-            y[e] = valid ? v : 0.0f;
+            y[e] = valid ? v * qscale : 0.0f;
         }
         qop[ks] = pack8(y);
     }
@@ -267,10 +269,12 @@ __device__ __forceinline__ void win_body(
     bf16x8 qop[RT][C::NKS];
     f32x4 O[RT][C::NDT];
     float ls[RT], mr[RT];
+    const float es = FIXED ? 1.0f : sl2;   // log2 units per S^T unit (FIXED: folded into the query operand)
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
         const int i = q0 + 16 * rt + l16;
-        qoperand<D>(q, qsb, qsn, qsh, qgain, eps, cosT, sinT, b, i, h, i < n, true, lg, qop[rt]);
+        qoperand<D>(q, qsb, qsn, qsh, qgain, eps, cosT, sinT, b, i, h, i < n, true, lg, FIXED ? sl2 : 1.0f,
+                    qop[rt]);
 #pragma unroll
         for (int dt = 0; dt < C::NDT; ++dt) O[rt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
         ls[rt] = 0.0f;
@@ -337,7 +341,7 @@ __device__ __forceinline__ void win_body(
                     for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
                         for (int mt = 0; mt < 4; ++mt) {
-                            Sa[rt][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+                            Sa[rt][mt] = f32x4{-bl2, -bl2, -bl2, -bl2};   // operand carries scale*log2(e)
 #pragma unroll
                             for (int ks = 0; ks < C::NKS; ++ks) Sa[rt][mt] = mma(kf[mt][ks], qop[rt][ks], Sa[rt][mt]);
                         }
@@ -348,7 +352,7 @@ __device__ __forceinline__ void win_body(
 #pragma unroll
                         for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-                            for (int e = 0; e < 4; ++e) p[mt >> 1][(mt & 1) * 4 + e] = ex2(fmaf(Sa[rt][mt][e], sl2, -bl2));
+                            for (int e = 0; e < 4; ++e) p[mt >> 1][(mt & 1) * 4 + e] = ex2(Sa[rt][mt][e]);
                         pf[rt][0] = pack8(p[0]);
                         pf[rt][1] = pack8(p[1]);
                         ls[rt] = sum8(pf[rt][1], sum8(pf[rt][0], ls[rt]));
@@ -409,7 +413,7 @@ __device__ __forceinline__ void win_body(
 #pragma unroll
                         for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-                            for (int e = 0; e < 4; ++e) p[mt >> 1][(mt & 1) * 4 + e] = ex2(fmaf(Sa[mt][e], sl2, -shift));
+                            for (int e = 0; e < 4; ++e) p[mt >> 1][(mt & 1) * 4 + e] = ex2(fmaf(Sa[mt][e], es, -shift));
                     } else {
                         // masked keys: the exp2 argument is selected to -inf (no branch per element)
 #pragma unroll
@@ -418,7 +422,7 @@ __device__ __forceinline__ void win_body(
                             for (int e = 0; e < 4; ++e) {
                                 const int j = kl + 32 * (mt >> 1) + 4 * (mt & 1) + e;
                                 const bool ok = (j >= jlo) & (j <= jhi);
-                                const float a = fmaf(Sa[mt][e], sl2, -shift);
+                                const float a = fmaf(Sa[mt][e], es, -shift);
                                 p[mt >> 1][(mt & 1) * 4 + e] = ex2(ok ? a : -INFINITY);
                             }
                     }
@@ -512,10 +516,15 @@ __device__ __forceinline__ void rt_update(const bf16_t *Ks, const bf16_t *Vs, co
                                           int64_t icol, bool colok, int S, int nmt, float sl2, float bl2,
                                           int l16, int lg) {
     constexpr int NKS = D / 32, NDT = D / 16;
+    // fixed shift, block columns: the query operand carries scale*log2(e), so
+    // S^T starts at -shift (a column whose query did not pick the block at
+    // -inf) and its exp2 needs no other operation
+    const bool cinit = FIXED && mode == RM_COL;
+    const float c0 = cinit ? (colok ? -bl2 : -INFINITY) : 0.0f;
     f32x4 Sa[4];
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) {
-        Sa[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        Sa[mt] = f32x4{c0, c0, c0, c0};
         if (mt < nmt) {
             const int r = permk(mt, l16);
             const bf16_t *kp = Ks + r * D;
@@ -546,7 +555,12 @@ __device__ __forceinline__ void rt_update(const bf16_t *Ks, const bf16_t *Vs, co
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) O[dt] *= alpha;
     }
-    if (mode == RM_COL) {
+    if (cinit) {
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) p[mt >> 1][(mt & 1) * 4 + e] = ex2(Sa[mt][e]);
+    } else if (mode == RM_COL) {
         // a column whose query did not pick the block: shift +inf, so every
         // exp2 argument is -inf (no select per element)
         const float sh = colok ? shift : INFINITY;
@@ -687,7 +701,7 @@ __device__ __forceinline__ void routed_body(
 #pragma unroll
         for (int dt = 0; dt < C::NDT; ++dt) O[t][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
         qoperand<D>(q, qsb, qsn, qsh, qgain, eps, nullptr, nullptr, b, icol[t], g * G + hh, cok[t], false, lg,
-                    qop[t]);
+                    FIXED ? sl2 : 1.0f, qop[t]);
     }
     __syncthreads();
     const int ne = nlist;
@@ -711,7 +725,7 @@ __device__ __forceinline__ void routed_body(
         for (int tt = 0; tt < PTW; ++tt) {
             if (i0 + (int64_t)(w * PTW + tt) * QPT >= n) break;
             rt_update<D, FIXED>(Ks, Ks + 64 * D, qop[tt], O[tt], mrun[tt], lsum[tt], RM_SINK, icol[tt], cok[tt], S,
-                                nmt, sl2, bl2, l16, lg);
+                                nmt, FIXED ? 1.0f : sl2, bl2, l16, lg);
         }
     }
     uint32_t qw[PTW], ww[PTW];   // this lane's query's / this row tile's bits of the current word
@@ -743,7 +757,7 @@ __device__ __forceinline__ void routed_body(
                 const bf16_t *Ks = ring + (e % C::NS) * C::SLOT;
                 const bool hit = (qw[tt] >> (sh + j)) & 1u;
                 rt_update<D, FIXED>(Ks, Ks + 64 * D, qop[tt], O[tt], mrun[tt], lsum[tt], RM_COL, icol[tt], hit, S,
-                                    4, sl2, bl2, l16, lg);
+                                    4, FIXED ? 1.0f : sl2, bl2, l16, lg);
             }
         }
     }
