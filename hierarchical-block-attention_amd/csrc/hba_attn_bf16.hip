@@ -79,15 +79,17 @@ __device__ __forceinline__ bf16x8 pack8(const float (&x)[8]) {
     return r;
 }
 
-// acc + the sum of 8 bf16 values (v_dot2 against ones: the products are exact)
-__device__ __forceinline__ float sum8(bf16x8 v, float acc) {
-    const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+// Sum over a 64-key block of one column's probabilities (P^T halves p0 =
+// keys 0..31, p1 = keys 32..63 in the B layout), on the MFMA: a ones A
+// operand makes every row of the product the column sum.  Each lane receives
+// its column's full sum.
+__device__ __forceinline__ float colsum(bf16x8 p0, bf16x8 p1) {
+    bf16x8 ones;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const bf16x2 pr = {v[2 * k], v[2 * k + 1]};
-        acc = __builtin_amdgcn_fdot2_f32_bf16(pr, one, acc, false);
-    }
-    return acc;
+    for (int e = 0; e < 8; ++e) ones[e] = (__bf16)1.0f;
+    f32x4 t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, p0, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+    t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, p1, t, 0, 0, 0);
+    return t[0];
 }
 
 // Query operand of one lane's column (query i, head h) for S^T = K . Q^T:
@@ -355,7 +357,7 @@ __device__ __forceinline__ void win_body(
                             for (int e = 0; e < 4; ++e) p[mt >> 1][(mt & 1) * 4 + e] = ex2(Sa[rt][mt][e]);
                         pf[rt][0] = pack8(p[0]);
                         pf[rt][1] = pack8(p[1]);
-                        ls[rt] = sum8(pf[rt][1], sum8(pf[rt][0], ls[rt]));
+                        ls[rt] += colsum(pf[rt][0], pf[rt][1]);
                     }
 #pragma unroll
                     for (int dt = 0; dt < C::NDT; ++dt) {
@@ -428,7 +430,7 @@ __device__ __forceinline__ void win_body(
                     }
                     pb[rt][0] = pack8(p[0]);
                     pb[rt][1] = pack8(p[1]);
-                    ls[rt] = sum8(pb[rt][1], sum8(pb[rt][0], ls[rt]));
+                    ls[rt] += colsum(pb[rt][0], pb[rt][1]);
                 }
                 // O^T += V^T . P^T; each V^T fragment read once
 #pragma unroll
@@ -451,9 +453,7 @@ __device__ __forceinline__ void win_body(
     // normalise and store the window's rows and their LSE
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
-        float l = ls[rt];
-        l += __shfl_xor(l, 16, 64);
-        l += __shfl_xor(l, 32, 64);
+        const float l = ls[rt];   // the column's full sum in every lane
         const int i = q0 + 16 * rt + l16;
         if (i >= n || !hv) continue;
         const float inv = (l > 0.0f) ? 1.0f / l : 0.0f;
@@ -580,7 +580,7 @@ __device__ __forceinline__ void rt_update(const bf16_t *Ks, const bf16_t *Vs, co
             }
     }
     const bf16x8 pb0 = pack8(p[0]), pb1 = pack8(p[1]);
-    lsum = sum8(pb1, sum8(pb0, lsum));
+    lsum += colsum(pb0, pb1);
     const bool two = mode != RM_SINK || nmt > 2;        // keys 32..63 can be valid
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) {
@@ -765,9 +765,7 @@ __device__ __forceinline__ void routed_body(
     // ------------------- merge with the window's (out, LSE), normalise, store
 #pragma unroll
     for (int t = 0; t < PTW; ++t) {
-        float l = lsum[t];
-        l += __shfl_xor(l, 16, 64);
-        l += __shfl_xor(l, 32, 64);
+        const float l = lsum[t];   // the column's full sum in every lane
         if (!cok[t]) continue;
         const int h = g * G + hh;
         const int64_t i = icol[t];
