@@ -12,6 +12,8 @@ bounded sample of the same workload.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-decode]
   python bench.py --copy-probe MIB      # plain device copy, for counter calibration
+  python bench.py --config hier128k     # hierarchical selection at 128K vs the flat scan
+  python bench.py --config donor        # 28/4-head d=128 layer at 64K, B=2, + 64 decode steps
 """
 import argparse
 import json
@@ -245,6 +247,136 @@ def cpu_baseline(res, budget_s=20.0):
                       f"{t_rows:.1f}s, extrapolated to {n} rows; host {cpu_model()}"}
 
 
+def _timed(fn, reps=5):
+    """Mean ms of fn() over reps calls (HIP events on the current stream), after one warm call."""
+    import torch
+    out = fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        out = fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps, out
+
+
+def bench_hier128k(dev):
+    """Hierarchical tree selection at 128K (B=1, 14/2 heads, d=64, 2048 blocks,
+    super-summaries over 16 blocks, beam 8, top-16, log-length temperature
+    active, needles as in the 32K workload): flat and hierarchical selection
+    timed, their set agreement over all queries and the last one, the
+    comparisons per query, and the union attention over the hierarchical
+    selection."""
+    import torch
+    import hba_amd
+    from hba_amd import ops, synth
+    from hba_amd.config import union_scale
+    from hba_amd.synth import ncand
+    n, Hq, Hkv, d, m, S, W, k, F, beam = 131072, 14, 2, 64, 4, 4, 1024, 16, 16, 8
+    cfg = hba_amd.HBAConfig(n_heads=Hq, n_kv=Hkv, head_dim=d, sinks=S, window=W, block=64, slots=m, k_blocks=k,
+                            fanout=F, beam=beam)
+    x = synth.layer_inputs(1, n, Hq, Hkv, d, m=m, dtype=torch.bfloat16, device=dev, seed=0, sharp=True,
+                           needles=True, window=W)
+    prm = synth.Params(x["q_gain"], x["k_gain"], x["probes"], x["proj"])
+    cos, sin = hba_amd.rope_tables(n, d, cfg.rope_theta, dev)
+    scale = union_scale(cfg, d, n)
+    t_prep, (kc, kr, vt) = _timed(lambda: ops.prep_keys(x["k"], x["v"], prm.k.gain, 1e-6, cos, sin))
+    t_summ, S0 = _timed(lambda: ops.summarize(kc, prm.probes, prm.proj))
+    t_flat, (fi, fv, fc) = _timed(lambda: ops.score_select(x["q"], prm.q.gain, 1e-6, S0, W, k, scale))
+    t_sup, S1 = _timed(lambda: ops.build_super(S0, F))
+    t_hier, (hi, hv, hc) = _timed(lambda: ops.hier_select(x["q"], prm.q.gain, 1e-6, S0, S1, W, k, F, beam, scale))
+    t_attn, _ = _timed(lambda: ops.attn_fwd(x["q"], prm.q.gain, prm.k.gain, 1e-6, kc, kr, vt, cos, sin, hi, hc,
+                                            S, W, scale), reps=3)
+    # set agreement |flat & hier| / |flat| per (KV head, query) with a non-empty flat set
+    fi, fc, hi, hc = fi[0].cpu(), fc[0].cpu(), hi[0].cpu(), hc[0].cpu()
+    agree = tot = 0
+    last = []
+    for g in range(Hkv):
+        fs = fi[g].clone()
+        fs[torch.arange(k)[None, :] >= fc[g][:, None]] = -1
+        hs = hi[g].clone()
+        hs[torch.arange(k)[None, :] >= hc[g][:, None]] = -2
+        inter = (fs[:, :, None] == hs[:, None, :]).any(-1).sum(-1)
+        ok = fc[g] > 0
+        agree += int(inter[ok].sum())
+        tot += int(fc[g][ok].sum())
+        last.append(float(inter[-1]) / max(1, int(fc[g][-1])))
+    nsup = (n // 64 + F - 1) // F
+    return {"metric": "HBA hierarchical selection at 128K: time vs flat scan, set agreement",
+            "config": {"workload": "hba_hier_select_128k", "batch": 1, "seq_len": n, "q_heads": Hq, "kv_heads": Hkv,
+                       "head_dim": d, "fanout": F, "beam": beam, "top_k": k, "needles": 16,
+                       "temperature": round(scale / union_scale(cfg, d, 32768), 6)},
+            "ms": {"prep": round(t_prep, 4), "summ": round(t_summ, 4), "flat_select": round(t_flat, 4),
+                   "build_super": round(t_sup, 4), "hier_select": round(t_hier, 4),
+                   "attn_on_hier": round(t_attn, 4)},
+            "hier_vs_flat_select_speedup": round(t_flat / (t_sup + t_hier), 3),
+            "agreement_all_queries": round(agree / max(1, tot), 4),
+            "agreement_last_query": round(sum(last) / len(last), 4),
+            "comparisons_per_query": {"hier": nsup + beam * F, "flat": int(ncand(n - 1, 64, W)),
+                                      "ratio": round(ncand(n - 1, 64, W) / (nsup + beam * F), 2)}}
+
+
+def bench_donor(dev, steps=64):
+    """Donor-shaped layer: B=2, n=65536, 28/4 heads, d=128, 8 sinks, window
+    1024, top-16, bf16, N(0,1) inputs from a seed: the prefill forward (stages
+    timed), then a 64-step batched decode continuation from that cache, each
+    step appending one new token per sequence and decoding its query."""
+    import torch
+    import hba_amd
+    from hba_amd import ops, synth
+    from hba_amd.config import union_scale
+    B, n, Hq, Hkv, d, m, S, W, k = 2, 65536, 28, 4, 128, 4, 8, 1024, 16
+    cfg = hba_amd.HBAConfig(n_heads=Hq, n_kv=Hkv, head_dim=d, sinks=S, window=W, block=64, slots=m, k_blocks=k)
+    x = synth.layer_inputs(B, n, Hq, Hkv, d, m=m, dtype=torch.bfloat16, device=dev, seed=0, sharp=True,
+                           needles=False, window=W)
+    prm = synth.Params(x["q_gain"], x["k_gain"], x["probes"], x["proj"])
+    Lmax = n + steps
+    cos, sin = hba_amd.rope_tables(Lmax, d, cfg.rope_theta, dev)
+    scale = union_scale(cfg, d, n)
+    t_prep, (kc, kr, vt) = _timed(lambda: ops.prep_keys(x["k"], x["v"], prm.k.gain, 1e-6, cos, sin), reps=3)
+    t_summ, S0 = _timed(lambda: ops.summarize(kc, prm.probes, prm.proj), reps=3)
+    t_sel, (idx, val, cnt) = _timed(lambda: ops.score_select(x["q"], prm.q.gain, 1e-6, S0, W, k, scale), reps=3)
+    t_attn, _ = _timed(lambda: ops.attn_fwd(x["q"], prm.q.gain, prm.k.gain, 1e-6, kc, kr, vt, cos, sin, idx, cnt,
+                                            S, W, scale), reps=3)
+    t_layer = t_prep + t_summ + t_sel + t_attn
+    flop = (synth.attention_flops(B, n, Hq, d, S, W, 64, k) + synth.scoring_flops(B, n, Hkv, d, m, 64, W) +
+            synth.summarizer_flops(B, n, Hkv, d, m, 64))
+    # decode continuation from the prefill cache
+    cache = hba_amd.PagedKVCache(cfg, B, Lmax, torch.bfloat16, dev)
+    for s_ in range(B):
+        cache.load(s_, kc[s_].transpose(0, 1), kr[s_].transpose(0, 1), x["v"][s_], prm)
+    del kc, kr, vt, idx, val, cnt
+    g = torch.Generator().manual_seed(1)
+    qs = torch.randn(steps, B, Hq, d, generator=g).to(torch.bfloat16).to(dev)
+    ks = torch.randn(steps, B, Hkv, d, generator=g).to(torch.bfloat16).to(dev)
+    vs = torch.randn(steps, B, Hkv, d, generator=g).to(torch.bfloat16).to(dev)
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for st in range(steps):
+        cache.append(ks[st], vs[st], prm, prm, cos, sin)
+        ev[st][0].record()
+        hba_amd.hba_decode_step(qs[st], cache, cfg, prm, cos, sin)
+        ev[st][1].record()
+    t1.record()
+    torch.cuda.synchronize()
+    step_us = sorted(a.elapsed_time(b) * 1000.0 for a, b in ev)
+    return {"metric": "HBA donor-shaped layer: prefill tokens/s; decode continuation us/step",
+            "config": {"workload": "hba_layer_fwd_donor_64k_d128", "batch": B, "seq_len": n, "q_heads": Hq,
+                       "kv_heads": Hkv, "head_dim": d, "sinks": S, "window": W, "top_k": k, "decode_steps": steps},
+            "prefill": {"tokens_per_s": round(B * n / (t_layer * 1e-3), 1), "ms": round(t_layer, 4),
+                        "stage_ms": {"prep": round(t_prep, 4), "summ": round(t_summ, 4), "select": round(t_sel, 4),
+                                     "attn": round(t_attn, 4)},
+                        "mfma_frac": round(flop / (t_layer * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)},
+            "decode": {"step_us_median": round(step_us[len(step_us) // 2], 2),
+                       "step_us_min": round(step_us[0], 2),
+                       "append_plus_step_us": round(t0.elapsed_time(t1) * 1000.0 / steps, 2),
+                       "lengths": [n + 1, n + steps]}}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -255,6 +387,9 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run 3 plain device copies of MIB MiB (counter calibration) and exit")
+    ap.add_argument("--config", choices=["layer32k", "hier128k", "donor"], default="layer32k",
+                    help="layer32k: the headline line (default); hier128k / donor: the other measured "
+                         "workloads, one JSON line each")
     a = ap.parse_args()
     if a.copy_probe:
         import torch
@@ -273,6 +408,11 @@ def main():
         sys.exit(2)
     import torch
     dev = torch.device("cuda:0")
+    if a.config != "layer32k":
+        line = bench_hier128k(dev) if a.config == "hier128k" else bench_donor(dev)
+        line.update({"n_gpus": 1, "dtype": "bf16", "data": "synthetic"})
+        print(json.dumps(line))
+        return
     res = bench_layer(dev, a.steps, a.warmup)
     ms = res["ms"]
     attn_ms = res["stage_ms"]["attn"]
