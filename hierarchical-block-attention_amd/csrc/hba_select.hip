@@ -236,26 +236,36 @@ __device__ __forceinline__ int sw(int r) {
 }
 }  // namespace sel
 
-template <int D, int KMAX>
+// HIER: the two-level beam descent (hier_select) on the same machinery.  A
+// scan over the super-summaries S1 keeps, per query, the top-min(beam, ns)
+// supers holding a candidate child (score desc, super asc); the block scan
+// then inserts only children of those supers.  On a GPU tile of 64 queries
+// the kept supers cover nearly every super, so the children are scored as the
+// flat GEMM and filtered, not gathered.
+constexpr int SEL_PMW = 64;   // most words of the per-query super bitmask: ns <= 2048
+template <int D, int KMAX, bool HIER>
 __global__ __launch_bounds__(256) void score_select_mfma_kernel(
     const bf16_t *__restrict__ q, int64_t qsb, int64_t qsn, int64_t qsh, const float *__restrict__ qgain,
     float eps, const bf16_t *__restrict__ S0, int64_t n, int Hq, int Hkv, int64_t nb, int64_t W, int kk,
     float scale, int32_t *__restrict__ idx, float *__restrict__ val, int32_t *__restrict__ cnt,
-    float *__restrict__ scores) {
+    float *__restrict__ scores, const bf16_t *__restrict__ S1, int F, int beam, float *__restrict__ sup_scores) {
     using namespace sel;
     constexpr int NKS = D / 32;
     constexpr int CPR = D / 8;                         // 16-byte chunks per summary row
     constexpr int ROWQ = D + 8;                        // padded LDS row of the routing queries
     constexpr int SROWS = CB * 4;                      // rows per stage
     constexpr int PPW = SROWS * D * 2 / 1024 / 4;      // 1 KB DMA parts per wave per stage
+    constexpr int BEAMMAX = 16;
+    constexpr int LK = (HIER && BEAMMAX > KMAX) ? BEAMMAX : KMAX;   // lane list length held in LDS
     // LDS: the routing queries; the stage ring, reused for the lane lists
     constexpr int RING_BYTES = NSS * SROWS * D * 2;
-    constexpr int LIST_BYTES = 64 * 4 * KMAX * 8;
+    constexpr int LIST_BYTES = 64 * 4 * LK * 8;
     __shared__ __align__(16) bf16_t qgs[64 * ROWQ];
     __shared__ __align__(16) char pool[RING_BYTES > LIST_BYTES ? RING_BYTES : LIST_BYTES];
+    extern __shared__ uint32_t pmask[];                // HIER: [64][ceil(ns / 32)], sized at launch
     bf16_t *ring = reinterpret_cast<bf16_t *>(pool);
-    float (*mv)[4][KMAX] = reinterpret_cast<float (*)[4][KMAX]>(pool);
-    int (*mi)[4][KMAX] = reinterpret_cast<int (*)[4][KMAX]>(pool + 64 * 4 * KMAX * 4);
+    float *lv = reinterpret_cast<float *>(pool);                       // [64][4][LK]
+    int *li = reinterpret_cast<int *>(pool + 64 * 4 * LK * 4);
 
     const int tid = threadIdx.x;
     const int w = tid >> 6, lane = tid & 63, l16 = lane & 15, lg = lane >> 4;
@@ -279,81 +289,64 @@ __global__ __launch_bounds__(256) void score_select_mfma_kernel(
     const int64_t bmax = (iq < n) ? cand_bmax(iq, 64, W) : 0;
     const int64_t last = (i0 + 63 < n) ? i0 + 63 : n - 1;
     const int64_t tile_bmax = cand_bmax(last, 64, W);
-    const int nst = (tile_bmax >= 1) ? (int)((tile_bmax + CB - 1) / CB) : 0;   // stages: blocks 1..tile_bmax
-    const bf16_t *Sg = S0 + (b * Hkv + g) * nb * 4 * D;
     const uint32_t ring_lds = lds_offset(ring);
 
-    // this wave's DMA parts of stage st into ring slot st % NSS (rows past
-    // tile_bmax read block tile_bmax: never scored)
-    auto fill = [&](int st) {
-        const uint32_t slot = ring_lds + (uint32_t)((st % NSS) * SROWS * D * 2);
+    // Stream rows [first, first + count) of a [*, 4, D] summary array through
+    // the ring; visit(row index, slot-max score) per lane for each.
+    auto scan = [&](const bf16_t *Src, int64_t first, int64_t count, auto &&visit) {
+        const int nst = (count > 0) ? (int)((count + CB - 1) / CB) : 0;
+        const int64_t lastr = first + count - 1;
+        auto fill = [&](int st) {
+            const uint32_t slot = ring_lds + (uint32_t)((st % NSS) * SROWS * D * 2);
 #pragma unroll
-        for (int pp = 0; pp < PPW; ++pp) {
-            const int part = w * PPW + pp;
-            const int p = part * 64 + lane;              // physical chunk index in the stage
-            const int r = p / CPR, c = (p % CPR) ^ sw<D>(r & 15);
-            int64_t blk = 1 + (int64_t)st * CB + r / 4;
-            blk = (blk <= tile_bmax) ? blk : tile_bmax;
-            dma16(Sg + (blk * 4 + (r & 3)) * D + 8 * c, slot + (uint32_t)part * 1024u);
-        }
-    };
-    float vals[KMAX];
-    int ids[KMAX];
+            for (int pp = 0; pp < PPW; ++pp) {
+                const int part = w * PPW + pp;
+                const int p = part * 64 + lane;          // physical chunk index in the stage
+                const int r = p / CPR, c = (p % CPR) ^ sw<D>(r & 15);
+                int64_t blk = first + (int64_t)st * CB + r / 4;
+                blk = (blk <= lastr) ? blk : lastr;      // rows past the end: never visited
+                dma16(Src + (blk * 4 + (r & 3)) * D + 8 * c, slot + (uint32_t)part * 1024u);
+            }
+        };
+        for (int st = 0; st < NSS - 1 && st < nst; ++st) fill(st);
+        for (int st = 0; st < nst; ++st) {
+            const int ahead = (nst - 1 - st < NSS - 2) ? nst - 1 - st : NSS - 2;
+            wait_vm_n(ahead * PPW);
+            __syncthreads();   // stage st landed everywhere; stage st-1 is consumed
+            if (st + NSS - 1 < nst) fill(st + NSS - 1);
+            const bf16_t *Ss = ring + (st % NSS) * SROWS * D;
+            const int64_t b0 = first + (int64_t)st * CB;
 #pragma unroll
-    for (int j = 0; j < KMAX; ++j) {
-        vals[j] = -INFINITY;
-        ids[j] = -1;
-    }
-    for (int st = 0; st < NSS - 1 && st < nst; ++st) fill(st);
-    for (int st = 0; st < nst; ++st) {
-        const int ahead = (nst - 1 - st < NSS - 2) ? nst - 1 - st : NSS - 2;
-        wait_vm_n(ahead * PPW);
-        __syncthreads();   // stage st landed everywhere; stage st-1 is consumed
-        if (st + NSS - 1 < nst) fill(st + NSS - 1);
-        const bf16_t *Ss = ring + (st % NSS) * SROWS * D;
-        const int64_t b0 = 1 + (int64_t)st * CB;
+            for (int mt = 0; mt < 4; ++mt) {
+                const int r = mt * 16 + l16;
+                const bf16_t *ar = Ss + r * D;
+                f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-            const int r = mt * 16 + l16;
-            const bf16_t *ar = Ss + r * D;
-            f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int ks = 0; ks < NKS; ++ks)
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ldb8(ar + 8 * ((4 * ks + lg) ^ sw<D>(r & 15))), qb[ks],
-                                                             acc, 0, 0, 0);
-            const int64_t blk = b0 + 4 * mt + lg;
-            float best = acc[0];
-            best = (acc[1] > best) ? acc[1] : best;
-            best = (acc[2] > best) ? acc[2] : best;
-            best = (acc[3] > best) ? acc[3] : best;
-            const float v = best * scale;
-            if (blk <= bmax && blk <= tile_bmax) {
-                if (scores) scores[((b * Hkv + g) * n + iq) * nb + blk] = v;
-                insert_inorder<KMAX>(vals, ids, v, (int)blk);
+                for (int ks = 0; ks < NKS; ++ks)
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ldb8(ar + 8 * ((4 * ks + lg) ^ sw<D>(r & 15))),
+                                                                 qb[ks], acc, 0, 0, 0);
+                const int64_t blk = b0 + 4 * mt + lg;
+                float best = acc[0];
+                best = (acc[1] > best) ? acc[1] : best;
+                best = (acc[2] > best) ? acc[2] : best;
+                best = (acc[3] > best) ? acc[3] : best;
+                if (blk <= lastr) visit((int)blk, best * scale);
             }
         }
-    }
-    // merge the four lane groups of each query (the lists reuse the ring)
-    __syncthreads();
-#pragma unroll
-    for (int j = 0; j < KMAX; ++j) {
-        mv[qcol][lg][j] = vals[j];
-        mi[qcol][lg][j] = ids[j];
-    }
-    __syncthreads();
-    if (tid < 64 && i0 + tid < n) {
-        const int64_t i = i0 + tid;
+        __syncthreads();   // the ring is free again
+    };
+    // the four lane lists of query t (LDS, length LEN) merged under (score
+    // desc, id asc): calls take(j, v, id) for the best `want`
+    auto merge4 = [&](int t, int LEN, int want, auto &&take) {
         int hp[4] = {0, 0, 0, 0};
-        const int64_t o = ((b * Hkv + g) * n + i) * kk;
-        int c = 0;
-        for (int j = 0; j < kk; ++j) {
+        for (int j = 0; j < want; ++j) {
             int bestl = -1;
             float bv = -INFINITY;
             int bi = 0x7fffffff;
             for (int l = 0; l < 4; ++l) {
-                if (hp[l] >= KMAX) continue;
-                const float v = mv[tid][l][hp[l]];
-                const int id = mi[tid][l][hp[l]];
+                if (hp[l] >= LEN) continue;
+                const float v = lv[(t * 4 + l) * LK + hp[l]];
+                const int id = li[(t * 4 + l) * LK + hp[l]];
                 if (id < 0) continue;
                 if (bestl < 0 || better(v, id, bv, bi)) {
                     bestl = l;
@@ -361,15 +354,85 @@ __global__ __launch_bounds__(256) void score_select_mfma_kernel(
                     bi = id;
                 }
             }
-            if (bestl < 0) {
-                idx[o + j] = -1;
-                val[o + j] = -INFINITY;
-            } else {
-                idx[o + j] = bi;
-                val[o + j] = bv;
-                ++hp[bestl];
-                ++c;
+            if (bestl < 0) break;
+            ++hp[bestl];
+            take(j, bv, bi);
+        }
+    };
+
+    const int nw = HIER ? (int)(((nb + F - 1) / F + 31) / 32) : 0;
+    int kout = kk;
+    if constexpr (HIER) {
+        // ---- level 1: supers holding at least one candidate child
+        const int64_t ns = (nb + F - 1) / F;
+        const int beff = (int)((beam < ns) ? beam : ns);
+        kout = (kk < beff * F) ? kk : beff * F;
+        const int64_t nsup = (tile_bmax >= 1) ? tile_bmax / F + 1 : 0;   // supers any query of the tile may keep
+        float pv[BEAMMAX];
+        int pid[BEAMMAX];
+#pragma unroll
+        for (int j = 0; j < BEAMMAX; ++j) {
+            pv[j] = -INFINITY;
+            pid[j] = -1;
+        }
+        const bf16_t *S1g = S1 + (b * Hkv + g) * ns * 4 * D;
+        scan(S1g, 0, nsup, [&](int p, float v) {
+            const int64_t lo = (int64_t)p * F;
+            const int64_t hi = (lo + F - 1 < nb - 1) ? lo + F - 1 : nb - 1;
+            if (bmax >= 1 && lo <= bmax && hi >= 1) {
+                if (sup_scores) sup_scores[((b * Hkv + g) * n + iq) * ns + p] = v;
+                insert_inorder<BEAMMAX>(pv, pid, v, p);
             }
+        });
+#pragma unroll
+        for (int j = 0; j < BEAMMAX; ++j) {
+            lv[(qcol * 4 + lg) * LK + j] = pv[j];
+            li[(qcol * 4 + lg) * LK + j] = pid[j];
+        }
+        for (int e = tid; e < 64 * nw; e += 256) pmask[e] = 0u;
+        __syncthreads();
+        if (tid < 64)
+            merge4(tid, BEAMMAX, beff, [&](int, float, int p) { pmask[tid * nw + (p >> 5)] |= 1u << (p & 31); });
+        __syncthreads();
+    }
+    // ---- blocks (children of the kept supers, for HIER)
+    float vals[KMAX];
+    int ids[KMAX];
+#pragma unroll
+    for (int j = 0; j < KMAX; ++j) {
+        vals[j] = -INFINITY;
+        ids[j] = -1;
+    }
+    const bf16_t *Sg = S0 + (b * Hkv + g) * nb * 4 * D;
+    scan(Sg, 1, tile_bmax, [&](int blk, float v) {
+        bool ok = blk <= bmax;
+        if constexpr (HIER) {
+            const int p = blk / F;
+            ok = ok && ((pmask[qcol * nw + (p >> 5)] >> (p & 31)) & 1u);
+        }
+        if (ok) {
+            if (scores) scores[((b * Hkv + g) * n + iq) * nb + blk] = v;
+            insert_inorder<KMAX>(vals, ids, v, blk);
+        }
+    });
+#pragma unroll
+    for (int j = 0; j < KMAX; ++j) {
+        lv[(qcol * 4 + lg) * LK + j] = vals[j];
+        li[(qcol * 4 + lg) * LK + j] = ids[j];
+    }
+    __syncthreads();
+    if (tid < 64 && i0 + tid < n) {
+        const int64_t i = i0 + tid;
+        const int64_t o = ((b * Hkv + g) * n + i) * kk;
+        int c = 0;
+        merge4(tid, KMAX, kout, [&](int j, float v, int id) {
+            idx[o + j] = id;
+            val[o + j] = v;
+            c = j + 1;
+        });
+        for (int j = c; j < kk; ++j) {
+            idx[o + j] = -1;
+            val[o + j] = -INFINITY;
         }
         cnt[(b * Hkv + g) * n + i] = c;
     }
@@ -483,9 +546,9 @@ void launch_flat(const void *q, const int64_t *qs, const float *qgain, float eps
                  int32_t *idx, float *val, int32_t *cnt, float *scores, hipStream_t s) {
     dim3 grid((unsigned)((n + SEL_WG - 1) / SEL_WG), (unsigned)Hkv, (unsigned)B);
     if constexpr (DT == 1 && M == 4 && KMAX <= 32) {
-        hipLaunchKernelGGL((score_select_mfma_kernel<D, KMAX>), grid, dim3(256), 0, s, (const bf16_t *)q,
+        hipLaunchKernelGGL((score_select_mfma_kernel<D, KMAX, false>), grid, dim3(256), 0, s, (const bf16_t *)q,
                            qs[0], qs[1], qs[2], qgain, eps, (const bf16_t *)S0, n, (int)Hq, (int)Hkv,
-                           n / 64, W, (int)k, scale, idx, val, cnt, scores);
+                           n / 64, W, (int)k, scale, idx, val, cnt, scores, nullptr, 1, 1, nullptr);
     } else {
         hipLaunchKernelGGL((score_select_kernel<DT, D, M, KMAX>), grid, dim3(SEL_WG), 0, s,
                            (const typename St<DT>::T *)q, qs[0], qs[1], qs[2], qgain, eps,
@@ -498,7 +561,19 @@ template <int DT, int D, int M, int KMAX>
 void launch_hier(const void *q, const int64_t *qs, const float *qgain, float eps, const void *S0,
                  const void *S1, int64_t B, int64_t n, int64_t Hq, int64_t Hkv, int64_t W, int64_t k,
                  int64_t F, int64_t beam, float scale, int32_t *idx, float *val, int32_t *cnt,
-                 hipStream_t s) {
+                 float *scores, float *sup_scores, hipStream_t s) {
+    const int64_t ns = (n / 64 + F - 1) / F;
+    if constexpr (DT == 1 && M == 4 && KMAX <= 32) {
+        if (ns <= 32 * SEL_PMW) {
+            dim3 grid((unsigned)((n + 63) / 64), (unsigned)Hkv, (unsigned)B);
+            const size_t pm = (size_t)64 * ((ns + 31) / 32) * sizeof(uint32_t);
+            hipLaunchKernelGGL((score_select_mfma_kernel<D, KMAX, true>), grid, dim3(256), pm, s, (const bf16_t *)q,
+                               qs[0], qs[1], qs[2], qgain, eps, (const bf16_t *)S0, n, (int)Hq, (int)Hkv, n / 64,
+                               W, (int)k, scale, idx, val, cnt, scores, (const bf16_t *)S1, (int)F, (int)beam,
+                               sup_scores);
+            return;
+        }
+    }
     dim3 grid((unsigned)((n + SEL_WG - 1) / SEL_WG), (unsigned)Hkv, (unsigned)B);
     hipLaunchKernelGGL((hier_select_kernel<DT, D, M, KMAX>), grid, dim3(SEL_WG), 0, s,
                        (const typename St<DT>::T *)q, qs[0], qs[1], qs[2], qgain, eps,
@@ -544,7 +619,8 @@ extern "C" int hba_hier_select(int dtype, const void *q, const int64_t q_strides
                                const float *q_gain, float eps, const void *S0, const void *S1,
                                int64_t B, int64_t n, int64_t Hq, int64_t Hkv, int64_t d, int64_t m,
                                int64_t Bk, int64_t W, int64_t k, int64_t fanout, int64_t beam,
-                               float scale, int32_t *idx, float *val, int32_t *cnt, void *stream) {
+                               float scale, int32_t *idx, float *val, int32_t *cnt, float *scores,
+                               float *sup_scores, void *stream) {
     int st = select_checks(dtype, q, q_strides, S0, B, n, Hq, Hkv, d, m, Bk, W, k, idx, val, cnt);
     if (st) return st;
     if (!S1 || fanout < 1 || beam < 1) return HBA_ERR_INVALID_ARG;
@@ -552,7 +628,7 @@ extern "C" int hba_hier_select(int dtype, const void *q, const int64_t q_strides
     hipStream_t s = (hipStream_t)stream;
 #define HBA_HIER(DT, D)                                                                            \
     HBA_SEL_DISPATCH_M(launch_hier, DT, D, q, q_strides, q_gain, eps, S0, S1, B, n, Hq, Hkv, W, k,   \
-                       fanout, beam, scale, idx, val, cnt, s)
+                       fanout, beam, scale, idx, val, cnt, scores, sup_scores, s)
     HBA_DISPATCH_DT_D(dtype, d, HBA_HIER);
 #undef HBA_HIER
     HBA_LAUNCH_CHECK();

@@ -198,6 +198,22 @@ def _(q, q_gain, eps, S0, window, k, scale):
 @torch.library.custom_op("hba::hier_select", mutates_args=(), device_types="cuda")
 def hier_select(q: Tensor, q_gain: Optional[Tensor], eps: float, S0: Tensor, S1: Tensor, window: int,
                 k: int, fanout: int, beam: int, scale: float) -> Tuple[Tensor, Tensor, Tensor]:
+    return _hier_select(q, q_gain, eps, S0, S1, window, k, fanout, beam, scale, None, None)
+
+
+def hier_select_with_scores(q, q_gain, eps, S0, S1, window, k, fanout, beam, scale):
+    """hier_select that also returns the fp32 scores it ranked: children of the
+    kept supers [B, Hkv, n, nb] and candidate-bearing supers [B, Hkv, n, ns]
+    (-inf elsewhere; the super array is filled by the bf16 GEMM path only).
+    The verification form, not a torch op."""
+    B, n = q.shape[0], q.shape[1]
+    Hkv, nb, ns = S0.shape[1], S0.shape[2], S1.shape[2]
+    scores = torch.full((B, Hkv, n, nb), float("-inf"), dtype=torch.float32, device=q.device)
+    sup = torch.full((B, Hkv, n, ns), float("-inf"), dtype=torch.float32, device=q.device)
+    return (*_hier_select(q, q_gain, eps, S0, S1, window, k, fanout, beam, scale, scores, sup), scores, sup)
+
+
+def _hier_select(q, q_gain, eps, S0, S1, window, k, fanout, beam, scale, scores, sup_scores):
     dev = _dev(q)
     _rows(q, "q")
     B, n, Hq, d = q.shape
@@ -211,7 +227,7 @@ def hier_select(q: Tensor, q_gain: Optional[Tensor], eps: float, S0: Tensor, S1:
     with torch.cuda.device(dev):
         st = lib().hba_hier_select(_code(q), _p(q), strides3(q), _p(qg), eps, _p(S0), _p(S1), B, n, Hq,
                                    Hkv, d, m, BLOCK, window, k, fanout, beam, scale, _p(idx), _p(val),
-                                   _p(cnt), _stream(dev))
+                                   _p(cnt), _p(scores), _p(sup_scores), _stream(dev))
     check(st, "hba_hier_select")
     return idx, val, cnt
 

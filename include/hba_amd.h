@@ -119,14 +119,20 @@ int hba_score_select(int dtype, const void *q, const int64_t q_strides[3],
  * min(beam, ns) supers that hold a candidate, score their children, keep the
  * top min(k, beam*fanout).  Same outputs and tie rule as hba_score_select.
  *   replaces: hier_select  src/hba/attention.py:217-246 (eval :690-693)
- * 1 <= beam <= 16, fanout <= 64.
+ * 1 <= beam <= 16, fanout <= 64.  fp32 inputs follow the oracle bit-exactly;
+ * bf16 inputs with m == 4, k <= 32 and at most 2048 supers are scored as bf16
+ * MFMA GEMMs.  Optional dumps (NULL to skip), entries written only where the
+ * kernel ranked a score: sup_scores fp32 [B, Hkv, n, ns] with the score of
+ * every super holding a candidate child, scores fp32 [B, Hkv, n, n/Bk] with
+ * the score of every candidate child of a kept super.  sup_scores is written
+ * by the MFMA path only.
  */
 int hba_hier_select(int dtype, const void *q, const int64_t q_strides[3],
                     const float *q_gain, float eps, const void *S0, const void *S1,
                     int64_t B, int64_t n, int64_t Hq, int64_t Hkv, int64_t d,
                     int64_t m, int64_t Bk, int64_t W, int64_t k, int64_t fanout,
                     int64_t beam, float scale, int32_t *idx, float *val, int32_t *cnt,
-                    void *stream);
+                    float *scores, float *sup_scores, void *stream);
 
 /*
  * Union attention forward: one softmax per (query, head) over the NoPE sinks

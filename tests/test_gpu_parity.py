@@ -206,26 +206,118 @@ HIER_CASES = [
     dict(dt="bf16", n=4096, W=1024, k=16, fanout=16, beam=2),
     dict(dt="bf16", n=8192, W=1024, k=16, fanout=16, beam=8, needles=True),
     dict(dt="f32", n=2048, W=256, k=16, fanout=8, beam=16, d=128, Hq=28, Hkv=4),
+    dict(dt="bf16", n=2048, W=256, k=32, fanout=8, beam=16, d=128, Hq=28, Hkv=4, B=2),   # beam > supers
+    dict(dt="bf16", n=4096, W=512, k=8, fanout=4, beam=3, m=2),                          # scalar bf16 path
+    dict(dt="bf16", n=6144, W=700, k=12, fanout=5, beam=4),                              # ragged last super
+    dict(dt="bf16", n=1024, W=1024, k=16, fanout=16, beam=2),                            # no candidates
 ]
 
 
+def hier_uses_mfma(dt, m, k, nb, F):
+    return uses_mfma(dt, m, k) and (nb + F - 1) // F <= 2048
+
+
+def check_hier_dumps(qg, S0, S1, F, beam, kk, scale, W, ki, kv, kc_, sc, sup):
+    """The bf16 GEMM path of hier_select for one KV head, through the scores
+    it ranked: the super set and the child set it scored are exactly the
+    oracle's rules, both score arrays agree with the declared-order fp32
+    scores to GEMM rounding, and the picks are the oracle's top-k of the
+    kernel's own scores (bit-exact)."""
+    n, nb = sc.shape
+    ns = sup.shape[1]
+    beff = min(beam, ns)
+    kout = min(kk, beff * F)
+    bmax = np.array([O.cand_bmax(i, 64, W) for i in range(n)])
+    lo = np.arange(ns) * F
+    hi = np.minimum(lo + F - 1, nb - 1)
+    valid = (bmax[:, None] >= 1) & (lo[None, :] <= bmax[:, None]) & (hi[None, :] >= 1)
+    assert np.array_equal(np.isfinite(sup), valid)
+    if valid.any():
+        # supers: float64 scores, max over slots
+        ex = (qg.astype(np.float64) @ S1.reshape(-1, S1.shape[-1]).T.astype(np.float64))
+        ex = ex.reshape(n, ns, -1).max(-1) * scale
+        assert np.abs(sup[valid] - ex[valid]).max() <= 2e-6 * max(1.0, np.abs(ex[valid]).max())
+    pi, pv, pc = O.topk(sup, beff)
+    kept = np.zeros((n, nb), dtype=bool)
+    for r in range(n):
+        for p in pi[r, : pc[r]]:
+            kept[r, p * F: min(nb, p * F + F)] = True
+    blk = np.arange(nb)
+    cand = (blk[None, :] >= 1) & (blk[None, :] <= bmax[:, None])
+    assert np.array_equal(np.isfinite(sc), kept & cand)
+    osc = O.block_scores(qg, S0, np.arange(n), scale, 64, W)
+    fin = np.isfinite(sc)
+    if fin.any():
+        assert np.abs(sc[fin] - osc[fin]).max() <= 2e-6 * max(1.0, np.abs(osc[fin]).max())
+    ti, tv, tc = O.topk(sc, kout)
+    pad = kk - kout
+    ti = np.concatenate([ti, np.full((n, pad), -1, np.int32)], 1)
+    tv = np.concatenate([tv, np.full((n, pad), -np.inf, np.float32)], 1)
+    assert np.array_equal(ti, ki) and np.array_equal(tv, kv) and np.array_equal(tc, kc_)
+
+
 @pytest.mark.parametrize("case", HIER_CASES, ids=lambda c: "-".join(f"{k}{v}" for k, v in c.items()))
-def test_hier_select_bit_exact(dev, case):
+def test_hier_select(dev, case):
+    """fp32, and bf16 off the GEMM path: bit-exact against the oracle's
+    hier_select.  bf16 on the GEMM path (m == 4, k <= 32): the dump check
+    above on the kernel's own super and child scores."""
     c = dict(case)
     dt = c.pop("dt")
     cfg, x, prm, cos, sin = make(dev, dt, **c)
     r = hba_amd.forward_stages(x["q"], x["k"], x["v"], cos, sin, cfg, prm, prm, hier=True)
     torch.cuda.synchronize()
-    n = x["q"].shape[1]
-    P = oracle_prep(cfg, x, cos, sin, dt, 0, f(r["S0"])[0])
-    S1 = f(r["S1"])[0]
-    for g in range(S1.shape[0]):
-        assert np.array_equal(S1[g], O.build_super(P.S0[g], cfg.fanout, dt))
-    idx, val, cnt = O.hier_select(P.qg, P.S0, S1, cfg.fanout, cfg.beam, min(cfg.k_blocks, n // 64),
-                                  r["sel_scale"], 64, cfg.window)
-    assert np.array_equal(r["cnt"][0].cpu().numpy(), cnt)
-    assert np.array_equal(r["idx"][0].cpu().numpy(), idx)
-    assert np.array_equal(r["val"][0].cpu().numpy(), val)
+    B, n = x["q"].shape[:2]
+    kk = min(cfg.k_blocks, n // 64)
+    mfma = hier_uses_mfma(dt, cfg.slots, kk, n // 64, cfg.fanout)
+    if mfma:
+        idx, val, cnt, scores, sup = ops.hier_select_with_scores(
+            x["q"], prm.q.gain, 1e-6, r["S0"], r["S1"], cfg.window, kk, cfg.fanout, cfg.beam, r["sel_scale"])
+        torch.cuda.synchronize()
+        for t, u in ((idx, r["idx"]), (val, r["val"]), (cnt, r["cnt"])):
+            assert torch.equal(t, u)   # the dumps do not change the picks
+        sc, sp = scores.cpu().numpy(), sup.cpu().numpy()
+    for b in range(B):
+        P = oracle_prep(cfg, x, cos, sin, dt, b, f(r["S0"])[b])
+        S1 = f(r["S1"])[b]
+        for g in range(S1.shape[0]):
+            assert np.array_equal(S1[g], O.build_super(P.S0[g], cfg.fanout, dt))
+        ki, kv, kc_ = (r[t][b].cpu().numpy() for t in ("idx", "val", "cnt"))
+        if not mfma:
+            idx, val, cnt = O.hier_select(P.qg, P.S0, S1, cfg.fanout, cfg.beam, kk, r["sel_scale"], 64,
+                                          cfg.window)
+            assert np.array_equal(kc_, cnt) and np.array_equal(ki, idx) and np.array_equal(kv, val)
+            continue
+        for g in range(S1.shape[0]):
+            check_hier_dumps(P.qg[g], P.S0[g], S1[g], cfg.fanout, cfg.beam, kk, r["sel_scale"], cfg.window,
+                             ki[g], kv[g], kc_[g], sc[b, g], sp[b, g])
+
+
+@pytest.mark.parametrize("pattern", ["ties", "lane0"])
+def test_hier_select_adversarial(dev, pattern):
+    """bf16 GEMM path of hier_select on tied and lane-aligned block layouts:
+    equal super scores must resolve to the lowest super, equal child scores
+    to the lowest block."""
+    torch.manual_seed(5)
+    n, Hkv, Hq, d, m, W, kk, F, beam = 8192, 2, 14, 64, 4, 512, 16, 8, 4
+    nb = n // 64
+    q = torch.randn(1, n, Hq, d, device=dev).to(torch.bfloat16)
+    gq = torch.full((Hq,), d ** 0.25, device=dev)
+    v = torch.randn(d)
+    if pattern == "lane0":
+        a = torch.ones(nb)
+        a[1::4] = 4.0 + torch.arange(a[1::4].numel()) / 64.0
+    else:
+        a = (torch.arange(nb) % 3).float() + 1.0
+    S0 = (a[:, None, None] * v[None, None, :]).expand(nb, m, d).contiguous()
+    S0 = S0[None, None].expand(1, Hkv, nb, m, d).contiguous().to(torch.bfloat16).to(dev)
+    S1 = ops.build_super(S0, F)
+    idx, val, cnt, scores, sup = ops.hier_select_with_scores(q, gq, 1e-6, S0, S1, W, kk, F, beam, 0.125)
+    torch.cuda.synchronize()
+    qg = O.grouped_query(O.qknorm(f(q)[0], f(gq), 1e-6, "bf16"), Hkv, "bf16")
+    for g in range(Hkv):
+        check_hier_dumps(qg[g], f(S0)[0, g], f(S1)[0, g], F, beam, kk, 0.125, W, idx[0, g].cpu().numpy(),
+                         val[0, g].cpu().numpy(), cnt[0, g].cpu().numpy(), scores[0, g].cpu().numpy(),
+                         sup[0, g].cpu().numpy())
 
 
 # ------------------------------------------------------------- attention -----
