@@ -192,28 +192,6 @@ struct RtCfg {
     static_assert(DPW * WAVES == 2 * KPARTS, "parts split evenly over the waves");
 };
 
-// The wave's share of one block into ring slot `slot`: the block's K tile
-// (kc rows blk*64..+63) and V^T tile (vt columns blk*64..+63), swizzled.
-template <int D>
-__device__ __forceinline__ void ring_fill(const bf16_t *KC, const bf16_t *VT, int64_t n, int blk,
-                                          uint32_t slot_lds, int w, int lane) {
-    using C = RtCfg<D>;
-    constexpr int CPR = D / 8;                          // 16-byte chunks per K row
-#pragma unroll
-    for (int pp = 0; pp < C::DPW; ++pp) {
-        const int part = w + C::WAVES * pp;
-        const int p = (part % C::KPARTS) * 64 + lane;   // physical chunk index in its tile
-        if (part < C::KPARTS) {
-            const int r = p / CPR, c = (p % CPR) ^ swzK(p / CPR);
-            dma16(KC + ((int64_t)blk * 64 + r) * D + 8 * c, slot_lds + (uint32_t)part * 1024u);
-        } else {
-            const int r = p >> 3, c = (p & 7) ^ swzV(p >> 3);
-            dma16(VT + (int64_t)r * n + (int64_t)blk * 64 + 8 * c, slot_lds + (uint32_t)part * 1024u);
-        }
-    }
-}
-
-
 // ======================================================= window kernel ====
 template <int D, int RT>
 struct WinCfg {
@@ -625,25 +603,73 @@ __device__ __forceinline__ void routed_body(
     uint32_t *qbits = reinterpret_cast<uint32_t *>(list + ((nb + 1) & ~1LL));   // per query, over entries
     uint32_t *wbits = qbits + QT * nbw;                      // per row tile: OR of its queries' qbits
 
+    // A ring slot holds a block's K tile (kc rows blk*64..+63) and V^T tile
+    // (vt columns blk*64..+63) in 1 KB parts, swizzled; part w + WAVES*pp is
+    // this wave's.  Each lane's source at block 0 and the wave-uniform stride
+    // per block are set once, so a fill is one address add per part.
+    const bf16_t *dsrc[C::DPW];
+    int64_t dstr[C::DPW];
+#pragma unroll
+    for (int pp = 0; pp < C::DPW; ++pp) {
+        const int part = w + C::WAVES * pp;
+        const int pc = (part % C::KPARTS) * 64 + lane;
+        if (part < C::KPARTS) {
+            const int r = pc / (D / 8), c = (pc % (D / 8)) ^ swzK(pc / (D / 8));
+            dsrc[pp] = KC + r * D + 8 * c;
+            dstr[pp] = 64 * D;
+        } else {
+            const int r = pc >> 3, c = (pc & 7) ^ swzV(pc >> 3);
+            dsrc[pp] = VT + (int64_t)r * n + 8 * c;
+            dstr[pp] = 64;
+        }
+    }
+    auto fill = [&](int blk, int slot) {
+#pragma unroll
+        for (int pp = 0; pp < C::DPW; ++pp)
+            dma16(dsrc[pp] + (int64_t)blk * dstr[pp],
+                  ring_lds + (uint32_t)(slot * C::SLOT * 2) + (uint32_t)(w + C::WAVES * pp) * 1024u);
+    };
+    // sinks: block 0 into the last ring slot (free until the first refill),
+    // landing during the set-up
+    if (S > 0) fill(0, C::NS - 1);
+
+    // ----------------------------------------------------- per-row state --
+    // (first, so that the query loads overlap the selection set-up)
+    const int qs = l16 / G;
+    const int hh = l16 % G;
+    const bool colv = l16 < QPT * G;
+    bf16x8 qop[PTW][C::NKS];
+    f32x4 O[PTW][C::NDT];
+    float mrun[PTW], lsum[PTW];
+    int64_t icol[PTW];
+    bool cok[PTW];
+#pragma unroll
+    for (int t = 0; t < PTW; ++t) {
+        icol[t] = i0 + (int64_t)(w * PTW + t) * QPT + qs;
+        cok[t] = colv && icol[t] < n;
+        mrun[t] = -INFINITY;
+        lsum[t] = 0.0f;
+#pragma unroll
+        for (int dt = 0; dt < C::NDT; ++dt) O[t][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        qoperand<D>(q, qsb, qsn, qsh, qgain, eps, nullptr, nullptr, b, icol[t], g * G + hh, cok[t], false, lg,
+                    FIXED ? sl2 : 1.0f, qop[t]);
+    }
+
     // ------------------------------------- selection lists and their union
     for (int e = tid; e < nbw; e += C::NTHR) bitmap[e] = 0u;
     for (int e = tid; e < (QT + C::WAVES * PTW) * nbw; e += C::NTHR) qbits[e] = 0u;
     __syncthreads();
-    for (int qq = tid; qq < QT; qq += C::NTHR) {
-        int16_t *sl = sel + qq * kk;
+    // one thread per (query, pick); invalid picks become SENT in place
+    for (int t = tid; t < QT * kk; t += C::NTHR) {
+        const int qq = t / kk, r = t - qq * kk;
         const int64_t i = i0 + qq;
-        int m2 = 0;
-        if (i < n) {
-            const int c = min(max(cnt[bh * n + i], 0), kk);
-            const int32_t *ix = idx + (bh * n + i) * kk;
-            for (int r = 0; r < c; ++r) {
-                const int v = ix[r];
-                if (v < 1 || v >= nb) continue;          // block 0 is never routed
-                sl[m2++] = (int16_t)v;
-                atomicOr(&bitmap[v >> 5], 1u << (v & 31));
-            }
+        int v = SENT;
+        if (i < n && r < min(max(cnt[bh * n + i], 0), kk)) {
+            v = idx[(bh * n + i) * kk + r];
+            if (v < 1 || v >= nb) v = SENT;                // block 0 is never routed
+            else atomicOr(&bitmap[v >> 5], 1u << (v & 31));
         }
-        for (int r = m2; r < kk; ++r) sl[r] = SENT;
+        sel[t] = (int16_t)v;
     }
     __syncthreads();
     if (w == 0) {
@@ -669,42 +695,19 @@ __device__ __forceinline__ void routed_body(
         if (lane == 0) nlist = base;
     }
     __syncthreads();
-    // each query's picks as union entry indices: its own bits, and its row tile's
-    for (int qq = tid; qq < QT; qq += C::NTHR) {
-        const int16_t *sl = sel + qq * kk;
-        uint32_t *qb = qbits + qq * nbw;
-        uint32_t *wb = wbits + (qq / QPT) * nbw;              // row tile qq / QPT = w * PTW + tt
-        for (int r = 0; r < kk; ++r) {
-            const int v = sl[r];
-            if (v == SENT) break;
-            const int e = pre[v >> 5] + __popc(bitmap[v >> 5] & ((1u << (v & 31)) - 1u));
-            qb[e >> 5] |= 1u << (e & 31);
-            atomicOr(&wb[e >> 5], 1u << (e & 31));
-        }
+    const int ne = nlist;
+    auto entry_of = [&](int v) { return pre[v >> 5] + __popc(bitmap[v >> 5] & ((1u << (v & 31)) - 1u)); };
+    // each pick as a union entry index: its query's bits, and its row tile's
+    for (int t = tid; t < QT * kk; t += C::NTHR) {
+        const int v = sel[t];
+        if (v == SENT) continue;
+        const int qq = t / kk;
+        const int e = entry_of(v);
+        atomicOr(&qbits[qq * nbw + (e >> 5)], 1u << (e & 31));
+        atomicOr(&wbits[(qq / QPT) * nbw + (e >> 5)], 1u << (e & 31));   // row tile qq / QPT
     }
 
-    // ----------------------------------------------------- per-row state --
-    const int qs = l16 / G;
-    const int hh = l16 % G;
-    const bool colv = l16 < QPT * G;
-    bf16x8 qop[PTW][C::NKS];
-    f32x4 O[PTW][C::NDT];
-    float mrun[PTW], lsum[PTW];
-    int64_t icol[PTW];
-    bool cok[PTW];
-#pragma unroll
-    for (int t = 0; t < PTW; ++t) {
-        icol[t] = i0 + (int64_t)(w * PTW + t) * QPT + qs;
-        cok[t] = colv && icol[t] < n;
-        mrun[t] = -INFINITY;
-        lsum[t] = 0.0f;
-#pragma unroll
-        for (int dt = 0; dt < C::NDT; ++dt) O[t][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-        qoperand<D>(q, qsb, qsn, qsh, qgain, eps, nullptr, nullptr, b, icol[t], g * G + hh, cok[t], false, lg,
-                    FIXED ? sl2 : 1.0f, qop[t]);
-    }
     __syncthreads();
-    const int ne = nlist;
 
     // The ring holds NPH phases of PH blocks, with one barrier per phase: a
     // block's hits fall on few of the 16 waves, and a phase of several blocks
@@ -712,10 +715,7 @@ __device__ __forceinline__ void routed_body(
     constexpr int P = C::PH, NPH = C::NS / C::PH;
     static_assert(32 % P == 0, "a phase's entries lie in one bitmap word");
     const int npro = min(ne, (NPH - 1) * P);
-    // sinks: block 0 into the last slot (free until the first refill), ahead of the prologue
-    if (S > 0) ring_fill<D>(KC, VT, n, 0, ring_lds + (uint32_t)((C::NS - 1) * C::SLOT * 2), w, lane);
-    for (int e = 0; e < npro; ++e)
-        ring_fill<D>(KC, VT, n, list[e], ring_lds + (uint32_t)(e * C::SLOT * 2), w, lane);
+    for (int e = 0; e < npro; ++e) fill(list[e], e);
     if (S > 0) {
         wait_vm_n(npro * C::DPW);
         __syncthreads();   // every share of block 0 landed
@@ -736,8 +736,12 @@ __device__ __forceinline__ void routed_body(
         wait_vm_n(max(0, issued - (e0 + P)) * C::DPW);
         __syncthreads();   // every share of this phase landed; the previous phase (and the sinks) consumed
         const int nf = min(ne, e0 + NPH * P);
-        for (int e = issued; e < nf; ++e)
-            ring_fill<D>(KC, VT, n, list[e], ring_lds + (uint32_t)((e % C::NS) * C::SLOT * 2), w, lane);
+        int nxt[P];   // the refill's block ids, read before the first DMA is issued
+#pragma unroll
+        for (int j = 0; j < P; ++j) nxt[j] = (issued + j < nf) ? list[issued + j] : 0;
+#pragma unroll
+        for (int j = 0; j < P; ++j)
+            if (issued + j < nf) fill(nxt[j], (issued + j) % C::NS);
         const int sh = e0 & 31;
         if (sh == 0) {
 #pragma unroll
