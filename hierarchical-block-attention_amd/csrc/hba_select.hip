@@ -236,6 +236,126 @@ __device__ __forceinline__ int sw(int r) {
 }
 }  // namespace sel
 
+// Lane l's copy of lane l ^ 16 / l ^ 32 (wave64), from v_permlane16_swap /
+// v_permlane32_swap with the same register as both operands: the swap leaves
+// the partner row's value in the first result on odd rows (upper half) and in
+// the second on even rows (lower half).
+__device__ __forceinline__ uint32_t lane_xor16(uint32_t x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+    return (threadIdx.x & 16) ? r[0] : r[1];
+}
+__device__ __forceinline__ uint32_t lane_xor32(uint32_t x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    return (threadIdx.x & 32) ? r[0] : r[1];
+}
+__device__ __forceinline__ float lane_xor(float x, int o) {
+    const uint32_t u = __float_as_uint(x);
+    return __uint_as_float(o == 16 ? lane_xor16(u) : lane_xor32(u));
+}
+__device__ __forceinline__ int lane_xor(int x, int o) {
+    return (int)(o == 16 ? lane_xor16((uint32_t)x) : lane_xor32((uint32_t)x));
+}
+
+// The four sorted lane lists of a query (lanes l16, l16+16, l16+32, l16+48)
+// merged under (score desc, id asc) in registers: each step takes the best
+// head over the four lanes (their ids are disjoint) and its lane pops it.
+// take(j, v, id) runs in all four lanes for each of the best `want`; the
+// count taken is returned.  Empty heads are (-inf, -1).
+template <int K, class Take>
+__device__ __forceinline__ int merge_lanes(float (&v)[K], int (&id)[K], int want, Take &&take) {
+    int c = 0;
+    for (int j = 0; j < want; ++j) {
+        float bv = v[0];
+        int bi = id[0];
+#pragma unroll
+        for (int o = 16; o <= 32; o <<= 1) {
+            const float ov = lane_xor(bv, o);
+            const int oi = lane_xor(bi, o);
+            if (oi >= 0 && (bi < 0 || better(ov, oi, bv, bi))) {
+                bv = ov;
+                bi = oi;
+            }
+        }
+        if (bi < 0) break;   // every list of the query is empty (the same in its four lanes)
+        if (id[0] == bi) {
+#pragma unroll
+            for (int k = 0; k + 1 < K; ++k) {
+                v[k] = v[k + 1];
+                id[k] = id[k + 1];
+            }
+            v[K - 1] = -INFINITY;
+            id[K - 1] = -1;
+        }
+        take(j, bv, bi);
+        c = j + 1;
+    }
+    return c;
+}
+
+// The bf16 routing queries of the 64 queries i0 .. i0+63 (clamped to n-1)
+// of KV head g into qgs[64][ROWQ], in routing_query's operation order.  Four
+// lanes per query, D/4 dims each; q is read once.  A head's QKNorm sum of
+// squares runs as one sequential chain over d, passed from lane to lane of
+// the query; every lane then normalises its dims and adds them to the
+// head-ordered sum.  Needs 256 threads.
+template <int D, int ROWQ>
+__device__ __forceinline__ void routing_queries_tile(const bf16_t *q, int64_t qsb, int64_t qsn, int64_t qsh,
+                                                     const float *qgain, float eps, int64_t b, int64_t i0,
+                                                     int64_t n, int g, int G, bf16_t *qgs, int tid) {
+    constexpr int DP = D / 4, NC = DP / 8;   // dims and 16-byte chunks per lane
+    const int qq = tid >> 2, part = tid & 3, lane = tid & 63;
+    const int64_t i = (i0 + qq < n) ? i0 + qq : n - 1;
+    const bf16_t *base = q + b * qsb + i * qsn + (int64_t)g * G * qsh + part * DP;
+    constexpr int HB = 8;                     // heads whose dims are loaded together
+    float acc[DP];
+    for (int h0 = 0; h0 < G; h0 += HB) {
+        uint4 raw[HB][NC];
+#pragma unroll
+        for (int hb = 0; hb < HB; ++hb)
+            if (h0 + hb < G) {
+#pragma unroll
+                for (int c = 0; c < NC; ++c) raw[hb][c] = reinterpret_cast<const uint4 *>(base + (int64_t)(h0 + hb) * qsh)[c];
+            }
+#pragma unroll
+        for (int hb = 0; hb < HB; ++hb) {
+            const int h = h0 + hb;
+            if (h >= G) break;
+            float x[DP];
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                const uint32_t wd[4] = {raw[hb][c].x, raw[hb][c].y, raw[hb][c].z, raw[hb][c].w};
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    x[8 * c + e] = (e & 1) ? __uint_as_float(wd[e >> 1] & 0xffff0000u) : __uint_as_float(wd[e >> 1] << 16);
+            }
+            if (qgain) {
+                // ss = fma(x_t, x_t, ss) for t = 0 .. D-1: lane `part` continues the chain of lane part-1
+                float ss = 0.0f;
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    const float in = (s == 0) ? 0.0f : __shfl(ss, (lane & ~3) | (s - 1), 64);
+                    if (part == s) {
+                        float t = in;
+#pragma unroll
+                        for (int e = 0; e < DP; ++e) t = fmaf(x[e], x[e], t);
+                        ss = t;
+                    }
+                }
+                ss = __shfl(ss, (lane & ~3) | 3, 64);
+                float ms = ss / (float)D;
+                if (ms < eps) ms = eps;
+                const float r = sqrtf(ms), gn = qgain[g * G + h];
+#pragma unroll
+                for (int e = 0; e < DP; ++e) x[e] = rnd_bf16((x[e] / r) * gn);
+            }
+#pragma unroll
+            for (int e = 0; e < DP; ++e) acc[e] = (h == 0) ? x[e] : acc[e] + x[e];
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < DP; ++e) qgs[qq * ROWQ + part * DP + e] = f2bf(acc[e]);
+}
+
 // HIER: the two-level beam descent (hier_select) on the same machinery.  A
 // scan over the super-summaries S1 keeps, per query, the top-min(beam, ns)
 // supers holding a candidate child (score desc, super asc); the block scan
@@ -256,16 +376,12 @@ __global__ __launch_bounds__(256) void score_select_mfma_kernel(
     constexpr int SROWS = CB * 4;                      // rows per stage
     constexpr int PPW = SROWS * D * 2 / 1024 / 4;      // 1 KB DMA parts per wave per stage
     constexpr int BEAMMAX = 16;
-    constexpr int LK = (HIER && BEAMMAX > KMAX) ? BEAMMAX : KMAX;   // lane list length held in LDS
-    // LDS: the routing queries; the stage ring, reused for the lane lists
+    // LDS: the routing queries; the stage ring
     constexpr int RING_BYTES = NSS * SROWS * D * 2;
-    constexpr int LIST_BYTES = 64 * 4 * LK * 8;
     __shared__ __align__(16) bf16_t qgs[64 * ROWQ];
-    __shared__ __align__(16) char pool[RING_BYTES > LIST_BYTES ? RING_BYTES : LIST_BYTES];
+    __shared__ __align__(16) char pool[RING_BYTES];
     extern __shared__ uint32_t pmask[];                // HIER: [64][ceil(ns / 32)], sized at launch
     bf16_t *ring = reinterpret_cast<bf16_t *>(pool);
-    float *lv = reinterpret_cast<float *>(pool);                       // [64][4][LK]
-    int *li = reinterpret_cast<int *>(pool + 64 * 4 * LK * 4);
 
     const int tid = threadIdx.x;
     const int w = tid >> 6, lane = tid & 63, l16 = lane & 15, lg = lane >> 4;
@@ -273,13 +389,7 @@ __global__ __launch_bounds__(256) void score_select_mfma_kernel(
     const int64_t b = blockIdx.z;
     const int G = Hq / Hkv;
     const int64_t i0 = (int64_t)blockIdx.x * 64;
-    if (tid < 64) {
-        const int64_t i = (i0 + tid < n) ? i0 + tid : n - 1;
-        float qg[D];
-        routing_query<1, D>(q, qsb, qsn, qsh, qgain, eps, b, i, g, G, qg);
-#pragma unroll
-        for (int t = 0; t < D; ++t) qgs[tid * ROWQ + t] = f2bf(qg[t]);
-    }
+    routing_queries_tile<D, ROWQ>(q, qsb, qsn, qsh, qgain, eps, b, i0, n, g, G, qgs, tid);
     __syncthreads();
     const int qcol = 16 * w + l16;
     const int64_t iq = i0 + qcol;
@@ -293,7 +403,7 @@ __global__ __launch_bounds__(256) void score_select_mfma_kernel(
 
     // Stream rows [first, first + count) of a [*, 4, D] summary array through
     // the ring; visit(row index, slot-max score) per lane for each.
-    auto scan = [&](const bf16_t *Src, int64_t first, int64_t count, auto &&visit) {
+    auto scan = [&](const bf16_t *Src, int64_t first, int64_t count, auto &&visit, auto &&refresh) {
         const int nst = (count > 0) ? (int)((count + CB - 1) / CB) : 0;
         const int64_t lastr = first + count - 1;
         auto fill = [&](int st) {
@@ -332,34 +442,17 @@ __global__ __launch_bounds__(256) void score_select_mfma_kernel(
                 best = (acc[3] > best) ? acc[3] : best;
                 if (blk <= lastr) visit((int)blk, best * scale);
             }
+            refresh();
         }
         __syncthreads();   // the ring is free again
     };
-    // the four lane lists of query t (LDS, length LEN) merged under (score
-    // desc, id asc): calls take(j, v, id) for the best `want`
-    auto merge4 = [&](int t, int LEN, int want, auto &&take) {
-        int hp[4] = {0, 0, 0, 0};
-        for (int j = 0; j < want; ++j) {
-            int bestl = -1;
-            float bv = -INFINITY;
-            int bi = 0x7fffffff;
-            for (int l = 0; l < 4; ++l) {
-                if (hp[l] >= LEN) continue;
-                const float v = lv[(t * 4 + l) * LK + hp[l]];
-                const int id = li[(t * 4 + l) * LK + hp[l]];
-                if (id < 0) continue;
-                if (bestl < 0 || better(v, id, bv, bi)) {
-                    bestl = l;
-                    bv = v;
-                    bi = id;
-                }
-            }
-            if (bestl < 0) break;
-            ++hp[bestl];
-            take(j, bv, bi);
-        }
+    // Max over a query's four lanes of their lists' last entries: every
+    // lane of the query holds LEN entries >= it, so the query's final picks
+    // are all >= it and a lower score can be skipped without changing them.
+    auto qfloor = [&](float last) {
+        last = fmaxf(last, lane_xor(last, 16));
+        return fmaxf(last, lane_xor(last, 32));
     };
-
     const int nw = HIER ? (int)(((nb + F - 1) / F + 31) / 32) : 0;
     int kout = kk;
     if constexpr (HIER) {
@@ -376,23 +469,20 @@ __global__ __launch_bounds__(256) void score_select_mfma_kernel(
             pid[j] = -1;
         }
         const bf16_t *S1g = S1 + (b * Hkv + g) * ns * 4 * D;
+        float pfloor = -INFINITY;
         scan(S1g, 0, nsup, [&](int p, float v) {
             const int64_t lo = (int64_t)p * F;
             const int64_t hi = (lo + F - 1 < nb - 1) ? lo + F - 1 : nb - 1;
             if (bmax >= 1 && lo <= bmax && hi >= 1) {
                 if (sup_scores) sup_scores[((b * Hkv + g) * n + iq) * ns + p] = v;
-                insert_inorder<BEAMMAX>(pv, pid, v, p);
+                if (v >= pfloor) insert_inorder<BEAMMAX>(pv, pid, v, p);
             }
-        });
-#pragma unroll
-        for (int j = 0; j < BEAMMAX; ++j) {
-            lv[(qcol * 4 + lg) * LK + j] = pv[j];
-            li[(qcol * 4 + lg) * LK + j] = pid[j];
-        }
+        }, [&]() { pfloor = qfloor(pv[BEAMMAX - 1]); });
         for (int e = tid; e < 64 * nw; e += 256) pmask[e] = 0u;
         __syncthreads();
-        if (tid < 64)
-            merge4(tid, BEAMMAX, beff, [&](int, float, int p) { pmask[tid * nw + (p >> 5)] |= 1u << (p & 31); });
+        merge_lanes<BEAMMAX>(pv, pid, beff, [&](int, float, int p) {
+            if (lg == 0) pmask[qcol * nw + (p >> 5)] |= 1u << (p & 31);
+        });
         __syncthreads();
     }
     // ---- blocks (children of the kept supers, for HIER)
@@ -404,6 +494,7 @@ __global__ __launch_bounds__(256) void score_select_mfma_kernel(
         ids[j] = -1;
     }
     const bf16_t *Sg = S0 + (b * Hkv + g) * nb * 4 * D;
+    float floor_ = -INFINITY;
     scan(Sg, 1, tile_bmax, [&](int blk, float v) {
         bool ok = blk <= bmax;
         if constexpr (HIER) {
@@ -412,29 +503,24 @@ __global__ __launch_bounds__(256) void score_select_mfma_kernel(
         }
         if (ok) {
             if (scores) scores[((b * Hkv + g) * n + iq) * nb + blk] = v;
-            insert_inorder<KMAX>(vals, ids, v, blk);
+            if (v >= floor_) insert_inorder<KMAX>(vals, ids, v, blk);
         }
-    });
-#pragma unroll
-    for (int j = 0; j < KMAX; ++j) {
-        lv[(qcol * 4 + lg) * LK + j] = vals[j];
-        li[(qcol * 4 + lg) * LK + j] = ids[j];
-    }
-    __syncthreads();
-    if (tid < 64 && i0 + tid < n) {
-        const int64_t i = i0 + tid;
-        const int64_t o = ((b * Hkv + g) * n + i) * kk;
-        int c = 0;
-        merge4(tid, KMAX, kout, [&](int j, float v, int id) {
+    }, [&]() { floor_ = qfloor(vals[KMAX - 1]); });
+    // the query's picks, element j stored by lane group j % 4
+    const int64_t o = ((b * Hkv + g) * n + iq) * kk;
+    const bool live = iq < n;
+    const int c = merge_lanes<KMAX>(vals, ids, kout, [&](int j, float v, int id) {
+        if (live && (j & 3) == lg) {
             idx[o + j] = id;
             val[o + j] = v;
-            c = j + 1;
-        });
-        for (int j = c; j < kk; ++j) {
+        }
+    });
+    if (live) {
+        for (int j = c + ((lg - c) & 3); j < kk; j += 4) {
             idx[o + j] = -1;
             val[o + j] = -INFINITY;
         }
-        cnt[(b * Hkv + g) * n + i] = c;
+        if (lg == 0) cnt[(b * Hkv + g) * n + iq] = c;
     }
 }
 
