@@ -10,18 +10,20 @@
 // attn_win_kernel -- the RoPE window.  Workgroup = (batch, KV head, QT
 //   consecutive queries); one wave per (head, 16*RT consecutive queries).  The
 //   MFMA rows of a 16-row tile are 16 consecutive queries of one head, so no
-//   row of a tile is idle.  64-key tiles of kr and vt go through an LDS double
-//   buffer (register prefetch of the next tile), shared by every wave, and
-//   each K / V^T fragment read from LDS feeds the wave's RT row tiles.  Only
-//   tiles on a window's edges are masked.  Output: the window's normalised
-//   rows (bf16, into out) and their LSE (fp32 workspace).
+//   row of a tile is idle.  64-key tiles of kr and vt go through a two-slot
+//   LDS ring by direct-to-LDS DMA (the next tile lands during this one),
+//   shared by every wave, and each K / V^T fragment read from LDS feeds the
+//   wave's RT row tiles.  Only tiles on a window's edges are masked.  Output:
+//   the window's normalised rows (bf16, into out) and their LSE (fp32
+//   workspace).
 // attn_routed_kernel -- sinks and routed blocks.  Workgroup = (batch, KV head,
 //   QT queries); the rows of a 16-row tile are the G heads of 16/G queries
 //   (the rows that share a routed block).  The sorted union of the tile's
 //   selections, preceded by block 0 for the sinks, streams through an LDS
-//   ring by direct-to-LDS DMA several blocks ahead, one barrier per block;
-//   a wave updates a tile only if one of its queries picked the block.  The
-//   partial then merges with the window's (out, LSE) and the row is stored.
+//   ring by direct-to-LDS DMA one phase of PH blocks ahead, one barrier per
+//   phase; a wave updates a tile only if one of its queries picked the
+//   block.  The partial then merges with the window's (out, LSE) and the row
+//   is stored.
 //
 // Scores are S^T = K . Q^T with v_mfma_f32_16x16x32_bf16: key rows of the A
 // operand are permuted (permk) so that the probabilities leave the
