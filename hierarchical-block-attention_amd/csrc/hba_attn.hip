@@ -173,3 +173,66 @@ extern "C" int hba_attn_fwd(int dtype, const void *q, const int64_t q_strides[3]
     HBA_LAUNCH_CHECK();
     return HBA_OK;
 }
+
+// The bf16 union attention's two launches as separate calls, so that a caller
+// can run the window (which needs no selection) concurrently with the
+// selection on another stream.  Same arguments and checks as hba_attn_fwd.
+static int attn_split_checks(const void *q, const int64_t *q_strides, int64_t B, int64_t n, int64_t Hq,
+                             int64_t Hkv, int64_t d, int64_t S, int64_t Bk, void *workspace, size_t ws_bytes,
+                             void *out, const int64_t *out_strides) {
+    int st = abi::check_dtype_dim(HBA_DTYPE_BF16, d);
+    if (st) return st;
+    if (!q || !q_strides || !out || !out_strides) return HBA_ERR_INVALID_ARG;
+    if (B <= 0 || n <= 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv != 0 || S < 0) return HBA_ERR_INVALID_ARG;
+    if (Bk != 64) return HBA_ERR_UNSUPPORTED;
+    if (n % Bk != 0 || S > Bk) return HBA_ERR_INVALID_ARG;
+    if (!abi::rows_aligned(HBA_DTYPE_BF16, q, q_strides) || !abi::rows_aligned(HBA_DTYPE_BF16, out, out_strides))
+        return HBA_ERR_UNSUPPORTED;
+    if (B > 65535 || Hq > 65535) return HBA_ERR_UNSUPPORTED;
+    size_t need = 0;
+    hba_attn_workspace_size(HBA_DTYPE_BF16, B, n, Hq, &need);
+    if (!workspace || ws_bytes < need || !abi::aligned16(workspace)) return HBA_ERR_INVALID_ARG;
+    return HBA_OK;
+}
+
+extern "C" int hba_attn_window_fwd(const void *q, const int64_t q_strides[3], const float *q_gain,
+                                   const float *k_gain, float eps, const void *kr, const void *vt,
+                                   const float *cos_tab, const float *sin_tab, int64_t B, int64_t n, int64_t Hq,
+                                   int64_t Hkv, int64_t d, int64_t S, int64_t W, int64_t Bk, float scale,
+                                   void *workspace, size_t ws_bytes, void *out, const int64_t out_strides[3],
+                                   void *stream) {
+    int st = attn_split_checks(q, q_strides, B, n, Hq, Hkv, d, S, Bk, workspace, ws_bytes, out, out_strides);
+    if (st) return st;
+    if (!kr || !vt || !cos_tab || !sin_tab || W < 1) return HBA_ERR_INVALID_ARG;
+    if (!abi::aligned16(kr) || !abi::aligned16(vt)) return HBA_ERR_UNSUPPORTED;
+    hipStream_t s = (hipStream_t)stream;
+    float *lse = (float *)workspace;
+    st = (d == 64) ? launch_attn_bf16_window<64>(q, q_strides, q_gain, k_gain, eps, kr, vt, cos_tab, sin_tab, B, n,
+                                                 Hq, Hkv, S, W, scale, out, out_strides, lse, s)
+                   : launch_attn_bf16_window<128>(q, q_strides, q_gain, k_gain, eps, kr, vt, cos_tab, sin_tab, B, n,
+                                                  Hq, Hkv, S, W, scale, out, out_strides, lse, s);
+    if (st) return st;
+    HBA_LAUNCH_CHECK();
+    return HBA_OK;
+}
+
+extern "C" int hba_attn_routed_fwd(const void *q, const int64_t q_strides[3], const float *q_gain,
+                                   const float *k_gain, float eps, const void *kc, const void *vt,
+                                   const int32_t *idx, const int32_t *cnt, int64_t B, int64_t n, int64_t Hq,
+                                   int64_t Hkv, int64_t d, int64_t S, int64_t Bk, int64_t k, float scale,
+                                   void *workspace, size_t ws_bytes, void *out, const int64_t out_strides[3],
+                                   void *stream) {
+    int st = attn_split_checks(q, q_strides, B, n, Hq, Hkv, d, S, Bk, workspace, ws_bytes, out, out_strides);
+    if (st) return st;
+    if (!kc || !vt || !idx || !cnt || k < 1) return HBA_ERR_INVALID_ARG;
+    if (!abi::aligned16(kc) || !abi::aligned16(vt)) return HBA_ERR_UNSUPPORTED;
+    hipStream_t s = (hipStream_t)stream;
+    const float *lse = (const float *)workspace;
+    st = (d == 64) ? launch_attn_bf16_routed<64>(q, q_strides, q_gain, k_gain, eps, kc, vt, idx, cnt, B, n, Hq,
+                                                 Hkv, S, k, scale, out, out_strides, lse, s)
+                   : launch_attn_bf16_routed<128>(q, q_strides, q_gain, k_gain, eps, kc, vt, idx, cnt, B, n, Hq,
+                                                  Hkv, S, k, scale, out, out_strides, lse, s);
+    if (st) return st;
+    HBA_LAUNCH_CHECK();
+    return HBA_OK;
+}

@@ -14,4 +14,16 @@ int launch_attn_bf16(const void *q, const int64_t *qs, const float *qgain, const
                      int64_t S, int64_t W, int64_t k, float scale, void *out, const int64_t *os, float *lse,
                      hipStream_t s);
 
+// The two launches separately (window; then sinks + routed, ordered after it).
+template <int D>
+int launch_attn_bf16_window(const void *q, const int64_t *qs, const float *qgain, const float *kgain, float eps,
+                            const void *kr, const void *vt, const float *cosT, const float *sinT, int64_t B,
+                            int64_t n, int64_t Hq, int64_t Hkv, int64_t S, int64_t W, float scale, void *out,
+                            const int64_t *os, float *lse, hipStream_t s);
+template <int D>
+int launch_attn_bf16_routed(const void *q, const int64_t *qs, const float *qgain, const float *kgain, float eps,
+                            const void *kc, const void *vt, const int32_t *idx, const int32_t *cnt, int64_t B,
+                            int64_t n, int64_t Hq, int64_t Hkv, int64_t S, int64_t k, float scale, void *out,
+                            const int64_t *os, const float *lse, hipStream_t s);
+
 }  // namespace hba

@@ -924,21 +924,55 @@ static int launch_routed(const void *q, const int64_t *qs, const float *qgain, c
 }  // namespace ab
 
 template <int D>
+int launch_attn_bf16_window(const void *q, const int64_t *qs, const float *qgain, const float *kgain, float eps,
+                            const void *kr, const void *vt, const float *cosT, const float *sinT, int64_t B,
+                            int64_t n, int64_t Hq, int64_t Hkv, int64_t S, int64_t W, float scale, void *out,
+                            const int64_t *os, float *lse, hipStream_t s) {
+    using namespace ab;
+    const int G = (int)(Hq / Hkv);
+    if (G > 16 || n / 64 >= SENT) return HBA_ERR_UNSUPPORTED;
+    constexpr int RT = (D == 64) ? 2 : 1;      // row tiles per wave within 168 VGPRs (3 waves per SIMD)
+    return launch_win<D, RT>(q, qs, qgain, kgain, eps, kr, vt, cosT, sinT, B, n, Hq, Hkv, S, W, scale, out, os,
+                             lse, s);
+}
+
+template <int D>
+int launch_attn_bf16_routed(const void *q, const int64_t *qs, const float *qgain, const float *kgain, float eps,
+                            const void *kc, const void *vt, const int32_t *idx, const int32_t *cnt, int64_t B,
+                            int64_t n, int64_t Hq, int64_t Hkv, int64_t S, int64_t k, float scale, void *out,
+                            const int64_t *os, const float *lse, hipStream_t s) {
+    using namespace ab;
+    const int G = (int)(Hq / Hkv);
+    if (G > 16 || n / 64 >= SENT) return HBA_ERR_UNSUPPORTED;
+    return launch_routed<D>(q, qs, qgain, kgain, eps, kc, vt, idx, cnt, B, n, Hq, Hkv, S, k, scale, out, os, lse,
+                            s);
+}
+
+template <int D>
 int launch_attn_bf16(const void *q, const int64_t *qs, const float *qgain, const float *kgain, float eps,
                      const void *kc, const void *kr, const void *vt, const float *cosT, const float *sinT,
                      const int32_t *idx, const int32_t *cnt, int64_t B, int64_t n, int64_t Hq, int64_t Hkv,
                      int64_t S, int64_t W, int64_t k, float scale, void *out, const int64_t *os, float *lse,
                      hipStream_t s) {
-    using namespace ab;
-    const int G = (int)(Hq / Hkv);
-    if (G > 16 || n / 64 >= SENT) return HBA_ERR_UNSUPPORTED;
-    constexpr int RT = (D == 64) ? 2 : 1;      // row tiles per wave within 168 VGPRs (3 waves per SIMD)
-    int st = launch_win<D, RT>(q, qs, qgain, kgain, eps, kr, vt, cosT, sinT, B, n, Hq, Hkv, S, W, scale, out, os,
-                               lse, s);
+    int st = launch_attn_bf16_window<D>(q, qs, qgain, kgain, eps, kr, vt, cosT, sinT, B, n, Hq, Hkv, S, W, scale,
+                                        out, os, lse, s);
     if (st) return st;
-    return launch_routed<D>(q, qs, qgain, kgain, eps, kc, vt, idx, cnt, B, n, Hq, Hkv, S, k, scale, out, os, lse,
-                            s);
+    return launch_attn_bf16_routed<D>(q, qs, qgain, kgain, eps, kc, vt, idx, cnt, B, n, Hq, Hkv, S, k, scale, out,
+                                      os, lse, s);
 }
+
+#define HBA_INST_WIN(D)                                                                                       \
+    template int launch_attn_bf16_window<D>(const void *, const int64_t *, const float *, const float *, float, \
+                                            const void *, const void *, const float *, const float *, int64_t,  \
+                                            int64_t, int64_t, int64_t, int64_t, int64_t, float, void *,        \
+                                            const int64_t *, float *, hipStream_t);                             \
+    template int launch_attn_bf16_routed<D>(const void *, const int64_t *, const float *, const float *, float, \
+                                            const void *, const void *, const int32_t *, const int32_t *,      \
+                                            int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, float,       \
+                                            void *, const int64_t *, const float *, hipStream_t);
+HBA_INST_WIN(64)
+HBA_INST_WIN(128)
+#undef HBA_INST_WIN
 
 template int launch_attn_bf16<64>(const void *, const int64_t *, const float *, const float *, float,
                                      const void *, const void *, const void *, const float *, const float *,

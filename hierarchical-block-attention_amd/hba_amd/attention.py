@@ -40,16 +40,33 @@ def forward_stages(q, k, v, cos, sin, cfg, summ, qkn, hier=False, dense_route=Fa
     sel_scale = route_scale(cfg, dh) if dense_route else scale
     r = {"scale": scale, "sel_scale": sel_scale}
     r["kc"], r["kr"], r["vt"] = ops.prep_keys(k, v, kg, keps, cos, sin)
-    r["S0"] = ops.summarize(r["kc"], summ.probes, summ.proj)
     kk = min(cfg.k_blocks, n // cfg.block)
+    # bf16: the window launch needs no selection, so it runs on a second
+    # stream while the summaries and the selection run on this one
+    split = q.dtype == torch.bfloat16
+    if split:
+        main = torch.cuda.current_stream(q.device)
+        side = ops.side_stream(q.device)
+        out, ws = ops.attn_buffers(q, k.shape[2])
+        side.wait_stream(main)
+        with torch.cuda.stream(side):
+            ops.attn_window_(q, qg, kg, qeps, r["kr"], r["vt"], cos, sin, cfg.sinks, cfg.window, scale, out, ws)
+        for t in (out, ws, r["kr"], r["vt"]):
+            t.record_stream(side)
+    r["S0"] = ops.summarize(r["kc"], summ.probes, summ.proj)
     if hier:
         r["S1"] = ops.build_super(r["S0"], cfg.fanout)
         r["idx"], r["val"], r["cnt"] = ops.hier_select(q, qg, qeps, r["S0"], r["S1"], cfg.window, kk,
                                                        cfg.fanout, cfg.beam, sel_scale)
     else:
         r["idx"], r["val"], r["cnt"] = ops.score_select(q, qg, qeps, r["S0"], cfg.window, kk, sel_scale)
-    r["out"] = ops.attn_fwd(q, qg, kg, qeps, r["kc"], r["kr"], r["vt"], cos, sin, r["idx"], r["cnt"],
-                            cfg.sinks, cfg.window, scale)
+    if split:
+        main.wait_stream(side)
+        r["out"] = ops.attn_routed_(q, qg, kg, qeps, r["kc"], r["vt"], r["idx"], r["cnt"], cfg.sinks, scale,
+                                    out, ws)
+    else:
+        r["out"] = ops.attn_fwd(q, qg, kg, qeps, r["kc"], r["kr"], r["vt"], cos, sin, r["idx"], r["cnt"],
+                                cfg.sinks, cfg.window, scale)
     return r
 
 

@@ -273,6 +273,77 @@ def attn_fwd(q: Tensor, q_gain: Optional[Tensor], k_gain: Optional[Tensor], eps:
     return out
 
 
+def attn_buffers(q, Hkv):
+    """Output and workspace of the two-launch bf16 attention (attn_window_ /
+    attn_routed_): out [B, n, Hq, d] in q's dtype and the LSE workspace."""
+    dev = _dev(q)
+    B, n, Hq, d = q.shape
+    nbytes = ctypes.c_size_t(0)
+    check(lib().hba_attn_workspace_size(_code(q), B, n, Hq, ctypes.byref(nbytes)), "hba_attn_workspace_size")
+    return (torch.empty(B, n, Hq, d, dtype=q.dtype, device=dev),
+            torch.empty(max(int(nbytes.value), 16), dtype=torch.uint8, device=dev))
+
+
+def attn_window_(q, q_gain, k_gain, eps, kr, vt, cos, sin, sinks, window, scale, out, ws):
+    """The window launch of the bf16 attention on the current stream: the
+    window rows into out, their LSE into ws (hba_attn_window_fwd)."""
+    dev = _dev(q)
+    _rows(q, "q")
+    B, n, Hq, d = q.shape
+    Hkv = kr.shape[1]
+    if q.dtype != torch.bfloat16:
+        raise TypeError("the two-launch attention is bf16 only; use attn_fwd")
+    if kr.shape != (B, Hkv, n, d) or vt.shape != (B, Hkv, d, n) or out.shape != q.shape:
+        raise ValueError("kr/vt/out do not match q")
+    cos, sin = _tables(cos, sin, n, d, dev)
+    qg = _f32c(q_gain, dev, Hq, "q_gain")
+    kg = _f32c(k_gain, dev, Hkv, "k_gain")
+    with torch.cuda.device(dev):
+        st = lib().hba_attn_window_fwd(_p(q), strides3(q), _p(qg), _p(kg), eps, _p(kr.contiguous()),
+                                       _p(vt.contiguous()), _p(cos), _p(sin), B, n, Hq, Hkv, d, sinks, window,
+                                       BLOCK, scale, _p(ws), ws.numel(), _p(out), strides3(out), _stream(dev))
+    check(st, "hba_attn_window_fwd")
+    return out
+
+
+def attn_routed_(q, q_gain, k_gain, eps, kc, vt, idx, cnt, sinks, scale, out, ws):
+    """The sinks + routed launch of the bf16 attention on the current stream,
+    merged into the window rows in out (hba_attn_routed_fwd); must follow
+    attn_window_ on the same out and ws."""
+    dev = _dev(q)
+    _rows(q, "q")
+    B, n, Hq, d = q.shape
+    Hkv = kc.shape[1]
+    if kc.shape != (B, Hkv, n, d) or vt.shape != (B, Hkv, d, n) or out.shape != q.shape:
+        raise ValueError("kc/vt/out do not match q")
+    if idx.shape[:3] != (B, Hkv, n) or cnt.shape != (B, Hkv, n):
+        raise ValueError("idx/cnt do not match q")
+    if idx.dtype != torch.int32 or cnt.dtype != torch.int32:
+        raise TypeError("idx/cnt must be int32")
+    qg = _f32c(q_gain, dev, Hq, "q_gain")
+    kg = _f32c(k_gain, dev, Hkv, "k_gain")
+    idx = idx.contiguous()
+    cnt = cnt.contiguous()
+    with torch.cuda.device(dev):
+        st = lib().hba_attn_routed_fwd(_p(q), strides3(q), _p(qg), _p(kg), eps, _p(kc.contiguous()),
+                                       _p(vt.contiguous()), _p(idx), _p(cnt), B, n, Hq, Hkv, d, sinks, BLOCK,
+                                       idx.shape[3], scale, _p(ws), ws.numel(), _p(out), strides3(out),
+                                       _stream(dev))
+    check(st, "hba_attn_routed_fwd")
+    return out
+
+
+_SIDE = {}
+
+
+def side_stream(dev):
+    """A second stream per device (default priority) for the window launch."""
+    key = torch.device(dev).index
+    if key not in _SIDE:
+        _SIDE[key] = torch.cuda.Stream(device=dev)
+    return _SIDE[key]
+
+
 @attn_fwd.register_fake
 def _(q, q_gain, k_gain, eps, kc, kr, vt, cos, sin, idx, cnt, sinks, window, scale):
     return q.new_empty(q.shape)

@@ -163,6 +163,37 @@ int hba_attn_fwd(int dtype, const void *q, const int64_t q_strides[3],
 int hba_attn_workspace_size(int dtype, int64_t B, int64_t n, int64_t Hq, size_t *bytes);
 
 /*
+ * The two launches of the bf16 hba_attn_fwd as separate calls, for callers
+ * that run the window (which needs no selection) concurrently with
+ * summarisation and selection on another stream.  Same arguments, checks
+ * and workspace as hba_attn_fwd (bf16 only).
+ *   hba_attn_window_fwd: the RoPE window region
+ *     (attention.py:342-356 window term); writes its normalised rows into
+ *     out and their log-sum-exp into workspace.
+ *   hba_attn_routed_fwd: the sinks and the routed blocks (the rest of the
+ *     union softmax), merged by LSE into out.  It must be ordered after
+ *     hba_attn_window_fwd on the same out and workspace (same stream, or an
+ *     event wait).
+ * hba_attn_fwd is hba_attn_window_fwd then hba_attn_routed_fwd on one stream.
+ */
+int hba_attn_window_fwd(const void *q, const int64_t q_strides[3],
+                        const float *q_gain, const float *k_gain, float eps,
+                        const void *kr, const void *vt,
+                        const float *cos_tab, const float *sin_tab,
+                        int64_t B, int64_t n, int64_t Hq, int64_t Hkv, int64_t d,
+                        int64_t S, int64_t W, int64_t Bk, float scale,
+                        void *workspace, size_t ws_bytes,
+                        void *out, const int64_t out_strides[3], void *stream);
+int hba_attn_routed_fwd(const void *q, const int64_t q_strides[3],
+                        const float *q_gain, const float *k_gain, float eps,
+                        const void *kc, const void *vt,
+                        const int32_t *idx, const int32_t *cnt,
+                        int64_t B, int64_t n, int64_t Hq, int64_t Hkv, int64_t d,
+                        int64_t S, int64_t Bk, int64_t k, float scale,
+                        void *workspace, size_t ws_bytes,
+                        void *out, const int64_t out_strides[3], void *stream);
+
+/*
  * Paged KV cache (decode).  Page = Bk tokens of one sequence; all tensors
  * page-major:  kc_pages [P, Hkv, Bk, d] (QKNorm'd NoPE keys), kr_pages
  * [P, Hkv, Bk, d] (the same keys rotated at their own positions: hba_prep_keys'

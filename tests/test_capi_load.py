@@ -58,6 +58,15 @@ def test_argument_checks_run_before_any_launch():
     st = L.hba_attn_fwd(1, fake, s3, None, None, 1e-6, fake, fake, fake, fake, fake, fake, fake, 1, 128, 14,
                         2, 64, 4, 1024, 64, 16, 0.1, fake, 16, fake, s3, None)
     assert st == -1                                    # workspace smaller than B*Hq*n*4
+    st = L.hba_attn_window_fwd(fake, s3, None, None, 1e-6, fake, fake, fake, fake, 1, 100, 14, 2, 64, 4, 1024,
+                               64, 0.1, fake, 1 << 20, fake, s3, None)
+    assert st == -1                                    # n % 64 != 0
+    st = L.hba_attn_routed_fwd(fake, s3, None, None, 1e-6, fake, fake, fake, fake, 1, 128, 14, 2, 64, 4, 64, 16,
+                               0.1, fake, 16, fake, s3, None)
+    assert st == -1                                    # workspace smaller than B*Hq*n*4
+    st = L.hba_attn_window_fwd(fake, s3, None, None, 1e-6, fake, fake, fake, fake, 1, 128, 14, 2, 96, 4, 1024,
+                               64, 0.1, fake, 1 << 20, fake, s3, None)
+    assert st == -2                                    # d = 96 unsupported
     nbytes = ctypes.c_size_t(0)
     assert L.hba_attn_workspace_size(1, 2, 128, 14, ctypes.byref(nbytes)) == 0 and nbytes.value == 2 * 14 * 128 * 4
     assert L.hba_attn_workspace_size(0, 2, 128, 14, ctypes.byref(nbytes)) == 0 and nbytes.value == 0

@@ -425,6 +425,19 @@ def test_invalid_arguments_raise(dev):
                                    cprm, cprm, None)
 
 
+def test_overlapped_schedule_equals_one_stream(dev):
+    """forward_stages runs the bf16 window launch on a second stream while the
+    selection runs; its output must be bit-identical to hba_attn_fwd (both
+    launches on one stream) on the same selection."""
+    cfg, x, prm, cos, sin = make(dev, "bf16", n=4096, W=1024, k=16, needles=True)
+    for _ in range(3):   # repeated calls reuse the side stream and the allocator's blocks
+        r = hba_amd.forward_stages(x["q"], x["k"], x["v"], cos, sin, cfg, prm, prm)
+        ref = ops.attn_fwd(x["q"], prm.q.gain, prm.k.gain, 1e-6, r["kc"], r["kr"], r["vt"], cos, sin, r["idx"],
+                           r["cnt"], cfg.sinks, cfg.window, r["scale"])
+        torch.cuda.synchronize()
+        assert torch.equal(r["out"], ref)
+
+
 def test_causality(dev):
     """gates.py:101-126: randomising tokens after t leaves rows <= t unchanged."""
     cfg, x, prm, cos, sin = make(dev, "bf16", n=2048, W=256, k=8)
