@@ -182,9 +182,12 @@ template <int D>
 struct RtCfg {
     static constexpr int NKS = D / 32;
     static constexpr int NDT = D / 16;
-    static constexpr int WAVES = 16;                   // 4 per SIMD: latency hiding
+    // d = 64: 16 waves (4 per SIMD) of 2 row tiles each, within 128 VGPRs.
+    // d = 128: 8 waves (2 per SIMD) of 3 row tiles within 256 VGPRs, so that a
+    // workgroup covers 48 queries and each staged block serves more of them.
+    static constexpr int WAVES = (D == 64) ? 16 : 8;
     static constexpr int NTHR = WAVES * 64;
-    static constexpr int PTW = (D == 64) ? 2 : 1;      // max 16-row tiles per wave (<= 128 VGPRs)
+    static constexpr int PTW = (D == 64) ? 2 : 3;      // max 16-row tiles per wave
     static constexpr int SLOT = 2 * 64 * D;            // bf16 per ring slot (K + V^T)
     static constexpr int NS = (D == 64) ? 8 : 4;       // ring depth (blocks, 128 KB)
     static constexpr int PH = NS / 2;                  // blocks per barrier phase
@@ -712,7 +715,7 @@ __device__ __forceinline__ void routed_body(
     __syncthreads();
 
     // The ring holds NPH phases of PH blocks, with one barrier per phase: a
-    // block's hits fall on few of the 16 waves, and a phase of several blocks
+    // block's hits fall on few of the waves, and a phase of several blocks
     // evens the waves' work out before they meet again.
     constexpr int P = C::PH, NPH = C::NS / C::PH;
     static_assert(32 % P == 0, "a phase's entries lie in one bitmap word");
@@ -801,7 +804,7 @@ __device__ __forceinline__ void routed_body(
 }
 
 template <int D, int PTW>
-__global__ __launch_bounds__(1024) void attn_routed_kernel(
+__global__ __launch_bounds__(RtCfg<D>::NTHR, RtCfg<D>::NTHR / 256) void attn_routed_kernel(
     const bf16_t *__restrict__ q, int64_t qsb, int64_t qsn, int64_t qsh, const float *__restrict__ qgain,
     const float *__restrict__ kgain, float eps, const bf16_t *__restrict__ kc, const bf16_t *__restrict__ vt,
     const int32_t *__restrict__ idx, const int32_t *__restrict__ cnt, int64_t n, int Hq, int Hkv, int S,
