@@ -100,6 +100,10 @@ SEL_CASES = [
     dict(dt="f32", n=1024, W=128, k=16, d=128, m=2, Hq=28, Hkv=4),
     dict(dt="bf16", n=1024, W=256, k=32, d=64, m=8, B=2),
     dict(dt="f32", n=768, W=64, k=64, d=64, m=4),            # select-all (k >= candidates)
+    dict(dt="bf16", n=4096, W=512, k=32, d=64, m=4),          # GEMM path, 32-entry lane lists
+    dict(dt="bf16", n=2048, W=256, k=16, d=128, m=4, Hq=28, Hkv=4, B=2),   # GEMM path, d = 128
+    dict(dt="bf16", n=2048, W=512, k=8, d=64, m=4, qknorm=False),         # routing query without gains
+    dict(dt="bf16", n=1088, W=256, k=16, d=64, m=4, Hq=8, Hkv=2),         # G = 4; ragged routed tile
 ]
 
 
@@ -142,7 +146,8 @@ def test_flat_select(dev, case):
     n = x["q"].shape[1]
     kk = min(cfg.k_blocks, n // 64)
     r = hba_amd.forward_stages(x["q"], x["k"], x["v"], cos, sin, cfg, prm, prm)
-    idx, val, cnt, scores = ops.score_select_with_scores(x["q"], x["q_gain"], 1e-6, r["S0"], cfg.window,
+    qg = x["q_gain"] if cfg.qknorm else None
+    idx, val, cnt, scores = ops.score_select_with_scores(x["q"], qg, 1e-6, r["S0"], cfg.window,
                                                          kk, r["sel_scale"])
     torch.cuda.synchronize()
     assert torch.equal(idx, r["idx"]) and torch.equal(cnt, r["cnt"])
@@ -332,6 +337,8 @@ ATTN_CASES = [
     dict(dt="bf16", n=2048, W=384, k=8, qknorm=False, sharp=False),
     dict(dt="f32", n=2048, W=512, k=8, native_ctx=512, temp_c=0.1),   # temperature active
     dict(dt="bf16", n=1024, W=200, k=6, Hq=16, Hkv=2, content_scale_mode="inv_sqrt_d"),
+    dict(dt="bf16", n=1088, W=256, k=16, Hq=8, Hkv=2),        # G = 4: 128-query routed tiles, the last ragged
+    dict(dt="bf16", n=2048, W=384, k=12, d=128, Hq=28, Hkv=4, B=2, needles=True),   # d = 128, 48-query tiles
 ]
 
 
