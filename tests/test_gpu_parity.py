@@ -104,6 +104,7 @@ SEL_CASES = [
     dict(dt="bf16", n=2048, W=256, k=16, d=128, m=4, Hq=28, Hkv=4, B=2),   # GEMM path, d = 128
     dict(dt="bf16", n=2048, W=512, k=8, d=64, m=4, qknorm=False),         # routing query without gains
     dict(dt="bf16", n=1088, W=256, k=16, d=64, m=4, Hq=8, Hkv=2),         # G = 4; ragged routed tile
+    dict(dt="bf16", n=4096, W=512, k=48, d=64, m=4),          # k > 32: the declared-order kernel in bf16
 ]
 
 
@@ -215,6 +216,7 @@ HIER_CASES = [
     dict(dt="bf16", n=4096, W=512, k=8, fanout=4, beam=3, m=2),                          # scalar bf16 path
     dict(dt="bf16", n=6144, W=700, k=12, fanout=5, beam=4),                              # ragged last super
     dict(dt="bf16", n=1024, W=1024, k=16, fanout=16, beam=2),                            # no candidates
+    dict(dt="bf16", n=4096, W=512, k=40, fanout=8, beam=6),                              # k > 32: declared order
 ]
 
 
