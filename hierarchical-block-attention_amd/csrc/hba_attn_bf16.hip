@@ -356,6 +356,54 @@ __device__ __forceinline__ void win_body(
                     }
                     continue;
                 }
+                bool allact = true;
+#pragma unroll
+                for (int rt = 0; rt < RT; ++rt) allact = allact && act[rt];
+                if (FIXED && RT > 1 && allact) {
+                    // edge tile needed by every row tile: as the interior
+                    // path, with the keys outside a column's window masked
+                    // in the exponent
+                    bf16x8 pf[RT][2];
+#pragma unroll
+                    for (int rt = 0; rt < RT; ++rt) {
+                        f32x4 Sa1[4];
+#pragma unroll
+                        for (int mt = 0; mt < 4; ++mt) {
+                            Sa1[mt] = f32x4{-bl2, -bl2, -bl2, -bl2};
+#pragma unroll
+                            for (int ks = 0; ks < C::NKS; ++ks) Sa1[mt] = mma(kf[mt][ks], qop[rt][ks], Sa1[mt]);
+                        }
+                        const int i = q0 + 16 * rt + l16;
+                        const int jlo = ((S > i - W + 1) ? S : i - W + 1) - kb;
+                        const int jhi = i - kb;
+                        const bool fullt = full[rt];
+                        float p[2][8];
+#pragma unroll
+                        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) {
+                                const int j = kl + 32 * (mt >> 1) + 4 * (mt & 1) + e;
+                                const bool ok = fullt | ((j >= jlo) & (j <= jhi));
+                                p[mt >> 1][(mt & 1) * 4 + e] = ex2(ok ? Sa1[mt][e] : -INFINITY);
+                            }
+                        pf[rt][0] = pack8(p[0]);
+                        pf[rt][1] = pack8(p[1]);
+                        ls[rt] += colsum(pf[rt][0], pf[rt][1]);
+                    }
+#pragma unroll
+                    for (int dt = 0; dt < C::NDT; ++dt) {
+                        const int r = 16 * dt + l16;
+                        const bf16_t *vp = Vs + r * 64;
+                        const int sw = swzV(r);
+                        const bf16x8 v0 = ldb8(vp + 8 * (lg ^ sw)), v1 = ldb8(vp + 8 * ((lg + 4) ^ sw));
+#pragma unroll
+                        for (int rt = 0; rt < RT; ++rt) {
+                            O[rt][dt] = mma(v0, pf[rt][0], O[rt][dt]);
+                            O[rt][dt] = mma(v1, pf[rt][1], O[rt][dt]);
+                        }
+                    }
+                    continue;
+                }
                 // per row tile: S^T, probabilities, packed P^T
                 bf16x8 pb[RT][2];
 #pragma unroll
