@@ -44,7 +44,7 @@ ATTN_KERNELS = "hba_attn_fwd = attn_win_kernel<64,2> + attn_routed_kernel<64,2>"
 # FETCH_SIZE and WRITE_SIZE summed over the two kernels, each divided by the
 # counter's reading per byte of a plain device copy (python bench.py
 # --copy-probe 1024); profiles/hba_attn_32k_traffic.md.
-ATTN_TRAFFIC_BYTES = 776279056
+ATTN_TRAFFIC_BYTES = 767784019
 
 
 def cpu_model():
