@@ -651,6 +651,17 @@ __global__ __launch_bounds__(64) void decode_d3_kernel(const float *__restrict__
     constexpr int PR = dec_prow(D);
     const float *part = ws_part + ((int64_t)s * Hkv + g) * np * G * PR + (int64_t)h * PR;
     const int64_t cs = (int64_t)G * PR;               // stride between partials
+    constexpr int TPL = D / 64;                       // elements per lane
+    // up to NPR partials' numerators are loaded with the maxima, so that the
+    // merge costs one memory round trip
+    constexpr int NPR = 48;
+    float pv[NPR][TPL];
+    if (np <= NPR) {
+#pragma unroll
+        for (int c = 0; c < NPR; ++c)
+#pragma unroll
+            for (int e = 0; e < TPL; ++e) pv[c][e] = (c < np) ? part[c * cs + ln + 64 * e] : 0.0f;
+    }
     float mc[2], lc[2];
     float mloc = -INFINITY;
 #pragma unroll
@@ -671,15 +682,25 @@ __global__ __launch_bounds__(64) void decode_d3_kernel(const float *__restrict__
     }
     dsum = wave_sum(dsum);
     __syncthreads();
-    constexpr int TPL = D / 64;                       // elements per lane
     float num[TPL];
 #pragma unroll
     for (int e = 0; e < TPL; ++e) num[e] = 0.0f;
-#pragma unroll 8
-    for (int c = 0; c < np; ++c) {
-        const float wv = wgt[c];
+    if (np <= NPR) {
 #pragma unroll
-        for (int e = 0; e < TPL; ++e) num[e] = fmaf(part[c * cs + ln + 64 * e], wv, num[e]);
+        for (int c = 0; c < NPR; ++c) {
+            if (c < np) {
+                const float wv = wgt[c];
+#pragma unroll
+                for (int e = 0; e < TPL; ++e) num[e] = fmaf(pv[c][e], wv, num[e]);
+            }
+        }
+    } else {
+#pragma unroll 8
+        for (int c = 0; c < np; ++c) {
+            const float wv = wgt[c];
+#pragma unroll
+            for (int e = 0; e < TPL; ++e) num[e] = fmaf(part[c * cs + ln + 64 * e], wv, num[e]);
+        }
     }
 #pragma unroll
     for (int e = 0; e < TPL; ++e)
