@@ -301,6 +301,30 @@ def _timed(fn, reps=5):
     return e0.elapsed_time(e1) / reps, out
 
 
+def bench_equiv32k(dev):
+    """Dense uniform-RoPE causal attention (the equiv=True mode) at 32K: B=1,
+    14/2 heads, d=64, QKNorm with the sharp gains, bf16: key preparation plus
+    the window kernel with no sinks and a whole-sequence window.  FLOP counted
+    as 4*d per (query, head, key <= query)."""
+    import torch
+    import hba_amd
+    from hba_amd import synth
+    w = WORKLOAD
+    n, Hq, Hkv, d = w["seq_len"], w["q_heads"], w["kv_heads"], w["head_dim"]
+    cfg = hba_amd.HBAConfig(n_heads=Hq, n_kv=Hkv, head_dim=d)
+    x = synth.layer_inputs(1, n, Hq, Hkv, d, dtype=torch.bfloat16, device=dev, seed=0, sharp=True)
+    prm = synth.Params(x["q_gain"], x["k_gain"], x["probes"], x["proj"])
+    cos, sin = hba_amd.rope_tables(n, d, cfg.rope_theta, dev)
+    ms, _ = _timed(lambda: hba_amd.equiv_attention(x["q"], x["k"], x["v"], cos, sin, cfg, prm), reps=5)
+    flop = 4.0 * d * Hq * n * (n + 1) / 2
+    tflops = flop / (ms * 1e-3) / 1e12
+    return {"metric": "dense causal uniform-RoPE attention (equiv mode) tokens/s at 32K",
+            "config": {"workload": "hba_equiv_32k", "batch": 1, "seq_len": n, "q_heads": Hq, "kv_heads": Hkv,
+                       "head_dim": d},
+            "tokens_per_s": round(n / (ms * 1e-3), 1), "ms": round(ms, 4), "flop": flop,
+            "achieved_TFLOPs": round(tflops, 1), "mfma_frac": round(tflops / PEAK_BF16_TFLOPS, 4)}
+
+
 def bench_hier128k(dev):
     """Hierarchical tree selection at 128K (B=1, 14/2 heads, d=64, 2048 blocks,
     super-summaries over 16 blocks, beam 8, top-16, log-length temperature
@@ -427,9 +451,9 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run 3 plain device copies of MIB MiB (counter calibration) and exit")
-    ap.add_argument("--config", choices=["layer32k", "hier128k", "donor"], default="layer32k",
-                    help="layer32k: the headline line (default); hier128k / donor: the other measured "
-                         "workloads, one JSON line each")
+    ap.add_argument("--config", choices=["layer32k", "hier128k", "donor", "equiv32k"], default="layer32k",
+                    help="layer32k: the headline line (default); hier128k / donor / equiv32k: the other "
+                         "measured workloads, one JSON line each")
     a = ap.parse_args()
     if a.copy_probe:
         import torch
@@ -449,7 +473,7 @@ def main():
     import torch
     dev = torch.device("cuda:0")
     if a.config != "layer32k":
-        line = bench_hier128k(dev) if a.config == "hier128k" else bench_donor(dev)
+        line = {"hier128k": bench_hier128k, "donor": bench_donor, "equiv32k": bench_equiv32k}[a.config](dev)
         line.update({"n_gpus": 1, "dtype": "bf16", "data": "synthetic"})
         print(json.dumps(line))
         return

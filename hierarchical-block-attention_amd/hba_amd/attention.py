@@ -1,10 +1,11 @@
 """Drop-in attention functions with the reference's signatures, backed by the
 HIP kernels (forward only).
 
-  hba_attention_eval(q, k, v, cos, sin, cfg, summ, qkn, cap, hier=False)
-      src/hba/attention.py:610-713
-  hba_attention_dense(q, k, v, cos, sin, cfg, summ, qkn) -> (out, aux=0)
-      src/hba/attention.py:306-356 (forward; the aux-KL teacher is training-only)
+  hba_attention_eval(q, k, v, cos, sin, cfg, summ, qkn, cap, hier=False, equiv=False)
+      src/hba/attention.py:610-713 (equiv=True: :634-649)
+  hba_attention_dense(q, k, v, cos, sin, cfg, summ, qkn, equiv=False) -> (out, aux=0)
+      src/hba/attention.py:306-356 (forward; the aux-KL teacher is training-only;
+      equiv=True: :330-336)
   hba_attention_fused(q, k, v, cos, sin, cfg, summ, qkn) -> (out, aux=0)
       src/hba/attention.py:552-607 (forward: same math as dense)
 
@@ -14,7 +15,9 @@ contiguous), cos/sin fp32 [n, d] from rope_tables.  `cfg` is read duck-typed
 .proj [Hkv, d, d], `qkn` .q.gain/.k.gain/.q.eps/.k.eps.  The output is a new
 tensor of q's shape and dtype; inputs are not modified.  Errors follow the
 reference: AssertionError for n % block != 0, ValueError for an unknown
-content_scale_mode.
+content_scale_mode.  equiv=True is dense causal attention with RoPE on every
+query and key; the kernels tile keys in 64s, so it raises ValueError for a
+sequence length that is not a multiple of 64.
 """
 import torch
 
@@ -70,21 +73,42 @@ def forward_stages(q, k, v, cos, sin, cfg, summ, qkn, hier=False, dense_route=Fa
     return r
 
 
+def equiv_attention(q, k, v, cos, sin, cfg, qkn):
+    """Dense uniform-RoPE causal attention (the equiv=True branch,
+    attention.py:330-336 and :634-649): the same QKNorm and union scale as the
+    HBA path, RoPE on every query and key, every key j <= i attended.  It is
+    the union kernel with no sinks, a window covering the whole sequence and
+    no routed blocks (in bf16, the window launch alone)."""
+    B, n, Hq, dh = q.shape
+    Hkv = k.shape[2]
+    if n % ops.BLOCK:
+        raise ValueError(f"equiv attention needs a sequence length that is a multiple of {ops.BLOCK}, got {n}")
+    qg, kg, qeps, keps = _qk(cfg, qkn)
+    scale = union_scale(cfg, dh, n)
+    kc, kr, vt = ops.prep_keys(k, v, kg, keps, cos, sin)
+    if q.dtype == torch.bfloat16:
+        out, ws = ops.attn_buffers(q, Hkv)
+        return ops.attn_window_(q, qg, kg, qeps, kr, vt, cos, sin, 0, n, scale, out, ws)
+    idx = torch.zeros(B, Hkv, n, 1, dtype=torch.int32, device=q.device)
+    cnt = torch.zeros(B, Hkv, n, dtype=torch.int32, device=q.device)
+    return ops.attn_fwd(q, qg, kg, qeps, kc, kr, vt, cos, sin, idx, cnt, 0, n, scale)
+
+
 def hba_attention_eval(q, k, v, cos, sin, cfg, summ, qkn, cap=None, hier=False, equiv=False):
     """Gathered union attention with flat or hierarchical selection; `cap`
-    (the reference's memory cap for its chunk loop) is accepted and unused."""
+    (the reference's memory cap for its chunk loop) is accepted and unused.
+    equiv=True: dense uniform-RoPE causal attention (equiv_attention)."""
     if equiv:
-        raise NotImplementedError("equiv=True (dense uniform-RoPE attention) is not part of the "
-                                  "HBA operator")
+        return equiv_attention(q, k, v, cos, sin, cfg, qkn)
     return forward_stages(q, k, v, cos, sin, cfg, summ, qkn, hier=hier)["out"]
 
 
 def hba_attention_dense(q, k, v, cos, sin, cfg, summ, qkn, equiv=False):
     """Forward of the reference's naive path: selection with route_topk's
-    scale (no temperature), attention with the union scale.  aux = 0."""
+    scale (no temperature), attention with the union scale.  aux = 0.
+    equiv=True: dense uniform-RoPE causal attention (equiv_attention)."""
     if equiv:
-        raise NotImplementedError("equiv=True (dense uniform-RoPE attention) is not part of the "
-                                  "HBA operator")
+        return equiv_attention(q, k, v, cos, sin, cfg, qkn), q.new_zeros(())
     out = forward_stages(q, k, v, cos, sin, cfg, summ, qkn, dense_route=True)["out"]
     return out, q.new_zeros(())
 

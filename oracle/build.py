@@ -2,7 +2,7 @@
 
 Compiles oracle/hba_oracle.c with gcc into oracle/_build/libhba_oracle.so.
 No reference sources are compiled: the reference is pure Python and ships no
-C/C++ (see DESIGN.md), so there is no oracle/_ref build.
+C/C++, so there is no oracle/_ref build.
 """
 import os
 import subprocess

@@ -19,6 +19,7 @@ What it restates (reference file:line):
   build_super / hier_select             src/hba/attention.py:202-246   (C, declared order)
   hba_attention_dense (forward)         src/hba/attention.py:306-356   (row-sampled)
   hba_attention_eval (flat and hier)    src/hba/attention.py:610-713   (row-sampled)
+  equiv=True (uniform-RoPE causal)      src/hba/attention.py:330-336, 634-649 (row-sampled)
   decode step = prefill row L-1         (no reference function; defined from the above)
 
 Arrays are numpy float32 arrays that hold values of the storage dtype
@@ -38,7 +39,10 @@ Pinning (each check lives in tests/test_oracle_*.py):
     hierarchy comparison counts 5.2x/7.9x/10.6x (docs/design.md:79,113);
   * invariants: hier == flat when the beam covers every candidate super,
     select-all eval == masked dense, causality, brute-force loops on tiny
-    inputs, and planted mistakes that those checks must catch.
+    inputs, and planted mistakes that those checks must catch;
+  * equiv rows against torch's scaled_dot_product_attention (a library
+    routine, causal, GQA heads expanded) and against the union rows with no
+    sinks, a whole-sequence window and no routed blocks.
 """
 import ctypes
 import math
@@ -487,6 +491,39 @@ def forward_dense(q, k, v, cos, sin, cfg, probes, proj, q_gain, k_gain, eps, dty
                                cfg.window, cfg.block, rows))
         sels.append((idx, val, cnt))
     return np.stack(outs), sels
+
+
+def equiv_rows(qr, kr, v, scale, rows):
+    """Dense uniform-RoPE causal attention rows, float64: the equiv=True branch
+    of hba_attention_dense (attention.py:330-336) and hba_attention_eval
+    (:634-649).  Query i attends every key j <= i through the rotated q and k,
+    one softmax; head h reads KV head h // G.  qr [n, Hq, d]; kr, v [n, Hkv, d].
+    Returns [len(rows), Hq, d] float64."""
+    n, Hq, d = qr.shape
+    G = Hq // kr.shape[1]
+    out = np.zeros((len(rows), Hq, d))
+    for r, i in enumerate(rows):
+        i = int(i)
+        for h in range(Hq):
+            s = (kr[: i + 1, h // G].astype(np.float64) @ qr[i, h].astype(np.float64)) * scale
+            p = np.exp(s - s.max())
+            out[r, h] = (p / p.sum()) @ v[: i + 1, h // G].astype(np.float64)
+    return out
+
+
+def forward_equiv(q, k, v, cos, sin, cfg, q_gain, k_gain, eps, dtype, rows=None):
+    """hba_attention_eval/dense with equiv=True for q/k/v [B, n, H, d]: the same
+    QKNorm and union scale (_content_qk, attention.py:173-198), RoPE on q and k,
+    then equiv_rows.  Returns [B, r, Hq, d] float64."""
+    B, n = q.shape[0], q.shape[1]
+    rows = np.arange(n) if rows is None else np.asarray(rows)
+    outs = []
+    for b in range(B):
+        qc, kc, scale = content_qk(q[b], k[b], cfg, q_gain, k_gain, eps, n, dtype)
+        qr = apply_rope(qc, cos[:n], sin[:n], dtype)
+        kr = apply_rope(kc, cos[:n], sin[:n], dtype)
+        outs.append(equiv_rows(qr, kr, _f32(v[b]), scale, rows))
+    return np.stack(outs)
 
 
 def decode_row(q_new, kc_seq, v_seq, cos, sin, cfg, S0_seq, q_gain, eps, dtype, scale):

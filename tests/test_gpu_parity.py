@@ -447,6 +447,30 @@ def test_overlapped_schedule_equals_one_stream(dev):
         assert torch.equal(r["out"], ref)
 
 
+@pytest.mark.parametrize("dt,qknorm,n", [("bf16", True, 2048), ("bf16", False, 1024), ("f32", True, 512)])
+def test_equiv_matches_oracle(dev, dt, qknorm, n):
+    """equiv=True (attention.py:330-336, 634-649): dense uniform-RoPE causal
+    attention, through the eval and dense drop-ins."""
+    cfg, x, prm, cos, sin = make(dev, dt, n=n, qknorm=qknorm)
+    out = hba_amd.hba_attention_eval(x["q"], x["k"], x["v"], cos, sin, cfg, prm, prm, None, equiv=True)
+    out2, aux = hba_amd.hba_attention_dense(x["q"], x["k"], x["v"], cos, sin, cfg, prm, prm, equiv=True)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out2) and float(aux) == 0.0
+    rows = np.unique(np.concatenate([[0, 1, 2, 63, 64, 65, n // 2, n - 1],
+                                     np.random.RandomState(0).randint(0, n, 24)]))
+    ref = O.forward_equiv(f(x["q"]), f(x["k"]), f(x["v"]), f(cos), f(sin), cfg, f(x["q_gain"]), f(x["k_gain"]),
+                          1e-6, dt, rows)
+    err = np.abs(f(out)[:, rows] - ref).max()
+    assert err <= TOL[dt], err
+
+
+def test_equiv_rejects_ragged_length(dev):
+    cfg, x, prm, cos, sin = make(dev, "bf16", n=128)
+    with pytest.raises(ValueError):
+        hba_amd.hba_attention_eval(x["q"][:, :100], x["k"][:, :100], x["v"][:, :100], cos[:100], sin[:100], cfg,
+                                   prm, prm, None, equiv=True)
+
+
 def test_causality(dev):
     """gates.py:101-126: randomising tokens after t leaves rows <= t unchanged."""
     cfg, x, prm, cos, sin = make(dev, "bf16", n=2048, W=256, k=8)
@@ -488,21 +512,32 @@ def cache_summaries(cache, s, nfull):
     return f(cache.summ_pages[torch.tensor(pt, dtype=torch.long)]).transpose(1, 0, 2, 3)
 
 
-@pytest.mark.parametrize("dt", ["f32", "bf16"])
-def test_decode_matches_oracle(dev, dt):
-    lens = [1, 3, 70, 1100, 1200, 2500, 2049, 4096, 3333]
-    cfg, x, prm, cos, sin, cache, kcs, qn = build_cache(dev, dt, lens, W=1024, k=16)
+def _decode_vs_oracle(dev, dt, lens, **kw):
+    cfg, x, prm, cos, sin, cache, kcs, qn = build_cache(dev, dt, lens, **kw)
     out, sidx, scnt = hba_amd.hba_decode_step(qn, cache, cfg, prm, cos, sin)
     torch.cuda.synchronize()
+    d = cfg.head_dim
     for s, L in enumerate(lens):
         S0s = cache_summaries(cache, s, L // 64)
-        scale = hba_amd.union_scale(cfg, 64, L)
+        scale = hba_amd.union_scale(cfg, d, L)
         ref, (idx, val, cnt) = O.decode_row(f(qn[s]), f(kcs[s]), f(x["v"][s, :L]), f(cos), f(sin), cfg,
                                             S0s, f(x["q_gain"]), 1e-6, dt, scale)
         assert np.array_equal(scnt[s].cpu().numpy(), cnt), s
         for g in range(cfg.n_kv):
             assert list(sidx[s, g, : cnt[g]].cpu().numpy()) == list(idx[g, : cnt[g]]), (s, g)
         assert np.abs(f(out[s]) - ref).max() <= TOL[dt], (s, np.abs(f(out[s]) - ref).max())
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_decode_matches_oracle(dev, dt):
+    _decode_vs_oracle(dev, dt, [1, 3, 70, 1100, 1200, 2500, 2049, 4096, 3333], W=1024, k=16)
+
+
+@pytest.mark.parametrize("d,k,Hq,Hkv,S", [(128, 16, 28, 4, 8), (64, 40, 14, 2, 4), (64, 64, 8, 1, 0)])
+def test_decode_bf16_shapes(dev, d, k, Hq, Hkv, S):
+    """bf16 decode at d = 128 (8-wave routed/merge workgroups), and with more
+    picks than waves (k = 40, 64: each wave runs several routed pages)."""
+    _decode_vs_oracle(dev, "bf16", [70, 700, 2500, 4096], Hq=Hq, Hkv=Hkv, d=d, S=S, W=512, k=k)
 
 
 def test_decode_equals_prefill_last_row(dev):

@@ -347,6 +347,60 @@ def _eval_vs_brute(cfg, q, k, v, pr, pj, qg, kg, cos, sin, rows):
     return worst
 
 
+def test_equiv_rows_match_library_sdpa_and_union_limit():
+    """equiv=True (attention.py:330-336, 634-649) is causal attention over the
+    rotated q and k.  Checked against torch's scaled_dot_product_attention
+    (float64, causal, GQA heads expanded) and against the union rows with no
+    sinks, a whole-sequence window and no routed blocks."""
+    import torch
+    import torch.nn.functional as F
+    rs = RS(11)
+    n, Hq, Hkv, d = 96, 6, 2, 16
+    G = Hq // Hkv
+    qr = rs.standard_normal((n, Hq, d)).astype(np.float32)
+    kr = rs.standard_normal((n, Hkv, d)).astype(np.float32)
+    v = rs.standard_normal((n, Hkv, d)).astype(np.float32)
+    scale = 0.31
+    rows = np.arange(n)
+    got = O.equiv_rows(qr, kr, v, scale, rows)
+    Q = torch.from_numpy(qr).double().permute(1, 0, 2)[None]
+    K = torch.from_numpy(kr).double().permute(1, 0, 2).repeat_interleave(G, 0)[None]
+    V = torch.from_numpy(v).double().permute(1, 0, 2).repeat_interleave(G, 0)[None]
+    ref = F.scaled_dot_product_attention(Q, K, V, is_causal=True, scale=scale)[0].permute(1, 0, 2).numpy()
+    assert np.abs(got - ref).max() < 1e-12
+    idx = np.full((Hkv, n, 1), -1, dtype=np.int32)
+    cnt = np.zeros((Hkv, n), dtype=np.int32)
+    union = O.attn_rows(qr, qr, kr, kr, v, idx, cnt, scale, 0, n, 16, rows)
+    assert np.abs(got - union).max() < 1e-12
+    # a dropped causal mask (every key attended) is caught by the library check
+    full = F.scaled_dot_product_attention(Q, K, V, is_causal=False, scale=scale)[0].permute(1, 0, 2).numpy()
+    assert np.abs(got - full).max() > 1e-3
+
+
+def test_forward_equiv_applies_qknorm_rope_and_scale():
+    """forward_equiv = content_qk (QKNorm, union scale) + RoPE on q and k +
+    equiv_rows; without QKNorm the scale is d**-0.5 and q, k pass through."""
+    rs = RS(12)
+    n, Hq, Hkv, d = 64, 4, 2, 8
+    cfg = tiny_cfg(head_dim=d)
+    q = rs.standard_normal((1, n, Hq, d)).astype(np.float32)
+    k = rs.standard_normal((1, n, Hkv, d)).astype(np.float32)
+    v = rs.standard_normal((1, n, Hkv, d)).astype(np.float32)
+    cos, sin = O.rope_tables(n, d, 1e6)
+    gq = rs.uniform(0.5, 2.0, Hq).astype(np.float32)
+    gk = rs.uniform(0.5, 2.0, Hkv).astype(np.float32)
+    rows = np.array([0, 5, 31, 63])
+    for qk in (True, False):
+        cfg.qknorm = qk
+        got = O.forward_equiv(q, k, v, cos, sin, cfg, gq, gk, 1e-6, "f32", rows)[0]
+        qc = O.qknorm(q[0], gq, 1e-6, "f32") if qk else q[0]
+        kc = O.qknorm(k[0], gk, 1e-6, "f32") if qk else k[0]
+        scale = O.union_scale(cfg, d, n) if qk else d ** -0.5
+        want = O.equiv_rows(O.apply_rope(qc, cos, sin, "f32"), O.apply_rope(kc, cos, sin, "f32"), v[0],
+                            scale, rows)
+        assert np.abs(got - want).max() < 1e-12
+
+
 def test_planted_mistakes_are_caught(monkeypatch):
     cfg, q, k, v, pr, pj, qg, kg, cos, sin = _tiny_problem(n=192)
     rows = [1, 40, 100, 150, 191]
