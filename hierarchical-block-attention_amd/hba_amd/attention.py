@@ -1,5 +1,5 @@
 """Drop-in attention functions with the reference's signatures, backed by the
-HIP kernels (forward only).
+HIP kernels (forward, and the backward through autograd).
 
   hba_attention_eval(q, k, v, cos, sin, cfg, summ, qkn, cap, hier=False, equiv=False)
       src/hba/attention.py:610-713 (equiv=True: :634-649)
@@ -8,6 +8,12 @@ HIP kernels (forward only).
       equiv=True: :330-336)
   hba_attention_fused(q, k, v, cos, sin, cfg, summ, qkn) -> (out, aux=0)
       src/hba/attention.py:552-607 (forward: same math as dense)
+
+Gradients: when grad mode is on and q, k, v or the QKNorm gains require grad,
+the output carries an autograd node whose backward is the HIP backward
+(ops.attn_bwd): dq, dk, dv and the gain gradients, the selection held fixed
+(the reference routes on detached q/k, attention.py:288-303).  The aux-KL
+teacher is not provided (aux = 0).
 
 Tensors: q [B, n, Hq, d], k, v [B, n, Hkv, d] (token-major views, last dim
 contiguous), cos/sin fp32 [n, d] from rope_tables.  `cfg` is read duck-typed
@@ -73,6 +79,63 @@ def forward_stages(q, k, v, cos, sin, cfg, summ, qkn, hier=False, dense_route=Fa
     return r
 
 
+class _Gains:
+    """QKNorm stand-in (.q/.k with .gain and .eps) holding detached gains."""
+
+    class _One:
+        def __init__(self, gain, eps):
+            self.gain, self.eps = gain, eps
+
+    def __init__(self, qg, kg, qeps, keps):
+        self.q, self.k = self._One(qg, qeps), self._One(kg, keps)
+
+
+class _UnionAttention(torch.autograd.Function):
+    """Forward: the HIP forward (forward_stages, or equiv_attention); backward:
+    hba_attn_bwd on the saved inputs, prepared keys and selection."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, q_gain, k_gain, cos, sin, cfg, summ, qeps, keps, mode):
+        qkn = _Gains(None if q_gain is None else q_gain.detach(), None if k_gain is None else k_gain.detach(),
+                     qeps, keps)
+        B, n, Hq, dh = q.shape
+        if mode == "equiv":
+            out = equiv_attention(q, k, v, cos, sin, cfg, qkn)
+            kc, kr, _ = ops.prep_keys(k, v, qkn.k.gain, keps, cos, sin)
+            idx = torch.zeros(B, k.shape[2], n, 1, dtype=torch.int32, device=q.device)
+            cnt = torch.zeros(B, k.shape[2], n, dtype=torch.int32, device=q.device)
+            S, W = 0, n
+        else:
+            r = forward_stages(q, k, v, cos, sin, cfg, summ, qkn, hier=mode == "hier",
+                               dense_route=mode == "dense")
+            out, kc, kr, idx, cnt = r["out"], r["kc"], r["kr"], r["idx"], r["cnt"]
+            S, W = cfg.sinks, cfg.window
+        ctx.save_for_backward(q, k, v, q_gain, k_gain, cos, sin, kc, kr, idx, cnt, out)
+        ctx.meta = (S, W, union_scale(cfg, dh, n), qeps)
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        q, k, v, q_gain, k_gain, cos, sin, kc, kr, idx, cnt, out = ctx.saved_tensors
+        S, W, scale, eps = ctx.meta
+        dq, dk, dv, dqg, dkg = ops.attn_bwd(q, k, v, kc, kr, q_gain, k_gain, eps, cos, sin, idx, cnt, out,
+                                            dout.contiguous(), S, W, scale)
+        gq = dqg.to(q_gain.dtype) if q_gain is not None and ctx.needs_input_grad[3] else None
+        gk = dkg.to(k_gain.dtype) if k_gain is not None and ctx.needs_input_grad[4] else None
+        return dq, dk, dv, gq, gk, None, None, None, None, None, None, None
+
+
+def _with_grad(q, k, v, cos, sin, cfg, summ, qkn, mode):
+    """The output with an autograd node when anything upstream needs a
+    gradient; None otherwise (the caller runs the plain forward)."""
+    qg, kg, qeps, keps = _qk(cfg, qkn)
+    if not torch.is_grad_enabled() or not any(t is not None and t.requires_grad for t in (q, k, v, qg, kg)):
+        return None
+    if qg is not None and qeps != keps:
+        raise NotImplementedError("the backward takes one QKNorm eps for q and k")
+    return _UnionAttention.apply(q, k, v, qg, kg, cos, sin, cfg, summ, qeps, keps, mode)
+
+
 def equiv_attention(q, k, v, cos, sin, cfg, qkn):
     """Dense uniform-RoPE causal attention (the equiv=True branch,
     attention.py:330-336 and :634-649): the same QKNorm and union scale as the
@@ -98,6 +161,10 @@ def hba_attention_eval(q, k, v, cos, sin, cfg, summ, qkn, cap=None, hier=False, 
     """Gathered union attention with flat or hierarchical selection; `cap`
     (the reference's memory cap for its chunk loop) is accepted and unused.
     equiv=True: dense uniform-RoPE causal attention (equiv_attention)."""
+    mode = "equiv" if equiv else ("hier" if hier else "eval")
+    out = _with_grad(q, k, v, cos, sin, cfg, summ, qkn, mode)
+    if out is not None:
+        return out
     if equiv:
         return equiv_attention(q, k, v, cos, sin, cfg, qkn)
     return forward_stages(q, k, v, cos, sin, cfg, summ, qkn, hier=hier)["out"]
@@ -107,6 +174,9 @@ def hba_attention_dense(q, k, v, cos, sin, cfg, summ, qkn, equiv=False):
     """Forward of the reference's naive path: selection with route_topk's
     scale (no temperature), attention with the union scale.  aux = 0.
     equiv=True: dense uniform-RoPE causal attention (equiv_attention)."""
+    out = _with_grad(q, k, v, cos, sin, cfg, summ, qkn, "equiv" if equiv else "dense")
+    if out is not None:
+        return out, q.new_zeros(())
     if equiv:
         return equiv_attention(q, k, v, cos, sin, cfg, qkn), q.new_zeros(())
     out = forward_stages(q, k, v, cos, sin, cfg, summ, qkn, dense_route=True)["out"]

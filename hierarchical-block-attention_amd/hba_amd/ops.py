@@ -11,6 +11,7 @@ device.
     hba::score_select     flat top-k block selection
     hba::hier_select      two-level beam selection
     hba::attn_fwd         union attention forward (prefill)
+    hba::attn_bwd         union attention backward (dq, dk, dv, QKNorm gain grads)
     hba::kv_append        paged-cache append (mutates the pages)
     hba::summarize_pages  summaries of listed pages (mutates summ_pages)
     hba::decode_fwd       decode step over the paged cache
@@ -347,6 +348,57 @@ def side_stream(dev):
 @attn_fwd.register_fake
 def _(q, q_gain, k_gain, eps, kc, kr, vt, cos, sin, idx, cnt, sinks, window, scale):
     return q.new_empty(q.shape)
+
+
+# ------------------------------------------------------------- backward ----
+@torch.library.custom_op("hba::attn_bwd", mutates_args=(), device_types="cuda")
+def attn_bwd(q: Tensor, k: Tensor, v: Tensor, kc: Tensor, kr: Tensor, q_gain: Optional[Tensor],
+             k_gain: Optional[Tensor], eps: float, cos: Tensor, sin: Tensor, idx: Tensor, cnt: Tensor,
+             out: Tensor, dout: Tensor, sinks: int, window: int, scale: float
+             ) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """Gradients of the union attention output (hba_attn_bwd): dq, dk, dv in
+    q's dtype and the QKNorm gain gradients dq_gain [Hq], dk_gain [Hkv] (fp32;
+    zeros without QKNorm), the selection idx/cnt held fixed."""
+    dev = _dev(q)
+    B, n, Hq, d = q.shape
+    Hkv = k.shape[2]
+    if k.shape != (B, n, Hkv, d) or v.shape != k.shape or out.shape != q.shape or dout.shape != q.shape:
+        raise ValueError("k/v/out/dout do not match q")
+    if kc.shape != (B, Hkv, n, d) or kr.shape != kc.shape:
+        raise ValueError("kc/kr do not match q")
+    if idx.shape[:3] != (B, Hkv, n) or cnt.shape != (B, Hkv, n):
+        raise ValueError("idx/cnt do not match q")
+    if idx.dtype != torch.int32 or cnt.dtype != torch.int32:
+        raise TypeError("idx/cnt must be int32")
+    if not (q.dtype == k.dtype == v.dtype == kc.dtype == kr.dtype == out.dtype == dout.dtype):
+        raise TypeError("q, k, v, kc, kr, out and dout must share one dtype")
+    cos, sin = _tables(cos, sin, n, d, dev)
+    qg = _f32c(q_gain, dev, Hq, "q_gain")
+    kg = _f32c(k_gain, dev, Hkv, "k_gain")
+    if (qg is None) != (kg is None):
+        raise ValueError("q_gain and k_gain are both given (QKNorm) or both None")
+    q, k, v, kc, kr, out, dout = (t.contiguous() for t in (q, k, v, kc, kr, out, dout))
+    idx = idx.contiguous()
+    cnt = cnt.contiguous()
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    dqg = torch.zeros(Hq, dtype=torch.float32, device=dev)
+    dkg = torch.zeros(Hkv, dtype=torch.float32, device=dev)
+    nbytes = ctypes.c_size_t(0)
+    check(lib().hba_attn_bwd_workspace_size(B, n, Hq, d, ctypes.byref(nbytes)), "hba_attn_bwd_workspace_size")
+    ws = torch.empty(max(int(nbytes.value), 16), dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev):
+        st = lib().hba_attn_bwd(_code(q), _p(q), _p(k), _p(v), _p(kc), _p(kr), _p(qg), _p(kg), eps, _p(cos),
+                                _p(sin), _p(idx), _p(cnt), _p(out), _p(dout), B, n, Hq, Hkv, d, sinks, window,
+                                BLOCK, idx.shape[3], scale, _p(ws), int(nbytes.value), _p(dq), _p(dk), _p(dv),
+                                _p(dqg), _p(dkg), _stream(dev))
+    check(st, "hba_attn_bwd")
+    return dq, dk, dv, dqg, dkg
+
+
+@attn_bwd.register_fake
+def _(q, k, v, kc, kr, q_gain, k_gain, eps, cos, sin, idx, cnt, out, dout, sinks, window, scale):
+    return (q.new_empty(q.shape), k.new_empty(k.shape), v.new_empty(v.shape),
+            q.new_empty(q.shape[2], dtype=torch.float32), k.new_empty(k.shape[2], dtype=torch.float32))
 
 
 # ---------------------------------------------------------------- decode ----

@@ -252,6 +252,34 @@ int hba_decode_fwd(int dtype, const void *q, const float *q_gain, float eps,
                    void *workspace, size_t ws_bytes, void *out,
                    int32_t *sel_idx, int32_t *sel_cnt, void *stream);
 
+/*
+ * Backward of the union attention (replaces the autograd backward of
+ * hba_attention_dense / hba_attention_fused, src/hba/attention.py:306-356,
+ * 552-607; the routing is on detached q/k there, :288-303, so the selection
+ * idx/cnt is an input and gets no gradient).  Given the forward's raw q
+ * [B, n, Hq, d], k, v [B, n, Hkv, d], its prepared keys kc, kr [B, Hkv, n, d]
+ * (hba_prep_keys), its selection, its output out and the output cotangent
+ * dout [B, n, Hq, d] (all contiguous, storage dtype), writes dq, dk, dv
+ * (contiguous, storage dtype) and ADDS the QKNorm gain gradients into
+ * dq_gain fp32 [Hq] and dk_gain fp32 [Hkv] (q_gain == NULL: no QKNorm, the
+ * gain outputs are ignored).  scale is the union scale of the forward.
+ * Arithmetic is fp32.  Same shape rules as hba_attn_fwd; G = Hq/Hkv <= 16.
+ */
+int hba_attn_bwd(int dtype, const void *q, const void *k, const void *v,
+                 const void *kc, const void *kr,
+                 const float *q_gain, const float *k_gain, float eps,
+                 const float *cos_tab, const float *sin_tab,
+                 const int32_t *idx, const int32_t *cnt,
+                 const void *out, const void *dout,
+                 int64_t B, int64_t n, int64_t Hq, int64_t Hkv, int64_t d,
+                 int64_t S, int64_t W, int64_t Bk, int64_t k_blocks, float scale,
+                 void *workspace, size_t ws_bytes,
+                 void *dq, void *dk, void *dv, float *dq_gain, float *dk_gain, void *stream);
+
+/* Scratch bytes hba_attn_bwd needs: the QKNorm'd and rotated query rows
+ * (2*B*n*Hq*d fp32) and the per-row LSE and <dout, out> (2*B*Hq*n fp32). */
+int hba_attn_bwd_workspace_size(int64_t B, int64_t n, int64_t Hq, int64_t d, size_t *bytes);
+
 #ifdef __cplusplus
 }
 #endif

@@ -20,6 +20,7 @@ What it restates (reference file:line):
   hba_attention_dense (forward)         src/hba/attention.py:306-356   (row-sampled)
   hba_attention_eval (flat and hier)    src/hba/attention.py:610-713   (row-sampled)
   equiv=True (uniform-RoPE causal)      src/hba/attention.py:330-336, 634-649 (row-sampled)
+  backward of the union attention       autograd of src/hba/attention.py:306-356 (selection fixed)
   decode step = prefill row L-1         (no reference function; defined from the above)
 
 Arrays are numpy float32 arrays that hold values of the storage dtype
@@ -42,7 +43,9 @@ Pinning (each check lives in tests/test_oracle_*.py):
     inputs, and planted mistakes that those checks must catch;
   * equiv rows against torch's scaled_dot_product_attention (a library
     routine, causal, GQA heads expanded) and against the union rows with no
-    sinks, a whole-sequence window and no routed blocks.
+    sinks, a whole-sequence window and no routed blocks;
+  * the backward against torch autograd (float64) of a torch restatement of
+    the masked dense union softmax, through QKNorm and RoPE.
 """
 import ctypes
 import math
@@ -524,6 +527,95 @@ def forward_equiv(q, k, v, cos, sin, cfg, q_gain, k_gain, eps, dtype, rows=None)
         kr = apply_rope(kc, cos[:n], sin[:n], dtype)
         outs.append(equiv_rows(qr, kr, _f32(v[b]), scale, rows))
     return np.stack(outs)
+
+
+def union_backward(q, k, v, cos, sin, scale, q_gain, k_gain, eps, idx, cnt, dout, S, W, Bk, qknorm=True):
+    """Gradients of the union attention output, float64, for ONE batch row
+    with the selection fixed (autograd of hba_attention_dense,
+    attention.py:306-356; the routing there is on detached q/k, :288-303).
+    q [n, Hq, d], k, v [n, Hkv, d] raw; cos/sin [>= n, d]; idx [Hkv, n, kk],
+    cnt [Hkv, n]; dout [n, Hq, d].  Returns (dq, dk, dv, dq_gain [Hq],
+    dk_gain [Hkv]); the gain gradients are zero without QKNorm.
+
+    With p the union softmax of query row (i, h), D = <dO, O>:
+      ds_j = p_j (<dO, v_j> - D) * scale,
+      d(q-side) += ds_j y_j, d(y_j) += ds_j x, dv_j += p_j dO
+    (x, y: NoPE rows for sinks and routed keys, rotated rows for the window),
+    then rope^T(zc, zr) = zc + zr cos + rot^T(zr sin) with rot^T(z) = [z2, -z1],
+    then the QKNorm backward dx = g/r y - [ms >= eps] x g <y, x> / (d r^3),
+    dg = sum <y, x> / r, r = sqrt(max(mean(x^2), eps))."""
+    f = np.float64
+    q, k, v, dout = (np.asarray(a, dtype=f) for a in (q, k, v, dout))
+    n, Hq, d = q.shape
+    Hkv = k.shape[1]
+    G = Hq // Hkv
+    nb = n // Bk
+    kk = idx.shape[2]
+    H2 = d // 2
+
+    def norm(x, gain):
+        ms = (x * x).mean(-1, keepdims=True)
+        r = np.sqrt(np.maximum(ms, eps))
+        return x / r * np.asarray(gain, dtype=f)[None, :, None], r, ms
+
+    if qknorm:
+        qc, rq, msq = norm(q, q_gain)
+        kc, rk, msk = norm(k, k_gain)
+    else:
+        qc, kc = q, k
+    c = np.asarray(cos, dtype=f)[:n, None, :]
+    sn = np.asarray(sin, dtype=f)[:n, None, :]
+
+    def rot(x):
+        return np.concatenate([-x[..., H2:], x[..., :H2]], -1)
+
+    def rotT(z):
+        return np.concatenate([z[..., H2:], -z[..., :H2]], -1)
+
+    qr = qc * c + rot(qc) * sn
+    kr = kc * c + rot(kc) * sn
+    dqc, dqr = np.zeros_like(qc), np.zeros_like(qc)
+    dkc, dkr, dv = np.zeros_like(kc), np.zeros_like(kc), np.zeros_like(v)
+    ar = np.arange(Bk)
+    for i in range(n):
+        js = np.arange(min(S, i + 1))
+        jw = np.arange(max(S, i - W + 1), i + 1)
+        for g in range(Hkv):
+            nc = min(max(int(cnt[g, i]), 0), kk)
+            blocks = np.array([b for b in idx[g, i, :nc] if 1 <= b < nb], dtype=np.int64)
+            jr = (blocks[:, None] * Bk + ar[None, :]).reshape(-1)
+            jn = np.concatenate([js, jr]).astype(np.int64)
+            hs = slice(g * G, (g + 1) * G)
+            Qn, Qr = qc[i, hs], qr[i, hs]
+            sc = np.concatenate([Qn @ kc[jn, g].T, Qr @ kr[jw, g].T], 1) * scale
+            p = np.exp(sc - sc.max(1, keepdims=True))
+            p /= p.sum(1, keepdims=True)
+            J = np.concatenate([jn, jw])
+            Vj = v[J, g]
+            dO = dout[i, hs]
+            Dv = (dO * (p @ Vj)).sum(1)
+            ds = p * (dO @ Vj.T - Dv[:, None]) * scale
+            m = len(jn)
+            dqc[i, hs] += ds[:, :m] @ kc[jn, g]
+            dqr[i, hs] += ds[:, m:] @ kr[jw, g]
+            np.add.at(dkc[:, g], jn, ds[:, :m].T @ Qn)
+            np.add.at(dkr[:, g], jw, ds[:, m:].T @ Qr)
+            np.add.at(dv[:, g], J, p.T @ dO)
+    yq = dqc + dqr * c + rotT(dqr * sn)
+    yk = dkc + dkr * c + rotT(dkr * sn)
+
+    def normT(x, y, gain, r, ms):
+        g_ = np.asarray(gain, dtype=f)[None, :, None]
+        yx = (y * x).sum(-1, keepdims=True)
+        dx = g_ / r * y - (ms >= eps) * x * g_ * yx / (d * r ** 3)
+        return dx, (yx / r).sum(axis=(0, 2))
+
+    if qknorm:
+        dq, dgq = normT(q, yq, q_gain, rq, msq)
+        dk, dgk = normT(k, yk, k_gain, rk, msk)
+    else:
+        dq, dgq, dk, dgk = yq, np.zeros(Hq), yk, np.zeros(Hkv)
+    return dq, dk, dv, dgq, dgk
 
 
 def decode_row(q_new, kc_seq, v_seq, cos, sin, cfg, S0_seq, q_gain, eps, dtype, scale):

@@ -471,6 +471,62 @@ def test_equiv_rejects_ragged_length(dev):
                                    prm, prm, None, equiv=True)
 
 
+# -------------------------------------------------------------- backward -----
+# gates.py:247 holds input gradients to 2e-3 relative to their magnitude
+# (fp32); bf16 storage of q/k/v and of the forward's QKNorm/RoPE rows moves
+# the recomputed probabilities by about one bf16 ulp, hence 5e-2 there.
+GRAD_TOL = {"f32": 2e-3, "bf16": 5e-2}
+
+
+@pytest.mark.parametrize("dt,qknorm,mode", [("f32", True, "dense"), ("f32", False, "eval"), ("bf16", True, "eval"),
+                                            ("f32", True, "equiv"), ("bf16", True, "hier")])
+def test_backward_matches_oracle(dev, dt, qknorm, mode):
+    """hba_attn_bwd through autograd of the drop-ins against the oracle's
+    float64 backward on the forward's own selection: dq, dk, dv and the
+    QKNorm gain gradients."""
+    n = 512
+    kw = dict(fanout=4, beam=2) if mode == "hier" else {}
+    cfg, x, prm, cos, sin = make(dev, dt, n=n, W=128, k=4, S=4, qknorm=qknorm, **kw)
+    q, k, v = (x[t].clone().requires_grad_(True) for t in ("q", "k", "v"))
+    gq = x["q_gain"].clone().requires_grad_(qknorm)
+    gk = x["k_gain"].clone().requires_grad_(qknorm)
+    qkn = synth.Params(gq, gk, x["probes"], x["proj"])
+    if mode == "dense":
+        out = hba_amd.hba_attention_dense(q, k, v, cos, sin, cfg, qkn, qkn)[0]
+    else:
+        out = hba_amd.hba_attention_eval(q, k, v, cos, sin, cfg, qkn, qkn, None, hier=mode == "hier",
+                                         equiv=mode == "equiv")
+    dout = torch.randn(out.shape, generator=torch.Generator().manual_seed(7)).to(out.dtype).to(dev)
+    out.backward(dout)
+    torch.cuda.synchronize()
+    if mode == "equiv":
+        idx = np.zeros((cfg.n_kv, n, 1), dtype=np.int32)
+        cnt = np.zeros((cfg.n_kv, n), dtype=np.int32)
+        S, W = 0, n
+    else:
+        with torch.no_grad():
+            r = hba_amd.forward_stages(x["q"], x["k"], x["v"], cos, sin, cfg, qkn, qkn, hier=mode == "hier",
+                                       dense_route=mode == "dense")
+            assert torch.equal(r["out"], out.detach())          # the same forward, the same selection
+        idx, cnt = r["idx"][0].cpu().numpy(), r["cnt"][0].cpu().numpy()
+        S, W = cfg.sinks, cfg.window
+    scale = hba_amd.union_scale(cfg, cfg.head_dim, n)
+    ref = O.union_backward(f(x["q"])[0], f(x["k"])[0], f(x["v"])[0], f(cos), f(sin), scale, f(x["q_gain"]),
+                           f(x["k_gain"]), 1e-6, idx, cnt, f(dout)[0], S, W, 64, qknorm)
+    got = [f(q.grad)[0], f(k.grad)[0], f(v.grad)[0]]
+    if qknorm:
+        got += [f(gq.grad), f(gk.grad)]
+    for name, a, b in zip(["dq", "dk", "dv", "dq_gain", "dk_gain"], got, ref):
+        rel = np.abs(a - b).max() / max(np.abs(b).max(), 1e-6)
+        assert rel < GRAD_TOL[dt], (name, rel)
+
+
+def test_backward_no_grad_inputs_stays_forward_only(dev):
+    cfg, x, prm, cos, sin = make(dev, "bf16", n=256, W=64, k=2)
+    out = hba_amd.hba_attention_eval(x["q"], x["k"], x["v"], cos, sin, cfg, prm, prm, None)
+    assert out.grad_fn is None
+
+
 def test_causality(dev):
     """gates.py:101-126: randomising tokens after t leaves rows <= t unchanged."""
     cfg, x, prm, cos, sin = make(dev, "bf16", n=2048, W=256, k=8)

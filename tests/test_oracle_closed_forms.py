@@ -401,6 +401,79 @@ def test_forward_equiv_applies_qknorm_rope_and_scale():
         assert np.abs(got - want).max() < 1e-12
 
 
+def _torch_union_forward(q, k, v, cos, sin, scale, gq, gk, eps, idx, cnt, S, W, Bk, qknorm):
+    """hba_attention_dense's masked dense union softmax (attention.py:306-356)
+    in torch float64 with a given selection, for autograd."""
+    import torch
+    n, Hq, d = q.shape
+    Hkv = k.shape[1]
+    G = Hq // Hkv
+
+    def norm(x, g):
+        return x / (x * x).mean(-1, keepdim=True).clamp_min(eps).sqrt() * g[None, :, None]
+
+    def rope(x):
+        c, s = cos[:n, None, :], sin[:n, None, :]
+        return x * c + torch.cat([-x[..., d // 2:], x[..., : d // 2]], -1) * s
+
+    qc, kc = (norm(q, gq), norm(k, gk)) if qknorm else (q, k)
+    qr, kr = rope(qc), rope(kc)
+    i = torch.arange(n)[:, None]
+    j = torch.arange(n)[None, :]
+    sink = (j < S) & (j <= i)
+    win = (j >= S) & (j <= i) & (j > i - W)
+    outs = []
+    for h in range(Hq):
+        g = h // G
+        rout = torch.zeros(n, n, dtype=torch.bool)
+        for ii in range(n):
+            for b in idx[g, ii, : cnt[g, ii]]:
+                if 1 <= b < n // Bk:
+                    rout[ii, b * Bk:(b + 1) * Bk] = True
+        sN = qc[:, h] @ kc[:, g].T * scale
+        sR = qr[:, h] @ kr[:, g].T * scale
+        sc = torch.where(win, sR, sN).masked_fill(~(sink | win | rout), float("-inf"))
+        outs.append(sc.softmax(-1) @ v[:, g])
+    return torch.stack(outs, 1)
+
+
+@pytest.mark.parametrize("qknorm", [True, False])
+def test_union_backward_matches_torch_autograd(qknorm):
+    """The oracle backward against torch autograd (float64) of the masked
+    dense union softmax through QKNorm and RoPE, on a selection with routed
+    blocks, sinks and a window."""
+    import torch
+    rs = RS(21)
+    n, Hq, Hkv, d, Bk, S, W, kk = 128, 4, 2, 8, 16, 2, 32, 3
+    q = rs.standard_normal((n, Hq, d)) * 1.5
+    k = rs.standard_normal((n, Hkv, d)) * 1.5
+    v = rs.standard_normal((n, Hkv, d))
+    dout = rs.standard_normal((n, Hq, d))
+    gq = rs.uniform(0.5, 2.0, Hq)
+    gk = rs.uniform(0.5, 2.0, Hkv)
+    cos, sin = O.rope_tables(n, d, 1e4)
+    idx = np.full((Hkv, n, kk), -1, dtype=np.int32)
+    cnt = np.zeros((Hkv, n), dtype=np.int32)
+    for g in range(Hkv):
+        for i in range(n):
+            bm = O.cand_bmax(i, Bk, W)
+            if bm >= 1:
+                picks = rs.permutation(np.arange(1, bm + 1))[:kk]
+                idx[g, i, : len(picks)] = picks
+                cnt[g, i] = len(picks)
+    assert cnt.max() == kk
+    scale = 0.3
+    got = O.union_backward(q, k, v, cos, sin, scale, gq, gk, 1e-6, idx, cnt, dout, S, W, Bk, qknorm)
+    T = [torch.tensor(a, dtype=torch.float64, requires_grad=True) for a in (q, k, v, gq, gk)]
+    out = _torch_union_forward(*T[:3], torch.tensor(cos, dtype=torch.float64),
+                               torch.tensor(sin, dtype=torch.float64), scale, T[3], T[4], 1e-6, idx, cnt, S, W,
+                               Bk, qknorm)
+    out.backward(torch.tensor(dout))
+    for a, t in zip(got, T):
+        ref = t.grad.numpy() if t.grad is not None else np.zeros(t.shape)
+        assert np.abs(a - ref).max() <= 1e-9 * max(1.0, np.abs(ref).max())
+
+
 def test_planted_mistakes_are_caught(monkeypatch):
     cfg, q, k, v, pr, pj, qg, kg, cos, sin = _tiny_problem(n=192)
     rows = [1, 40, 100, 150, 191]
