@@ -325,6 +325,45 @@ def bench_equiv32k(dev):
             "achieved_TFLOPs": round(tflops, 1), "mfma_frac": round(tflops / PEAK_BF16_TFLOPS, 4)}
 
 
+def bench_bwd32k(dev, reps=3):
+    """Backward of the HBA layer at 32K (the layer32k workload, bf16): the
+    forward through hba_attention_dense with q, k, v and the QKNorm gains
+    requiring grad, then hba_attn_bwd timed alone (HIP events around
+    out.backward, graph retained).  FLOP counted as 10*d per attended
+    (query, head, key): S, dP, dQ, dK and dV, 2.5x the forward's count."""
+    import torch
+    import hba_amd
+    from hba_amd import synth
+    cfg, x, prm, cos, sin = layer_setup(dev)
+    q, k, v = (x[t].clone().requires_grad_(True) for t in ("q", "k", "v"))
+    gq = x["q_gain"].clone().requires_grad_(True)
+    gk = x["k_gain"].clone().requires_grad_(True)
+    qkn = synth.Params(gq, gk, x["probes"], x["proj"])
+    out = hba_amd.hba_attention_dense(q, k, v, cos, sin, cfg, qkn, qkn)[0]
+    dout = torch.randn(out.shape, generator=torch.Generator().manual_seed(1)).to(out.dtype).to(dev)
+    out.backward(dout, retain_graph=True)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        out.backward(dout, retain_graph=True)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    w = WORKLOAD
+    # attention_flops counts 4*d per attended (query, head, key); the backward 10*d
+    flop = 2.5 * synth.attention_flops(w["batch"], w["seq_len"], w["q_heads"], w["head_dim"], w["sinks"],
+                                       w["window"], w["block"], w["top_k"])
+    tflops = flop / (ms * 1e-3) / 1e12
+    return {"metric": "HBA layer backward tokens/s at 32K (dq, dk, dv, QKNorm gain grads; selection fixed)",
+            "config": {"workload": "hba_layer_bwd_32k", "batch": 1, "seq_len": w["seq_len"], "q_heads": w["q_heads"],
+                       "kv_heads": w["kv_heads"], "head_dim": w["head_dim"], "top_k": w["top_k"]},
+            "tokens_per_s": round(w["seq_len"] / (ms * 1e-3), 1), "ms": round(ms, 3), "flop": flop,
+            "achieved_TFLOPs": round(tflops, 2), "mfma_frac": round(tflops / PEAK_BF16_TFLOPS, 5),
+            "kernels": "bwd_dq (one wave per query and KV head, fp32 VALU) + bwd_dkv (one workgroup per KV head "
+                       "and 64-key block, fp32 VALU)"}
+
+
 def bench_hier128k(dev):
     """Hierarchical tree selection at 128K (B=1, 14/2 heads, d=64, 2048 blocks,
     super-summaries over 16 blocks, beam 8, top-16, log-length temperature
@@ -451,7 +490,8 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run 3 plain device copies of MIB MiB (counter calibration) and exit")
-    ap.add_argument("--config", choices=["layer32k", "hier128k", "donor", "equiv32k"], default="layer32k",
+    ap.add_argument("--config", choices=["layer32k", "hier128k", "donor", "equiv32k", "bwd32k"],
+                    default="layer32k",
                     help="layer32k: the headline line (default); hier128k / donor / equiv32k: the other "
                          "measured workloads, one JSON line each")
     a = ap.parse_args()
@@ -473,7 +513,8 @@ def main():
     import torch
     dev = torch.device("cuda:0")
     if a.config != "layer32k":
-        line = {"hier128k": bench_hier128k, "donor": bench_donor, "equiv32k": bench_equiv32k}[a.config](dev)
+        line = {"hier128k": bench_hier128k, "donor": bench_donor, "equiv32k": bench_equiv32k,
+                "bwd32k": bench_bwd32k}[a.config](dev)
         line.update({"n_gpus": 1, "dtype": "bf16", "data": "synthetic"})
         print(json.dumps(line))
         return
