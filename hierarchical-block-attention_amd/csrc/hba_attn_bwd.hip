@@ -36,9 +36,34 @@ namespace bw {
 
 constexpr int BW_GMAX = 16;
 
+// Cross-lane sums on DPP (no LDS round trip): quad xor 1, quad xor 2,
+// half-row mirror, row mirror leave every lane of a 16-lane row with the
+// row's sum; the four rows are then added from their first lanes.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float quad_sum(float v) {
+    v += dpp_mov<0xb1>(v);    // quad_perm [1,0,3,2]
+    v += dpp_mov<0x4e>(v);    // quad_perm [2,3,0,1]
+    return v;
+}
+__device__ __forceinline__ float oct_sum(float v) {
+    v = quad_sum(v);
+    return v + dpp_mov<0x141>(v);   // row_half_mirror: the other quad of the 8
+}
+__device__ __forceinline__ float row16_sum(float v) {
+    v = oct_sum(v);
+    return v + dpp_mov<0x140>(v);   // row_mirror: the other 8 of the 16
+}
 template <int D>
 __device__ __forceinline__ float wsum(float v) {
-    return wave_sum(v);
+    v = row16_sum(v);
+    const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return (a + b) + (c + d);
 }
 
 // element e of lane l is t = l + 64 e; GM = the largest group size held
@@ -50,7 +75,8 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(
     const int32_t *__restrict__ idx, const int32_t *__restrict__ cnt, const typename St<DT>::T *__restrict__ out,
     const typename St<DT>::T *__restrict__ dout, int B, int64_t n, int Hq, int Hkv, int S, int64_t W, int kk,
     float scale, float *__restrict__ qc_ws, float *__restrict__ qr_ws, float *__restrict__ lse_ws,
-    float *__restrict__ dd_ws, typename St<DT>::T *__restrict__ dq, float *__restrict__ dq_gain) {
+    float *__restrict__ dd_ws, float *__restrict__ sink_acc, typename St<DT>::T *__restrict__ dq,
+    float *__restrict__ dq_gain) {
     constexpr int E = D / 64;
     const int lane = threadIdx.x & 63;
     const int64_t wid = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -60,6 +86,14 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(
     const int b = (int)(wid / (n * Hkv));
     const int G = Hq / Hkv;
     const int64_t nb = n / 64;
+    if (i < 64) {   // clear key row i of the sink accumulators (bwd_sink adds into them next)
+        float *acc = sink_acc + (((int64_t)b * Hkv + g) * 2 * 64 + i) * D;
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            acc[lane + 64 * e] = 0.0f;
+            acc[64 * D + lane + 64 * e] = 0.0f;
+        }
+    }
 
     float xr[GM][E], qcv[GM][E], qrv[GM][E], dov[GM][E];
     float rr[GM], msr[GM], dd[GM];
@@ -235,7 +269,9 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(
 }
 
 // ------------------------------------------------------------- bwd_dkv ----
-// Lane (kl, c) of wave w: key j = 64 blk + KW w + kl, elements 16c .. 16c+15.
+// Lane (kl, c) = (lane / NC, lane % NC) of wave w: key j = 64 blk + KW w + kl,
+// elements 16c .. 16c+15; a key's chunks sit on NC adjacent lanes, so its
+// sums are DPP steps within a quad (NC = 4) or an 8-lane group (NC = 8).
 template <int D>
 struct DkvCfg {
     static constexpr int NC = D / 16;          // 16-element chunks per key
@@ -246,16 +282,110 @@ struct DkvCfg {
 
 template <int D>
 __device__ __forceinline__ float chunk_sum(float v) {
-    constexpr int KW = DkvCfg<D>::KW;
-#pragma unroll
-    for (int o = KW; o < 64; o <<= 1) v += __shfl_xor(v, o, 64);
-    return v;
+    if constexpr (DkvCfg<D>::NC == 4) return quad_sum(v);
+    else return oct_sum(v);
 }
 
 template <int DT>
 __device__ __forceinline__ void ld16(const typename St<DT>::T *p, float (&x)[16]) {
 #pragma unroll
     for (int e = 0; e < 16; ++e) x[e] = St<DT>::ld(p, e);
+}
+
+// nrows query rows (row_of(r)), all G heads of KV head g, against this lane's
+// key j: accumulates gk += ds * x (x = the stored query rows qx_ws: NoPE or
+// rotated) and gv += p * dO.  mode 0: window rows (j >= S, j <= i <= j+W-1),
+// 1: sink rows (j < S, i >= j), 2: routed rows (every key of the block).  The
+// next row's operands are loaded while the current one is computed.
+template <int DT, int D, typename RowOf>
+__device__ __forceinline__ void dkv_rows(RowOf row_of, int64_t nrows, int mode, int64_t j, int S, int64_t W,
+                                         const float *qx_ws, const typename St<DT>::T *dout,
+                                         const float *lse_ws, const float *dd_ws, int b, int64_t n, int Hq,
+                                         int g, int G, int c, float scale, const float (&ky)[16],
+                                         const float (&vv)[16], float (&gk)[16], float (&gv)[16]) {
+    const int64_t total = nrows * G;
+    if (total <= 0) return;
+    auto load = [&](int64_t u, float (&x)[16], float (&dv)[16], float &lse, float &dd, int64_t &i) {
+        i = row_of(u / G);
+        const int h = g * G + (int)(u % G);
+        const int64_t ro = (((int64_t)b * n + i) * Hq + h) * D + 16 * c;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) x[e] = qx_ws[ro + e];
+        ld16<DT>(dout + ro, dv);
+        const int64_t so = ((int64_t)b * Hq + h) * n + i;
+        lse = lse_ws[so];
+        dd = dd_ws[so];
+    };
+    auto compute = [&](const float (&x)[16], const float (&dov)[16], float lse, float dd, int64_t i) {
+        const bool valid = (mode == 0) ? (j >= S && i >= j && i <= j + W - 1) : (mode == 1) ? (j < S && i >= j)
+                                                                                           : true;
+        float pr = 0.0f, pd = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            pr = fmaf(x[e], ky[e], pr);
+            pd = fmaf(dov[e], vv[e], pd);
+        }
+        const float sc = chunk_sum<D>(pr) * scale;
+        const float dp = chunk_sum<D>(pd);
+        const float p = valid ? __expf(sc - lse) : 0.0f;
+        const float ds = p * (dp - dd) * scale;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            gv[e] = fmaf(p, dov[e], gv[e]);
+            gk[e] = fmaf(ds, x[e], gk[e]);
+        }
+    };
+    float xa[16], da[16], xb[16], db[16], la, ldd, lb, ldb;
+    int64_t ia, ib;
+    load(0, xa, da, la, ldd, ia);
+    for (int64_t u = 0; u < total; u += 2) {
+        if (u + 1 < total) load(u + 1, xb, db, lb, ldb, ib);
+        compute(xa, da, la, ldd, ia);
+        if (u + 1 >= total) break;
+        if (u + 2 < total) load(u + 2, xa, da, la, ldd, ia);
+        compute(xb, db, lb, ldb, ib);
+    }
+}
+
+// Sink keys (block 0, j < S) against query rows [r0, r0 + SINK_ROWS): one
+// workgroup per (b, g, row range), the lanes laid out as in bwd_dkv; the
+// partial gradients are added (fp32 atomics) into sink_acc [B, Hkv, 2, 64, D]
+// (dk then dv), which bwd_dkv's block-0 workgroup reads.
+constexpr int SINK_ROWS = 256;
+
+template <int DT, int D>
+__global__ __launch_bounds__(DkvCfg<D>::NT) void bwd_sink_kernel(
+    const typename St<DT>::T *__restrict__ kc, const typename St<DT>::T *__restrict__ v,
+    const typename St<DT>::T *__restrict__ dout, int64_t n, int Hq, int Hkv, int S, int nsplit, float scale,
+    const float *__restrict__ qc_ws, const float *__restrict__ lse_ws, const float *__restrict__ dd_ws,
+    float *__restrict__ sink_acc) {
+    using C = DkvCfg<D>;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int kl = lane / C::NC, c = lane % C::NC;
+    const int split = (int)(blockIdx.x % nsplit);
+    const int g = (int)((blockIdx.x / nsplit) % Hkv);
+    const int b = (int)(blockIdx.x / ((int64_t)nsplit * Hkv));
+    const int G = Hq / Hkv;
+    if (C::KW * w >= S) return;                                   // wave-uniform; no barrier follows
+    const int64_t j = C::KW * w + kl;
+    const int64_t bg = (int64_t)b * Hkv + g;
+    float kcv[16], vv[16], gkc[16], gv[16];
+    ld16<DT>(kc + (bg * n + j) * D + 16 * c, kcv);
+    ld16<DT>(v + (((int64_t)b * n + j) * Hkv + g) * D + 16 * c, vv);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) gkc[e] = gv[e] = 0.0f;
+    const int64_t r0 = (int64_t)split * SINK_ROWS;
+    const int64_t r1 = min(n, r0 + SINK_ROWS);
+    dkv_rows<DT, D>([&](int64_t r) { return r0 + r; }, r1 - r0, 1, j, S, 0, qc_ws, dout, lse_ws, dd_ws, b, n, Hq, g,
+                    G, c, scale, kcv, vv, gkc, gv);
+    if (j < S) {
+        float *acc = sink_acc + (bg * 2 * 64 + j) * D + 16 * c;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            atomicAdd(acc + e, gkc[e]);
+            atomicAdd(acc + 64 * D + e, gv[e]);
+        }
+    }
 }
 
 template <int DT, int D>
@@ -266,12 +396,13 @@ __global__ __launch_bounds__(DkvCfg<D>::NT) void bwd_dkv_kernel(
     const int32_t *__restrict__ idx, const int32_t *__restrict__ cnt, const typename St<DT>::T *__restrict__ dout,
     int64_t n, int Hq, int Hkv, int S, int64_t W, int kk, float scale, const float *__restrict__ qc_ws,
     const float *__restrict__ qr_ws, const float *__restrict__ lse_ws, const float *__restrict__ dd_ws,
-    typename St<DT>::T *__restrict__ dk, typename St<DT>::T *__restrict__ dv, float *__restrict__ dk_gain) {
+    const float *__restrict__ sink_acc, typename St<DT>::T *__restrict__ dk, typename St<DT>::T *__restrict__ dv,
+    float *__restrict__ dk_gain) {
     using C = DkvCfg<D>;
     __shared__ int rows[C::NT];
     __shared__ int wcount[C::WAVES];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int kl = lane % C::KW, c = lane / C::KW;
+    const int kl = lane / C::NC, c = lane % C::NC;
     const int64_t nb = n / 64;
     const int blk = (int)(blockIdx.x % nb);
     const int g = (int)((blockIdx.x / nb) % Hkv);
@@ -288,46 +419,22 @@ __global__ __launch_bounds__(DkvCfg<D>::NT) void bwd_dkv_kernel(
 #pragma unroll
     for (int e = 0; e < 16; ++e) gkc[e] = gkr[e] = gv[e] = 0.0f;
 
-    // one query row (i, all G heads) against this lane's key; rope selects
-    // the rotated operands; valid is the lane's own mask
-    auto row_update = [&](int64_t i, bool rope, bool valid) {
-        for (int hh = 0; hh < G; ++hh) {
-            const int h = g * G + hh;
-            const int64_t ro = (((int64_t)b * n + i) * Hq + h) * D + 16 * c;
-            float x[16], dov[16];
-#pragma unroll
-            for (int e = 0; e < 16; ++e) x[e] = (rope ? qr_ws : qc_ws)[ro + e];
-            ld16<DT>(dout + ro, dov);
-            const int64_t so = ((int64_t)b * Hq + h) * n + i;
-            const float lse = lse_ws[so], ddv = dd_ws[so];
-            float pr = 0.0f, pd = 0.0f;
-#pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                pr = fmaf(x[e], rope ? krv[e] : kcv[e], pr);
-                pd = fmaf(dov[e], vv[e], pd);
-            }
-            const float s = chunk_sum<D>(pr) * scale;
-            const float dp = chunk_sum<D>(pd);
-            const float p = valid ? __expf(s - lse) : 0.0f;
-            const float ds = p * (dp - ddv) * scale;
-#pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                gv[e] = fmaf(p, dov[e], gv[e]);
-                if (rope) gkr[e] = fmaf(ds, x[e], gkr[e]);
-                else gkc[e] = fmaf(ds, x[e], gkc[e]);
-            }
-        }
-    };
-
-    // window rows: key j >= S is in the window of queries j .. j + W - 1
+    // window rows (rotated): key j >= S is in the window of queries j .. j + W - 1
     {
         const int64_t j0 = 64 * (int64_t)blk + C::KW * w;           // the wave's first key
         const int64_t ihi = min(n - 1, j0 + C::KW - 1 + W - 1);
-        for (int64_t i = j0; i <= ihi; ++i) row_update(i, true, j >= S && i >= j && i <= j + W - 1);
+        dkv_rows<DT, D>([&](int64_t r) { return j0 + r; }, ihi - j0 + 1, 0, j, S, W, qr_ws, dout, lse_ws, dd_ws, b,
+                        n, Hq, g, G, c, scale, krv, vv, gkr, gv);
     }
-    // sink rows (NoPE): key j < S is attended by every query i >= j
-    if (blk == 0 && C::KW * w < S) {
-        for (int64_t i = C::KW * w; i < n; ++i) row_update(i, false, j < S && i >= j);
+    // sink keys (NoPE): every query i >= j; their rows were split over the
+    // bwd_sink workgroups, whose sums are added here
+    if (blk == 0 && j < S) {
+        const float *acc = sink_acc + (bg * 2 * 64 + j) * D + 16 * c;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            gkc[e] += acc[e];
+            gv[e] += acc[64 * D + e];
+        }
     }
     // routed rows (NoPE): the queries whose selection holds this block
     if (blk >= 1) {
@@ -349,7 +456,8 @@ __global__ __launch_bounds__(DkvCfg<D>::NT) void bwd_dkv_kernel(
             }
             if (picked) rows[base + __popcll(bal & ((1ull << lane) - 1ull))] = (int)i;
             __syncthreads();
-            for (int e = 0; e < tot; ++e) row_update(rows[e], false, true);
+            dkv_rows<DT, D>([&](int64_t r) { return (int64_t)rows[r]; }, tot, 2, j, S, W, qc_ws, dout, lse_ws, dd_ws,
+                            b, n, Hq, g, G, c, scale, kcv, vv, gkc, gv);
             __syncthreads();                                     // rows[] and wcount[] reused
         }
     }
@@ -363,7 +471,7 @@ __global__ __launch_bounds__(DkvCfg<D>::NT) void bwd_dkv_kernel(
         for (int e = 0; e < 16; ++e) zs[e] = gkr[e] * St<DT>::rnd(sp[e]);
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
-            const float pv = __shfl_xor(zs[e], 32, 64);             // chunk c ^ (NC/2): element t ^ (D/2)
+            const float pv = __shfl_xor(zs[e], C::NC / 2, 64);      // chunk c ^ (NC/2): element t ^ (D/2)
             y[e] = gkc[e] + gkr[e] * St<DT>::rnd(cp[e]) + ((c < C::NC / 2) ? pv : -pv);
         }
     }
@@ -399,7 +507,7 @@ using namespace hba;
 
 extern "C" int hba_attn_bwd_workspace_size(int64_t B, int64_t n, int64_t Hq, int64_t d, size_t *bytes) {
     if (!bytes || B <= 0 || n <= 0 || Hq <= 0 || d <= 0) return HBA_ERR_INVALID_ARG;
-    *bytes = (size_t)(2 * B * n * Hq * d + 2 * B * Hq * n) * 4;
+    *bytes = (size_t)(2 * B * n * Hq * d + 2 * B * Hq * n + B * Hq * 2 * 64 * d) * 4;
     return HBA_OK;
 }
 
@@ -428,10 +536,13 @@ extern "C" int hba_attn_bwd(int dtype, const void *q, const void *k, const void 
     float *qr_ws = qc_ws + B * n * Hq * d;
     float *lse_ws = qr_ws + B * n * Hq * d;
     float *dd_ws = lse_ws + B * Hq * n;
+    float *sink_acc = dd_ws + B * Hq * n;                          // [B, Hkv, 2, 64, d] (Hkv <= Hq)
     hipStream_t s = (hipStream_t)stream;
     const int64_t nwaves = B * Hkv * n;
     const int64_t g1 = (nwaves + 3) / 4;
     const int64_t g2 = B * Hkv * (n / 64);
+    const int nsplit = (int)((n + bw::SINK_ROWS - 1) / bw::SINK_ROWS);
+    const int64_t gs = B * Hkv * nsplit;
 #define HBA_BWD(DT, D)                                                                                          \
     do {                                                                                                        \
         using T = St<DT>::T;                                                                                    \
@@ -439,16 +550,22 @@ extern "C" int hba_attn_bwd(int dtype, const void *q, const void *k, const void 
             hipLaunchKernelGGL((bw::bwd_dq_kernel<DT, D, 8>), dim3((unsigned)g1), dim3(256), 0, s,               \
                                (const T *)q, (const T *)kc, (const T *)kr, (const T *)v, q_gain, eps, cos_tab,   \
                                sin_tab, idx, cnt, (const T *)out, (const T *)dout, (int)B, n, (int)Hq, (int)Hkv, \
-                               (int)S, W, (int)k_blocks, scale, qc_ws, qr_ws, lse_ws, dd_ws, (T *)dq, dq_gain);  \
+                               (int)S, W, (int)k_blocks, scale, qc_ws, qr_ws, lse_ws, dd_ws, sink_acc, (T *)dq,   \
+                               dq_gain);                                                                        \
         else                                                                                                    \
             hipLaunchKernelGGL((bw::bwd_dq_kernel<DT, D, bw::BW_GMAX>), dim3((unsigned)g1), dim3(256), 0, s,     \
                                (const T *)q, (const T *)kc, (const T *)kr, (const T *)v, q_gain, eps, cos_tab,   \
                                sin_tab, idx, cnt, (const T *)out, (const T *)dout, (int)B, n, (int)Hq, (int)Hkv, \
-                               (int)S, W, (int)k_blocks, scale, qc_ws, qr_ws, lse_ws, dd_ws, (T *)dq, dq_gain);  \
+                               (int)S, W, (int)k_blocks, scale, qc_ws, qr_ws, lse_ws, dd_ws, sink_acc, (T *)dq,   \
+                               dq_gain);                                                                        \
+        if (S > 0)                                                                                              \
+            hipLaunchKernelGGL((bw::bwd_sink_kernel<DT, D>), dim3((unsigned)gs), dim3(bw::DkvCfg<D>::NT), 0, s,  \
+                               (const T *)kc, (const T *)v, (const T *)dout, n, (int)Hq, (int)Hkv, (int)S,       \
+                               nsplit, scale, qc_ws, lse_ws, dd_ws, sink_acc);                                   \
         hipLaunchKernelGGL((bw::bwd_dkv_kernel<DT, D>), dim3((unsigned)g2), dim3(bw::DkvCfg<D>::NT), 0, s,       \
                            (const T *)k, (const T *)kc, (const T *)kr, (const T *)v, k_gain, eps, cos_tab,       \
                            sin_tab, idx, cnt, (const T *)dout, n, (int)Hq, (int)Hkv, (int)S, W, (int)k_blocks,   \
-                           scale, qc_ws, qr_ws, lse_ws, dd_ws, (T *)dk, (T *)dv, dk_gain);                       \
+                           scale, qc_ws, qr_ws, lse_ws, dd_ws, sink_acc, (T *)dk, (T *)dv, dk_gain);             \
     } while (0)
     HBA_DISPATCH_DT_D(dtype, d, HBA_BWD);
 #undef HBA_BWD

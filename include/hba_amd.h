@@ -277,7 +277,8 @@ int hba_attn_bwd(int dtype, const void *q, const void *k, const void *v,
                  void *dq, void *dk, void *dv, float *dq_gain, float *dk_gain, void *stream);
 
 /* Scratch bytes hba_attn_bwd needs: the QKNorm'd and rotated query rows
- * (2*B*n*Hq*d fp32) and the per-row LSE and <dout, out> (2*B*Hq*n fp32). */
+ * (2*B*n*Hq*d fp32), the per-row LSE and <dout, out> (2*B*Hq*n fp32) and the
+ * sink-key accumulators (2*B*Hq*64*d fp32). */
 int hba_attn_bwd_workspace_size(int64_t B, int64_t n, int64_t Hq, int64_t d, size_t *bytes);
 
 #ifdef __cplusplus
