@@ -268,6 +268,281 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(
     }
 }
 
+// -------------------------------------------------- bwd_dq on MFMA (bf16) ----
+// The same gradient as bwd_dq_kernel, one wave per (b, i, g), with the keys
+// taken in 64-key units (the sink unit, the window pages, the routed blocks)
+// and every product on v_mfma_f32_16x16x32_bf16; the G heads are the 16
+// columns (l16 = head):
+//   S^T  = K . Q^T     (A: K rows in the permuted slot order kslot)
+//   dP^T = V . dO^T    (A: V rows, same order)
+//   dQ^T += K^T . dS^T (A: the transposed keys kct / krt; B: dS^T straight
+//                       from the accumulators, which the slot order puts in
+//                       the B-operand layout)
+// Lane (l16, lg) holds, per M-tile mt, keys 32(mt>>1) + 8lg + 4(mt&1) + e of
+// column l16, and of dQ^T the elements d = 16 dt + 4 lg + e.
+typedef unsigned int u32x4b __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ bf16x8 ld_b8(const bf16_t *p) {
+    return __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4b *>(p));
+}
+__device__ __forceinline__ bf16x8 pack_b8(const float (&x)[8]) {
+    u32x4b u;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) u[e] = (uint32_t)f2bf(x[2 * e]) | ((uint32_t)f2bf(x[2 * e + 1]) << 16);
+    return __builtin_bit_cast(bf16x8, u);
+}
+__device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ int kslot(int mt, int r) { return 32 * (mt >> 1) + 8 * (r >> 2) + 4 * (mt & 1) + (r & 3); }
+__device__ __forceinline__ int kkey(int mt, int lg, int e) { return 32 * (mt >> 1) + 8 * lg + 4 * (mt & 1) + e; }
+__device__ __forceinline__ float col_max(float v) {   // over the 4 lanes of a column (lg)
+    v = fmaxf(v, __shfl_xor(v, 16, 64));
+    return fmaxf(v, __shfl_xor(v, 32, 64));
+}
+__device__ __forceinline__ float col_sum(float v) {
+    v += __shfl_xor(v, 16, 64);
+    return v + __shfl_xor(v, 32, 64);
+}
+
+// transposed prepared keys, kct / krt [B, Hkv, d, n]: one workgroup per 64-key tile
+template <int D>
+__global__ __launch_bounds__(256) void bwd_kt_kernel(const bf16_t *__restrict__ kc, const bf16_t *__restrict__ kr,
+                                                     bf16_t *__restrict__ kct, bf16_t *__restrict__ krt, int64_t n) {
+    __shared__ bf16_t tile[64][D + 2];
+    const int64_t nt = n / 64;
+    const int64_t bg = blockIdx.x / nt, kb = (blockIdx.x % nt) * 64;
+    for (int pass = 0; pass < 2; ++pass) {
+        const bf16_t *src = (pass ? kr : kc) + (bg * n + kb) * D;
+        bf16_t *dst = (pass ? krt : kct) + bg * D * n + kb;
+        for (int e = threadIdx.x; e < 64 * D; e += 256) tile[e / D][e % D] = src[e];
+        __syncthreads();
+        for (int e = threadIdx.x; e < 64 * D; e += 256) dst[(int64_t)(e / 64) * n + (e % 64)] = tile[e % 64][e / 64];
+        __syncthreads();
+    }
+}
+
+template <int D>
+__global__ __launch_bounds__(256) void bwd_dq_mfma_kernel(
+    const bf16_t *__restrict__ q, const bf16_t *__restrict__ kc, const bf16_t *__restrict__ kr,
+    const bf16_t *__restrict__ kct, const bf16_t *__restrict__ krt, const bf16_t *__restrict__ v,
+    const float *__restrict__ qgain, float eps, const float *__restrict__ cosT, const float *__restrict__ sinT,
+    const int32_t *__restrict__ idx, const int32_t *__restrict__ cnt, const bf16_t *__restrict__ out,
+    const bf16_t *__restrict__ dout, int B, int64_t n, int Hq, int Hkv, int S, int64_t W, int kk, float scale,
+    float *__restrict__ qc_ws, float *__restrict__ qr_ws, float *__restrict__ lse_ws, float *__restrict__ dd_ws,
+    float *__restrict__ sink_acc, bf16_t *__restrict__ dq, float *__restrict__ dq_gain) {
+    constexpr int NKS = D / 32, NDT = D / 16, E = D / 64;
+    const int lane = threadIdx.x & 63, l16 = lane & 15, lg = lane >> 4;
+    const int64_t wid = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (wid >= (int64_t)B * Hkv * n) return;                      // wave-uniform; no barrier follows
+    const int64_t i = wid % n;
+    const int g = (int)((wid / n) % Hkv);
+    const int b = (int)(wid / (n * Hkv));
+    const int G = Hq / Hkv;
+    const int64_t nb = n / 64;
+    const int64_t bg = (int64_t)b * Hkv + g;
+    if (i < 64) {   // clear key row i of the sink accumulators (bwd_sink adds into them next)
+        float *acc = sink_acc + (bg * 2 * 64 + i) * D;
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            acc[lane + 64 * e] = 0.0f;
+            acc[64 * D + lane + 64 * e] = 0.0f;
+        }
+    }
+    const bool hv = l16 < G;
+    const int h = g * G + (hv ? l16 : 0);
+    const int64_t row = (((int64_t)b * n + i) * Hq + h) * D;
+
+    // query row elements t = 32 ks + 8 lg + e of head l16: raw, dO, O
+    float x[NKS][8], dov[NKS][8];
+    float ss = 0.0f, od = 0.0f;
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int64_t o = row + 32 * ks + 8 * lg + e;
+            x[ks][e] = hv ? bf2f(q[o]) : 0.0f;
+            dov[ks][e] = hv ? bf2f(dout[o]) : 0.0f;
+            ss = fmaf(x[ks][e], x[ks][e], ss);
+            od = fmaf(dov[ks][e], hv ? bf2f(out[o]) : 0.0f, od);
+        }
+    const float ms = col_sum(ss) / (float)D;
+    const float rq = sqrtf(fmaxf(ms, eps));
+    const float Dh = col_sum(od);
+    const float gn = (qgain && hv) ? qgain[h] : 1.0f;
+    float qcv[NKS][8];
+    bf16x8 qopc[NKS], qopr[NKS], dop[NKS];
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qcv[ks][e] = qgain ? rnd_bf16((x[ks][e] / rq) * gn) : x[ks][e];
+        qopc[ks] = pack_b8(qcv[ks]);
+        dop[ks] = pack_b8(dov[ks]);
+    }
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+        float qrv[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int t = 32 * ks + 8 * lg + e;
+            const float pv = qcv[ks ^ (NKS / 2)][e];                    // element t ^ (D/2)
+            const float rot = (t < D / 2) ? -pv : pv;
+            const float c = rnd_bf16(cosT[i * D + t]), sn = rnd_bf16(sinT[i * D + t]);
+            qrv[e] = rnd_bf16(rnd_bf16(qcv[ks][e] * c) + rnd_bf16(rot * sn));
+            if (hv) {
+                qc_ws[row + t] = qcv[ks][e];
+                qr_ws[row + t] = qrv[e];
+            }
+        }
+        qopr[ks] = pack_b8(qrv);
+    }
+
+    // the units: the sink unit, the window pages, the routed picks
+    const int64_t nsink = ((int64_t)S < i + 1) ? (int64_t)S : i + 1;
+    const int64_t wlo = (S > i - W + 1) ? (int64_t)S : i - W + 1;
+    const int64_t nwu = (i >= wlo) ? i / 64 - wlo / 64 + 1 : 0;
+    const int ncnt = min(max(cnt[bg * n + i], 0), kk);
+    const int32_t *sel = idx + (bg * n + i) * kk;
+    const int hs = nsink > 0 ? 1 : 0;
+    const int64_t nunits = hs + nwu + ncnt;
+    auto unit = [&](int64_t u, int64_t &kb, int64_t &lo, int64_t &hi, bool &rope) -> bool {
+        rope = false;
+        if (u < hs) {
+            kb = 0;
+            lo = 0;
+            hi = nsink - 1;
+            return true;
+        }
+        u -= hs;
+        if (u < nwu) {
+            rope = true;
+            kb = 64 * (wlo / 64 + u);
+            lo = (wlo > kb) ? wlo : kb;
+            hi = (i < kb + 63) ? i : kb + 63;
+            return true;
+        }
+        const int blk = sel[u - nwu];
+        kb = 64 * (int64_t)blk;
+        lo = kb;
+        hi = kb + 63;
+        return blk >= 1 && (int64_t)blk < nb;
+    };
+    auto scores = [&](int64_t kb, bool rope, f32x4 (&Sa)[4]) {
+        const bf16_t *K = (rope ? kr : kc) + (bg * n + kb) * D;
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+            const bf16_t *kp = K + (int64_t)kslot(mt, l16) * D + 8 * lg;
+            Sa[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < NKS; ++ks) Sa[mt] = mfma16(ld_b8(kp + 32 * ks), rope ? qopr[ks] : qopc[ks], Sa[mt]);
+        }
+    };
+
+    // pass 1: the union LSE of column l16
+    float m = -INFINITY, l = 0.0f;
+    for (int64_t u = 0; u < nunits; ++u) {
+        int64_t kb, lo, hi;
+        bool rope;
+        if (!unit(u, kb, lo, hi, rope)) continue;
+        f32x4 Sa[4];
+        scores(kb, rope, Sa);
+        float mu = -INFINITY;
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int64_t key = kb + kkey(mt, lg, e);
+                if (key >= lo && key <= hi) mu = fmaxf(mu, Sa[mt][e] * scale);
+            }
+        mu = col_max(mu);
+        const float mn = fmaxf(m, mu);
+        float ps = 0.0f;
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int64_t key = kb + kkey(mt, lg, e);
+                if (key >= lo && key <= hi) ps += __expf(Sa[mt][e] * scale - mn);
+            }
+        l = l * __expf(m - mn) + col_sum(ps);
+        m = mn;
+    }
+    const float lse = (l > 0.0f) ? m + __logf(l) : INFINITY;
+    if (hv && lg == 0) {
+        lse_ws[((int64_t)b * Hq + h) * n + i] = lse;
+        dd_ws[((int64_t)b * Hq + h) * n + i] = Dh;
+    }
+
+    // pass 2: dq^T (NoPE and rotated parts)
+    f32x4 gc[NDT], gr[NDT];
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) gc[dt] = gr[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int64_t u = 0; u < nunits; ++u) {
+        int64_t kb, lo, hi;
+        bool rope;
+        if (!unit(u, kb, lo, hi, rope)) continue;
+        f32x4 Sa[4], Pa[4];
+        scores(kb, rope, Sa);
+        const bf16_t *V = v + (((int64_t)b * n + kb) * Hkv + g) * D;
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+            const bf16_t *vp = V + (int64_t)kslot(mt, l16) * Hkv * D + 8 * lg;
+            Pa[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < NKS; ++ks) Pa[mt] = mfma16(ld_b8(vp + 32 * ks), dop[ks], Pa[mt]);
+        }
+        float dsv[2][8];
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int64_t key = kb + kkey(mt, lg, e);
+                const float p = (key >= lo && key <= hi) ? __expf(Sa[mt][e] * scale - lse) : 0.0f;
+                dsv[mt >> 1][(mt & 1) * 4 + e] = p * (Pa[mt][e] - Dh) * scale;
+            }
+        const bf16x8 db0 = pack_b8(dsv[0]), db1 = pack_b8(dsv[1]);
+        const bf16_t *KT = (rope ? krt : kct) + bg * D * n + kb + 8 * lg;
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) {
+            const bf16_t *ktp = KT + (int64_t)(16 * dt + l16) * n;
+            f32x4 a = rope ? gr[dt] : gc[dt];
+            a = mfma16(ld_b8(ktp), db0, a);
+            a = mfma16(ld_b8(ktp + 32), db1, a);
+            if (rope) gr[dt] = a;
+            else gc[dt] = a;
+        }
+    }
+
+    // rope^T and the QKNorm backward on elements d = 16 dt + 4 lg + e
+    float y[NDT][4], xr[NDT][4];
+    float yx = 0.0f;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int d = 16 * dt + 4 * lg + e;
+            const float zp = gr[dt ^ (NDT / 2)][e] * rnd_bf16(sinT[i * D + (d ^ (D / 2))]);   // (z sin) at d ^ D/2
+            y[dt][e] = gc[dt][e] + gr[dt][e] * rnd_bf16(cosT[i * D + d]) + ((d < D / 2) ? zp : -zp);
+            xr[dt][e] = hv ? bf2f(q[row + d]) : 0.0f;
+            yx = fmaf(y[dt][e], xr[dt][e], yx);
+        }
+    yx = col_sum(yx);
+    if (qgain) {
+        const float corr = (ms >= eps) ? gn * yx / ((float)D * rq * rq * rq) : 0.0f;
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) y[dt][e] = (gn / rq) * y[dt][e] - xr[dt][e] * corr;
+        if (hv && lg == 0 && dq_gain) atomicAdd(&dq_gain[h], yx / rq);
+    }
+    if (hv) {
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) dq[row + 16 * dt + 4 * lg + e] = f2bf(y[dt][e]);
+    }
+}
+
 // ------------------------------------------------------------- bwd_dkv ----
 // Lane (kl, c) = (lane / NC, lane % NC) of wave w: key j = 64 blk + KW w + kl,
 // elements 16c .. 16c+15; a key's chunks sit on NC adjacent lanes, so its
@@ -507,7 +782,8 @@ using namespace hba;
 
 extern "C" int hba_attn_bwd_workspace_size(int64_t B, int64_t n, int64_t Hq, int64_t d, size_t *bytes) {
     if (!bytes || B <= 0 || n <= 0 || Hq <= 0 || d <= 0) return HBA_ERR_INVALID_ARG;
-    *bytes = (size_t)(2 * B * n * Hq * d + 2 * B * Hq * n + B * Hq * 2 * 64 * d) * 4;
+    // fp32: query rows (2), LSE and D, sink accumulators; bf16: transposed keys (2)
+    *bytes = (size_t)(2 * B * n * Hq * d + 2 * B * Hq * n + B * Hq * 2 * 64 * d) * 4 + (size_t)(2 * B * Hq * n * d) * 2;
     return HBA_OK;
 }
 
@@ -537,6 +813,8 @@ extern "C" int hba_attn_bwd(int dtype, const void *q, const void *k, const void 
     float *lse_ws = qr_ws + B * n * Hq * d;
     float *dd_ws = lse_ws + B * Hq * n;
     float *sink_acc = dd_ws + B * Hq * n;                          // [B, Hkv, 2, 64, d] (Hkv <= Hq)
+    bf16_t *kct = reinterpret_cast<bf16_t *>(sink_acc + B * Hq * 2 * 64 * d);   // [B, Hkv, d, n] (bf16 path)
+    bf16_t *krt = kct + B * Hkv * d * n;
     hipStream_t s = (hipStream_t)stream;
     const int64_t nwaves = B * Hkv * n;
     const int64_t g1 = (nwaves + 3) / 4;
@@ -546,7 +824,15 @@ extern "C" int hba_attn_bwd(int dtype, const void *q, const void *k, const void 
 #define HBA_BWD(DT, D)                                                                                          \
     do {                                                                                                        \
         using T = St<DT>::T;                                                                                    \
-        if (Hq / Hkv <= 8)                                                                                      \
+        if constexpr (DT == 1) {                                                                                \
+            hipLaunchKernelGGL((bw::bwd_kt_kernel<D>), dim3((unsigned)g2), dim3(256), 0, s, (const bf16_t *)kc,  \
+                               (const bf16_t *)kr, kct, krt, n);                                                 \
+            hipLaunchKernelGGL((bw::bwd_dq_mfma_kernel<D>), dim3((unsigned)g1), dim3(256), 0, s,                 \
+                               (const bf16_t *)q, (const bf16_t *)kc, (const bf16_t *)kr, kct, krt,             \
+                               (const bf16_t *)v, q_gain, eps, cos_tab, sin_tab, idx, cnt, (const bf16_t *)out,  \
+                               (const bf16_t *)dout, (int)B, n, (int)Hq, (int)Hkv, (int)S, W, (int)k_blocks,     \
+                               scale, qc_ws, qr_ws, lse_ws, dd_ws, sink_acc, (bf16_t *)dq, dq_gain);             \
+        } else if (Hq / Hkv <= 8)                                                                               \
             hipLaunchKernelGGL((bw::bwd_dq_kernel<DT, D, 8>), dim3((unsigned)g1), dim3(256), 0, s,               \
                                (const T *)q, (const T *)kc, (const T *)kr, (const T *)v, q_gain, eps, cos_tab,   \
                                sin_tab, idx, cnt, (const T *)out, (const T *)dout, (int)B, n, (int)Hq, (int)Hkv, \
