@@ -18,7 +18,7 @@
 // fp32 throughout; storage roundings of the forward are treated as identity,
 // as autograd treats the reference's casts.
 //
-// Two kernels:
+// fp32 inputs take two VALU kernels:
 //   bwd_dq:  one wave per (b, i, KV head g), lanes over d, the G heads of the
 //            group in registers.  Pass 1 recomputes the union LSE, pass 2
 //            accumulates dq; it also leaves the QKNorm'd and rotated query
@@ -28,6 +28,12 @@
 //            query rows that attend its keys: the window rows, the sink rows
 //            (block 0), and the rows whose selection holds the block (found by
 //            scanning the selection lists into LDS).
+// bf16 inputs take the same gradients on MFMA: bwd_kt (transposed keys),
+// bwd_dq_mfma (the G heads are the columns of 16-wide tiles), bwd_dkv_mfma
+// (32 (row, head) pairs per tile, one workgroup per key block and row range)
+// and bwd_dkv_fin (rope^T and the QKNorm backward of the key rows).  Both
+// paths share bwd_sink for the sink keys, whose rows are split over
+// workgroups.
 #include "hba_abi.h"
 #include "hba_common.h"
 
@@ -305,13 +311,20 @@ __device__ __forceinline__ float col_sum(float v) {
     return v + __shfl_xor(v, 32, 64);
 }
 
-// transposed prepared keys, kct / krt [B, Hkv, d, n]: one workgroup per 64-key tile
+// transposed prepared keys, kct / krt [B, Hkv, d, n]: one workgroup per 64-key
+// tile; it also clears the tile's rows of the dk / dv accumulator dkv_acc
+// [B, Hkv, n, 3, d] (bwd_dkv_mfma adds into it next)
 template <int D>
 __global__ __launch_bounds__(256) void bwd_kt_kernel(const bf16_t *__restrict__ kc, const bf16_t *__restrict__ kr,
-                                                     bf16_t *__restrict__ kct, bf16_t *__restrict__ krt, int64_t n) {
+                                                     bf16_t *__restrict__ kct, bf16_t *__restrict__ krt, int64_t n,
+                                                     float *__restrict__ dkv_acc) {
     __shared__ bf16_t tile[64][D + 2];
     const int64_t nt = n / 64;
     const int64_t bg = blockIdx.x / nt, kb = (blockIdx.x % nt) * 64;
+    {
+        f32x4 *acc = reinterpret_cast<f32x4 *>(dkv_acc + (bg * n + kb) * 3 * D);
+        for (int e = threadIdx.x; e < 64 * 3 * D / 4; e += 256) acc[e] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
     for (int pass = 0; pass < 2; ++pass) {
         const bf16_t *src = (pass ? kr : kc) + (bg * n + kb) * D;
         bf16_t *dst = (pass ? krt : kct) + bg * D * n + kb;
@@ -775,6 +788,308 @@ __global__ __launch_bounds__(DkvCfg<D>::NT) void bwd_dkv_kernel(
     }
 }
 
+// ------------------------------------------------ bwd_dkv on MFMA (bf16) ----
+// dK and dV of one 64-key block from the (query row, head) pairs that attend
+// it, 32 pairs per tile staged in LDS twice (row-major and transposed); wave w
+// owns keys kb + 16 w .. kb + 16 w + 15:
+//   S   = X . K^T    (A: staged query rows X, pairs in the slot order pslot;
+//                     B: the wave's key rows, held in registers)
+//   dP  = dO . V^T   (A: staged dO rows; B: the wave's V rows)
+//   dV += P^T . dO   (A: P^T straight from the accumulators, which the slot
+//                     order puts in the A-operand layout; B: dO^T from the
+//                     transposed copy)
+//   dK += dS^T . X   (A: dS^T the same way; B: X^T)
+// Lane (l16, lg) holds S and dP of key l16 and pairs 8 lg + 4 mt + e, and of
+// dV / dK the element d = 16 dt + l16 of keys 16 w + 4 lg + e.
+// One workgroup per (b, g, 64-key block, range of DKV_ROWS query rows): the
+// window rows (rotated, X = qr) and the routed rows (NoPE, X = qc; found by
+// scanning the range's selection lists) of its range.  Its sums are added
+// (fp32 atomics) into dkv_acc [B, Hkv, n, 3, d] (NoPE dk, rotated dk, dv),
+// which bwd_dkv_fin turns into dk and dv.  The split over row ranges keeps a
+// block that nearly every query selects from becoming the tail.
+constexpr int DKV_ROWS = 4096;
+constexpr int DKV_TP = 32;   // pairs per tile
+
+__device__ __forceinline__ int pslot(int mt, int r) { return 8 * (r >> 2) + 4 * mt + (r & 3); }
+
+template <int D>
+struct DkvTile {
+    static constexpr int XP = D + 8;        // padded row of the row-major copies
+    static constexpr int TP = DKV_TP + 8;   // padded row of the transposed copies
+    alignas(16) bf16_t xs[DKV_TP * XP];
+    alignas(16) bf16_t os[DKV_TP * XP];
+    alignas(16) bf16_t xt[D * TP];
+    alignas(16) bf16_t ot[D * TP];
+    alignas(16) float lse[DKV_TP];
+    alignas(16) float dd[DKV_TP];
+    alignas(16) int row[DKV_TP];
+};
+
+template <int D>
+__global__ __launch_bounds__(256) void bwd_dkv_mfma_kernel(
+    const bf16_t *__restrict__ kc, const bf16_t *__restrict__ kr, const bf16_t *__restrict__ v,
+    const int32_t *__restrict__ idx, const int32_t *__restrict__ cnt, const bf16_t *__restrict__ dout, int64_t n,
+    int Hq, int Hkv, int S, int64_t W, int kk, float scale, int nsplit, const float *__restrict__ qc_ws,
+    const float *__restrict__ qr_ws, const float *__restrict__ lse_ws, const float *__restrict__ dd_ws,
+    float *__restrict__ dkv_acc) {
+    constexpr int NKS = D / 32, NDT = D / 16, NCH = D / 8, CPT = DKV_TP * NCH / 256;
+    using Tl = DkvTile<D>;
+    constexpr int XP = Tl::XP, TP = Tl::TP;
+    __shared__ Tl tl[2];
+    __shared__ int rows[256];
+    __shared__ int wcount[4];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, l16 = lane & 15, lg = lane >> 4;
+    const int64_t nb = n / 64;
+    const int split = (int)(blockIdx.x % nsplit);
+    const int64_t blk = (blockIdx.x / nsplit) % nb;
+    const int64_t bg = blockIdx.x / ((int64_t)nsplit * nb);
+    const int g = (int)(bg % Hkv), b = (int)(bg / Hkv);
+    const int G = Hq / Hkv;
+    const int64_t kb = 64 * blk;
+    const int64_t r0 = (int64_t)split * DKV_ROWS, r1 = min(n, r0 + DKV_ROWS);
+    const int64_t jl = kb + 16 * w + l16;   // the key of this lane's S / dP column
+
+    bf16x8 kcb[NKS], krb[NKS], vb[NKS];
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+        kcb[ks] = ld_b8(kc + (bg * n + jl) * D + 32 * ks + 8 * lg);
+        krb[ks] = ld_b8(kr + (bg * n + jl) * D + 32 * ks + 8 * lg);
+        vb[ks] = ld_b8(v + (((int64_t)b * n + jl) * Hkv + g) * D + 32 * ks + 8 * lg);
+    }
+    f32x4 gkc[NDT], gkr[NDT], gv[NDT];
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) gkc[dt] = gkr[dt] = gv[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    // pairs gp = 0 .. total-1: query row row_of(gp / G), head g G + gp % G
+    auto run = [&](int64_t total, auto row_of, bool rope) {
+        const float *qx = rope ? qr_ws : qc_ws;
+        const int64_t ntl = (total + DKV_TP - 1) / DKV_TP;
+        f32x4 xr[CPT][2];
+        u32x4b orr[CPT];
+        float plse[CPT], pdd[CPT];
+        int prow[CPT];
+        auto load = [&](int64_t t) {
+#pragma unroll
+            for (int r = 0; r < CPT; ++r) {
+                const int q = tid + 256 * r, p = q / NCH, c = q % NCH;
+                const int64_t gp = t * DKV_TP + p;
+                plse[r] = INFINITY;
+                pdd[r] = 0.0f;
+                prow[r] = -1;
+                if (gp < total) {
+                    const int64_t i = row_of(gp / G);
+                    const int h = g * G + (int)(gp % G);
+                    const int64_t ro = (((int64_t)b * n + i) * Hq + h) * D + 8 * c;
+                    xr[r][0] = *reinterpret_cast<const f32x4 *>(qx + ro);
+                    xr[r][1] = *reinterpret_cast<const f32x4 *>(qx + ro + 4);
+                    orr[r] = *reinterpret_cast<const u32x4b *>(dout + ro);
+                    if (c == 0) {
+                        const int64_t so = ((int64_t)b * Hq + h) * n + i;
+                        plse[r] = lse_ws[so];
+                        pdd[r] = dd_ws[so];
+                        prow[r] = (int)i;
+                    }
+                } else {
+                    xr[r][0] = xr[r][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+                    orr[r] = u32x4b{0u, 0u, 0u, 0u};
+                }
+            }
+        };
+        auto store = [&](Tl &T) {
+#pragma unroll
+            for (int r = 0; r < CPT; ++r) {
+                const int q = tid + 256 * r, p = q / NCH, c = q % NCH;
+                u32x4b xp;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const f32x4 &h4 = xr[r][e >> 1];
+                    xp[e] = (uint32_t)f2bf(h4[2 * (e & 1)]) | ((uint32_t)f2bf(h4[2 * (e & 1) + 1]) << 16);
+                }
+                *reinterpret_cast<u32x4b *>(&T.xs[p * XP + 8 * c]) = xp;
+                *reinterpret_cast<u32x4b *>(&T.os[p * XP + 8 * c]) = orr[r];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    T.xt[(8 * c + e) * TP + p] = (bf16_t)(xp[e >> 1] >> (16 * (e & 1)));
+                    T.ot[(8 * c + e) * TP + p] = (bf16_t)(orr[r][e >> 1] >> (16 * (e & 1)));
+                }
+                if (c == 0) {
+                    T.lse[p] = plse[r];
+                    T.dd[p] = pdd[r];
+                    T.row[p] = prow[r];
+                }
+            }
+        };
+        auto compute = [&](const Tl &T) {
+            f32x4 Sa[2], Pa[2];
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt) {
+                const bf16_t *xa = &T.xs[pslot(mt, l16) * XP + 8 * lg];
+                const bf16_t *oa = &T.os[pslot(mt, l16) * XP + 8 * lg];
+                Sa[mt] = Pa[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int ks = 0; ks < NKS; ++ks) {
+                    Sa[mt] = mfma16(ld_b8(xa + 32 * ks), rope ? krb[ks] : kcb[ks], Sa[mt]);
+                    Pa[mt] = mfma16(ld_b8(oa + 32 * ks), vb[ks], Pa[mt]);
+                }
+            }
+            float pk[8], dk[8];
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt) {
+                const int pp = 8 * lg + 4 * mt;
+                const f32x4 ls = *reinterpret_cast<const f32x4 *>(&T.lse[pp]);
+                const f32x4 ds = *reinterpret_cast<const f32x4 *>(&T.dd[pp]);
+                const int4 rw = *reinterpret_cast<const int4 *>(&T.row[pp]);
+                const int ri[4] = {rw.x, rw.y, rw.z, rw.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int64_t i = ri[e];
+                    const bool valid = rope ? (jl >= S && i >= jl && i <= jl + W - 1) : (i >= 0);
+                    const float p = valid ? __expf(Sa[mt][e] * scale - ls[e]) : 0.0f;
+                    pk[4 * mt + e] = p;
+                    dk[4 * mt + e] = p * (Pa[mt][e] - ds[e]) * scale;
+                }
+            }
+            const bf16x8 pa = pack_b8(pk), da = pack_b8(dk);
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt) {
+                gv[dt] = mfma16(pa, ld_b8(&T.ot[(16 * dt + l16) * TP + 8 * lg]), gv[dt]);
+                const bf16x8 xb = ld_b8(&T.xt[(16 * dt + l16) * TP + 8 * lg]);
+                if (rope) gkr[dt] = mfma16(da, xb, gkr[dt]);
+                else gkc[dt] = mfma16(da, xb, gkc[dt]);
+            }
+        };
+        if (ntl <= 0) return;
+        load(0);
+        store(tl[0]);
+        __syncthreads();
+        for (int64_t t = 0; t < ntl; ++t) {
+            if (t + 1 < ntl) load(t + 1);
+            compute(tl[t & 1]);
+            if (t + 1 < ntl) store(tl[(t + 1) & 1]);
+            __syncthreads();
+        }
+    };
+
+    bool had_win = false, had_rt = false;
+    // window rows: key j >= S is in the window of queries j .. j + W - 1
+    {
+        const int64_t wa = max(kb, r0);
+        const int64_t wb = min(min(n - 1, kb + 63 + W - 1), r1 - 1);
+        if (wb >= wa) {
+            had_win = true;
+            run((wb - wa + 1) * G, [&](int64_t r) { return wa + r; }, true);
+        }
+    }
+    // routed rows: the queries of the range whose selection holds this block
+    if (blk >= 1) {
+        for (int64_t i0 = r0; i0 < r1; i0 += 256) {
+            const int64_t i = i0 + tid;
+            bool picked = false;
+            if (i < r1) {
+                const int nc = min(max(cnt[bg * n + i], 0), kk);
+                const int32_t *sl = idx + (bg * n + i) * kk;
+                for (int r = 0; r < nc; ++r) picked |= sl[r] == (int32_t)blk;
+            }
+            const uint64_t bal = __ballot(picked);
+            if (lane == 0) wcount[w] = __popcll(bal);
+            __syncthreads();
+            int base = 0, tot = 0;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                if (u < w) base += wcount[u];
+                tot += wcount[u];
+            }
+            if (picked) rows[base + __popcll(bal & ((1ull << lane) - 1ull))] = (int)i;
+            __syncthreads();
+            if (tot > 0) {
+                had_rt = true;
+                run((int64_t)tot * G, [&](int64_t r) { return (int64_t)rows[r]; }, false);
+            }
+            __syncthreads();                                      // rows[] and wcount[] reused
+        }
+    }
+
+    float *acc = dkv_acc + (bg * n + kb + 16 * w + 4 * lg) * 3 * D + l16;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            float *a = acc + e * 3 * D + 16 * dt;
+            if (had_rt) unsafeAtomicAdd(a, gkc[dt][e]);
+            if (had_win) unsafeAtomicAdd(a + D, gkr[dt][e]);
+            if (had_rt || had_win) unsafeAtomicAdd(a + 2 * D, gv[dt][e]);
+        }
+}
+
+// dk / dv of key row (b, j, g), one wave each, lane = element d (and d + 64):
+// the summed NoPE / rotated dk and dv (plus the sink accumulators for j < S),
+// rope^T at position j, then the QKNorm backward of k row (b, j, g); the gain
+// gradient is summed over the workgroup's four rows before its one atomic add
+template <int D>
+__global__ __launch_bounds__(256) void bwd_dkv_fin_kernel(
+    const bf16_t *__restrict__ k, const float *__restrict__ kgain, float eps, const float *__restrict__ cosT,
+    const float *__restrict__ sinT, int64_t n, int Hkv, int S, const float *__restrict__ dkv_acc,
+    const float *__restrict__ sink_acc, bf16_t *__restrict__ dk, bf16_t *__restrict__ dv,
+    float *__restrict__ dk_gain) {
+    constexpr int E = D / 64;
+    __shared__ float gsum[4];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int64_t wid = (int64_t)blockIdx.x * 4 + w;     // bg n + j; n % 4 == 0, so one bg per workgroup
+    const int64_t j = wid % n, bg = wid / n;
+    const int g = (int)(bg % Hkv), b = (int)(bg / Hkv);
+    const float *a = dkv_acc + wid * 3 * D;
+    float gkc[E], gkr[E], gv[E], zs[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        const int d = lane + 64 * e;
+        gkc[e] = a[d];
+        gkr[e] = a[D + d];
+        gv[e] = a[2 * D + d];
+        if (j < S) {
+            const float *sa = sink_acc + (bg * 2 * 64 + j) * D;
+            gkc[e] += sa[d];
+            gv[e] += sa[64 * D + d];
+        }
+        zs[e] = gkr[e] * rnd_bf16(sinT[j * D + d]);
+    }
+    float y[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        const int d = lane + 64 * e;
+        const float pv = (E == 1) ? __shfl_xor(zs[0], 32, 64) : zs[e ^ 1];   // element d ^ (D/2)
+        y[e] = gkc[e] + gkr[e] * rnd_bf16(cosT[j * D + d]) + ((d < D / 2) ? pv : -pv);
+    }
+    const int64_t rro = (((int64_t)b * n + j) * Hkv + g) * D;
+    float gsv = 0.0f;
+    if (kgain) {
+        float x[E], ss = 0.0f, yx = 0.0f;
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            x[e] = bf2f(k[rro + lane + 64 * e]);
+            ss = fmaf(x[e], x[e], ss);
+            yx = fmaf(y[e], x[e], yx);
+        }
+        const float ms = wsum<D>(ss) / (float)D;
+        yx = wsum<D>(yx);
+        const float r = sqrtf(fmaxf(ms, eps));
+        const float gn = kgain[g];
+        const float corr = (ms >= eps) ? gn * yx / ((float)D * r * r * r) : 0.0f;
+#pragma unroll
+        for (int e = 0; e < E; ++e) y[e] = (gn / r) * y[e] - x[e] * corr;
+        gsv = yx / r;
+    }
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        dk[rro + lane + 64 * e] = f2bf(y[e]);
+        dv[rro + lane + 64 * e] = f2bf(gv[e]);
+    }
+    if (kgain && dk_gain) {
+        if (lane == 0) gsum[w] = gsv;
+        __syncthreads();
+        if (threadIdx.x == 0) unsafeAtomicAdd(&dk_gain[g], (gsum[0] + gsum[1]) + (gsum[2] + gsum[3]));
+    }
+}
+
 }  // namespace bw
 }  // namespace hba
 
@@ -782,8 +1097,11 @@ using namespace hba;
 
 extern "C" int hba_attn_bwd_workspace_size(int64_t B, int64_t n, int64_t Hq, int64_t d, size_t *bytes) {
     if (!bytes || B <= 0 || n <= 0 || Hq <= 0 || d <= 0) return HBA_ERR_INVALID_ARG;
-    // fp32: query rows (2), LSE and D, sink accumulators; bf16: transposed keys (2)
-    *bytes = (size_t)(2 * B * n * Hq * d + 2 * B * Hq * n + B * Hq * 2 * 64 * d) * 4 + (size_t)(2 * B * Hq * n * d) * 2;
+    // fp32: query rows (2), LSE and D, sink accumulators; bf16: transposed keys
+    // (2); fp32: the dk / dv accumulators of the MFMA path (Hkv <= Hq bounds
+    // the KV-head dimension of the last three)
+    *bytes = (size_t)(2 * B * n * Hq * d + 2 * B * Hq * n + B * Hq * 2 * 64 * d) * 4 + (size_t)(2 * B * Hq * n * d) * 2 +
+             (size_t)(B * Hq * n * 3 * d) * 4;
     return HBA_OK;
 }
 
@@ -815,18 +1133,23 @@ extern "C" int hba_attn_bwd(int dtype, const void *q, const void *k, const void 
     float *sink_acc = dd_ws + B * Hq * n;                          // [B, Hkv, 2, 64, d] (Hkv <= Hq)
     bf16_t *kct = reinterpret_cast<bf16_t *>(sink_acc + B * Hq * 2 * 64 * d);   // [B, Hkv, d, n] (bf16 path)
     bf16_t *krt = kct + B * Hkv * d * n;
+    float *dkv_acc = reinterpret_cast<float *>(kct + 2 * B * Hq * n * d);   // [B, Hkv, n, 3, d] (bf16 path)
     hipStream_t s = (hipStream_t)stream;
     const int64_t nwaves = B * Hkv * n;
     const int64_t g1 = (nwaves + 3) / 4;
     const int64_t g2 = B * Hkv * (n / 64);
     const int nsplit = (int)((n + bw::SINK_ROWS - 1) / bw::SINK_ROWS);
     const int64_t gs = B * Hkv * nsplit;
+    const int nsplit_kv = (int)((n + bw::DKV_ROWS - 1) / bw::DKV_ROWS);
+    const int64_t g3 = B * Hkv * (n / 64) * nsplit_kv;
+    const int64_t g4 = B * Hkv * n / 4;
+    if (g3 > 0x7fffffffLL) return HBA_ERR_UNSUPPORTED;
 #define HBA_BWD(DT, D)                                                                                          \
     do {                                                                                                        \
         using T = St<DT>::T;                                                                                    \
         if constexpr (DT == 1) {                                                                                \
             hipLaunchKernelGGL((bw::bwd_kt_kernel<D>), dim3((unsigned)g2), dim3(256), 0, s, (const bf16_t *)kc,  \
-                               (const bf16_t *)kr, kct, krt, n);                                                 \
+                               (const bf16_t *)kr, kct, krt, n, dkv_acc);                                        \
             hipLaunchKernelGGL((bw::bwd_dq_mfma_kernel<D>), dim3((unsigned)g1), dim3(256), 0, s,                 \
                                (const bf16_t *)q, (const bf16_t *)kc, (const bf16_t *)kr, kct, krt,             \
                                (const bf16_t *)v, q_gain, eps, cos_tab, sin_tab, idx, cnt, (const bf16_t *)out,  \
@@ -848,10 +1171,20 @@ extern "C" int hba_attn_bwd(int dtype, const void *q, const void *k, const void 
             hipLaunchKernelGGL((bw::bwd_sink_kernel<DT, D>), dim3((unsigned)gs), dim3(bw::DkvCfg<D>::NT), 0, s,  \
                                (const T *)kc, (const T *)v, (const T *)dout, n, (int)Hq, (int)Hkv, (int)S,       \
                                nsplit, scale, qc_ws, lse_ws, dd_ws, sink_acc);                                   \
-        hipLaunchKernelGGL((bw::bwd_dkv_kernel<DT, D>), dim3((unsigned)g2), dim3(bw::DkvCfg<D>::NT), 0, s,       \
-                           (const T *)k, (const T *)kc, (const T *)kr, (const T *)v, k_gain, eps, cos_tab,       \
-                           sin_tab, idx, cnt, (const T *)dout, n, (int)Hq, (int)Hkv, (int)S, W, (int)k_blocks,   \
-                           scale, qc_ws, qr_ws, lse_ws, dd_ws, sink_acc, (T *)dk, (T *)dv, dk_gain);             \
+        if constexpr (DT == 1) {                                                                                \
+            hipLaunchKernelGGL((bw::bwd_dkv_mfma_kernel<D>), dim3((unsigned)g3), dim3(256), 0, s,                \
+                               (const bf16_t *)kc, (const bf16_t *)kr, (const bf16_t *)v, idx, cnt,              \
+                               (const bf16_t *)dout, n, (int)Hq, (int)Hkv, (int)S, W, (int)k_blocks, scale,      \
+                               nsplit_kv, qc_ws, qr_ws, lse_ws, dd_ws, dkv_acc);                                 \
+            hipLaunchKernelGGL((bw::bwd_dkv_fin_kernel<D>), dim3((unsigned)g4), dim3(256), 0, s,                 \
+                               (const bf16_t *)k, k_gain, eps, cos_tab, sin_tab, n, (int)Hkv, (int)S, dkv_acc,    \
+                               sink_acc, (bf16_t *)dk, (bf16_t *)dv, dk_gain);                                   \
+        } else                                                                                                  \
+            hipLaunchKernelGGL((bw::bwd_dkv_kernel<DT, D>), dim3((unsigned)g2), dim3(bw::DkvCfg<D>::NT), 0, s,   \
+                               (const T *)k, (const T *)kc, (const T *)kr, (const T *)v, k_gain, eps, cos_tab,   \
+                               sin_tab, idx, cnt, (const T *)dout, n, (int)Hq, (int)Hkv, (int)S, W,              \
+                               (int)k_blocks, scale, qc_ws, qr_ws, lse_ws, dd_ws, sink_acc, (T *)dk, (T *)dv,    \
+                               dk_gain);                                                                        \
     } while (0)
     HBA_DISPATCH_DT_D(dtype, d, HBA_BWD);
 #undef HBA_BWD

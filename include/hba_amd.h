@@ -263,7 +263,11 @@ int hba_decode_fwd(int dtype, const void *q, const float *q_gain, float eps,
  * (contiguous, storage dtype) and ADDS the QKNorm gain gradients into
  * dq_gain fp32 [Hq] and dk_gain fp32 [Hkv] (q_gain == NULL: no QKNorm, the
  * gain outputs are ignored).  scale is the union scale of the forward.
- * Arithmetic is fp32.  Same shape rules as hba_attn_fwd; G = Hq/Hkv <= 16.
+ * fp32 storage: fp32 VALU arithmetic.  bf16 storage: bf16 MFMA products
+ * with fp32 accumulation; the probabilities and dS enter the dk/dv/dq
+ * products rounded to bf16, and dk/dv are summed with fp32 atomics, so the
+ * bf16 result is not bit-reproducible from run to run.  Same shape rules as
+ * hba_attn_fwd; G = Hq/Hkv <= 16.
  */
 int hba_attn_bwd(int dtype, const void *q, const void *k, const void *v,
                  const void *kc, const void *kr,
@@ -277,8 +281,11 @@ int hba_attn_bwd(int dtype, const void *q, const void *k, const void *v,
                  void *dq, void *dk, void *dv, float *dq_gain, float *dk_gain, void *stream);
 
 /* Scratch bytes hba_attn_bwd needs: the QKNorm'd and rotated query rows
- * (2*B*n*Hq*d fp32), the per-row LSE and <dout, out> (2*B*Hq*n fp32) and the
- * sink-key accumulators (2*B*Hq*64*d fp32). */
+ * (2*B*n*Hq*d fp32), the per-row LSE and <dout, out> (2*B*Hq*n fp32), the
+ * sink-key accumulators (2*B*Hq*64*d fp32), the transposed prepared keys
+ * (2*B*Hq*n*d bf16) and the dk/dv accumulators (3*B*Hq*n*d fp32); the last
+ * two are used by the bf16 path only.  Hq bounds the KV-head count of the
+ * last three. */
 int hba_attn_bwd_workspace_size(int64_t B, int64_t n, int64_t Hq, int64_t d, size_t *bytes);
 
 #ifdef __cplusplus
