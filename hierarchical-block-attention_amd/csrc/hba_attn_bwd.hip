@@ -342,31 +342,38 @@ __global__ __launch_bounds__(256) void bwd_dq_mfma_kernel(
     const float *__restrict__ qgain, float eps, const float *__restrict__ cosT, const float *__restrict__ sinT,
     const int32_t *__restrict__ idx, const int32_t *__restrict__ cnt, const bf16_t *__restrict__ out,
     const bf16_t *__restrict__ dout, int B, int64_t n, int Hq, int Hkv, int S, int64_t W, int kk, float scale,
-    float *__restrict__ qc_ws, float *__restrict__ qr_ws, float *__restrict__ lse_ws, float *__restrict__ dd_ws,
-    float *__restrict__ sink_acc, bf16_t *__restrict__ dq, float *__restrict__ dq_gain) {
+    int qpw, float *__restrict__ qc_ws, float *__restrict__ qr_ws, float *__restrict__ lse_ws,
+    float *__restrict__ dd_ws, float *__restrict__ sink_acc, bf16_t *__restrict__ dq, float *__restrict__ dq_gain) {
     constexpr int NKS = D / 32, NDT = D / 16, E = D / 64;
     const int lane = threadIdx.x & 63, l16 = lane & 15, lg = lane >> 4;
-    const int64_t wid = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (wid >= (int64_t)B * Hkv * n) return;                      // wave-uniform; no barrier follows
-    const int64_t i = wid % n;
-    const int g = (int)((wid / n) % Hkv);
-    const int b = (int)(wid / (n * Hkv));
     const int G = Hq / Hkv;
+    const int64_t nw = (n + qpw - 1) / qpw;
+    const int64_t wid = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (wid >= (int64_t)B * Hkv * nw) return;                     // wave-uniform; no barrier follows
+    const int64_t i0 = (wid % nw) * qpw;                          // the wave's first query row
+    const int g = (int)((wid / nw) % Hkv);
+    const int b = (int)(wid / (nw * Hkv));
     const int64_t nb = n / 64;
     const int64_t bg = (int64_t)b * Hkv + g;
-    if (i < 64) {   // clear key row i of the sink accumulators (bwd_sink adds into them next)
-        float *acc = sink_acc + (bg * 2 * 64 + i) * D;
+    for (int qq = 0; qq < qpw; ++qq) {   // clear key row i of the sink accumulators (bwd_sink adds into them next)
+        const int64_t ic = i0 + qq;
+        if (ic >= 64 || ic >= n) break;
+        float *acc = sink_acc + (bg * 2 * 64 + ic) * D;
 #pragma unroll
         for (int e = 0; e < E; ++e) {
             acc[lane + 64 * e] = 0.0f;
             acc[64 * D + lane + 64 * e] = 0.0f;
         }
     }
-    const bool hv = l16 < G;
-    const int h = g * G + (hv ? l16 : 0);
+    // column l16 = (query qs of the wave, head l16 - qs G)
+    const int qs = l16 / G;
+    const int64_t iq = i0 + qs;
+    const bool hv = qs < qpw && iq < n;
+    const int64_t i = hv ? iq : i0;                               // a row in range for every column
+    const int h = g * G + (hv ? l16 - qs * G : 0);
     const int64_t row = (((int64_t)b * n + i) * Hq + h) * D;
 
-    // query row elements t = 32 ks + 8 lg + e of head l16: raw, dO, O
+    // query row elements t = 32 ks + 8 lg + e of this column: raw, dO, O
     float x[NKS][8], dov[NKS][8];
     float ss = 0.0f, od = 0.0f;
 #pragma unroll
@@ -410,14 +417,33 @@ __global__ __launch_bounds__(256) void bwd_dq_mfma_kernel(
         qopr[ks] = pack_b8(qrv);
     }
 
-    // the units: the sink unit, the window pages, the routed picks
-    const int64_t nsink = ((int64_t)S < i + 1) ? (int64_t)S : i + 1;
+    // the units, shared by the wave's queries: the sink unit, the window pages
+    // from the first query's window start to the last query, then the routed
+    // picks of each query in turn; a block an earlier query of the wave also
+    // picked is skipped (it was taken then, for every query that holds it)
+    const int64_t nsink = hv ? (((int64_t)S < i + 1) ? (int64_t)S : i + 1) : 0;
     const int64_t wlo = (S > i - W + 1) ? (int64_t)S : i - W + 1;
-    const int64_t nwu = (i >= wlo) ? i / 64 - wlo / 64 + 1 : 0;
-    const int ncnt = min(max(cnt[bg * n + i], 0), kk);
-    const int32_t *sel = idx + (bg * n + i) * kk;
-    const int hs = nsink > 0 ? 1 : 0;
-    const int64_t nunits = hs + nwu + ncnt;
+    const int64_t ilast = min(n - 1, i0 + qpw - 1);
+    const int64_t wlo0 = (S > i0 - W + 1) ? (int64_t)S : i0 - W + 1;
+    const int64_t nwu = (ilast >= wlo0) ? ilast / 64 - wlo0 / 64 + 1 : 0;
+    const int hs = S > 0 ? 1 : 0;
+    int ncq[4];                                                    // picks per query of the wave (qpw <= 4)
+    int nrt = 0;
+#pragma unroll
+    for (int qq = 0; qq < 4; ++qq) {
+        ncq[qq] = (qq < qpw && i0 + qq < n) ? min(max(cnt[bg * n + i0 + qq], 0), kk) : 0;
+        nrt += ncq[qq];
+    }
+    // the picks of the wave, one per lane (entry lane + 64 t = query x kk + r)
+    int ent[2], entq[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        const int en = lane + 64 * t, qe = en / kk, r = en % kk;
+        const bool ok = qe < qpw && i0 + qe < n && r < min(max(cnt[bg * n + min(i0 + qe, n - 1)], 0), kk);
+        ent[t] = ok ? idx[(bg * n + i0 + qe) * kk + r] : -1;
+        entq[t] = qe;
+    }
+    const int64_t nunits = hs + nwu + nrt;
     auto unit = [&](int64_t u, int64_t &kb, int64_t &lo, int64_t &hi, bool &rope) -> bool {
         rope = false;
         if (u < hs) {
@@ -429,16 +455,31 @@ __global__ __launch_bounds__(256) void bwd_dq_mfma_kernel(
         u -= hs;
         if (u < nwu) {
             rope = true;
-            kb = 64 * (wlo / 64 + u);
+            kb = 64 * (wlo0 / 64 + u);
             lo = (wlo > kb) ? wlo : kb;
-            hi = (i < kb + 63) ? i : kb + 63;
+            hi = !hv ? kb - 1 : (i < kb + 63) ? i : kb + 63;
             return true;
         }
-        const int blk = sel[u - nwu];
+        int e = (int)(u - nwu), qp = 0;
+#pragma unroll
+        for (int qq = 0; qq < 3; ++qq)
+            if (qp == qq && e >= ncq[qq]) {
+                e -= ncq[qq];
+                qp = qq + 1;
+            }
+        const int blk = idx[(bg * n + i0 + qp) * kk + e];
+        if (blk < 1 || (int64_t)blk >= nb) return false;
+        unsigned has = 1u << qp;                                   // its own query, whatever kk
+#pragma unroll
+        for (int qq = 0; qq < 4; ++qq) {
+            const bool m0 = ent[0] == blk && entq[0] == qq, m1 = ent[1] == blk && entq[1] == qq;
+            if (__ballot(m0) | __ballot(m1)) has |= 1u << qq;
+        }
+        if (has & ((1u << qp) - 1u)) return false;                // an earlier query of the wave took it
         kb = 64 * (int64_t)blk;
         lo = kb;
-        hi = kb + 63;
-        return blk >= 1 && (int64_t)blk < nb;
+        hi = (hv && ((has >> qs) & 1u)) ? kb + 63 : kb - 1;
+        return true;
     };
     auto scores = [&](int64_t kb, bool rope, f32x4 (&Sa)[4]) {
         const bf16_t *K = (rope ? kr : kc) + (bg * n + kb) * D;
@@ -451,7 +492,7 @@ __global__ __launch_bounds__(256) void bwd_dq_mfma_kernel(
         }
     };
 
-    // pass 1: the union LSE of column l16
+    // pass 1: the union LSE of column l16 (a unit may hold no key of a column)
     float m = -INFINITY, l = 0.0f;
     for (int64_t u = 0; u < nunits; ++u) {
         int64_t kb, lo, hi;
@@ -477,7 +518,7 @@ __global__ __launch_bounds__(256) void bwd_dq_mfma_kernel(
                 const int64_t key = kb + kkey(mt, lg, e);
                 if (key >= lo && key <= hi) ps += __expf(Sa[mt][e] * scale - mn);
             }
-        l = l * __expf(m - mn) + col_sum(ps);
+        l = l * ((m == -INFINITY) ? 0.0f : __expf(m - mn)) + col_sum(ps);
         m = mn;
     }
     const float lse = (l > 0.0f) ? m + __logf(l) : INFINITY;
@@ -1140,6 +1181,11 @@ extern "C" int hba_attn_bwd(int dtype, const void *q, const void *k, const void 
     const int64_t g2 = B * Hkv * (n / 64);
     const int nsplit = (int)((n + bw::SINK_ROWS - 1) / bw::SINK_ROWS);
     const int64_t gs = B * Hkv * nsplit;
+    // queries per bwd_dq_mfma wave: 16 / G tile columns, at most 4, with
+    // every pick of the wave's queries held one per lane in two registers
+    int qpw = (int)std::min<int64_t>(4, 16 / (Hq / Hkv));
+    while (qpw > 1 && qpw * k_blocks > 128) --qpw;
+    const int64_t g1q = (B * Hkv * ((n + qpw - 1) / qpw) + 3) / 4;
     const int nsplit_kv = (int)((n + bw::DKV_ROWS - 1) / bw::DKV_ROWS);
     const int64_t g3 = B * Hkv * (n / 64) * nsplit_kv;
     const int64_t g4 = B * Hkv * n / 4;
@@ -1150,11 +1196,11 @@ extern "C" int hba_attn_bwd(int dtype, const void *q, const void *k, const void 
         if constexpr (DT == 1) {                                                                                \
             hipLaunchKernelGGL((bw::bwd_kt_kernel<D>), dim3((unsigned)g2), dim3(256), 0, s, (const bf16_t *)kc,  \
                                (const bf16_t *)kr, kct, krt, n, dkv_acc);                                        \
-            hipLaunchKernelGGL((bw::bwd_dq_mfma_kernel<D>), dim3((unsigned)g1), dim3(256), 0, s,                 \
+            hipLaunchKernelGGL((bw::bwd_dq_mfma_kernel<D>), dim3((unsigned)g1q), dim3(256), 0, s,                \
                                (const bf16_t *)q, (const bf16_t *)kc, (const bf16_t *)kr, kct, krt,             \
                                (const bf16_t *)v, q_gain, eps, cos_tab, sin_tab, idx, cnt, (const bf16_t *)out,  \
                                (const bf16_t *)dout, (int)B, n, (int)Hq, (int)Hkv, (int)S, W, (int)k_blocks,     \
-                               scale, qc_ws, qr_ws, lse_ws, dd_ws, sink_acc, (bf16_t *)dq, dq_gain);             \
+                               scale, qpw, qc_ws, qr_ws, lse_ws, dd_ws, sink_acc, (bf16_t *)dq, dq_gain);        \
         } else if (Hq / Hkv <= 8)                                                                               \
             hipLaunchKernelGGL((bw::bwd_dq_kernel<DT, D, 8>), dim3((unsigned)g1), dim3(256), 0, s,               \
                                (const T *)q, (const T *)kc, (const T *)kr, (const T *)v, q_gain, eps, cos_tab,   \

@@ -548,6 +548,32 @@ def test_backward_row_ranges_matches_oracle(dev):
         assert rel < GRAD_TOL["bf16"], (name, rel)
 
 
+@pytest.mark.parametrize("Hq,Hkv,k", [(8, 2, 4), (10, 2, 8), (16, 1, 4)])
+def test_backward_group_sizes_match_oracle(dev, Hq, Hkv, k):
+    """bf16 backward with G = 4, 5 and 16 heads per KV head: the MFMA dq
+    waves then take 4, 3 (the last wave ragged, n % 3 != 0) and 1 queries."""
+    n = 512
+    cfg, x, prm, cos, sin = make(dev, "bf16", n=n, Hq=Hq, Hkv=Hkv, W=128, k=k, S=4, needles=True)
+    q, k_, v = (x[t].clone().requires_grad_(True) for t in ("q", "k", "v"))
+    gq = x["q_gain"].clone().requires_grad_(True)
+    gk = x["k_gain"].clone().requires_grad_(True)
+    qkn = synth.Params(gq, gk, x["probes"], x["proj"])
+    out = hba_amd.hba_attention_eval(q, k_, v, cos, sin, cfg, qkn, qkn, None)
+    dout = torch.randn(out.shape, generator=torch.Generator().manual_seed(5)).to(out.dtype).to(dev)
+    out.backward(dout)
+    torch.cuda.synchronize()
+    with torch.no_grad():
+        r = hba_amd.forward_stages(x["q"], x["k"], x["v"], cos, sin, cfg, qkn, qkn)
+    idx, cnt = r["idx"][0].cpu().numpy(), r["cnt"][0].cpu().numpy()
+    scale = hba_amd.union_scale(cfg, cfg.head_dim, n)
+    ref = O.union_backward(f(x["q"])[0], f(x["k"])[0], f(x["v"])[0], f(cos), f(sin), scale, f(x["q_gain"]),
+                           f(x["k_gain"]), 1e-6, idx, cnt, f(dout)[0], cfg.sinks, cfg.window, 64, True)
+    got = [f(q.grad)[0], f(k_.grad)[0], f(v.grad)[0], f(gq.grad), f(gk.grad)]
+    for name, a, b in zip(["dq", "dk", "dv", "dq_gain", "dk_gain"], got, ref):
+        rel = np.abs(a - b).max() / max(np.abs(b).max(), 1e-6)
+        assert rel < GRAD_TOL["bf16"], (name, rel)
+
+
 def test_backward_no_grad_inputs_stays_forward_only(dev):
     cfg, x, prm, cos, sin = make(dev, "bf16", n=256, W=64, k=2)
     out = hba_amd.hba_attention_eval(x["q"], x["k"], x["v"], cos, sin, cfg, prm, prm, None)
