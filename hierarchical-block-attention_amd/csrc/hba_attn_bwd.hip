@@ -31,9 +31,9 @@
 // bf16 inputs take the same gradients on MFMA: bwd_kt (transposed keys),
 // bwd_dq_mfma (the G heads are the columns of 16-wide tiles), bwd_dkv_mfma
 // (32 (row, head) pairs per tile, one workgroup per key block and row range)
-// and bwd_dkv_fin (rope^T and the QKNorm backward of the key rows).  Both
-// paths share bwd_sink for the sink keys, whose rows are split over
-// workgroups.
+// and bwd_dkv_fin (rope^T and the QKNorm backward of the key rows); a second
+// bwd_dkv_mfma launch takes the sink keys.  The fp32 path takes the sink keys
+// in bwd_sink.  Both split the sink keys' query rows over workgroups.
 #include "hba_abi.h"
 #include "hba_common.h"
 
@@ -848,6 +848,10 @@ __global__ __launch_bounds__(DkvCfg<D>::NT) void bwd_dkv_kernel(
 // (fp32 atomics) into dkv_acc [B, Hkv, n, 3, d] (NoPE dk, rotated dk, dv),
 // which bwd_dkv_fin turns into dk and dv.  The split over row ranges keeps a
 // block that nearly every query selects from becoming the tail.
+// With sink_rows > 0 the launch takes the sink keys instead: one workgroup
+// per (b, g, range of sink_rows rows) against block 0, every row of the range
+// attending the keys j < S with j <= i (NoPE); waves whose 16 keys hold no
+// sink skip the products.
 constexpr int DKV_ROWS = 4096;
 constexpr int DKV_TP = 32;   // pairs per tile
 
@@ -872,7 +876,7 @@ __global__ __launch_bounds__(256) void bwd_dkv_mfma_kernel(
     const int32_t *__restrict__ idx, const int32_t *__restrict__ cnt, const bf16_t *__restrict__ dout, int64_t n,
     int Hq, int Hkv, int S, int64_t W, int kk, float scale, int nsplit, const float *__restrict__ qc_ws,
     const float *__restrict__ qr_ws, const float *__restrict__ lse_ws, const float *__restrict__ dd_ws,
-    float *__restrict__ dkv_acc) {
+    float *__restrict__ dkv_acc, int sink_rows) {
     constexpr int NKS = D / 32, NDT = D / 16, NCH = D / 8, CPT = DKV_TP * NCH / 256;
     using Tl = DkvTile<D>;
     constexpr int XP = Tl::XP, TP = Tl::TP;
@@ -880,14 +884,16 @@ __global__ __launch_bounds__(256) void bwd_dkv_mfma_kernel(
     __shared__ int rows[256];
     __shared__ int wcount[4];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, l16 = lane & 15, lg = lane >> 4;
-    const int64_t nb = n / 64;
+    const bool sinks = sink_rows > 0;
+    const int64_t nb = sinks ? 1 : n / 64;
     const int split = (int)(blockIdx.x % nsplit);
     const int64_t blk = (blockIdx.x / nsplit) % nb;
     const int64_t bg = blockIdx.x / ((int64_t)nsplit * nb);
     const int g = (int)(bg % Hkv), b = (int)(bg / Hkv);
     const int G = Hq / Hkv;
     const int64_t kb = 64 * blk;
-    const int64_t r0 = (int64_t)split * DKV_ROWS, r1 = min(n, r0 + DKV_ROWS);
+    const int64_t rows_per = sinks ? (int64_t)sink_rows : (int64_t)DKV_ROWS;
+    const int64_t r0 = (int64_t)split * rows_per, r1 = min(n, r0 + rows_per);
     const int64_t jl = kb + 16 * w + l16;   // the key of this lane's S / dP column
 
     bf16x8 kcb[NKS], krb[NKS], vb[NKS];
@@ -901,8 +907,10 @@ __global__ __launch_bounds__(256) void bwd_dkv_mfma_kernel(
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) gkc[dt] = gkr[dt] = gv[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    // pairs gp = 0 .. total-1: query row row_of(gp / G), head g G + gp % G
-    auto run = [&](int64_t total, auto row_of, bool rope) {
+    // pairs gp = 0 .. total-1: query row row_of(gp / G), head g G + gp % G;
+    // mode 0: window rows (rotated), 1: routed rows, 2: sink rows (NoPE)
+    auto run = [&](int64_t total, auto row_of, int mode) {
+        const bool rope = mode == 0;
         const float *qx = rope ? qr_ws : qc_ws;
         const int64_t ntl = (total + DKV_TP - 1) / DKV_TP;
         f32x4 xr[CPT][2];
@@ -961,6 +969,7 @@ __global__ __launch_bounds__(256) void bwd_dkv_mfma_kernel(
             }
         };
         auto compute = [&](const Tl &T) {
+            if (mode == 2 && 16 * w >= S) return;                  // no sink among the wave's keys
             f32x4 Sa[2], Pa[2];
 #pragma unroll
             for (int mt = 0; mt < 2; ++mt) {
@@ -984,7 +993,9 @@ __global__ __launch_bounds__(256) void bwd_dkv_mfma_kernel(
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const int64_t i = ri[e];
-                    const bool valid = rope ? (jl >= S && i >= jl && i <= jl + W - 1) : (i >= 0);
+                    const bool valid = (mode == 0) ? (jl >= S && i >= jl && i <= jl + W - 1)
+                                     : (mode == 1) ? (i >= 0)
+                                                   : (jl < S && i >= jl);
                     const float p = valid ? __expf(Sa[mt][e] * scale - ls[e]) : 0.0f;
                     pk[4 * mt + e] = p;
                     dk[4 * mt + e] = p * (Pa[mt][e] - ds[e]) * scale;
@@ -1012,17 +1023,21 @@ __global__ __launch_bounds__(256) void bwd_dkv_mfma_kernel(
     };
 
     bool had_win = false, had_rt = false;
+    if (sinks) {
+        had_rt = true;
+        run((r1 - r0) * G, [&](int64_t r) { return r0 + r; }, 2);
+    }
     // window rows: key j >= S is in the window of queries j .. j + W - 1
-    {
+    if (!sinks) {
         const int64_t wa = max(kb, r0);
         const int64_t wb = min(min(n - 1, kb + 63 + W - 1), r1 - 1);
         if (wb >= wa) {
             had_win = true;
-            run((wb - wa + 1) * G, [&](int64_t r) { return wa + r; }, true);
+            run((wb - wa + 1) * G, [&](int64_t r) { return wa + r; }, 0);
         }
     }
     // routed rows: the queries of the range whose selection holds this block
-    if (blk >= 1) {
+    if (!sinks && blk >= 1) {
         for (int64_t i0 = r0; i0 < r1; i0 += 256) {
             const int64_t i = i0 + tid;
             bool picked = false;
@@ -1044,17 +1059,19 @@ __global__ __launch_bounds__(256) void bwd_dkv_mfma_kernel(
             __syncthreads();
             if (tot > 0) {
                 had_rt = true;
-                run((int64_t)tot * G, [&](int64_t r) { return (int64_t)rows[r]; }, false);
+                run((int64_t)tot * G, [&](int64_t r) { return (int64_t)rows[r]; }, 1);
             }
             __syncthreads();                                      // rows[] and wcount[] reused
         }
     }
 
+    if (sinks && 16 * w >= S) return;                              // after the last barrier
     float *acc = dkv_acc + (bg * n + kb + 16 * w + 4 * lg) * 3 * D + l16;
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
+            if (sinks && 16 * w + 4 * lg + e >= S) continue;
             float *a = acc + e * 3 * D + 16 * dt;
             if (had_rt) unsafeAtomicAdd(a, gkc[dt][e]);
             if (had_win) unsafeAtomicAdd(a + D, gkr[dt][e]);
@@ -1086,7 +1103,7 @@ __global__ __launch_bounds__(256) void bwd_dkv_fin_kernel(
         gkc[e] = a[d];
         gkr[e] = a[D + d];
         gv[e] = a[2 * D + d];
-        if (j < S) {
+        if (j < S && sink_acc) {
             const float *sa = sink_acc + (bg * 2 * 64 + j) * D;
             gkc[e] += sa[d];
             gv[e] += sa[64 * D + d];
@@ -1213,18 +1230,23 @@ extern "C" int hba_attn_bwd(int dtype, const void *q, const void *k, const void 
                                sin_tab, idx, cnt, (const T *)out, (const T *)dout, (int)B, n, (int)Hq, (int)Hkv, \
                                (int)S, W, (int)k_blocks, scale, qc_ws, qr_ws, lse_ws, dd_ws, sink_acc, (T *)dq,   \
                                dq_gain);                                                                        \
-        if (S > 0)                                                                                              \
+        if (S > 0 && DT == 0)                                                                                   \
             hipLaunchKernelGGL((bw::bwd_sink_kernel<DT, D>), dim3((unsigned)gs), dim3(bw::DkvCfg<D>::NT), 0, s,  \
                                (const T *)kc, (const T *)v, (const T *)dout, n, (int)Hq, (int)Hkv, (int)S,       \
                                nsplit, scale, qc_ws, lse_ws, dd_ws, sink_acc);                                   \
         if constexpr (DT == 1) {                                                                                \
+            if (S > 0)                                                                                          \
+                hipLaunchKernelGGL((bw::bwd_dkv_mfma_kernel<D>), dim3((unsigned)gs), dim3(256), 0, s,            \
+                                   (const bf16_t *)kc, (const bf16_t *)kr, (const bf16_t *)v, idx, cnt,          \
+                                   (const bf16_t *)dout, n, (int)Hq, (int)Hkv, (int)S, W, (int)k_blocks, scale,  \
+                                   nsplit, qc_ws, qr_ws, lse_ws, dd_ws, dkv_acc, bw::SINK_ROWS);                 \
             hipLaunchKernelGGL((bw::bwd_dkv_mfma_kernel<D>), dim3((unsigned)g3), dim3(256), 0, s,                \
                                (const bf16_t *)kc, (const bf16_t *)kr, (const bf16_t *)v, idx, cnt,              \
                                (const bf16_t *)dout, n, (int)Hq, (int)Hkv, (int)S, W, (int)k_blocks, scale,      \
-                               nsplit_kv, qc_ws, qr_ws, lse_ws, dd_ws, dkv_acc);                                 \
+                               nsplit_kv, qc_ws, qr_ws, lse_ws, dd_ws, dkv_acc, 0);                              \
             hipLaunchKernelGGL((bw::bwd_dkv_fin_kernel<D>), dim3((unsigned)g4), dim3(256), 0, s,                 \
                                (const bf16_t *)k, k_gain, eps, cos_tab, sin_tab, n, (int)Hkv, (int)S, dkv_acc,    \
-                               sink_acc, (bf16_t *)dk, (bf16_t *)dv, dk_gain);                                   \
+                               (const float *)nullptr, (bf16_t *)dk, (bf16_t *)dv, dk_gain);                     \
         } else                                                                                                  \
             hipLaunchKernelGGL((bw::bwd_dkv_kernel<DT, D>), dim3((unsigned)g2), dim3(bw::DkvCfg<D>::NT), 0, s,   \
                                (const T *)k, (const T *)kc, (const T *)kr, (const T *)v, k_gain, eps, cos_tab,   \
