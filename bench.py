@@ -364,9 +364,9 @@ def bench_bwd32k(dev, reps=5):
             "tokens_per_s": round(w["seq_len"] / (ms * 1e-3), 1), "ms": round(ms, 3), "flop": flop,
             "achieved_TFLOPs": round(tflops, 2), "mfma_frac": round(tflops / PEAK_BF16_TFLOPS, 5),
             "timing": f"median of {reps} backward calls",
-            "kernels": "bwd_kt (transposed keys) + bwd_dq_mfma (one wave per query and KV head, 64-key units on "
-                       "MFMA) + bwd_sink (sink keys, VALU) + bwd_dkv_mfma (one workgroup per KV head, 64-key block "
-                       "and 4096-row range, 32-pair tiles on MFMA) + bwd_dkv_fin (rope^T, QKNorm backward)"}
+            "kernels": "bwd_kt (transposed keys) + bwd_dq_mfma (16/G queries per wave, 64-key units on MFMA) + "
+                       "bwd_dkv_mfma (one workgroup per KV head, 64-key block and 4096-row range, 64-pair tiles "
+                       "on MFMA; a second launch for the sink keys) + bwd_dkv_fin (rope^T, QKNorm backward)"}
 
 
 def bench_hier128k(dev):

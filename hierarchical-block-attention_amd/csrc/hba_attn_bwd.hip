@@ -342,7 +342,7 @@ __global__ __launch_bounds__(256) void bwd_dq_mfma_kernel(
     const float *__restrict__ qgain, float eps, const float *__restrict__ cosT, const float *__restrict__ sinT,
     const int32_t *__restrict__ idx, const int32_t *__restrict__ cnt, const bf16_t *__restrict__ out,
     const bf16_t *__restrict__ dout, int B, int64_t n, int Hq, int Hkv, int S, int64_t W, int kk, float scale,
-    int qpw, float *__restrict__ qc_ws, float *__restrict__ qr_ws, float *__restrict__ lse_ws,
+    int qpw, bf16_t *__restrict__ qc_ws, bf16_t *__restrict__ qr_ws, float *__restrict__ lse_ws,
     float *__restrict__ dd_ws, float *__restrict__ sink_acc, bf16_t *__restrict__ dq, float *__restrict__ dq_gain) {
     constexpr int NKS = D / 32, NDT = D / 16, E = D / 64;
     const int lane = threadIdx.x & 63, l16 = lane & 15, lg = lane >> 4;
@@ -410,8 +410,8 @@ __global__ __launch_bounds__(256) void bwd_dq_mfma_kernel(
             const float c = rnd_bf16(cosT[i * D + t]), sn = rnd_bf16(sinT[i * D + t]);
             qrv[e] = rnd_bf16(rnd_bf16(qcv[ks][e] * c) + rnd_bf16(rot * sn));
             if (hv) {
-                qc_ws[row + t] = qcv[ks][e];
-                qr_ws[row + t] = qrv[e];
+                qc_ws[row + t] = f2bf(qcv[ks][e]);                      // bf16-exact values
+                qr_ws[row + t] = f2bf(qrv[e]);
             }
         }
         qopr[ks] = pack_b8(qrv);
@@ -831,7 +831,8 @@ __global__ __launch_bounds__(DkvCfg<D>::NT) void bwd_dkv_kernel(
 
 // ------------------------------------------------ bwd_dkv on MFMA (bf16) ----
 // dK and dV of one 64-key block from the (query row, head) pairs that attend
-// it, 32 pairs per tile staged in LDS twice (row-major and transposed); wave w
+// it, 64 pairs per tile staged in LDS twice (row-major and transposed), taken
+// as two halves of 32 (the contraction of one product); wave w
 // owns keys kb + 16 w .. kb + 16 w + 15:
 //   S   = X . K^T    (A: staged query rows X, pairs in the slot order pslot;
 //                     B: the wave's key rows, held in registers)
@@ -853,7 +854,7 @@ __global__ __launch_bounds__(DkvCfg<D>::NT) void bwd_dkv_kernel(
 // attending the keys j < S with j <= i (NoPE); waves whose 16 keys hold no
 // sink skip the products.
 constexpr int DKV_ROWS = 4096;
-constexpr int DKV_TP = 32;   // pairs per tile
+constexpr int DKV_TP = 64;   // pairs per tile: two halves of 32, the pair count of one product
 
 __device__ __forceinline__ int pslot(int mt, int r) { return 8 * (r >> 2) + 4 * mt + (r & 3); }
 
@@ -874,8 +875,8 @@ template <int D>
 __global__ __launch_bounds__(256) void bwd_dkv_mfma_kernel(
     const bf16_t *__restrict__ kc, const bf16_t *__restrict__ kr, const bf16_t *__restrict__ v,
     const int32_t *__restrict__ idx, const int32_t *__restrict__ cnt, const bf16_t *__restrict__ dout, int64_t n,
-    int Hq, int Hkv, int S, int64_t W, int kk, float scale, int nsplit, const float *__restrict__ qc_ws,
-    const float *__restrict__ qr_ws, const float *__restrict__ lse_ws, const float *__restrict__ dd_ws,
+    int Hq, int Hkv, int S, int64_t W, int kk, float scale, int nsplit, const bf16_t *__restrict__ qc_ws,
+    const bf16_t *__restrict__ qr_ws, const float *__restrict__ lse_ws, const float *__restrict__ dd_ws,
     float *__restrict__ dkv_acc, int sink_rows) {
     constexpr int NKS = D / 32, NDT = D / 16, NCH = D / 8, CPT = DKV_TP * NCH / 256;
     using Tl = DkvTile<D>;
@@ -911,10 +912,9 @@ __global__ __launch_bounds__(256) void bwd_dkv_mfma_kernel(
     // mode 0: window rows (rotated), 1: routed rows, 2: sink rows (NoPE)
     auto run = [&](int64_t total, auto row_of, int mode) {
         const bool rope = mode == 0;
-        const float *qx = rope ? qr_ws : qc_ws;
+        const bf16_t *qx = rope ? qr_ws : qc_ws;
         const int64_t ntl = (total + DKV_TP - 1) / DKV_TP;
-        f32x4 xr[CPT][2];
-        u32x4b orr[CPT];
+        u32x4b xr[CPT], orr[CPT];
         float plse[CPT], pdd[CPT];
         int prow[CPT];
         auto load = [&](int64_t t) {
@@ -929,8 +929,7 @@ __global__ __launch_bounds__(256) void bwd_dkv_mfma_kernel(
                     const int64_t i = row_of(gp / G);
                     const int h = g * G + (int)(gp % G);
                     const int64_t ro = (((int64_t)b * n + i) * Hq + h) * D + 8 * c;
-                    xr[r][0] = *reinterpret_cast<const f32x4 *>(qx + ro);
-                    xr[r][1] = *reinterpret_cast<const f32x4 *>(qx + ro + 4);
+                    xr[r] = *reinterpret_cast<const u32x4b *>(qx + ro);
                     orr[r] = *reinterpret_cast<const u32x4b *>(dout + ro);
                     if (c == 0) {
                         const int64_t so = ((int64_t)b * Hq + h) * n + i;
@@ -939,8 +938,7 @@ __global__ __launch_bounds__(256) void bwd_dkv_mfma_kernel(
                         prow[r] = (int)i;
                     }
                 } else {
-                    xr[r][0] = xr[r][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-                    orr[r] = u32x4b{0u, 0u, 0u, 0u};
+                    xr[r] = orr[r] = u32x4b{0u, 0u, 0u, 0u};
                 }
             }
         };
@@ -948,18 +946,14 @@ __global__ __launch_bounds__(256) void bwd_dkv_mfma_kernel(
 #pragma unroll
             for (int r = 0; r < CPT; ++r) {
                 const int q = tid + 256 * r, p = q / NCH, c = q % NCH;
-                u32x4b xp;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const f32x4 &h4 = xr[r][e >> 1];
-                    xp[e] = (uint32_t)f2bf(h4[2 * (e & 1)]) | ((uint32_t)f2bf(h4[2 * (e & 1) + 1]) << 16);
-                }
-                *reinterpret_cast<u32x4b *>(&T.xs[p * XP + 8 * c]) = xp;
+                *reinterpret_cast<u32x4b *>(&T.xs[p * XP + 8 * c]) = xr[r];
                 *reinterpret_cast<u32x4b *>(&T.os[p * XP + 8 * c]) = orr[r];
+                // transposed rows d = 8 c + e, this pair in 8-pair group (p >> 3) ^ (c & 7)
+                const int tc = ((((p >> 3) ^ c) & 7) << 3) | (p & 7);
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
-                    T.xt[(8 * c + e) * TP + p] = (bf16_t)(xp[e >> 1] >> (16 * (e & 1)));
-                    T.ot[(8 * c + e) * TP + p] = (bf16_t)(orr[r][e >> 1] >> (16 * (e & 1)));
+                    T.xt[(8 * c + e) * TP + tc] = (bf16_t)(xr[r][e >> 1] >> (16 * (e & 1)));
+                    T.ot[(8 * c + e) * TP + tc] = (bf16_t)(orr[r][e >> 1] >> (16 * (e & 1)));
                 }
                 if (c == 0) {
                     T.lse[p] = plse[r];
@@ -970,11 +964,14 @@ __global__ __launch_bounds__(256) void bwd_dkv_mfma_kernel(
         };
         auto compute = [&](const Tl &T) {
             if (mode == 2 && 16 * w >= S) return;                  // no sink among the wave's keys
+#pragma unroll
+          for (int hp = 0; hp < DKV_TP / 32; ++hp) {
+            if (T.row[32 * hp] < 0) break;                         // the rest is padding (pairs fill in order)
             f32x4 Sa[2], Pa[2];
 #pragma unroll
             for (int mt = 0; mt < 2; ++mt) {
-                const bf16_t *xa = &T.xs[pslot(mt, l16) * XP + 8 * lg];
-                const bf16_t *oa = &T.os[pslot(mt, l16) * XP + 8 * lg];
+                const bf16_t *xa = &T.xs[(32 * hp + pslot(mt, l16)) * XP + 8 * lg];
+                const bf16_t *oa = &T.os[(32 * hp + pslot(mt, l16)) * XP + 8 * lg];
                 Sa[mt] = Pa[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int ks = 0; ks < NKS; ++ks) {
@@ -985,7 +982,7 @@ __global__ __launch_bounds__(256) void bwd_dkv_mfma_kernel(
             float pk[8], dk[8];
 #pragma unroll
             for (int mt = 0; mt < 2; ++mt) {
-                const int pp = 8 * lg + 4 * mt;
+                const int pp = 32 * hp + 8 * lg + 4 * mt;
                 const f32x4 ls = *reinterpret_cast<const f32x4 *>(&T.lse[pp]);
                 const f32x4 ds = *reinterpret_cast<const f32x4 *>(&T.dd[pp]);
                 const int4 rw = *reinterpret_cast<const int4 *>(&T.row[pp]);
@@ -1004,11 +1001,14 @@ __global__ __launch_bounds__(256) void bwd_dkv_mfma_kernel(
             const bf16x8 pa = pack_b8(pk), da = pack_b8(dk);
 #pragma unroll
             for (int dt = 0; dt < NDT; ++dt) {
-                gv[dt] = mfma16(pa, ld_b8(&T.ot[(16 * dt + l16) * TP + 8 * lg]), gv[dt]);
-                const bf16x8 xb = ld_b8(&T.xt[(16 * dt + l16) * TP + 8 * lg]);
+                const int dr = 16 * dt + l16;                      // pairs 32 hp + 8 lg .. + 7 of row dr
+                const int to = dr * TP + ((((4 * hp + lg) ^ (dr >> 3)) & 7) << 3);
+                gv[dt] = mfma16(pa, ld_b8(&T.ot[to]), gv[dt]);
+                const bf16x8 xb = ld_b8(&T.xt[to]);
                 if (rope) gkr[dt] = mfma16(da, xb, gkr[dt]);
                 else gkc[dt] = mfma16(da, xb, gkc[dt]);
             }
+          }
         };
         if (ntl <= 0) return;
         load(0);
@@ -1186,6 +1186,8 @@ extern "C" int hba_attn_bwd(int dtype, const void *q, const void *k, const void 
     if (ws_bytes < need || !abi::aligned16(workspace)) return HBA_ERR_INVALID_ARG;
     float *qc_ws = (float *)workspace;
     float *qr_ws = qc_ws + B * n * Hq * d;
+    bf16_t *qcb_ws = reinterpret_cast<bf16_t *>(qc_ws);            // the bf16 path's query rows (half the room)
+    bf16_t *qrb_ws = reinterpret_cast<bf16_t *>(qr_ws);
     float *lse_ws = qr_ws + B * n * Hq * d;
     float *dd_ws = lse_ws + B * Hq * n;
     float *sink_acc = dd_ws + B * Hq * n;                          // [B, Hkv, 2, 64, d] (Hkv <= Hq)
@@ -1217,7 +1219,7 @@ extern "C" int hba_attn_bwd(int dtype, const void *q, const void *k, const void 
                                (const bf16_t *)q, (const bf16_t *)kc, (const bf16_t *)kr, kct, krt,             \
                                (const bf16_t *)v, q_gain, eps, cos_tab, sin_tab, idx, cnt, (const bf16_t *)out,  \
                                (const bf16_t *)dout, (int)B, n, (int)Hq, (int)Hkv, (int)S, W, (int)k_blocks,     \
-                               scale, qpw, qc_ws, qr_ws, lse_ws, dd_ws, sink_acc, (bf16_t *)dq, dq_gain);        \
+                               scale, qpw, qcb_ws, qrb_ws, lse_ws, dd_ws, sink_acc, (bf16_t *)dq, dq_gain);      \
         } else if (Hq / Hkv <= 8)                                                                               \
             hipLaunchKernelGGL((bw::bwd_dq_kernel<DT, D, 8>), dim3((unsigned)g1), dim3(256), 0, s,               \
                                (const T *)q, (const T *)kc, (const T *)kr, (const T *)v, q_gain, eps, cos_tab,   \
@@ -1239,11 +1241,11 @@ extern "C" int hba_attn_bwd(int dtype, const void *q, const void *k, const void 
                 hipLaunchKernelGGL((bw::bwd_dkv_mfma_kernel<D>), dim3((unsigned)gs), dim3(256), 0, s,            \
                                    (const bf16_t *)kc, (const bf16_t *)kr, (const bf16_t *)v, idx, cnt,          \
                                    (const bf16_t *)dout, n, (int)Hq, (int)Hkv, (int)S, W, (int)k_blocks, scale,  \
-                                   nsplit, qc_ws, qr_ws, lse_ws, dd_ws, dkv_acc, bw::SINK_ROWS);                 \
+                                   nsplit, qcb_ws, qrb_ws, lse_ws, dd_ws, dkv_acc, bw::SINK_ROWS);               \
             hipLaunchKernelGGL((bw::bwd_dkv_mfma_kernel<D>), dim3((unsigned)g3), dim3(256), 0, s,                \
                                (const bf16_t *)kc, (const bf16_t *)kr, (const bf16_t *)v, idx, cnt,              \
                                (const bf16_t *)dout, n, (int)Hq, (int)Hkv, (int)S, W, (int)k_blocks, scale,      \
-                               nsplit_kv, qc_ws, qr_ws, lse_ws, dd_ws, dkv_acc, 0);                              \
+                               nsplit_kv, qcb_ws, qrb_ws, lse_ws, dd_ws, dkv_acc, 0);                            \
             hipLaunchKernelGGL((bw::bwd_dkv_fin_kernel<D>), dim3((unsigned)g4), dim3(256), 0, s,                 \
                                (const bf16_t *)k, k_gain, eps, cos_tab, sin_tab, n, (int)Hkv, (int)S, dkv_acc,    \
                                (const float *)nullptr, (bf16_t *)dk, (bf16_t *)dv, dk_gain);                     \
