@@ -854,6 +854,7 @@ __global__ __launch_bounds__(DkvCfg<D>::NT) void bwd_dkv_kernel(
 // attending the keys j < S with j <= i (NoPE); waves whose 16 keys hold no
 // sink skip the products.
 constexpr int DKV_ROWS = 4096;
+constexpr int DKV_RL = 1024;   // routed rows collected before their tiles run
 constexpr int DKV_TP = 64;   // pairs per tile: two halves of 32, the pair count of one product
 
 __device__ __forceinline__ int pslot(int mt, int r) { return 8 * (r >> 2) + 4 * mt + (r & 3); }
@@ -882,7 +883,7 @@ __global__ __launch_bounds__(256) void bwd_dkv_mfma_kernel(
     using Tl = DkvTile<D>;
     constexpr int XP = Tl::XP, TP = Tl::TP;
     __shared__ Tl tl[2];
-    __shared__ int rows[256];
+    __shared__ int rows[DKV_RL];
     __shared__ int wcount[4];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, l16 = lane & 15, lg = lane >> 4;
     const bool sinks = sink_rows > 0;
@@ -1036,32 +1037,58 @@ __global__ __launch_bounds__(256) void bwd_dkv_mfma_kernel(
             run((wb - wa + 1) * G, [&](int64_t r) { return wa + r; }, 0);
         }
     }
-    // routed rows: the queries of the range whose selection holds this block
+    // routed rows: the queries of the range whose selection holds this block,
+    // collected over scan chunks of 512 rows (two per thread) until the list
+    // could overflow, then run as one pipelined series of tiles
     if (!sinks && blk >= 1) {
-        for (int64_t i0 = r0; i0 < r1; i0 += 256) {
-            const int64_t i = i0 + tid;
-            bool picked = false;
-            if (i < r1) {
-                const int nc = min(max(cnt[bg * n + i], 0), kk);
-                const int32_t *sl = idx + (bg * n + i) * kk;
-                for (int r = 0; r < nc; ++r) picked |= sl[r] == (int32_t)blk;
+        // 16-byte list loads when every row's list starts 16-byte aligned
+        const bool vec_idx = (kk & 3) == 0 && (reinterpret_cast<uintptr_t>(idx) & 15) == 0;
+        auto picks = [&](int64_t i) -> bool {
+            if (i >= r1) return false;
+            const int nc = min(max(cnt[bg * n + i], 0), kk);
+            const int32_t *sl = idx + (bg * n + i) * kk;
+            bool pk = false;
+            if (vec_idx) {
+                for (int r = 0; r < nc; r += 4) {
+                    const int4 v4 = *reinterpret_cast<const int4 *>(sl + r);
+                    pk |= (v4.x == (int32_t)blk) | ((r + 1 < nc) & (v4.y == (int32_t)blk)) |
+                          ((r + 2 < nc) & (v4.z == (int32_t)blk)) | ((r + 3 < nc) & (v4.w == (int32_t)blk));
+                }
+            } else {
+                for (int r = 0; r < nc; ++r) pk |= sl[r] == (int32_t)blk;
             }
-            const uint64_t bal = __ballot(picked);
-            if (lane == 0) wcount[w] = __popcll(bal);
-            __syncthreads();
-            int base = 0, tot = 0;
+            return pk;
+        };
+        int64_t i0 = r0;
+        while (i0 < r1) {
+            int tot = 0;
+            while (i0 < r1 && tot <= DKV_RL - 512) {
+                const bool pa = picks(i0 + tid), pb = picks(i0 + 256 + tid);
+                const uint64_t ba = __ballot(pa), bb = __ballot(pb);
+                if (lane == 0) wcount[w] = __popcll(ba) | (__popcll(bb) << 16);
+                __syncthreads();
+                int basea = 0, baseb = 0, ta = 0, tb = 0;
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                if (u < w) base += wcount[u];
-                tot += wcount[u];
+                for (int u = 0; u < 4; ++u) {
+                    const int wc = wcount[u];
+                    if (u < w) {
+                        basea += wc & 0xffff;
+                        baseb += wc >> 16;
+                    }
+                    ta += wc & 0xffff;
+                    tb += wc >> 16;
+                }
+                if (pa) rows[tot + basea + __popcll(ba & ((1ull << lane) - 1ull))] = (int)(i0 + tid);
+                if (pb) rows[tot + ta + baseb + __popcll(bb & ((1ull << lane) - 1ull))] = (int)(i0 + 256 + tid);
+                __syncthreads();                                  // rows[] complete; wcount[] reused
+                tot += ta + tb;
+                i0 += 512;
             }
-            if (picked) rows[base + __popcll(bal & ((1ull << lane) - 1ull))] = (int)i;
-            __syncthreads();
             if (tot > 0) {
                 had_rt = true;
                 run((int64_t)tot * G, [&](int64_t r) { return (int64_t)rows[r]; }, 1);
             }
-            __syncthreads();                                      // rows[] and wcount[] reused
+            __syncthreads();                                      // rows[] reused
         }
     }
 
