@@ -336,7 +336,7 @@ __global__ __launch_bounds__(256) void bwd_kt_kernel(const bf16_t *__restrict__ 
 }
 
 template <int D>
-__global__ __launch_bounds__(256) void bwd_dq_mfma_kernel(
+__global__ __launch_bounds__(256, D == 64 ? 2 : 1) void bwd_dq_mfma_kernel(
     const bf16_t *__restrict__ q, const bf16_t *__restrict__ kc, const bf16_t *__restrict__ kr,
     const bf16_t *__restrict__ kct, const bf16_t *__restrict__ krt, const bf16_t *__restrict__ v,
     const float *__restrict__ qgain, float eps, const float *__restrict__ cosT, const float *__restrict__ sinT,
@@ -345,17 +345,25 @@ __global__ __launch_bounds__(256) void bwd_dq_mfma_kernel(
     int qpw, bf16_t *__restrict__ qc_ws, bf16_t *__restrict__ qr_ws, float *__restrict__ lse_ws,
     float *__restrict__ dd_ws, float *__restrict__ sink_acc, bf16_t *__restrict__ dq, float *__restrict__ dq_gain) {
     constexpr int NKS = D / 32, NDT = D / 16, E = D / 64;
-    const int lane = threadIdx.x & 63, l16 = lane & 15, lg = lane >> 4;
+    // the window pages of the workgroup's queries, staged once for its four
+    // waves: K and V rows [64][D + 8], K^T rows [D][64 + 8]
+    constexpr int KS = D + 8, TS = 64 + 8, NCK = D / 8, CPK = D / 32;
+    __shared__ __align__(16) bf16_t wk[2][64 * KS];
+    __shared__ __align__(16) bf16_t wv[2][64 * KS];
+    __shared__ __align__(16) bf16_t wkt[2][D * TS];
+    const int tid = threadIdx.x, lane = tid & 63, l16 = lane & 15, lg = lane >> 4;
     const int G = Hq / Hkv;
-    const int64_t nw = (n + qpw - 1) / qpw;
-    const int64_t wid = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (wid >= (int64_t)B * Hkv * nw) return;                     // wave-uniform; no barrier follows
-    const int64_t i0 = (wid % nw) * qpw;                          // the wave's first query row
-    const int g = (int)((wid / nw) % Hkv);
-    const int b = (int)(wid / (nw * Hkv));
+    const int64_t nw = (n + qpw - 1) / qpw;                       // query waves per (b, g)
+    const int64_t nwg = (nw + 3) / 4;                             // workgroups per (b, g)
+    const int64_t wgi = blockIdx.x % nwg;
+    const int64_t wq = 4 * wgi + (tid >> 6);
+    const bool act = wq < nw;              // wave-uniform; an idle wave still stages and meets every barrier
+    const int64_t i0 = act ? wq * qpw : 0;                        // the wave's first query row
+    const int g = (int)((blockIdx.x / nwg) % Hkv);
+    const int b = (int)(blockIdx.x / (nwg * Hkv));
     const int64_t nb = n / 64;
     const int64_t bg = (int64_t)b * Hkv + g;
-    for (int qq = 0; qq < qpw; ++qq) {   // clear key row i of the sink accumulators (bwd_sink adds into them next)
+    for (int qq = 0; act && qq < qpw; ++qq) {   // clear key row i of the sink accumulators (bwd_sink adds into them next)
         const int64_t ic = i0 + qq;
         if (ic >= 64 || ic >= n) break;
         float *acc = sink_acc + (bg * 2 * 64 + ic) * D;
@@ -368,7 +376,7 @@ __global__ __launch_bounds__(256) void bwd_dq_mfma_kernel(
     // column l16 = (query qs of the wave, head l16 - qs G)
     const int qs = l16 / G;
     const int64_t iq = i0 + qs;
-    const bool hv = qs < qpw && iq < n;
+    const bool hv = act && qs < qpw && iq < n;
     const int64_t i = hv ? iq : i0;                               // a row in range for every column
     const int h = g * G + (hv ? l16 - qs * G : 0);
     const int64_t row = (((int64_t)b * n + i) * Hq + h) * D;
@@ -417,21 +425,23 @@ __global__ __launch_bounds__(256) void bwd_dq_mfma_kernel(
         qopr[ks] = pack_b8(qrv);
     }
 
-    // the units, shared by the wave's queries: the sink unit, the window pages
-    // from the first query's window start to the last query, then the routed
-    // picks of each query in turn; a block an earlier query of the wave also
-    // picked is skipped (it was taken then, for every query that holds it)
+    // the units of each wave, shared by its queries: the sink unit, then the
+    // routed picks of each query in turn; a block an earlier query of the wave
+    // also picked is skipped (it was taken then, for every query that holds
+    // it).  The window pages, from the workgroup's first query's window start
+    // to its last query, are taken by the whole workgroup from LDS.
     const int64_t nsink = hv ? (((int64_t)S < i + 1) ? (int64_t)S : i + 1) : 0;
     const int64_t wlo = (S > i - W + 1) ? (int64_t)S : i - W + 1;
-    const int64_t ilast = min(n - 1, i0 + qpw - 1);
-    const int64_t wlo0 = (S > i0 - W + 1) ? (int64_t)S : i0 - W + 1;
-    const int64_t nwu = (ilast >= wlo0) ? ilast / 64 - wlo0 / 64 + 1 : 0;
-    const int hs = S > 0 ? 1 : 0;
+    const int64_t iw0 = 4 * wgi * qpw, iw1 = min(n - 1, 4 * (wgi + 1) * qpw - 1);
+    const int64_t wlo0 = (S > iw0 - W + 1) ? (int64_t)S : iw0 - W + 1;
+    const int64_t npg = (iw1 >= wlo0) ? iw1 / 64 - wlo0 / 64 + 1 : 0;
+    const int64_t nwu = 0;
+    const int hs = (act && S > 0) ? 1 : 0;
     int ncq[4];                                                    // picks per query of the wave (qpw <= 4)
     int nrt = 0;
 #pragma unroll
     for (int qq = 0; qq < 4; ++qq) {
-        ncq[qq] = (qq < qpw && i0 + qq < n) ? min(max(cnt[bg * n + i0 + qq], 0), kk) : 0;
+        ncq[qq] = (act && qq < qpw && i0 + qq < n) ? min(max(cnt[bg * n + i0 + qq], 0), kk) : 0;
         nrt += ncq[qq];
     }
     // the picks of the wave, one per lane (entry lane + 64 t = query x kk + r)
@@ -439,7 +449,7 @@ __global__ __launch_bounds__(256) void bwd_dq_mfma_kernel(
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
         const int en = lane + 64 * t, qe = en / kk, r = en % kk;
-        const bool ok = qe < qpw && i0 + qe < n && r < min(max(cnt[bg * n + min(i0 + qe, n - 1)], 0), kk);
+        const bool ok = act && qe < qpw && i0 + qe < n && r < min(max(cnt[bg * n + min(i0 + qe, n - 1)], 0), kk);
         ent[t] = ok ? idx[(bg * n + i0 + qe) * kk + r] : -1;
         entq[t] = qe;
     }
@@ -492,14 +502,39 @@ __global__ __launch_bounds__(256) void bwd_dq_mfma_kernel(
         }
     };
 
+    // staging of window page kb: K rows (both passes), V and K^T rows (pass 2)
+    u32x4b rk[CPK], rv[CPK], rt[CPK];
+    auto wload = [&](int64_t kb, bool full) {
+#pragma unroll
+        for (int c = 0; c < CPK; ++c) {
+            const int qc = tid + 256 * c, kr_ = qc / NCK, kc_ = (qc % NCK) * 8, dr = qc / 8, kcol = (qc % 8) * 8;
+            rk[c] = *reinterpret_cast<const u32x4b *>(kr + (bg * n + kb + kr_) * D + kc_);
+            if (full) {
+                rv[c] = *reinterpret_cast<const u32x4b *>(v + (((int64_t)b * n + kb + kr_) * Hkv + g) * D + kc_);
+                rt[c] = *reinterpret_cast<const u32x4b *>(krt + (bg * D + dr) * n + kb + kcol);
+            }
+        }
+    };
+    auto wstore = [&](int bf, bool full) {
+#pragma unroll
+        for (int c = 0; c < CPK; ++c) {
+            const int qc = tid + 256 * c, kr_ = qc / NCK, kc_ = (qc % NCK) * 8, dr = qc / 8, kcol = (qc % 8) * 8;
+            *reinterpret_cast<u32x4b *>(&wk[bf][kr_ * KS + kc_]) = rk[c];
+            if (full) {
+                *reinterpret_cast<u32x4b *>(&wv[bf][kr_ * KS + kc_]) = rv[c];
+                *reinterpret_cast<u32x4b *>(&wkt[bf][dr * TS + kcol]) = rt[c];
+            }
+        }
+    };
+    // this column's keys of window page kb
+    auto wrange = [&](int64_t kb, int64_t &lo, int64_t &hi) {
+        lo = (wlo > kb) ? wlo : kb;
+        hi = !hv ? kb - 1 : (i < kb + 63) ? i : kb + 63;
+    };
+
     // pass 1: the union LSE of column l16 (a unit may hold no key of a column)
     float m = -INFINITY, l = 0.0f;
-    for (int64_t u = 0; u < nunits; ++u) {
-        int64_t kb, lo, hi;
-        bool rope;
-        if (!unit(u, kb, lo, hi, rope)) continue;
-        f32x4 Sa[4];
-        scores(kb, rope, Sa);
+    auto lse_acc = [&](const f32x4 (&Sa)[4], int64_t kb, int64_t lo, int64_t hi) {
         float mu = -INFINITY;
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt)
@@ -520,6 +555,39 @@ __global__ __launch_bounds__(256) void bwd_dq_mfma_kernel(
             }
         l = l * ((m == -INFINITY) ? 0.0f : __expf(m - mn)) + col_sum(ps);
         m = mn;
+    };
+    for (int64_t u = 0; u < nunits; ++u) {
+        int64_t kb, lo, hi;
+        bool rope;
+        if (!unit(u, kb, lo, hi, rope)) continue;
+        f32x4 Sa[4];
+        scores(kb, rope, Sa);
+        lse_acc(Sa, kb, lo, hi);
+    }
+    if (npg > 0) {                                                // workgroup-uniform
+        wload(64 * (wlo0 / 64), false);
+        wstore(0, false);
+        __syncthreads();
+        for (int64_t pg = 0; pg < npg; ++pg) {
+            const int64_t kb = 64 * (wlo0 / 64 + pg);
+            if (pg + 1 < npg) wload(kb + 64, false);
+            if (act) {
+                const bf16_t *Kp = wk[pg & 1];
+                f32x4 Sa[4];
+#pragma unroll
+                for (int mt = 0; mt < 4; ++mt) {
+                    Sa[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int ks = 0; ks < NKS; ++ks)
+                        Sa[mt] = mfma16(ld_b8(Kp + kslot(mt, l16) * KS + 8 * lg + 32 * ks), qopr[ks], Sa[mt]);
+                }
+                int64_t lo, hi;
+                wrange(kb, lo, hi);
+                lse_acc(Sa, kb, lo, hi);
+            }
+            if (pg + 1 < npg) wstore((pg + 1) & 1, false);
+            __syncthreads();
+        }
     }
     const float lse = (l > 0.0f) ? m + __logf(l) : INFINITY;
     if (hv && lg == 0) {
@@ -531,6 +599,30 @@ __global__ __launch_bounds__(256) void bwd_dq_mfma_kernel(
     f32x4 gc[NDT], gr[NDT];
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) gc[dt] = gr[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // Sa, Pa of a unit at keys kb..; KT = the unit's K^T rows (row stride kts)
+    // from this lane's key offset 8 lg
+    auto grad_acc = [&](const f32x4 (&Sa)[4], const f32x4 (&Pa)[4], int64_t kb, int64_t lo, int64_t hi,
+                        const bf16_t *KT, int64_t kts, bool rope) {
+        float dsv[2][8];
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int64_t key = kb + kkey(mt, lg, e);
+                const float p = (key >= lo && key <= hi) ? __expf(Sa[mt][e] * scale - lse) : 0.0f;
+                dsv[mt >> 1][(mt & 1) * 4 + e] = p * (Pa[mt][e] - Dh) * scale;
+            }
+        const bf16x8 db0 = pack_b8(dsv[0]), db1 = pack_b8(dsv[1]);
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) {
+            const bf16_t *ktp = KT + (int64_t)(16 * dt + l16) * kts;
+            f32x4 a = rope ? gr[dt] : gc[dt];
+            a = mfma16(ld_b8(ktp), db0, a);
+            a = mfma16(ld_b8(ktp + 32), db1, a);
+            if (rope) gr[dt] = a;
+            else gc[dt] = a;
+        }
+    };
     for (int64_t u = 0; u < nunits; ++u) {
         int64_t kb, lo, hi;
         bool rope;
@@ -545,25 +637,33 @@ __global__ __launch_bounds__(256) void bwd_dq_mfma_kernel(
 #pragma unroll
             for (int ks = 0; ks < NKS; ++ks) Pa[mt] = mfma16(ld_b8(vp + 32 * ks), dop[ks], Pa[mt]);
         }
-        float dsv[2][8];
+        grad_acc(Sa, Pa, kb, lo, hi, (rope ? krt : kct) + bg * D * n + kb + 8 * lg, n, rope);
+    }
+    if (npg > 0) {                                                // workgroup-uniform
+        wload(64 * (wlo0 / 64), true);
+        wstore(0, true);
+        __syncthreads();
+        for (int64_t pg = 0; pg < npg; ++pg) {
+            const int64_t kb = 64 * (wlo0 / 64 + pg);
+            if (pg + 1 < npg) wload(kb + 64, true);
+            if (act) {
+                const bf16_t *Kp = wk[pg & 1], *Vp = wv[pg & 1];
+                f32x4 Sa[4], Pa[4];
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
+                for (int mt = 0; mt < 4; ++mt) {
+                    Sa[mt] = Pa[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int64_t key = kb + kkey(mt, lg, e);
-                const float p = (key >= lo && key <= hi) ? __expf(Sa[mt][e] * scale - lse) : 0.0f;
-                dsv[mt >> 1][(mt & 1) * 4 + e] = p * (Pa[mt][e] - Dh) * scale;
+                    for (int ks = 0; ks < NKS; ++ks) {
+                        Sa[mt] = mfma16(ld_b8(Kp + kslot(mt, l16) * KS + 8 * lg + 32 * ks), qopr[ks], Sa[mt]);
+                        Pa[mt] = mfma16(ld_b8(Vp + kslot(mt, l16) * KS + 8 * lg + 32 * ks), dop[ks], Pa[mt]);
+                    }
+                }
+                int64_t lo, hi;
+                wrange(kb, lo, hi);
+                grad_acc(Sa, Pa, kb, lo, hi, wkt[pg & 1] + 8 * lg, TS, true);
             }
-        const bf16x8 db0 = pack_b8(dsv[0]), db1 = pack_b8(dsv[1]);
-        const bf16_t *KT = (rope ? krt : kct) + bg * D * n + kb + 8 * lg;
-#pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) {
-            const bf16_t *ktp = KT + (int64_t)(16 * dt + l16) * n;
-            f32x4 a = rope ? gr[dt] : gc[dt];
-            a = mfma16(ld_b8(ktp), db0, a);
-            a = mfma16(ld_b8(ktp + 32), db1, a);
-            if (rope) gr[dt] = a;
-            else gc[dt] = a;
+            if (pg + 1 < npg) wstore((pg + 1) & 1, true);
+            __syncthreads();
         }
     }
 
@@ -1231,7 +1331,7 @@ extern "C" int hba_attn_bwd(int dtype, const void *q, const void *k, const void 
     // every pick of the wave's queries held one per lane in two registers
     int qpw = (int)std::min<int64_t>(4, 16 / (Hq / Hkv));
     while (qpw > 1 && qpw * k_blocks > 128) --qpw;
-    const int64_t g1q = (B * Hkv * ((n + qpw - 1) / qpw) + 3) / 4;
+    const int64_t g1q = B * Hkv * (((n + qpw - 1) / qpw + 3) / 4);   // whole workgroups per (b, g)
     const int nsplit_kv = (int)((n + bw::DKV_ROWS - 1) / bw::DKV_ROWS);
     const int64_t g3 = B * Hkv * (n / 64) * nsplit_kv;
     const int64_t g4 = B * Hkv * n / 4;
