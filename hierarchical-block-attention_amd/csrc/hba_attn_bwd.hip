@@ -29,8 +29,9 @@
 //            (block 0), and the rows whose selection holds the block (found by
 //            scanning the selection lists into LDS).
 // bf16 inputs take the same gradients on MFMA: bwd_kt (transposed keys),
-// bwd_dq_mfma (the G heads are the columns of 16-wide tiles), bwd_dkv_mfma
-// (32 (row, head) pairs per tile, one workgroup per key block and row range)
+// bwd_dq_mfma (16/G queries per wave, their heads the columns of 16-wide
+// tiles, one online pass), bwd_dkv_mfma (64 (row, head) pairs per tile, one
+// workgroup per key block and row range)
 // and bwd_dkv_fin (rope^T and the QKNorm backward of the key rows); a second
 // bwd_dkv_mfma launch takes the sink keys.  The fp32 path takes the sink keys
 // in bwd_sink.  Both split the sink keys' query rows over workgroups.
@@ -275,15 +276,20 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(
 }
 
 // -------------------------------------------------- bwd_dq on MFMA (bf16) ----
-// The same gradient as bwd_dq_kernel, one wave per (b, i, g), with the keys
-// taken in 64-key units (the sink unit, the window pages, the routed blocks)
-// and every product on v_mfma_f32_16x16x32_bf16; the G heads are the 16
-// columns (l16 = head):
+// The same gradient as bwd_dq_kernel with every product on
+// v_mfma_f32_16x16x32_bf16.  A wave takes qpw = 16 / G consecutive queries
+// (at most 4) of one (b, g); the 16 tile columns are its (query, head) pairs
+// (l16 = column).  The keys come in 64-key units (the sink unit, the window
+// pages, the routed blocks):
 //   S^T  = K . Q^T     (A: K rows in the permuted slot order kslot)
 //   dP^T = V . dO^T    (A: V rows, same order)
 //   dQ^T += K^T . dS^T (A: the transposed keys kct / krt; B: dS^T straight
 //                       from the accumulators, which the slot order puts in
 //                       the B-operand layout)
+// One pass, online in the union softmax (running maximum, rescaled
+// accumulators), since dS needs only D = <dO, O> besides p.  The window
+// pages of a workgroup's four waves are staged once in LDS; the sink unit and
+// the routed blocks are read per wave.
 // Lane (l16, lg) holds, per M-tile mt, keys 32(mt>>1) + 8lg + 4(mt&1) + e of
 // column l16, and of dQ^T the elements d = 16 dt + 4 lg + e.
 typedef unsigned int u32x4b __attribute__((ext_vector_type(4)));
@@ -532,9 +538,19 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void bwd_dq_mfma_kernel(
         hi = !hv ? kb - 1 : (i < kb + 63) ? i : kb + 63;
     };
 
-    // pass 1: the union LSE of column l16 (a unit may hold no key of a column)
+    // one pass, online in the union softmax of column l16: with m the running
+    // maximum of its scaled scores and l = sum exp(s - m), the accumulators
+    // hold sum_j exp(s_j - m) (dP_j - D) scale k_j and are rescaled when m
+    // grows; dq = acc / l and the LSE m + log l at the end (D = <dO, O> needs
+    // no LSE).  A unit may hold no key of a column.
+    f32x4 gc[NDT], gr[NDT];
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) gc[dt] = gr[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
     float m = -INFINITY, l = 0.0f;
-    auto lse_acc = [&](const f32x4 (&Sa)[4], int64_t kb, int64_t lo, int64_t hi) {
+    // Sa, Pa of a unit at keys kb..; KT = the unit's K^T rows (row stride kts)
+    // from this lane's key offset 8 lg
+    auto grad_acc = [&](const f32x4 (&Sa)[4], const f32x4 (&Pa)[4], int64_t kb, int64_t lo, int64_t hi,
+                        const bf16_t *KT, int64_t kts, bool rope) {
         float mu = -INFINITY;
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt)
@@ -545,73 +561,24 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void bwd_dq_mfma_kernel(
             }
         mu = col_max(mu);
         const float mn = fmaxf(m, mu);
-        float ps = 0.0f;
+        const float alpha = (m == -INFINITY) ? 0.0f : __expf(m - mn);
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int64_t key = kb + kkey(mt, lg, e);
-                if (key >= lo && key <= hi) ps += __expf(Sa[mt][e] * scale - mn);
-            }
-        l = l * ((m == -INFINITY) ? 0.0f : __expf(m - mn)) + col_sum(ps);
-        m = mn;
-    };
-    for (int64_t u = 0; u < nunits; ++u) {
-        int64_t kb, lo, hi;
-        bool rope;
-        if (!unit(u, kb, lo, hi, rope)) continue;
-        f32x4 Sa[4];
-        scores(kb, rope, Sa);
-        lse_acc(Sa, kb, lo, hi);
-    }
-    if (npg > 0) {                                                // workgroup-uniform
-        wload(64 * (wlo0 / 64), false);
-        wstore(0, false);
-        __syncthreads();
-        for (int64_t pg = 0; pg < npg; ++pg) {
-            const int64_t kb = 64 * (wlo0 / 64 + pg);
-            if (pg + 1 < npg) wload(kb + 64, false);
-            if (act) {
-                const bf16_t *Kp = wk[pg & 1];
-                f32x4 Sa[4];
-#pragma unroll
-                for (int mt = 0; mt < 4; ++mt) {
-                    Sa[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                    for (int ks = 0; ks < NKS; ++ks)
-                        Sa[mt] = mfma16(ld_b8(Kp + kslot(mt, l16) * KS + 8 * lg + 32 * ks), qopr[ks], Sa[mt]);
-                }
-                int64_t lo, hi;
-                wrange(kb, lo, hi);
-                lse_acc(Sa, kb, lo, hi);
-            }
-            if (pg + 1 < npg) wstore((pg + 1) & 1, false);
-            __syncthreads();
+        for (int dt = 0; dt < NDT; ++dt) {
+            gc[dt] *= alpha;
+            gr[dt] *= alpha;
         }
-    }
-    const float lse = (l > 0.0f) ? m + __logf(l) : INFINITY;
-    if (hv && lg == 0) {
-        lse_ws[((int64_t)b * Hq + h) * n + i] = lse;
-        dd_ws[((int64_t)b * Hq + h) * n + i] = Dh;
-    }
-
-    // pass 2: dq^T (NoPE and rotated parts)
-    f32x4 gc[NDT], gr[NDT];
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) gc[dt] = gr[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    // Sa, Pa of a unit at keys kb..; KT = the unit's K^T rows (row stride kts)
-    // from this lane's key offset 8 lg
-    auto grad_acc = [&](const f32x4 (&Sa)[4], const f32x4 (&Pa)[4], int64_t kb, int64_t lo, int64_t hi,
-                        const bf16_t *KT, int64_t kts, bool rope) {
-        float dsv[2][8];
+        float dsv[2][8], ps = 0.0f;
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int64_t key = kb + kkey(mt, lg, e);
-                const float p = (key >= lo && key <= hi) ? __expf(Sa[mt][e] * scale - lse) : 0.0f;
+                const float p = (key >= lo && key <= hi) ? __expf(Sa[mt][e] * scale - mn) : 0.0f;
+                ps += p;
                 dsv[mt >> 1][(mt & 1) * 4 + e] = p * (Pa[mt][e] - Dh) * scale;
             }
+        l = l * alpha + col_sum(ps);
+        m = mn;
         const bf16x8 db0 = pack_b8(dsv[0]), db1 = pack_b8(dsv[1]);
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) {
@@ -664,6 +631,19 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void bwd_dq_mfma_kernel(
             }
             if (pg + 1 < npg) wstore((pg + 1) & 1, true);
             __syncthreads();
+        }
+    }
+    const float lse = (l > 0.0f) ? m + __logf(l) : INFINITY;
+    if (hv && lg == 0) {
+        lse_ws[((int64_t)b * Hq + h) * n + i] = lse;
+        dd_ws[((int64_t)b * Hq + h) * n + i] = Dh;
+    }
+    {
+        const float il = (l > 0.0f) ? 1.0f / l : 0.0f;
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) {
+            gc[dt] *= il;
+            gr[dt] *= il;
         }
     }
 
