@@ -667,13 +667,25 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void bwd_dq_mfma_kernel(
         for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
             for (int e = 0; e < 4; ++e) y[dt][e] = (gn / rq) * y[dt][e] - xr[dt][e] * corr;
-        if (hv && lg == 0 && dq_gain) atomicAdd(&dq_gain[h], yx / rq);
     }
     if (hv) {
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
             for (int e = 0; e < 4; ++e) dq[row + 16 * dt + 4 * lg + e] = f2bf(y[dt][e]);
+    }
+    // the gain gradient: summed over the workgroup's queries per head before
+    // one atomic add per head (the adds of all workgroups meet on Hq floats)
+    if (qgain && dq_gain) {                                       // workgroup-uniform
+        __shared__ float gqs[4][16];
+        if (lg == 0) gqs[tid >> 6][l16] = hv ? yx / rq : 0.0f;
+        __syncthreads();
+        if (tid < G) {
+            float t = 0.0f;
+            for (int w4 = 0; w4 < 4; ++w4)
+                for (int qq = 0; qq < qpw; ++qq) t += gqs[w4][qq * G + tid];
+            unsafeAtomicAdd(&dq_gain[g * G + tid], t);
+        }
     }
 }
 
@@ -1186,10 +1198,13 @@ __global__ __launch_bounds__(256) void bwd_dkv_mfma_kernel(
         }
 }
 
-// dk / dv of key row (b, j, g), one wave each, lane = element d (and d + 64):
-// the summed NoPE / rotated dk and dv (plus the sink accumulators for j < S),
-// rope^T at position j, then the QKNorm backward of k row (b, j, g); the gain
-// gradient is summed over the workgroup's four rows before its one atomic add
+// dk / dv of key rows (b, j, g), lane = element d (and d + 64); a wave takes
+// FIN_RPW consecutive rows, a workgroup one 64-key block: the summed NoPE /
+// rotated dk and dv (plus the sink accumulators for j < S), rope^T at
+// position j, then the QKNorm backward of k row (b, j, g).  The gain gradient
+// is summed over the workgroup's 64 rows before its one atomic add (the adds
+// of all workgroups meet on Hkv addresses).
+constexpr int FIN_RPW = 16;
 template <int D>
 __global__ __launch_bounds__(256) void bwd_dkv_fin_kernel(
     const bf16_t *__restrict__ k, const float *__restrict__ kgain, float eps, const float *__restrict__ cosT,
@@ -1199,54 +1214,57 @@ __global__ __launch_bounds__(256) void bwd_dkv_fin_kernel(
     constexpr int E = D / 64;
     __shared__ float gsum[4];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int64_t wid = (int64_t)blockIdx.x * 4 + w;     // bg n + j; n % 4 == 0, so one bg per workgroup
-    const int64_t j = wid % n, bg = wid / n;
+    const int64_t bg = blockIdx.x / (n / 64);                     // a workgroup never spans two (b, g)
     const int g = (int)(bg % Hkv), b = (int)(bg / Hkv);
-    const float *a = dkv_acc + wid * 3 * D;
-    float gkc[E], gkr[E], gv[E], zs[E];
-#pragma unroll
-    for (int e = 0; e < E; ++e) {
-        const int d = lane + 64 * e;
-        gkc[e] = a[d];
-        gkr[e] = a[D + d];
-        gv[e] = a[2 * D + d];
-        if (j < S && sink_acc) {
-            const float *sa = sink_acc + (bg * 2 * 64 + j) * D;
-            gkc[e] += sa[d];
-            gv[e] += sa[64 * D + d];
-        }
-        zs[e] = gkr[e] * rnd_bf16(sinT[j * D + d]);
-    }
-    float y[E];
-#pragma unroll
-    for (int e = 0; e < E; ++e) {
-        const int d = lane + 64 * e;
-        const float pv = (E == 1) ? __shfl_xor(zs[0], 32, 64) : zs[e ^ 1];   // element d ^ (D/2)
-        y[e] = gkc[e] + gkr[e] * rnd_bf16(cosT[j * D + d]) + ((d < D / 2) ? pv : -pv);
-    }
-    const int64_t rro = (((int64_t)b * n + j) * Hkv + g) * D;
     float gsv = 0.0f;
-    if (kgain) {
-        float x[E], ss = 0.0f, yx = 0.0f;
+    for (int rr = 0; rr < FIN_RPW; ++rr) {
+        const int64_t wid = (int64_t)blockIdx.x * 64 + w * FIN_RPW + rr;   // bg n + j
+        const int64_t j = wid % n;
+        const float *a = dkv_acc + wid * 3 * D;
+        float gkc[E], gkr[E], gv[E], zs[E];
 #pragma unroll
         for (int e = 0; e < E; ++e) {
-            x[e] = bf2f(k[rro + lane + 64 * e]);
-            ss = fmaf(x[e], x[e], ss);
-            yx = fmaf(y[e], x[e], yx);
+            const int d = lane + 64 * e;
+            gkc[e] = a[d];
+            gkr[e] = a[D + d];
+            gv[e] = a[2 * D + d];
+            if (j < S && sink_acc) {
+                const float *sa = sink_acc + (bg * 2 * 64 + j) * D;
+                gkc[e] += sa[d];
+                gv[e] += sa[64 * D + d];
+            }
+            zs[e] = gkr[e] * rnd_bf16(sinT[j * D + d]);
         }
-        const float ms = wsum<D>(ss) / (float)D;
-        yx = wsum<D>(yx);
-        const float r = sqrtf(fmaxf(ms, eps));
-        const float gn = kgain[g];
-        const float corr = (ms >= eps) ? gn * yx / ((float)D * r * r * r) : 0.0f;
+        float y[E];
 #pragma unroll
-        for (int e = 0; e < E; ++e) y[e] = (gn / r) * y[e] - x[e] * corr;
-        gsv = yx / r;
-    }
+        for (int e = 0; e < E; ++e) {
+            const int d = lane + 64 * e;
+            const float pv = (E == 1) ? __shfl_xor(zs[0], 32, 64) : zs[e ^ 1];   // element d ^ (D/2)
+            y[e] = gkc[e] + gkr[e] * rnd_bf16(cosT[j * D + d]) + ((d < D / 2) ? pv : -pv);
+        }
+        const int64_t rro = (((int64_t)b * n + j) * Hkv + g) * D;
+        if (kgain) {
+            float x[E], ss = 0.0f, yx = 0.0f;
 #pragma unroll
-    for (int e = 0; e < E; ++e) {
-        dk[rro + lane + 64 * e] = f2bf(y[e]);
-        dv[rro + lane + 64 * e] = f2bf(gv[e]);
+            for (int e = 0; e < E; ++e) {
+                x[e] = bf2f(k[rro + lane + 64 * e]);
+                ss = fmaf(x[e], x[e], ss);
+                yx = fmaf(y[e], x[e], yx);
+            }
+            const float ms = wsum<D>(ss) / (float)D;
+            yx = wsum<D>(yx);
+            const float r = sqrtf(fmaxf(ms, eps));
+            const float gn = kgain[g];
+            const float corr = (ms >= eps) ? gn * yx / ((float)D * r * r * r) : 0.0f;
+#pragma unroll
+            for (int e = 0; e < E; ++e) y[e] = (gn / r) * y[e] - x[e] * corr;
+            gsv += yx / r;
+        }
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            dk[rro + lane + 64 * e] = f2bf(y[e]);
+            dv[rro + lane + 64 * e] = f2bf(gv[e]);
+        }
     }
     if (kgain && dk_gain) {
         if (lane == 0) gsum[w] = gsv;
@@ -1314,7 +1332,7 @@ extern "C" int hba_attn_bwd(int dtype, const void *q, const void *k, const void 
     const int64_t g1q = B * Hkv * (((n + qpw - 1) / qpw + 3) / 4);   // whole workgroups per (b, g)
     const int nsplit_kv = (int)((n + bw::DKV_ROWS - 1) / bw::DKV_ROWS);
     const int64_t g3 = B * Hkv * (n / 64) * nsplit_kv;
-    const int64_t g4 = B * Hkv * n / 4;
+    const int64_t g4 = B * Hkv * (n / 64);                        // bwd_dkv_fin: one workgroup per 64-key block
     if (g3 > 0x7fffffffLL) return HBA_ERR_UNSUPPORTED;
 #define HBA_BWD(DT, D)                                                                                          \
     do {                                                                                                        \
