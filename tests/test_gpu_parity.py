@@ -548,12 +548,14 @@ def test_backward_row_ranges_matches_oracle(dev):
         assert rel < GRAD_TOL["bf16"], (name, rel)
 
 
-@pytest.mark.parametrize("Hq,Hkv,k", [(8, 2, 4), (10, 2, 8), (16, 1, 4)])
-def test_backward_group_sizes_match_oracle(dev, Hq, Hkv, k):
+@pytest.mark.parametrize("Hq,Hkv,k,d", [(8, 2, 4, 64), (10, 2, 8, 64), (16, 1, 4, 64), (7, 1, 4, 128),
+                                         (8, 2, 8, 128)])
+def test_backward_group_sizes_match_oracle(dev, Hq, Hkv, k, d):
     """bf16 backward with G = 4, 5 and 16 heads per KV head: the MFMA dq
-    waves then take 4, 3 (the last wave ragged, n % 3 != 0) and 1 queries."""
+    waves then take 4, 3 (the last wave ragged, n % 3 != 0) and 1 queries;
+    and at d = 128 (the donor head size) with G = 7 and 4."""
     n = 512
-    cfg, x, prm, cos, sin = make(dev, "bf16", n=n, Hq=Hq, Hkv=Hkv, W=128, k=k, S=4, needles=True)
+    cfg, x, prm, cos, sin = make(dev, "bf16", n=n, Hq=Hq, Hkv=Hkv, d=d, W=128, k=k, S=4, needles=True)
     q, k_, v = (x[t].clone().requires_grad_(True) for t in ("q", "k", "v"))
     gq = x["q_gain"].clone().requires_grad_(True)
     gk = x["k_gain"].clone().requires_grad_(True)
