@@ -337,6 +337,7 @@ def bench_bwd32k(dev, reps=5):
     import hba_amd
     from hba_amd import synth
     cfg, x, prm, cos, sin = layer_setup(dev)
+    cfg.aux_w = 0.0          # frozen summarizers: no aux-KL teacher (not provided by this backend)
     q, k, v = (x[t].clone().requires_grad_(True) for t in ("q", "k", "v"))
     gq = x["q_gain"].clone().requires_grad_(True)
     gk = x["k_gain"].clone().requires_grad_(True)

@@ -68,7 +68,7 @@ __global__ __launch_bounds__(64) void attn_f32_kernel(
     for (int64_t j = 0; j < s_end; ++j) mx = fmaxf(mx, dot_row<D>(qc, KC + j * D) * scale);
     for (int64_t j = w_beg; j <= i; ++j) mx = fmaxf(mx, dot_row<D>(qr, KR + j * D) * scale);
     for (int r = 0; r < c; ++r) {
-        if (ix[r] < 0 || ix[r] >= nb) continue;
+        if (ix[r] < 1 || ix[r] >= nb) continue;   // block 0 is never routed (sinks, window)
         int64_t j0 = (int64_t)ix[r] * 64;
         for (int64_t j = j0; j < j0 + 64; ++j) mx = fmaxf(mx, dot_row<D>(qc, KC + j * D) * scale);
     }
@@ -89,7 +89,7 @@ __global__ __launch_bounds__(64) void attn_f32_kernel(
         for (int t = 0; t < D; ++t) acc[t] = fmaf(p, VT[(int64_t)t * n + j], acc[t]);
     }
     for (int r = 0; r < c; ++r) {
-        if (ix[r] < 0 || ix[r] >= nb) continue;
+        if (ix[r] < 1 || ix[r] >= nb) continue;   // block 0 is never routed (sinks, window)
         int64_t j0 = (int64_t)ix[r] * 64;
         for (int64_t j = j0; j < j0 + 64; ++j) {
             float p = expf(dot_row<D>(qc, KC + j * D) * scale - mx);

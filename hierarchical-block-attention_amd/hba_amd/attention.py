@@ -170,10 +170,34 @@ def hba_attention_eval(q, k, v, cos, sin, cfg, summ, qkn, cap=None, hier=False, 
     return forward_stages(q, k, v, cos, sin, cfg, summ, qkn, hier=hier)["out"]
 
 
+def _refuse_aux_training(q, k, v, cfg, summ, qkn):
+    """The reference returns the aux-KL distillation loss as `aux` whenever
+    cfg.aux_w != 0 (attention.py:363-389, 605-606); it is the summarizer's only
+    gradient.  This build does not compute it, so a training call (grad mode
+    on, something upstream requiring grad) with aux_w != 0 raises instead of
+    returning a zero that would leave the summarizer silently untrained.  The
+    reference's own frozen-summarizer stage sets aux_w = 0.0, and then aux is
+    a graph-free zero there too (:363-364)."""
+    if getattr(cfg, "aux_w", 1.0) == 0.0 or not torch.is_grad_enabled():
+        return
+    ts = [q, k, v, getattr(summ, "probes", None), getattr(summ, "proj", None)]
+    if getattr(cfg, "qknorm", False):
+        ts += [qkn.q.gain, qkn.k.gain]
+    if any(isinstance(t, torch.Tensor) and t.requires_grad for t in ts):
+        raise NotImplementedError(
+            "hba_attention_dense/fused: the aux-KL teacher (the summarizer's gradient, "
+            "attention.py:358-389) is not implemented by the HIP backend; train with cfg.aux_w = 0.0 "
+            "(frozen summarizers) or run under torch.no_grad()")
+
+
 def hba_attention_dense(q, k, v, cos, sin, cfg, summ, qkn, equiv=False):
     """Forward of the reference's naive path: selection with route_topk's
-    scale (no temperature), attention with the union scale.  aux = 0.
-    equiv=True: dense uniform-RoPE causal attention (equiv_attention)."""
+    scale (no temperature), attention with the union scale.  aux = 0: a
+    training call with cfg.aux_w != 0 raises NotImplementedError
+    (_refuse_aux_training).  equiv=True: dense uniform-RoPE causal attention
+    (equiv_attention)."""
+    if not equiv:
+        _refuse_aux_training(q, k, v, cfg, summ, qkn)
     out = _with_grad(q, k, v, cos, sin, cfg, summ, qkn, "equiv" if equiv else "dense")
     if out is not None:
         return out, q.new_zeros(())

@@ -32,6 +32,7 @@ class HBAConfig:
     content_scale_mode: str = "inv_d"
     temp_c: float = 0.1
     n_cal: Optional[int] = None
+    aux_w: float = 1.0
     attn_backend: str = "hip"
 
     @property
@@ -40,9 +41,10 @@ class HBAConfig:
 
 
 def resolve_backend(cfg):
-    """Backend name for the attention call (config.py:187-194).  'hip' (and the
-    reference's 'fused'/'naive' train backends, forward-only here) all map to
-    the HIP kernels."""
+    """Backend name for the attention call (config.py:187-194).  'hip' and the
+    reference's 'fused'/'naive' train backends all map to the HIP kernels
+    (forward, and the backward of the attention output through autograd; the
+    aux-KL teacher is not provided, so training needs aux_w = 0)."""
     b = getattr(cfg, "attn_backend", "hip")
     if b in ("hip", "fused", "naive"):
         return "hip"

@@ -159,13 +159,18 @@ def route_scale(cfg, dh):
 
 # --------------------------------------------------------------------- RoPE ----
 def rope_tables(n, d, theta):
-    """attention.py:27-32, in float32."""
-    inv = (np.float32(1.0) / (np.float32(theta) ** (np.arange(0, d, 2, dtype=np.float32)
-                                                     / np.float32(d)))).astype(np.float32)
-    pos = np.arange(n, dtype=np.float32)
-    fr = np.outer(pos, inv).astype(np.float32)
-    emb = np.concatenate([fr, fr], axis=-1)
-    return np.cos(emb).astype(np.float32), np.sin(emb).astype(np.float32)
+    """attention.py:27-32, in float32, evaluated with torch on the CPU in the
+    reference's own operation order.  The angle pos * inv carries the last bit
+    of inv = 1 / theta^(2i/d) multiplied by the position, so a one-ulp
+    difference in the power (numpy's and torch's fp32 pow differ) moves the
+    tables by up to 8e-3 at 128K positions; only the reference's expression
+    reproduces its tables there (tests/test_oracle_bf16.py)."""
+    import torch
+    inv = 1.0 / (theta ** (torch.arange(0, d, 2).float() / d))
+    pos = torch.arange(n).float()
+    fr = torch.outer(pos, inv)
+    emb = torch.cat((fr, fr), dim=-1)
+    return emb.cos().numpy().astype(np.float32), emb.sin().numpy().astype(np.float32)
 
 
 def rot_half(x):

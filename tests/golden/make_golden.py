@@ -157,5 +157,120 @@ def main():
         print(f"{name}: wrote {path} ({os.path.getsize(path) / 1024:.0f} KiB) scale={scale:.6g}")
 
 
+BF16_CASES = {
+    # the kernels' geometries: 14/2 heads at d = 64 and the 28/4-head d = 128 shape
+    "d64": dict(B=1, n=128, Hq=14, Hkv=2, d=64, seed=21, F=(16, 5), nb=37),
+    "d128": dict(B=1, n=32, Hq=28, Hkv=4, d=128, seed=22, F=(16, 3), nb=20),
+}
+
+
+def gen_bf16_inputs(case):
+    """Seeded fp32 draws for the bf16 fixture (shared with the tests): q, k,
+    gains, S0, and rows that exercise QKNorm's eps clamp (an all-zero row and a
+    row far below eps in mean square)."""
+    rs = np.random.RandomState(case["seed"])
+    B, n, Hq, Hkv, d = case["B"], case["n"], case["Hq"], case["Hkv"], case["d"]
+    q = rs.standard_normal((B, n, Hq, d)).astype(np.float32)
+    k = rs.standard_normal((B, n, Hkv, d)).astype(np.float32)
+    q[0, 5, 3] = 0.0
+    q[0, 6, 1] *= 1e-5
+    k[0, 7, 1] = 0.0
+    k[0, 9, 0] *= 3e-5
+    q[0, 10] *= 40.0                                  # large-magnitude rows
+    qg_ = (d ** 0.25 * rs.uniform(0.5, 1.5, Hq)).astype(np.float32)
+    kg_ = (d ** 0.25 * rs.uniform(0.5, 1.5, Hkv)).astype(np.float32)
+    S0 = rs.standard_normal((B, case["nb"], 4, d)).astype(np.float32)
+    # far positions: RoPE angles at 128K, where the tables' bf16 rounding matters most
+    far = rs.standard_normal((1, 64, Hkv, d)).astype(np.float32)
+    return dict(q=q, k=k, q_gain=qg_, k_gain=kg_, S0=S0, far=far)
+
+
+def round_probe():
+    """fp32 values whose bf16 rounding is delicate: halfway ties (both
+    parities), values just either side of a tie, the overflow edge, fp32
+    subnormals, signed zeros, infinities, NaN, and random magnitudes."""
+    rs = np.random.RandomState(23)
+    one = np.float32(1.0)
+    ulp = np.float32(2.0 ** -7)
+    ties = [one + ulp / 2, one + 3 * ulp / 2, -(one + ulp / 2), np.float32(3.0) + np.float32(2.0 ** -7)]
+    near = [np.nextafter(t, np.float32(np.inf)) for t in ties] + [np.nextafter(t, np.float32(-np.inf))
+                                                                  for t in ties]
+    big = [np.float32(3.3895313892515355e38), np.float32(3.3961e38), np.float32(3.4028235e38),
+           np.float32(-3.39e38)]
+    tiny = [np.float32(1e-40), np.float32(-3e-39), np.float32(1.1754942e-38), np.float32(1e-45)]
+    special = [np.float32(0.0), np.float32(-0.0), np.float32(np.inf), np.float32(-np.inf), np.float32(np.nan)]
+    rnd = (rs.standard_normal(4096) * np.exp(rs.uniform(-30, 30, 4096))).astype(np.float32)
+    return np.concatenate([np.array(ties + near + big + tiny + special, np.float32), rnd])
+
+
+def bf16_bits(t):
+    """Raw bits of a torch bfloat16 tensor as uint16 (the fixture's storage)."""
+    import torch
+    return t.contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def from_bits(u):
+    """uint16 bf16 bits -> float32 values (exact)."""
+    return (np.asarray(u, dtype=np.uint32) << 16).view(np.float32)
+
+
+def main_bf16():
+    """Fixture of the reference's bf16 arithmetic (golden_bf16.npz): torch's
+    fp32 -> bf16 cast, _HeadRMSNorm on bf16 q/k (attention.py:88-94),
+    apply_rope on bf16 tensors (:40-44), grouped_query's bf16 head sum
+    (summarizer.py:50-54) and build_super's bf16 sum and divide
+    (attention.py:202-214)."""
+    tmp = tempfile.mkdtemp(prefix="hba-golden-")
+    for var in ("HBA_RESULTS_DIR", "HBA_DATA_DIR", "HBA_LOGS_DIR"):
+        os.environ[var] = tmp
+    sys.path.insert(0, REF_SRC)
+    import torch
+    from hba.attention import QKNorm, apply_rope, build_super, rope_tables
+    from hba.config import HBAConfig
+    from hba.summarizer import grouped_query
+
+    bf = torch.bfloat16
+    rec = {}
+    probe = round_probe()
+    rec["round_in"] = probe
+    rec["round_out"] = torch.from_numpy(probe).to(bf).float().numpy()
+    for name, case in BF16_CASES.items():
+        inp = gen_bf16_inputs(case)
+        B, n, Hq, Hkv, d = case["B"], case["n"], case["Hq"], case["Hkv"], case["d"]
+        cfg = HBAConfig(n_heads=Hq, n_kv=Hkv, head_dim=d, qknorm=True)
+        qkn = QKNorm(cfg)
+        with torch.no_grad():
+            qkn.q.gain.copy_(torch.from_numpy(inp["q_gain"]))
+            qkn.k.gain.copy_(torch.from_numpy(inp["k_gain"]))
+            q = torch.from_numpy(inp["q"]).to(bf)
+            k = torch.from_numpy(inp["k"]).to(bf)
+            qc, kc = qkn.q(q), qkn.k(k)
+            cos, sin = rope_tables(n, d, cfg.rope_theta, "cpu")
+            qr, kr = apply_rope(qc, cos, sin), apply_rope(kc, cos, sin)
+            qg = grouped_query(qc, cfg)
+            cf, sf = rope_tables(131072, d, cfg.rope_theta, "cpu")
+            far = qkn.k(torch.from_numpy(inp["far"]).to(bf))
+            far_r = apply_rope(far, cf[-64:], sf[-64:])
+            S0 = torch.from_numpy(inp["S0"]).to(bf)
+            for F in case["F"]:
+                S1, ns = build_super(S0, F)
+                assert S1.dtype == bf
+                rec[f"{name}_S1_F{F}"] = bf16_bits(S1)
+        for key, t in (("qc", qc), ("kc", kc), ("qr", qr), ("kr", kr), ("qg", qg), ("far_kc", far),
+                       ("far_kr", far_r)):
+            assert t.dtype == bf, key
+            rec[f"{name}_{key}"] = bf16_bits(t)
+        rec[f"{name}_far_cos"] = cf[-64:].numpy()
+        rec[f"{name}_far_sin"] = sf[-64:].numpy()
+        rec[f"{name}_ck_q"] = checksum(inp["q"])
+    path = os.path.join(HERE, "golden_bf16.npz")
+    np.savez_compressed(path, **rec)
+    print(f"bf16: wrote {path} ({os.path.getsize(path) / 1024:.0f} KiB)")
+
+
 if __name__ == "__main__":
-    main()
+    if "--bf16-only" in sys.argv:
+        main_bf16()
+    else:
+        main()
+        main_bf16()

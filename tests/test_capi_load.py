@@ -73,3 +73,28 @@ def test_argument_checks_run_before_any_launch():
     st = L.hba_score_select(1, fake, s3, None, 1e-6, fake, 1, 128, 14, 2, 96, 4, 64, 1024, 16, 0.1,
                             fake, fake, fake, None, None)
     assert st == -2                                    # d = 96 unsupported
+
+
+def test_training_with_aux_weight_is_refused():
+    """hba_attention_dense/fused do not compute the aux-KL teacher, so a
+    training call with aux_w != 0 raises (before any device work) instead of
+    returning an aux of 0 that would leave the summarizer untrained; aux_w = 0
+    or no_grad passes the guard (and then needs a GPU)."""
+    import torch
+    from hba_amd import synth
+    cfg = hba_amd.HBAConfig(window=64, k_blocks=2)
+    q = torch.zeros(1, 128, 14, 64, requires_grad=True)
+    k = torch.zeros(1, 128, 2, 64)
+    prm = synth.Params(torch.ones(14), torch.ones(2), torch.zeros(2, 4, 64), torch.zeros(2, 64, 64))
+    cos = sin = torch.zeros(128, 64)
+    for fn in (hba_amd.hba_attention_dense, hba_amd.hba_attention_fused):
+        with pytest.raises(NotImplementedError, match="aux-KL"):
+            fn(q, k, k, cos, sin, cfg, prm, prm)
+    cfg.aux_w = 0.0
+    with pytest.raises(Exception) as e:          # past the guard: no CPU path
+        hba_amd.hba_attention_dense(q, k, k, cos, sin, cfg, prm, prm)
+    assert "aux-KL" not in str(e.value)
+    cfg.aux_w = 1.0
+    with torch.no_grad(), pytest.raises(Exception) as e:
+        hba_amd.hba_attention_dense(q, k, k, cos, sin, cfg, prm, prm)
+    assert "aux-KL" not in str(e.value)

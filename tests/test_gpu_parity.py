@@ -486,7 +486,8 @@ def test_backward_matches_oracle(dev, dt, qknorm, mode):
     QKNorm gain gradients."""
     n = 512
     kw = dict(fanout=4, beam=2) if mode == "hier" else {}
-    cfg, x, prm, cos, sin = make(dev, dt, n=n, W=128, k=4, S=4, qknorm=qknorm, **kw)
+    # aux_w = 0: the frozen-summarizer setting, where the reference's aux is a zero too
+    cfg, x, prm, cos, sin = make(dev, dt, n=n, W=128, k=4, S=4, qknorm=qknorm, aux_w=0.0, **kw)
     q, k, v = (x[t].clone().requires_grad_(True) for t in ("q", "k", "v"))
     gq = x["q_gain"].clone().requires_grad_(qknorm)
     gk = x["k_gain"].clone().requires_grad_(qknorm)
