@@ -650,14 +650,11 @@ def decode_row(q_new, kc_seq, v_seq, cos, sin, cfg, S0_seq, q_gain, eps, dtype, 
             sc = block_scores(qfull, S0_seq[g][:nb], np.array([i]), scale, cfg.block, cfg.window)
             a, b_, c = topk(sc, kk)
             idx[g], val[g], cnt[g] = a[0], b_[0], c[0]
-    qc_full = np.zeros((L, Hq, d), dtype=np.float32)
-    qr_full = np.zeros((L, Hq, d), dtype=np.float32)
-    qc_full[i] = qc
-    qr_full[i] = qr
-    I = np.full((Hkv, L, kk), -1, dtype=np.int32)
-    C = np.zeros((Hkv, L), dtype=np.int32)
-    I[:, i] = idx
-    C[:, i] = cnt
-    out = attn_rows(qc_full, qr_full, kc_seq, kr, v_seq, I, C, scale, cfg.sinks, cfg.window,
+    # attn_rows indexes queries by position: give it a one-row view at i
+    qc_one = np.broadcast_to(qc[None], (L, Hq, d))
+    qr_one = np.broadcast_to(qr[None], (L, Hq, d))
+    I = np.broadcast_to(idx[:, None, :], (Hkv, L, kk))
+    C = np.broadcast_to(cnt[:, None], (Hkv, L))
+    out = attn_rows(qc_one, qr_one, kc_seq, kr, v_seq, I, C, scale, cfg.sinks, cfg.window,
                     cfg.block, [i])[0]
     return out, (idx, val, cnt)
