@@ -25,6 +25,8 @@
 // 16-wide tile: S^T = K.Q^T, softmax in registers, O^T = V^T.P^T, operands
 // loaded straight from the cache into registers); fp32 units run one per
 // workgroup with fp32 dot products through LDS.
+#include <mutex>
+
 #include "hba_common.h"
 #include "hba_abi.h"
 
@@ -739,14 +741,16 @@ extern "C" int hba_decode_workspace_size(int64_t Bd, int64_t Hq, int64_t Hkv, in
     return HBA_OK;
 }
 
-extern "C" int hba_decode_fwd(int dtype, const void *q, const float *q_gain, float eps,
-                              const void *kc_pages, const void *kr_pages, const void *v_pages,
-                              const void *summ_pages, const int32_t *page_table, int64_t max_pages,
-                              const int32_t *seq_lens, const float *cos_tab, const float *sin_tab,
-                              const float *scales, int64_t Bd, int64_t Hq, int64_t Hkv, int64_t d,
-                              int64_t m, int64_t S, int64_t W, int64_t Bk, int64_t k, int64_t max_len,
-                              void *workspace, size_t ws_bytes, void *out, int32_t *sel_idx,
-                              int32_t *sel_cnt, void *stream) {
+// The decode step on a given workspace; scratch_max > 0 marks the
+// no-allocation entry point, whose workspace is the fixed scratch array
+// (a request that does not fit it is HBA_ERR_SCRATCH).
+static int decode_fwd_ws(int dtype, const void *q, const float *q_gain, float eps, const void *kc_pages,
+                         const void *kr_pages, const void *v_pages, const void *summ_pages,
+                         const int32_t *page_table, int64_t max_pages, const int32_t *seq_lens,
+                         const float *cos_tab, const float *sin_tab, const float *scales, int64_t Bd,
+                         int64_t Hq, int64_t Hkv, int64_t d, int64_t m, int64_t S, int64_t W, int64_t Bk,
+                         int64_t k, int64_t max_len, void *workspace, size_t ws_bytes, size_t scratch_max,
+                         void *out, int32_t *sel_idx, int32_t *sel_cnt, void *stream) {
     int st = abi::check_dtype_dim(dtype, d);
     if (st) return st;
     if (!q || !kc_pages || !kr_pages || !v_pages || !summ_pages || !page_table || !seq_lens ||
@@ -769,6 +773,7 @@ extern "C" int hba_decode_fwd(int dtype, const void *q, const float *q_gain, flo
     if ((int64_t)gm.nsc * k > 2048 || gm.npart > DEC_PMAX) return HBA_ERR_UNSUPPORTED;
     size_t ov, oi, oph, oq, op, total;
     ws_layout(Bd, Hq, Hkv, d, k, gm, &ov, &oi, &oph, &oq, &op, &total);
+    if (scratch_max && total > scratch_max) return HBA_ERR_SCRATCH;
     if (ws_bytes < total) return HBA_ERR_INVALID_ARG;
     char *ws = (char *)workspace;
     float *wv = (float *)(ws + ov);
@@ -810,4 +815,63 @@ extern "C" int hba_decode_fwd(int dtype, const void *q, const float *q_gain, flo
 #undef HBA_D23
     HBA_LAUNCH_CHECK();
     return HBA_OK;
+}
+
+extern "C" int hba_decode_fwd(int dtype, const void *q, const float *q_gain, float eps,
+                              const void *kc_pages, const void *kr_pages, const void *v_pages,
+                              const void *summ_pages, const int32_t *page_table, int64_t max_pages,
+                              const int32_t *seq_lens, const float *cos_tab, const float *sin_tab,
+                              const float *scales, int64_t Bd, int64_t Hq, int64_t Hkv, int64_t d,
+                              int64_t m, int64_t S, int64_t W, int64_t Bk, int64_t k, int64_t max_len,
+                              void *workspace, size_t ws_bytes, void *out, int32_t *sel_idx,
+                              int32_t *sel_cnt, void *stream) {
+    return decode_fwd_ws(dtype, q, q_gain, eps, kc_pages, kr_pages, v_pages, summ_pages, page_table, max_pages,
+                         seq_lens, cos_tab, sin_tab, scales, Bd, Hq, Hkv, d, m, S, W, Bk, k, max_len, workspace,
+                         ws_bytes, 0, out, sel_idx, sel_cnt, stream);
+}
+
+// ------------------------------------------------ no-allocation variant ----
+// The decode workspace as a fixed device array, one copy per GPU the library
+// runs on, held until the process ends.  In host code `scratch` names a
+// host-side stand-in, never device memory: its device address on the current
+// device comes from hipGetSymbolAddress, looked up once per device and kept
+// in scratch_ptr.  Every call on a GPU shares that GPU's copy; the kernels
+// write every workspace entry they read within the same call, so nothing is
+// cleared between calls.  Calls that overlap on one GPU (different streams)
+// race on it.
+static __device__ __align__(256) char scratch[HBA_DECODE_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex scratch_mu;
+void *scratch_ptr[kMaxDevices];   // device address of `scratch` per device, or null
+
+int scratch_on_current_device(void **ptr) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return HBA_ERR_DEVICE;
+    std::lock_guard<std::mutex> lock(scratch_mu);
+    if (!scratch_ptr[dev]) {
+        void *p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return HBA_ERR_DEVICE;
+        scratch_ptr[dev] = p;
+    }
+    *ptr = scratch_ptr[dev];
+    return HBA_OK;
+}
+}  // namespace
+
+extern "C" int hba_decode_fwd_noalloc(int dtype, const void *q, const float *q_gain, float eps,
+                                      const void *kc_pages, const void *kr_pages, const void *v_pages,
+                                      const void *summ_pages, const int32_t *page_table, int64_t max_pages,
+                                      const int32_t *seq_lens, const float *cos_tab, const float *sin_tab,
+                                      const float *scales, int64_t Bd, int64_t Hq, int64_t Hkv, int64_t d,
+                                      int64_t m, int64_t S, int64_t W, int64_t Bk, int64_t k, int64_t max_len,
+                                      void *out, int32_t *sel_idx, int32_t *sel_cnt, void *stream) {
+    void *ws = nullptr;
+    const int st = scratch_on_current_device(&ws);
+    if (st) return st;
+    return decode_fwd_ws(dtype, q, q_gain, eps, kc_pages, kr_pages, v_pages, summ_pages, page_table, max_pages,
+                         seq_lens, cos_tab, sin_tab, scales, Bd, Hq, Hkv, d, m, S, W, Bk, k, max_len, ws,
+                         (size_t)HBA_DECODE_SCRATCH_BYTES, (size_t)HBA_DECODE_SCRATCH_BYTES, out, sel_idx,
+                         sel_cnt, stream);
 }

@@ -222,6 +222,7 @@ extern "C" const char *hba_status_string(int status) {
         case HBA_ERR_UNSUPPORTED: return "unsupported shape or dtype";
         case HBA_ERR_DEVICE: return "no gfx950 device";
         case HBA_ERR_LAUNCH: return "kernel launch failed";
+        case HBA_ERR_SCRATCH: return "request exceeds the fixed scratch of the no-allocation entry point";
         default: return "unknown status";
     }
 }

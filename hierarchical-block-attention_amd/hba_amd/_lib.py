@@ -48,6 +48,8 @@ SIGNATURES = {
     "hba_decode_fwd": [_i, _vp, _vp, _f, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _i64,
                        _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, ctypes.c_size_t,
                        _vp, _vp, _vp, _vp],
+    "hba_decode_fwd_noalloc": [_i, _vp, _vp, _f, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _i64,
+                               _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp],
 }
 
 _LIB = None

@@ -467,6 +467,38 @@ def decode_fwd(q: Tensor, q_gain: Optional[Tensor], eps: float, kc_pages: Tensor
     return out, sel_idx, sel_cnt
 
 
+def decode_fwd_noalloc(q, q_gain, eps, kc_pages, kr_pages, v_pages, summ_pages, page_table, seq_lens, cos, sin,
+                       scales, sinks, window, k, max_len, out, sel_idx=None, sel_cnt=None):
+    """decode_fwd through hba_decode_fwd_noalloc: the step runs in the
+    library's fixed per-GPU scratch and allocates nothing; the caller passes
+    the outputs (out [Bd, Hq, d] contiguous in q's dtype, optional sel_idx
+    int32 [Bd, Hkv, k] and sel_cnt int32 [Bd, Hkv]) and contiguous fp32
+    q_gain, cos/sin and scales already on the device.  Calls that overlap on
+    one GPU race on the scratch."""
+    dev = _dev(q)
+    Bd, Hq, d = q.shape
+    Hkv, m = summ_pages.shape[1], summ_pages.shape[2]
+    for t, what in ((q, "q"), (out, "out"), (cos, "cos"), (sin, "sin"), (scales, "scales")):
+        if not t.is_contiguous() or t.device != dev:
+            raise ValueError(f"{what} must be a contiguous tensor on {dev}")
+    if out.shape != q.shape or out.dtype != q.dtype:
+        raise ValueError("out must match q in shape and dtype")
+    if cos.dtype != torch.float32 or sin.dtype != torch.float32 or scales.dtype != torch.float32:
+        raise TypeError("cos, sin and scales must be float32")
+    if q_gain is not None and (q_gain.dtype != torch.float32 or not q_gain.is_contiguous()):
+        raise TypeError("q_gain must be a contiguous float32 tensor")
+    if cos.shape[0] < max_len or cos.shape[1] != d or sin.shape != cos.shape:
+        raise ValueError(f"cos/sin: expected [>= {max_len}, {d}] tables")
+    with torch.cuda.device(dev):
+        st = lib().hba_decode_fwd_noalloc(_code(q), _p(q), _p(q_gain), eps, _p(kc_pages), _p(kr_pages),
+                                          _p(v_pages), _p(summ_pages), _p(page_table), page_table.shape[1],
+                                          _p(seq_lens), _p(cos), _p(sin), _p(scales), Bd, Hq, Hkv, d, m, sinks,
+                                          window, BLOCK, k, max_len, _p(out), _p(sel_idx), _p(sel_cnt),
+                                          _stream(dev))
+    check(st, "hba_decode_fwd_noalloc")
+    return out
+
+
 @decode_fwd.register_fake
 def _(q, q_gain, eps, kc_pages, kr_pages, v_pages, summ_pages, page_table, seq_lens, cos, sin, scales,
       sinks, window, k, max_len):

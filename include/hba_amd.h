@@ -44,7 +44,8 @@ enum {
     HBA_ERR_INVALID_ARG = -1,   /* null pointer, bad size, n % block != 0, ... */
     HBA_ERR_UNSUPPORTED = -2,   /* shape/dtype outside what the kernels implement */
     HBA_ERR_DEVICE = -3,        /* no device, or the current device is not gfx950 */
-    HBA_ERR_LAUNCH = -4         /* the kernel launch itself failed */
+    HBA_ERR_LAUNCH = -4,        /* the kernel launch itself failed */
+    HBA_ERR_SCRATCH = -5        /* a no-allocation call needs more than its fixed scratch */
 };
 
 enum { HBA_DTYPE_F32 = 0, HBA_DTYPE_BF16 = 1 };
@@ -251,6 +252,28 @@ int hba_decode_fwd(int dtype, const void *q, const float *q_gain, float eps,
                    int64_t m, int64_t S, int64_t W, int64_t Bk, int64_t k, int64_t max_len,
                    void *workspace, size_t ws_bytes, void *out,
                    int32_t *sel_idx, int32_t *sel_cnt, void *stream);
+
+/*
+ * hba_decode_fwd without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference, which
+ * has no decode path.  The workspace is a fixed device array of
+ * HBA_DECODE_SCRATCH_BYTES per GPU, held until the process ends; a call whose
+ * hba_decode_workspace_size exceeds it returns HBA_ERR_SCRATCH and launches
+ * nothing (32 sequences of 32K tokens at 14/2 heads, d = 64, k = 16 need
+ * 4.8 MB).  The call allocates nothing.  Every call on a GPU shares that
+ * GPU's array: calls that overlap on one GPU (e.g. on two streams) race;
+ * consecutive calls on one stream are safe.  Same arguments, checks and
+ * results as hba_decode_fwd otherwise.
+ */
+#define HBA_DECODE_SCRATCH_BYTES (16u << 20)
+int hba_decode_fwd_noalloc(int dtype, const void *q, const float *q_gain, float eps,
+                           const void *kc_pages, const void *kr_pages, const void *v_pages,
+                           const void *summ_pages, const int32_t *page_table, int64_t max_pages,
+                           const int32_t *seq_lens, const float *cos_tab, const float *sin_tab,
+                           const float *scales, int64_t Bd, int64_t Hq, int64_t Hkv, int64_t d,
+                           int64_t m, int64_t S, int64_t W, int64_t Bk, int64_t k, int64_t max_len,
+                           void *out, int32_t *sel_idx, int32_t *sel_cnt, void *stream);
 
 /*
  * Backward of the union attention (replaces the autograd backward of
