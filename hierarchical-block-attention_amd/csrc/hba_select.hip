@@ -8,6 +8,8 @@
 // d -- the same operation order as the oracle, so scores and the selected
 // indices are bit-exact.  The top-k list is a register-resident sorted array
 // (score descending, block index ascending).
+#include <type_traits>
+
 #include "hba_common.h"
 #include "hba_abi.h"
 #include "hba_dma.h"
@@ -293,64 +295,91 @@ __device__ __forceinline__ int merge_lanes(float (&v)[K], int (&id)[K], int want
 }
 
 // The bf16 routing queries of the 64 queries i0 .. i0+63 (clamped to n-1)
-// of KV head g into qgs[64][ROWQ], in routing_query's operation order.  Four
-// lanes per query, D/4 dims each; q is read once.  A head's QKNorm sum of
-// squares runs as one sequential chain over d, passed from lane to lane of
-// the query; every lane then normalises its dims and adds them to the
-// head-ordered sum.  Needs 256 threads.
+// of KV head g into qgs[64][ROWQ], in routing_query's operation order.
+// Thread (query tid / 4, part tid % 4):
+//   1. the QKNorm sum of squares of heads part, part+4, ... (< G) over the
+//      whole row: the declared sequential FMA chain; a thread's chains are
+//      independent and interleave;
+//   2. every head's r = sqrt(max(ss / D, eps)), broadcast within the query's
+//      four threads;
+//   3. its D/4 dims of every head: x / r (the IEEE quotient, through
+//      div_rn_fast where that applies), times the gain, rounded to bf16, and
+//      summed in head order.
+// Needs 256 threads; G <= 16.
 template <int D, int ROWQ>
 __device__ __forceinline__ void routing_queries_tile(const bf16_t *q, int64_t qsb, int64_t qsn, int64_t qsh,
                                                      const float *qgain, float eps, int64_t b, int64_t i0,
                                                      int64_t n, int g, int G, bf16_t *qgs, int tid) {
-    constexpr int DP = D / 4, NC = DP / 8;   // dims and 16-byte chunks per lane
+    constexpr int DP = D / 4, NC = DP / 8;   // dims and 16-byte chunks per thread
+    constexpr int GMAX = 16;
     const int qq = tid >> 2, part = tid & 3, lane = tid & 63;
     const int64_t i = (i0 + qq < n) ? i0 + qq : n - 1;
-    const bf16_t *base = q + b * qsb + i * qsn + (int64_t)g * G * qsh + part * DP;
-    constexpr int HB = 8;                     // heads whose dims are loaded together
+    const bf16_t *row0 = q + b * qsb + i * qsn + (int64_t)g * G * qsh;
+    auto unpack = [](const uint4 &u, int e) {   // element e (0..7) of 8 packed bf16
+        const uint32_t wd = (e >> 1) == 0 ? u.x : (e >> 1) == 1 ? u.y : (e >> 1) == 2 ? u.z : u.w;
+        return (e & 1) ? __uint_as_float(wd & 0xffff0000u) : __uint_as_float(wd << 16);
+    };
+    float rr[GMAX / 4];
+#pragma unroll
+    for (int j = 0; j < GMAX / 4; ++j) rr[j] = 1.0f;
+    auto chains = [&](auto nj_const) {
+        constexpr int NJ = decltype(nj_const)::value;
+        uint4 rw[NJ][D / 8];
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            const int h = (part + 4 * j < G) ? part + 4 * j : G - 1;   // past G: a duplicate, unused
+#pragma unroll
+            for (int c = 0; c < D / 8; ++c) rw[j][c] = reinterpret_cast<const uint4 *>(row0 + (int64_t)h * qsh)[c];
+        }
+        float ss[NJ];
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) ss[j] = 0.0f;
+#pragma unroll
+        for (int t = 0; t < D; ++t)
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) {
+                const float x = unpack(rw[j][t >> 3], t & 7);
+                ss[j] = fmaf(x, x, ss[j]);
+            }
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            float ms = ss[j] / (float)D;
+            if (ms < eps) ms = eps;
+            rr[j] = sqrtf(ms);
+        }
+    };
+    if (qgain) {
+        if (G <= 8) chains(std::integral_constant<int, 2>());
+        else chains(std::integral_constant<int, 4>());
+    }
+    const bf16_t *base = row0 + part * DP;
     float acc[DP];
-    for (int h0 = 0; h0 < G; h0 += HB) {
-        uint4 raw[HB][NC];
 #pragma unroll
-        for (int hb = 0; hb < HB; ++hb)
-            if (h0 + hb < G) {
+    for (int h = 0; h < GMAX; ++h) {
+        if (h >= G) break;   // uniform
+        uint4 raw[NC];
 #pragma unroll
-                for (int c = 0; c < NC; ++c) raw[hb][c] = reinterpret_cast<const uint4 *>(base + (int64_t)(h0 + hb) * qsh)[c];
-            }
+        for (int c = 0; c < NC; ++c) raw[c] = reinterpret_cast<const uint4 *>(base + (int64_t)h * qsh)[c];
+        float x[DP];
 #pragma unroll
-        for (int hb = 0; hb < HB; ++hb) {
-            const int h = h0 + hb;
-            if (h >= G) break;
-            float x[DP];
+        for (int e = 0; e < DP; ++e) x[e] = unpack(raw[e >> 3], e & 7);
+        if (qgain) {
+            const float r = __shfl(rr[h >> 2], (lane & ~3) | (h & 3), 64);
+            const float gn = qgain[g * G + h];
+            bool slow = !div_rn_row_ok(r);
 #pragma unroll
-            for (int c = 0; c < NC; ++c) {
-                const uint32_t wd[4] = {raw[hb][c].x, raw[hb][c].y, raw[hb][c].z, raw[hb][c].w};
+            for (int e = 0; e < DP; ++e) slow = slow || div_rn_subnormal(x[e]);
+            if (!__any(slow)) {
+                const float inv = 1.0f / r;
 #pragma unroll
-                for (int e = 0; e < 8; ++e)
-                    x[8 * c + e] = (e & 1) ? __uint_as_float(wd[e >> 1] & 0xffff0000u) : __uint_as_float(wd[e >> 1] << 16);
-            }
-            if (qgain) {
-                // ss = fma(x_t, x_t, ss) for t = 0 .. D-1: lane `part` continues the chain of lane part-1
-                float ss = 0.0f;
-#pragma unroll
-                for (int s = 0; s < 4; ++s) {
-                    const float in = (s == 0) ? 0.0f : __shfl(ss, (lane & ~3) | (s - 1), 64);
-                    if (part == s) {
-                        float t = in;
-#pragma unroll
-                        for (int e = 0; e < DP; ++e) t = fmaf(x[e], x[e], t);
-                        ss = t;
-                    }
-                }
-                ss = __shfl(ss, (lane & ~3) | 3, 64);
-                float ms = ss / (float)D;
-                if (ms < eps) ms = eps;
-                const float r = sqrtf(ms), gn = qgain[g * G + h];
+                for (int e = 0; e < DP; ++e) x[e] = rnd_bf16(div_rn_fast(x[e], r, inv) * gn);
+            } else {
 #pragma unroll
                 for (int e = 0; e < DP; ++e) x[e] = rnd_bf16((x[e] / r) * gn);
             }
-#pragma unroll
-            for (int e = 0; e < DP; ++e) acc[e] = (h == 0) ? x[e] : acc[e] + x[e];
         }
+#pragma unroll
+        for (int e = 0; e < DP; ++e) acc[e] = (h == 0) ? x[e] : acc[e] + x[e];
     }
 #pragma unroll
     for (int e = 0; e < DP; ++e) qgs[qq * ROWQ + part * DP + e] = f2bf(acc[e]);
@@ -363,12 +392,26 @@ __device__ __forceinline__ void routing_queries_tile(const bf16_t *q, int64_t qs
 // the kept supers cover nearly every super, so the children are scored as the
 // flat GEMM and filtered, not gathered.
 constexpr int SEL_PMW = 64;   // most words of the per-query super bitmask: ns <= 2048
+constexpr int32_t SEL_OVERFLOW = -2;   // cnt marker: the threshold kernel left this query to the exact pass
+// marked_only: run only for a 64-query tile holding a query whose cnt is
+// SEL_OVERFLOW (the threshold kernel's overflow), and recompute the tile.
 template <int D, int KMAX, bool HIER>
 __global__ __launch_bounds__(256) void score_select_mfma_kernel(
     const bf16_t *__restrict__ q, int64_t qsb, int64_t qsn, int64_t qsh, const float *__restrict__ qgain,
     float eps, const bf16_t *__restrict__ S0, int64_t n, int Hq, int Hkv, int64_t nb, int64_t W, int kk,
     float scale, int32_t *__restrict__ idx, float *__restrict__ val, int32_t *__restrict__ cnt,
-    float *__restrict__ scores, const bf16_t *__restrict__ S1, int F, int beam, float *__restrict__ sup_scores) {
+    float *__restrict__ scores, const bf16_t *__restrict__ S1, int F, int beam, float *__restrict__ sup_scores,
+    int marked_only) {
+    if (marked_only) {
+        __shared__ int marked;
+        const int64_t ib = (int64_t)blockIdx.x * 64 + threadIdx.x;
+        if (threadIdx.x == 0) marked = 0;
+        __syncthreads();
+        if (threadIdx.x < 64 && ib < n && cnt[((int64_t)blockIdx.z * Hkv + blockIdx.y) * n + ib] == SEL_OVERFLOW)
+            marked = 1;
+        __syncthreads();
+        if (!marked) return;   // workgroup-uniform
+    }
     using namespace sel;
     constexpr int NKS = D / 32;
     constexpr int CPR = D / 8;                         // 16-byte chunks per summary row
@@ -524,6 +567,262 @@ __global__ __launch_bounds__(256) void score_select_mfma_kernel(
     }
 }
 
+// ---------------------------------------------- bf16 flat top-k, threshold ----
+// The same scores as score_select_mfma_kernel (the same MFMA operands in the
+// same order, so bit-identical), ranked without sorted lists.  Workgroup = 64
+// queries of one KV head (four 16-column MFMA tiles); the four waves split the
+// block stages (16 blocks each; wave w takes stages w, w+4, ...) and load
+// their A fragments straight from L2 into registers two stages ahead: no LDS
+// ring and no barrier in the scans.  A query's blocks are then spread over 16
+// lanes (4 waves x 4 lane groups).
+//   pass A  each lane keeps the 2 largest candidate scores it sees (values
+//           only, a max/min network).  The k-th largest tau of the query's 32
+//           values is a lower bound of its k-th score: at least k scores are
+//           >= tau, so the top-k is among the scores >= tau.
+//   pass B  the same scan appends every candidate scoring >= tau to the
+//           query's list in LDS (about k + 2 entries on random scores).
+//   rank    an entry's rank is the number of entries ordered before it under
+//           (score desc, block asc); ranks < k are the picks.
+// A query whose list overflows (many scores tied at tau) gets cnt =
+// SEL_OVERFLOW, and score_select_mfma_kernel (marked_only) recomputes its
+// 64-query tile exactly.
+namespace thr {
+constexpr int QW = 64;            // queries per workgroup
+constexpr int NCT = QW / 16;      // 16-column MFMA tiles
+constexpr int CB = 16;            // blocks per stage: 4 M-tiles of 4 blocks x 4 slots
+constexpr int LPQ = 16;           // lanes holding a query's blocks
+constexpr int TV = 2;             // values kept per lane
+template <int KMAX>
+struct Cfg {
+    static constexpr int CAP = (5 * KMAX) / 2;   // list entries per query
+};
+}  // namespace thr
+
+// (score, block) as one unsigned key ordered like (score desc, block asc):
+// the score's bits mapped to an order-preserving unsigned (a zero score
+// taken as +0, which the float comparison treats as equal to -0), then the
+// complement of the block.
+__device__ __forceinline__ uint64_t sel_key(float v, int blk) {
+    const uint32_t u = __float_as_uint(v + 0.0f);
+    const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((uint64_t)ord << 32) | (uint32_t)(0xffffffffu - (uint32_t)blk);
+}
+__device__ __forceinline__ float sel_key_score(uint64_t key) {
+    const uint32_t ord = (uint32_t)(key >> 32);
+    return __uint_as_float((ord & 0x80000000u) ? (ord & 0x7fffffffu) : ~ord);
+}
+__device__ __forceinline__ int sel_key_block(uint64_t key) { return (int)(0xffffffffu - (uint32_t)key); }
+
+template <int D, int KMAX>
+__global__ __launch_bounds__(256, (D == 64) ? 2 : 1) void score_select_thr_kernel(
+    const bf16_t *__restrict__ q, int64_t qsb, int64_t qsn, int64_t qsh, const float *__restrict__ qgain,
+    float eps, const bf16_t *__restrict__ S0, int64_t n, int Hq, int Hkv, int64_t nb, int64_t W, int kk,
+    float scale, int32_t *__restrict__ idx, float *__restrict__ val, int32_t *__restrict__ cnt,
+    float *__restrict__ scores, int ntiles) {
+    using namespace thr;
+    constexpr int CAP = Cfg<KMAX>::CAP;
+    constexpr int NKS = D / 32;
+    constexpr int ROWQ = D + 8;                        // padded LDS row of the routing queries
+    // LDS: phase 1 the routing queries and the kept values; phase 2 the lists
+    constexpr size_t P1 = (size_t)QW * ROWQ * 2 + (size_t)QW * LPQ * TV * 4;
+    constexpr size_t P2 = (size_t)QW * CAP * 8;
+    constexpr size_t UB = P1 > P2 ? P1 : P2;
+    __shared__ __align__(16) char pool[UB];
+    __shared__ float taus[QW];
+    __shared__ int qcnt[QW];
+    bf16_t *qgs = reinterpret_cast<bf16_t *>(pool);
+    float *tvs = reinterpret_cast<float *>(pool + (size_t)QW * ROWQ * 2);   // [query][lane][TV]
+    uint64_t *lk = reinterpret_cast<uint64_t *>(pool);                     // [query][CAP] keys
+
+    const int tid = threadIdx.x;
+    const int w = tid >> 6, lane = tid & 63, l16 = lane & 15, lg = lane >> 4;
+    const int g = blockIdx.y;
+    const int64_t b = blockIdx.z;
+    const int G = Hq / Hkv;
+    // deep and shallow tiles alternate in launch order
+    const int bx = blockIdx.x;
+    const int tile = (bx & 1) ? ntiles - 1 - (bx >> 1) : (bx >> 1);
+    const int64_t i0 = (int64_t)tile * QW;
+    routing_queries_tile<D, ROWQ>(q, qsb, qsn, qsh, qgain, eps, b, i0, n, g, G, qgs, tid);
+    __syncthreads();
+    bf16x8 qb[NCT][NKS];
+    int bmax[NCT];
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct) {
+        const int qc = 16 * ct + l16;
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) qb[ct][ks] = ldb8(qgs + qc * ROWQ + 32 * ks + 8 * lg);
+        const int64_t iq = i0 + qc;
+        bmax[ct] = (iq < n) ? (int)cand_bmax(iq, 64, W) : 0;
+    }
+    const int64_t last = (i0 + QW - 1 < n) ? i0 + QW - 1 : n - 1;
+    const int tile_bmax = (int)cand_bmax(last, 64, W);
+    // every query of the tile has the candidates 1 .. bmin (bmax grows with i)
+    const int bmin = (i0 + QW - 1 < n) ? (int)cand_bmax(i0, 64, W) : 0;
+    const int nst = (tile_bmax > 0) ? (tile_bmax + CB - 1) / CB : 0;
+    const bf16_t *Sg = S0 + (b * Hkv + g) * nb * 4 * D;
+
+    // This wave's stages w, w+4, ...: A row l16 of M-tile mt is slot l16 & 3
+    // of block 1 + 16 st + 4 mt + l16 / 4 (clamped to tile_bmax: rows past it
+    // are never visited); visit(ct, block, score, candidate) per lane and
+    // column tile.  Stages wholly within 1 .. bmin need no candidate mask.
+    auto load = [&](int st, bf16x8 (&af)[4][NKS]) {
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+            int blk = 1 + st * CB + 4 * mt + (l16 >> 2);
+            blk = (blk <= tile_bmax) ? blk : tile_bmax;
+            const bf16_t *src = Sg + ((int64_t)blk * 4 + (l16 & 3)) * D + 8 * lg;
+#pragma unroll
+            for (int ks = 0; ks < NKS; ++ks) af[mt][ks] = ldb8(src + 32 * ks);
+        }
+    };
+    auto scan = [&](auto &&visit) {
+        auto stage = [&](int st, const bf16x8 (&af)[4][NKS], auto mask_c) {
+            constexpr bool MASK = decltype(mask_c)::value;
+            const int b0 = 1 + st * CB;
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) {
+                const int blk = b0 + 4 * mt + lg;
+                // the column tiles' MFMA chains first (independent, so they
+                // pipeline), then the scores
+                f32x4 acc[NCT];
+#pragma unroll
+                for (int ct = 0; ct < NCT; ++ct) acc[ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int ks = 0; ks < NKS; ++ks)
+#pragma unroll
+                    for (int ct = 0; ct < NCT; ++ct)
+                        acc[ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[mt][ks], qb[ct][ks], acc[ct], 0, 0, 0);
+#pragma unroll
+                for (int ct = 0; ct < NCT; ++ct) {
+                    // the max is exact in any order (no NaN)
+                    const float best = fmaxf(fmaxf(acc[ct][0], acc[ct][1]), fmaxf(acc[ct][2], acc[ct][3]));
+                    visit(ct, blk, best * scale, !MASK || blk <= bmax[ct]);
+                }
+            }
+        };
+        auto run = [&](int st, const bf16x8 (&af)[4][NKS]) {
+            if (st * CB + CB <= bmin) stage(st, af, std::false_type());   // uniform
+            else stage(st, af, std::true_type());
+        };
+        bf16x8 a0[4][NKS], a1[4][NKS];
+        int st = w;
+        if (st < nst) load(st, a0);
+        if (st + 4 < nst) load(st + 4, a1);
+        while (st < nst) {
+            run(st, a0);
+            if (st + 8 < nst) load(st + 8, a0);
+            st += 4;
+            if (st >= nst) break;
+            run(st, a1);
+            if (st + 8 < nst) load(st + 8, a1);
+            st += 4;
+        }
+    };
+
+    // ---- pass A: the 2 largest candidate scores per lane and column tile
+    float t0[NCT], t1[NCT];
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct) t0[ct] = t1[ct] = -INFINITY;
+    auto keep2 = [&](int ct, float x) {
+        t1[ct] = fmaxf(t1[ct], fminf(t0[ct], x));
+        t0[ct] = fmaxf(t0[ct], x);
+    };
+    if (scores) {   // the verification dump: a separate scan keeps the other branch-free
+        scan([&](int ct, int blk, float v, bool ok) {
+            if (ok) scores[((b * Hkv + g) * n + i0 + 16 * ct + l16) * nb + blk] = v;
+            keep2(ct, ok ? v : -INFINITY);
+        });
+    } else {
+        scan([&](int ct, int, float v, bool ok) { keep2(ct, ok ? v : -INFINITY); });
+    }
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct) {
+        float *dst = tvs + ((16 * ct + l16) * LPQ + 4 * w + lg) * TV;
+        dst[0] = t0[ct];
+        dst[1] = t1[ct];
+    }
+    __syncthreads();
+    // tau of query tid / 4: the kk-th largest of its 32 values (the smallest
+    // value with fewer than kk values strictly above it), 8 values per thread
+    {
+        const int qc = tid >> 2, part = tid & 3;
+        const float4 *tq4 = reinterpret_cast<const float4 *>(tvs + qc * LPQ * TV);
+        float tq[LPQ * TV];
+#pragma unroll
+        for (int j = 0; j < LPQ * TV / 4; ++j) {
+            const float4 t4 = tq4[j];
+            tq[4 * j] = t4.x;
+            tq[4 * j + 1] = t4.y;
+            tq[4 * j + 2] = t4.z;
+            tq[4 * j + 3] = t4.w;
+        }
+        float best = INFINITY;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float v = tq[8 * part + j];
+            int gt = 0;
+#pragma unroll
+            for (int j2 = 0; j2 < LPQ * TV; ++j2) gt += (tq[j2] > v) ? 1 : 0;
+            best = (gt < kk) ? fminf(best, v) : best;
+        }
+        best = fminf(best, __shfl_xor(best, 1, 64));
+        best = fminf(best, __shfl_xor(best, 2, 64));
+        if (part == 0) taus[qc] = best;
+    }
+    __syncthreads();   // every tau is set; the values' LDS now holds the lists
+    float tau[NCT];
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct) tau[ct] = taus[16 * ct + l16];
+
+    // ---- pass B: every candidate scoring >= tau into its query's list
+    if (tid < QW) qcnt[tid] = 0;
+    __syncthreads();
+    scan([&](int ct, int blk, float v, bool ok) {
+        if (ok && v >= tau[ct]) {
+            const int qc = 16 * ct + l16;
+            const int pos = atomicAdd(&qcnt[qc], 1);
+            if (pos < CAP) lk[qc * CAP + pos] = sel_key(v, blk);
+        }
+    });
+    __syncthreads();
+
+    // ---- rank the listed entries of query tid / 4: an entry's rank is the
+    // number of keys above it; ranks < kk are the picks
+    {
+        const int qc = tid >> 2, part = tid & 3;
+        const int64_t iq = i0 + qc;
+        if (iq < n) {
+            const int64_t o = ((b * Hkv + g) * n + iq) * kk;
+            const int c = qcnt[qc];
+            if (c > CAP) {                             // overflow: the exact pass recomputes the tile
+                if (part == 0) cnt[(b * Hkv + g) * n + iq] = SEL_OVERFLOW;
+            } else {
+                const uint64_t *kl = lk + qc * CAP;
+                for (int j = part; j < c; j += 4) {
+                    const uint64_t key = kl[j];
+                    int rank = 0;
+                    for (int j2 = 0; j2 < c; j2 += 2) {   // CAP is even: the pair stays in the list
+                        const ulonglong2 k2 = *reinterpret_cast<const ulonglong2 *>(kl + j2);
+                        rank += (k2.x > key) ? 1 : 0;
+                        rank += (j2 + 1 < c && k2.y > key) ? 1 : 0;
+                    }
+                    if (rank < kk) {
+                        idx[o + rank] = sel_key_block(key);
+                        val[o + rank] = sel_key_score(key);
+                    }
+                }
+                const int taken = (c < kk) ? c : kk;
+                for (int j = taken + ((part - taken) & 3); j < kk; j += 4) {
+                    idx[o + j] = -1;
+                    val[o + j] = -INFINITY;
+                }
+                if (part == 0) cnt[(b * Hkv + g) * n + iq] = taken;
+            }
+        }
+    }
+}
+
 template <int DT, int D, int M, int KMAX>
 __global__ __launch_bounds__(SEL_WG) void hier_select_kernel(
     const typename St<DT>::T *__restrict__ q, int64_t qsb, int64_t qsn, int64_t qsh,
@@ -632,15 +931,23 @@ void launch_flat(const void *q, const int64_t *qs, const float *qgain, float eps
                  int32_t *idx, float *val, int32_t *cnt, float *scores, hipStream_t s) {
     dim3 grid((unsigned)((n + SEL_WG - 1) / SEL_WG), (unsigned)Hkv, (unsigned)B);
     if constexpr (DT == 1 && M == 4 && KMAX <= 32) {
-        hipLaunchKernelGGL((score_select_mfma_kernel<D, KMAX, false>), grid, dim3(256), 0, s, (const bf16_t *)q,
-                           qs[0], qs[1], qs[2], qgain, eps, (const bf16_t *)S0, n, (int)Hq, (int)Hkv,
-                           n / 64, W, (int)k, scale, idx, val, cnt, scores, nullptr, 1, 1, nullptr);
-    } else {
-        hipLaunchKernelGGL((score_select_kernel<DT, D, M, KMAX>), grid, dim3(SEL_WG), 0, s,
-                           (const typename St<DT>::T *)q, qs[0], qs[1], qs[2], qgain, eps,
-                           (const typename St<DT>::T *)S0, n, (int)Hq, (int)Hkv, n / 64, W, (int)k,
-                           scale, idx, val, cnt, scores);
+        if (Hq / Hkv <= 16) {   // the routing-query tile takes up to 16 heads per KV head
+            // threshold top-k, then the exact kernel on the tiles it marked
+            const int ntiles = (int)((n + thr::QW - 1) / thr::QW);
+            hipLaunchKernelGGL((score_select_thr_kernel<D, KMAX>),
+                               dim3((unsigned)ntiles, (unsigned)Hkv, (unsigned)B), dim3(256), 0, s,
+                               (const bf16_t *)q, qs[0], qs[1], qs[2], qgain, eps, (const bf16_t *)S0, n, (int)Hq,
+                               (int)Hkv, n / 64, W, (int)k, scale, idx, val, cnt, scores, ntiles);
+            hipLaunchKernelGGL((score_select_mfma_kernel<D, KMAX, false>), grid, dim3(256), 0, s,
+                               (const bf16_t *)q, qs[0], qs[1], qs[2], qgain, eps, (const bf16_t *)S0, n, (int)Hq,
+                               (int)Hkv, n / 64, W, (int)k, scale, idx, val, cnt, scores, nullptr, 1, 1, nullptr, 1);
+            return;
+        }
     }
+    hipLaunchKernelGGL((score_select_kernel<DT, D, M, KMAX>), grid, dim3(SEL_WG), 0, s,
+                       (const typename St<DT>::T *)q, qs[0], qs[1], qs[2], qgain, eps,
+                       (const typename St<DT>::T *)S0, n, (int)Hq, (int)Hkv, n / 64, W, (int)k,
+                       scale, idx, val, cnt, scores);
 }
 
 template <int DT, int D, int M, int KMAX>
@@ -650,13 +957,13 @@ void launch_hier(const void *q, const int64_t *qs, const float *qgain, float eps
                  float *scores, float *sup_scores, hipStream_t s) {
     const int64_t ns = (n / 64 + F - 1) / F;
     if constexpr (DT == 1 && M == 4 && KMAX <= 32) {
-        if (ns <= 32 * SEL_PMW) {
+        if (ns <= 32 * SEL_PMW && Hq / Hkv <= 16) {
             dim3 grid((unsigned)((n + 63) / 64), (unsigned)Hkv, (unsigned)B);
             const size_t pm = (size_t)64 * ((ns + 31) / 32) * sizeof(uint32_t);
             hipLaunchKernelGGL((score_select_mfma_kernel<D, KMAX, true>), grid, dim3(256), pm, s, (const bf16_t *)q,
                                qs[0], qs[1], qs[2], qgain, eps, (const bf16_t *)S0, n, (int)Hq, (int)Hkv, n / 64,
                                W, (int)k, scale, idx, val, cnt, scores, (const bf16_t *)S1, (int)F, (int)beam,
-                               sup_scores);
+                               sup_scores, 0);
             return;
         }
     }
