@@ -7,8 +7,9 @@ flat block selection and the union attention, all HIP kernels, inputs resident
 in HBM.  `value` = tokens/s of that forward.  The JSON line also carries the
 roofline of the dominant kernel (the union attention, MFMA-bound), the
 per-stage times, the 32K decode step (B=32 sequences, paged bf16 cache) as
-µs/step against the HBM roofline, and the oracle's CPU restatement timed on a
-bounded sample of the same workload.
+µs/step against the HBM roofline, and the CPU baseline: the reference's naive
+dense and gathered paths restated in torch (oracle/hba_cpu_torch.py), one
+4096-token fp32 layer forward on the host's cores, in a child process.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-decode]
   python bench.py --copy-probe MIB      # plain device copy, for counter calibration
@@ -252,39 +253,72 @@ def bench_decode(dev, iters=200):
                         "sink and routed page units on MFMA), decode_d3 (LSE merge), one HIP graph")
 
 
-def cpu_baseline(res, budget_s=20.0):
-    """The oracle's restatement of hba_attention_eval (gathered union softmax,
-    attention.py:610-713) on the host: the whole-sequence prologue (QKNorm,
-    RoPE, summaries, routing queries) plus per-row selection + attention on a
-    sample of query rows, extrapolated to all rows."""
-    import numpy as np
-    from threadpoolctl import threadpool_limits
+CPU_WORKLOAD = dict(batch=1, seq_len=4096, q_heads=14, kv_heads=2, head_dim=64, sinks=4, window=1024, block=64,
+                    slots=4, top_k=16, dtype="fp32", qknorm="gains 1", seed=0)
+CPU_FLOP = 2.233e10   # algorithmic FLOP of one forward at this workload (mean 1515 keys per query)
+
+
+def cpu_leg(reps=5):
+    """The CPU baseline itself, run in a child process that never touches the
+    GPU: one HBA layer forward at the 4096-token fp32 workload through the
+    oracle's torch restatements of the reference's naive dense path
+    (attention.py:306-356) and, timed separately, its gathered path
+    (:610-713), on the host's cores; 1 warmup, then the median of `reps`.
+    Prints one JSON line with its own peak RSS."""
+    import resource
+    import statistics
+    import torch
+    import hba_amd
+    import oracle.hba_cpu_torch as T
     import oracle.hba_oracle as O
-    cfg, x, prm = res["cfg"], res["x"], res["prm"]
-    f = lambda t: t.detach().float().cpu().numpy()
-    q, k, v = f(x["q"])[0], f(x["k"])[0], f(x["v"])[0]
-    cos, sin = f(res["cos"]), f(res["sin"])
-    n = q.shape[0]
-    with threadpool_limits(limits=1):
-        t0 = time.perf_counter()
-        P = O.prepare(q, k, v, cos, sin, cfg, f(prm.probes), f(prm.proj), f(prm.q.gain), f(prm.k.gain),
-                      1e-6, "bf16")
-        t_pro = time.perf_counter() - t0
-        rng = np.random.RandomState(0)
-        done, t_rows = 0, 0.0
-        while t_rows < budget_s and done < n:
-            rows = np.sort(rng.choice(n, 256, replace=False))
-            t0 = time.perf_counter()
-            idx, val, cnt = O.flat_select(P.qg, P.S0, P.scale, cfg.k_blocks, 64, cfg.window, rows)
-            I, C = O._scatter_rows(idx, cnt, rows, n)
-            O.attn_rows(P.qc, P.qr, P.kc, P.kr, P.v, I, C, P.scale, cfg.sinks, cfg.window, 64, rows)
-            t_rows += time.perf_counter() - t0
-            done += rows.size
-    total = t_pro + t_rows * n / done
-    return {"value": round(n / total, 1), "unit": "tokens/s", "cores": 1, "kind": "port",
-            "sample": f"oracle gathered path (hba_attention_eval restated, numpy/C, 1 thread) on the "
-                      f"same 32K workload: full prologue {t_pro:.1f}s + {done} sampled query rows in "
-                      f"{t_rows:.1f}s, extrapolated to {n} rows; host {cpu_model()}"}
+    from hba_amd import synth
+    threads = min(os.cpu_count() or 1, int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)))
+    torch.set_num_threads(threads)
+    w = CPU_WORKLOAD
+    cfg = hba_amd.HBAConfig(n_heads=w["q_heads"], n_kv=w["kv_heads"], head_dim=w["head_dim"], sinks=w["sinks"],
+                            window=w["window"], block=w["block"], slots=w["slots"], k_blocks=w["top_k"])
+    x = synth.layer_inputs(1, w["seq_len"], w["q_heads"], w["kv_heads"], w["head_dim"], m=w["slots"],
+                           dtype=torch.float32, seed=w["seed"], sharp=False)
+    cos, sin = (torch.from_numpy(t) for t in O.rope_tables(w["seq_len"], w["head_dim"], cfg.rope_theta))
+    args = (x["q"], x["k"], x["v"], cos, sin, cfg, x["probes"], x["proj"], x["q_gain"], x["k_gain"], 1e-6)
+    res = {}
+    with torch.no_grad():
+        for name, fn in (("dense", T.dense_forward), ("gathered", T.gathered_forward)):
+            fn(*args)
+            ts = []
+            for _ in range(reps):
+                t0 = time.perf_counter()
+                fn(*args)
+                ts.append(time.perf_counter() - t0)
+            res[name] = statistics.median(ts)
+    res["threads"] = torch.get_num_threads()
+    res["peak_rss_MiB"] = round(resource.getrusage(resource.RUSAGE_SELF).ru_maxrss / 1024.0, 1)
+    print(json.dumps(res))
+
+
+def cpu_baseline():
+    """cpu_leg in a child process (its peak RSS is its own), reported beside
+    the GPU numbers: value = tokens/s of the naive dense path; the gathered
+    path's time, threads, CPU model, peak RSS and GFLOP/s alongside."""
+    import subprocess
+    r = subprocess.run([sys.executable, os.path.abspath(__file__), "--cpu-leg"], capture_output=True, text=True,
+                       timeout=900)
+    if r.returncode != 0:
+        return {"value": None, "unit": "tokens/s", "error": r.stderr[-400:]}
+    d = json.loads(r.stdout.strip().splitlines()[-1])
+    n = CPU_WORKLOAD["seq_len"]
+    return {"value": round(n / d["dense"], 1), "unit": "tokens/s", "cores": d["threads"], "kind": "port",
+            "sample": f"the whole forward, not a sample: one HBA layer at seq 4096, 14/2 heads, d=64, fp32, "
+                      f"W=1024, k=16, seed 0, through the oracle's torch restatement of the reference's naive "
+                      f"dense path (attention.py:306-356), torch CPU on {d['threads']} threads, 1 warmup + "
+                      f"median of 5; host {cpu_model()}",
+            "workload": dict(CPU_WORKLOAD),
+            "dense_s_per_forward": round(d["dense"], 4),
+            "gathered_s_per_forward": round(d["gathered"], 4),
+            "gathered_tokens_per_s": round(n / d["gathered"], 1),
+            "gflops_dense": round(CPU_FLOP / d["dense"] / 1e9, 2),
+            "gflops_gathered": round(CPU_FLOP / d["gathered"] / 1e9, 2),
+            "peak_rss_MiB": d["peak_rss_MiB"]}
 
 
 def _timed(fn, reps=5):
@@ -493,7 +527,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
-    ap.add_argument("--cpu-budget", type=float, default=20.0)
+    ap.add_argument("--cpu-leg", action="store_true",
+                    help="internal: run only the CPU baseline (no GPU use) and print its JSON")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run 3 plain device copies of MIB MiB (counter calibration) and exit")
     ap.add_argument("--config", choices=["layer32k", "hier128k", "donor", "equiv32k", "bwd32k"],
@@ -501,6 +536,9 @@ def main():
                     help="layer32k: the headline line (default); hier128k / donor / equiv32k: the other "
                          "measured workloads, one JSON line each")
     a = ap.parse_args()
+    if a.cpu_leg:
+        cpu_leg()
+        return
     if a.copy_probe:
         import torch
         src = torch.empty(a.copy_probe << 20, dtype=torch.uint8, device="cuda:0").fill_(1)
@@ -529,7 +567,7 @@ def main():
     attn_ms = res["stage_ms"]["attn"]
     achieved = res["attn_flop"] / (attn_ms * 1e-3) / 1e12
     dec = None if a.no_decode else bench_decode(dev)
-    cpu = None if a.no_cpu else cpu_baseline(res, a.cpu_budget)
+    cpu = None if a.no_cpu else cpu_baseline()
     total_flop = res["attn_flop"] + res["score_flop"] + res["summ_flop"]
     line = {
         "metric": "HBA layer fwd tokens/s at 32K (% MFMA roofline); decode µs/step (% HBM BW)",
