@@ -249,8 +249,10 @@ def bench_decode(dev, iters=200):
     return dict(us_per_step=round(us, 3), algorithmic_bytes=nbytes, achieved_GBs=round(gbs, 1),
                 hbm_frac=round(gbs / PEAK_HBM_GBS, 4), graph_replay_matches_eager=ok,
                 batch=Bd, context="L ~ U[16384, 32768], paged bf16, shuffled page table",
-                kernels="decode_d1 (page scores, chunk top-k, query operands), decode_d2 (window, "
-                        "sink and routed page units on MFMA), decode_d3 (LSE merge), one HIP graph")
+                kernels="decode_fused_kernel: one launch (page scores and chunk top-k with the window "
+                        "and sink pages; the last score workgroup of a (sequence, KV head) merges the lists "
+                        "and runs the routed pages; the last workgroup merges the partial states), "
+                        "replayed from a HIP graph")
 
 
 CPU_WORKLOAD = dict(batch=1, seq_len=4096, q_heads=14, kv_heads=2, head_dim=64, sinks=4, window=1024, block=64,
@@ -531,10 +533,10 @@ def main():
                     help="internal: run only the CPU baseline (no GPU use) and print its JSON")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run 3 plain device copies of MIB MiB (counter calibration) and exit")
-    ap.add_argument("--config", choices=["layer32k", "hier128k", "donor", "equiv32k", "bwd32k"],
+    ap.add_argument("--config", choices=["layer32k", "hier128k", "donor", "equiv32k", "bwd32k", "decode32k"],
                     default="layer32k",
-                    help="layer32k: the headline line (default); hier128k / donor / equiv32k: the other "
-                         "measured workloads, one JSON line each")
+                    help="layer32k: the headline line (default); hier128k / donor / equiv32k / bwd32k / "
+                         "decode32k: the other measured workloads, one JSON line each")
     a = ap.parse_args()
     if a.cpu_leg:
         cpu_leg()
@@ -558,7 +560,9 @@ def main():
     dev = torch.device("cuda:0")
     if a.config != "layer32k":
         line = {"hier128k": bench_hier128k, "donor": bench_donor, "equiv32k": bench_equiv32k,
-                "bwd32k": bench_bwd32k}[a.config](dev)
+                "bwd32k": bench_bwd32k,
+                "decode32k": lambda d: {"metric": "HBA decode step µs (B=32, 16-32K paged bf16 cache)",
+                                        **bench_decode(d)}}[a.config](dev)
         line.update({"n_gpus": 1, "dtype": "bf16", "data": "synthetic"})
         print(json.dumps(line))
         return

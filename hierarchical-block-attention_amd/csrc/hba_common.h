@@ -60,6 +60,38 @@ __device__ __host__ __forceinline__ int64_t cand_bmax(int64_t i, int64_t Bk, int
     return lim / Bk - 1;
 }
 
+// Paged cache layouts (one page = 64 tokens of one KV head, D elements each),
+// ordered so that every 16-byte operand load of the decode MFMA tiles is part
+// of a contiguous 1 KB run across the wave's 64 lanes (lane L = l16 + 16*lg):
+//   keys  (kc_pages, kr_pages): key j, element t at
+//         ((mt * (D/32) + ks) * 64 + l16 + 16*lg) * 8 + e, where
+//         mt = 2*(j/32) + (j/4)%2, l16 = 4*((j%32)/8) + j%4  (the S^T tile row
+//         that holds key j), ks = t/32, lg = (t%32)/8, e = t%8;
+//   values (v_pages): key j, element t at
+//         ((dt * 2 + h) * 64 + l16 + 16*lg) * 8 + e, where
+//         dt = t/16, l16 = t%16, h = j/32, lg = (j%32)/8, e = j%8.
+__host__ __device__ __forceinline__ int64_t page_key_off(int j, int t, int D) {
+    const int mt = 2 * (j >> 5) + ((j >> 2) & 1);
+    const int l16 = 4 * ((j & 31) >> 3) + (j & 3);
+    return ((int64_t)(mt * (D / 32) + (t >> 5)) * 64 + l16 + 16 * ((t >> 3) & 3)) * 8 + (t & 7);
+}
+__host__ __device__ __forceinline__ int64_t page_val_off(int j, int t) {
+    return ((int64_t)((t >> 4) * 2 + (j >> 5)) * 64 + (t & 15) + 16 * ((j >> 3) & 3)) * 8 + (j & 7);
+}
+// Inverse for a chunk of 8 consecutive storage elements c*8 .. c*8+7: keys
+// hold key j, elements t0 .. t0+7; values hold element t, keys j0 .. j0+7.
+__host__ __device__ __forceinline__ void page_key_chunk(int c, int D, int &j, int &t0) {
+    const int L = c & 63, r = c >> 6, ks = r % (D / 32), mt = r / (D / 32);
+    const int l16 = L & 15, lg = L >> 4;
+    j = 32 * (mt >> 1) + 8 * (l16 >> 2) + 4 * (mt & 1) + (l16 & 3);
+    t0 = 32 * ks + 8 * lg;
+}
+__host__ __device__ __forceinline__ void page_val_chunk(int c, int &t, int &j0) {
+    const int L = c & 63, r = c >> 6;
+    t = 16 * (r >> 1) + (L & 15);
+    j0 = 32 * (r & 1) + 8 * (L >> 4);
+}
+
 // QKNorm of one row held in registers, declared order (see oracle):
 // ss = fma(x,x,ss) sequential, ms = ss/d, ms = max(ms, eps), r = sqrt(ms),
 // y = (x / r) * gain, rounded to the storage dtype.

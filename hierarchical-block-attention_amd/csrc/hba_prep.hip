@@ -117,7 +117,16 @@ __global__ __launch_bounds__(256) void summarize_kernel(
         src = kc + ((b * Hkv + g) * n + c * BK) * D;
         dst = out + ((b * Hkv + g) * nb + c) * m * D;
     }
-    for (int e = tid; e < BK * D; e += 256) kb[e / D][e % D] = St<DT>::ld(src, e);
+    if (pages) {   // a cache page: chunks of 8 elements in the page layout (page_key_chunk)
+        for (int c = tid; c < 8 * D; c += 256) {
+            int j, t0;
+            page_key_chunk(c, D, j, t0);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) kb[j][t0 + u] = St<DT>::ld(src, 8 * c + u);
+        }
+    } else {
+        for (int e = tid; e < BK * D; e += 256) kb[e / D][e % D] = St<DT>::ld(src, e);
+    }
     __syncthreads();
     const float *pr = probes + g * m * D;
     for (int e = tid; e < m * BK; e += 256) {
@@ -194,18 +203,25 @@ __global__ __launch_bounds__(256) void kv_append_kernel(
     // nothing to append, outside the page table or past the RoPE tables
     if (pos < 0 || pos / BK >= maxp || pos >= lmax) return;
     int64_t page = ptab[s * maxp + pos / BK];
-    int64_t dst = ((page * Hkv + g) * BK + pos % BK) * D;
+    const int64_t base = (page * Hkv + g) * BK * D;
+    const int j = (int)(pos % BK);
     float x[D], y[D];
     load_row<DT, D>(knew + gid * D, x);
     if (kgain) qknorm_row<DT, D>(x, kgain[g], eps);
-    store_row<DT, D>(kcp + dst, x);
     rope_row<DT, D>(x, y, cosT + pos * D, sinT + pos * D);
-    store_row<DT, D>(krp + dst, y);
-    load_row<DT, D>(vnew + gid * D, x);
-    // values are d-major within a page: element t of token pos at [t][pos % 64]
-    typename St<DT>::T *vcol = vp + (page * Hkv + g) * D * BK + pos % BK;
+    // keys: 8 consecutive elements per chunk of the page layout (page_key_off)
 #pragma unroll
-    for (int t = 0; t < D; ++t) St<DT>::st(vcol, (int64_t)t * BK, x[t]);
+    for (int t0 = 0; t0 < D; t0 += 8) {
+        const int64_t o = base + page_key_off(j, t0, D);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            St<DT>::st(kcp, o + u, x[t0 + u]);
+            St<DT>::st(krp, o + u, y[t0 + u]);
+        }
+    }
+    load_row<DT, D>(vnew + gid * D, x);
+#pragma unroll
+    for (int t = 0; t < D; ++t) St<DT>::st(vp, base + page_val_off(j, t), x[t]);
 }
 
 }  // namespace hba

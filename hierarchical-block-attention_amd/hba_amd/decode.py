@@ -4,12 +4,18 @@ The reference has no decode path or KV cache.  The decode step here is row
 L-1 of hba_attention_eval (src/hba/attention.py:610-713) for a sequence of
 length L, served from a cache laid out for the operator:
 
-  kc_pages   [P, Hkv, 64, d]  QKNorm'd NoPE keys (normalised once, on append)
-  kr_pages   [P, Hkv, 64, d]  the same keys rotated at their own positions
-  v_pages    [P, Hkv, d, 64]  values, d-major within a page (the P.V operand)
-  summ_pages [P, Hkv, m, d]   slot summaries of full pages
+  kc_pages   [P, Hkv, 64*d]  QKNorm'd NoPE keys (normalised once, on append)
+  kr_pages   [P, Hkv, 64*d]  the same keys rotated at their own positions
+  v_pages    [P, Hkv, 64*d]  values
+  summ_pages [P, Hkv, m, d]  slot summaries of full pages
   page_table int32 [batch, max_pages]  logical page -> physical page
-  seq_lens   int32 [batch]    tokens in the cache (the current one included)
+  seq_lens   int32 [batch]   tokens in the cache (the current one included)
+
+Within a page (64 tokens of one KV head) keys and values are stored in the
+order the decode kernel's MFMA tiles read them, so that each of its operand
+loads is one contiguous 1 KB run (key_offsets / value_offsets give the place
+of token j, element t; the kernels use the same formulas).  key_rows /
+value_rows read pages back as [.., Hkv, 64, d] token rows.
 
 A key's rotation depends only on its own position, so it is applied once, on
 append, and the window reads kr directly (the query is rotated in the kernel
@@ -25,6 +31,27 @@ from .config import union_scale
 PAGE = ops.BLOCK
 
 
+def key_offsets(d, device=None):
+    """Storage offset of key j, element t within a key page, as a [64, d]
+    int64 tensor: ((mt * d/32 + ks) * 64 + l16 + 16*lg) * 8 + e with
+    mt = 2*(j//32) + (j//4)%2, l16 = 4*((j%32)//8) + j%4, ks = t//32,
+    lg = (t%32)//8, e = t%8."""
+    j = torch.arange(PAGE, device=device)[:, None]
+    t = torch.arange(d, device=device)[None, :]
+    mt = 2 * (j // 32) + (j // 4) % 2
+    l16 = 4 * ((j % 32) // 8) + j % 4
+    return ((mt * (d // 32) + t // 32) * 64 + l16 + 16 * ((t % 32) // 8)) * 8 + t % 8
+
+
+def value_offsets(d, device=None):
+    """Storage offset of token j, element t within a value page, as a
+    [64, d] int64 tensor: ((t//16 * 2 + j//32) * 64 + t%16 + 16*((j%32)//8)) * 8
+    + j%8."""
+    j = torch.arange(PAGE, device=device)[:, None]
+    t = torch.arange(d, device=device)[None, :]
+    return (((t // 16) * 2 + j // 32) * 64 + t % 16 + 16 * ((j % 32) // 8)) * 8 + j % 8
+
+
 class PagedKVCache:
     def __init__(self, cfg, batch, max_len, dtype, device, num_pages=None):
         self.cfg = cfg
@@ -33,9 +60,11 @@ class PagedKVCache:
         self.max_pages = (max_len + PAGE - 1) // PAGE
         P = num_pages if num_pages is not None else batch * self.max_pages
         Hkv, d, m = cfg.n_kv, cfg.head_dim, cfg.slots
-        self.kc_pages = torch.zeros(P, Hkv, PAGE, d, dtype=dtype, device=device)
-        self.kr_pages = torch.zeros(P, Hkv, PAGE, d, dtype=dtype, device=device)
-        self.v_pages = torch.zeros(P, Hkv, d, PAGE, dtype=dtype, device=device)
+        self.kc_pages = torch.zeros(P, Hkv, PAGE * d, dtype=dtype, device=device)
+        self.kr_pages = torch.zeros(P, Hkv, PAGE * d, dtype=dtype, device=device)
+        self.v_pages = torch.zeros(P, Hkv, PAGE * d, dtype=dtype, device=device)
+        self._koff = key_offsets(d, device).reshape(-1)
+        self._voff = value_offsets(d, device).reshape(-1)
         self.summ_pages = torch.zeros(P, Hkv, m, d, dtype=dtype, device=device)
         self.page_table = torch.zeros(batch, self.max_pages, dtype=torch.int32, device=device)
         self.seq_lens = torch.zeros(batch, dtype=torch.int32, device=device)
@@ -73,12 +102,15 @@ class PagedKVCache:
         pad = npg * PAGE - L
         Hkv, d = kc_seq.shape[1], kc_seq.shape[2]
 
-        def paged(x):
-            return torch.nn.functional.pad(x, (0, 0, 0, 0, 0, pad)).view(npg, PAGE, Hkv, d)
+        def paged(x, off):
+            rows = torch.nn.functional.pad(x, (0, 0, 0, 0, 0, pad)).view(npg, PAGE, Hkv, d).transpose(1, 2)
+            out = torch.empty(npg, Hkv, PAGE * d, dtype=self.kc_pages.dtype, device=self.kc_pages.device)
+            out[:, :, off] = rows.reshape(npg, Hkv, PAGE * d).to(out.dtype)
+            return out
 
-        self.kc_pages[pages[:npg]] = paged(kc_seq).transpose(1, 2).to(self.kc_pages.dtype)
-        self.kr_pages[pages[:npg]] = paged(kr_seq).transpose(1, 2).to(self.kr_pages.dtype)
-        self.v_pages[pages[:npg]] = paged(v_seq).permute(0, 2, 3, 1).to(self.v_pages.dtype)
+        self.kc_pages[pages[:npg]] = paged(kc_seq, self._koff)
+        self.kr_pages[pages[:npg]] = paged(kr_seq, self._koff)
+        self.v_pages[pages[:npg]] = paged(v_seq, self._voff)
         self.lens[s] = L
         self._sync_table()
         full = pages[: L // PAGE]
@@ -105,6 +137,16 @@ class PagedKVCache:
         if done:
             ops.summarize_pages(self.kc_pages, torch.tensor(done, dtype=torch.int32), summ.probes,
                                 summ.proj, self.summ_pages)
+
+    def key_rows(self, pages, rotated=False):
+        """Keys of physical pages (int or index tensor) as token rows
+        [..., Hkv, 64, d] (the rotated copy with rotated=True)."""
+        src = (self.kr_pages if rotated else self.kc_pages)[pages]
+        return src[..., self._koff].unflatten(-1, (PAGE, self.cfg.head_dim))
+
+    def value_rows(self, pages):
+        """Values of physical pages as token rows [..., Hkv, 64, d]."""
+        return self.v_pages[pages][..., self._voff].unflatten(-1, (PAGE, self.cfg.head_dim))
 
     def scales(self, cfg=None):
         cfg = cfg or self.cfg

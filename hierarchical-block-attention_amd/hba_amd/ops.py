@@ -423,7 +423,10 @@ def kv_append(k_new: Tensor, v_new: Tensor, k_gain: Optional[Tensor], eps: float
 def summarize_pages(kc_pages: Tensor, pages: Tensor, probes: Tensor, proj: Tensor,
                     summ_pages: Tensor) -> None:
     dev = _dev(kc_pages)
-    P, Hkv, Bk, d = kc_pages.shape
+    P, Hkv = kc_pages.shape[:2]
+    Bk, d = BLOCK, probes.shape[-1]
+    if kc_pages[0, 0].numel() != Bk * d:
+        raise ValueError(f"kc_pages: expected {Bk * d} elements per page and KV head")
     m = probes.shape[1]
     pr = _f32c(probes, dev, Hkv * m * d, "probes")
     pj = _f32c(proj, dev, Hkv * d * d, "proj")
@@ -439,6 +442,24 @@ def decode_workspace_bytes(Bd, Hq, Hkv, d, k, window, max_len):
     check(lib().hba_decode_workspace_size(Bd, Hq, Hkv, d, k, BLOCK, window, max_len, ctypes.byref(n)),
           "hba_decode_workspace_size")
     return int(n.value)
+
+
+_DECODE_WS = {}   # device index -> the decode workspace (uint8, zero-filled when allocated)
+
+
+def _decode_workspace(dev, nbytes):
+    """The decode step's workspace on `dev`, one per device, grown on demand.
+    It is allocated zero-filled: it opens with completion counters that must
+    be zero before a step and that every step leaves zero.  Decode steps that
+    overlap on one device (two streams) race on it."""
+    ws = _DECODE_WS.get(dev.index)
+    if ws is None or ws.numel() < nbytes:
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("hba decode: the workspace would be allocated under graph capture; run one "
+                               "decode step of this size on the device before capturing")
+        ws = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+        _DECODE_WS[dev.index] = ws
+    return ws
 
 
 @torch.library.custom_op("hba::decode_fwd", mutates_args=(), device_types="cuda")
@@ -457,7 +478,7 @@ def decode_fwd(q: Tensor, q_gain: Optional[Tensor], eps: float, kc_pages: Tensor
     sel_idx = torch.empty(Bd, Hkv, k, dtype=torch.int32, device=dev)
     sel_cnt = torch.empty(Bd, Hkv, dtype=torch.int32, device=dev)
     nbytes = decode_workspace_bytes(Bd, Hq, Hkv, d, k, window, max_len)
-    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    ws = _decode_workspace(dev, nbytes)
     with torch.cuda.device(dev):
         st = lib().hba_decode_fwd(_code(q), _p(q), _p(qg), eps, _p(kc_pages), _p(kr_pages), _p(v_pages),
                                   _p(summ_pages), _p(page_table), page_table.shape[1], _p(seq_lens), _p(cos),

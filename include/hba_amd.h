@@ -195,13 +195,19 @@ int hba_attn_routed_fwd(const void *q, const int64_t q_strides[3],
                         void *out, const int64_t out_strides[3], void *stream);
 
 /*
- * Paged KV cache (decode).  Page = Bk tokens of one sequence; all tensors
- * page-major:  kc_pages [P, Hkv, Bk, d] (QKNorm'd NoPE keys), kr_pages
- * [P, Hkv, Bk, d] (the same keys rotated at their own positions: hba_prep_keys'
- * kr), v_pages [P, Hkv, d, Bk] (values, d-major within a page), summ_pages
- * [P, Hkv, m, d] (slot summaries of full pages);
+ * Paged KV cache (decode).  Page = Bk = 64 tokens of one sequence; all
+ * tensors page-major:  kc_pages [P, Hkv, 64*d] (QKNorm'd NoPE keys), kr_pages
+ * [P, Hkv, 64*d] (the same keys rotated at their own positions: hba_prep_keys'
+ * kr), v_pages [P, Hkv, 64*d] (values), summ_pages [P, Hkv, m, d] (slot
+ * summaries of full pages);
  * page_table int32 [Bd, max_pages] (logical page -> physical page);
  * seq_lens int32 [Bd] (tokens already in the cache, including the current one).
+ * Within a page and KV head, token j's element t lies at
+ *   keys:   ((mt * (d/32) + t/32) * 64 + l16 + 16 * ((t%32)/8)) * 8 + t%8,
+ *           mt = 2*(j/32) + (j/4)%2, l16 = 4*((j%32)/8) + j%4;
+ *   values: (((t/16) * 2 + j/32) * 64 + t%16 + 16 * ((j%32)/8)) * 8 + j%8,
+ * the order in which the decode kernel's MFMA tiles read them (each operand
+ * load of a wave is one contiguous 1 KB run).
  * There is no reference function for these: the decode step is defined as row
  * L-1 of hba_attention_eval (src/hba/attention.py:610-713) for a sequence of
  * length L.
@@ -229,7 +235,13 @@ int hba_summarize_pages(int dtype, const void *kc_pages, const int32_t *pages,
                         const float *probes, const float *proj, int64_t m,
                         void *summ_pages, void *stream);
 
-/* Scratch bytes hba_decode_fwd needs for these sizes (max_len = max seq_len). */
+/*
+ * Scratch bytes hba_decode_fwd needs for these sizes (max_len = max seq_len).
+ * The workspace must be zero-filled before its first call: it opens with
+ * per-(sequence, KV head) completion counters of the one-launch bf16 step,
+ * which every call leaves zero again, so a workspace is reused as is by later
+ * calls on the same stream (calls that overlap on it race).
+ */
 int hba_decode_workspace_size(int64_t Bd, int64_t Hq, int64_t Hkv, int64_t d, int64_t k,
                               int64_t Bk, int64_t W, int64_t max_len, size_t *bytes);
 

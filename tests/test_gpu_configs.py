@@ -224,14 +224,14 @@ def test_decode_d128_continuation_over_a_page_boundary(dev):
             pos = cache.lens[s] - 1
             page = cache._table[s][pos // 64]
             want = O.qknorm(f(kn)[s], gk, 1e-6, "bf16")
-            assert np.array_equal(f(cache.kc_pages[page, :, pos % 64]), want), (step, s)
+            assert np.array_equal(f(cache.key_rows(page)[:, pos % 64]), want), (step, s)
             rot = O.apply_rope(want[None], f(cos), f(sin), "bf16", positions=np.array([pos]))[0]
-            assert np.array_equal(f(cache.kr_pages[page, :, pos % 64]), rot), (step, s)
-            assert np.array_equal(f(cache.v_pages[page, :, :, pos % 64]), f(vn)[s]), (step, s)
+            assert np.array_equal(f(cache.key_rows(page, rotated=True)[:, pos % 64]), rot), (step, s)
+            assert np.array_equal(f(cache.value_rows(page)[:, pos % 64]), f(vn)[s]), (step, s)
             kcs[s] = np.concatenate([kcs[s], want[None]], 0)
             vs[s] = np.concatenate([vs[s], f(vn)[s][None]], 0)
             if cache.lens[s] % 64 == 0:            # the page just filled: its summary
-                kpage = f(cache.kc_pages[page]).transpose(1, 0, 2)
+                kpage = f(cache.key_rows(page)).transpose(1, 0, 2)
                 sref = O.summarize(kpage, f(prm.probes), f(prm.proj), 64)[:, 0]
                 assert np.abs(f(cache.summ_pages[page]) - sref).max() <= 2 ** -7 * max(1, np.abs(sref).max())
                 filled += 1

@@ -675,10 +675,10 @@ def test_kv_append_and_page_summaries(dev):
     for s, pos in enumerate([127, 60]):
         page = cache._table[s][pos // 64]
         want = O.qknorm(f(kn)[s], f(x["k_gain"]), 1e-6, "bf16")
-        assert np.array_equal(f(cache.kc_pages[page, :, pos % 64]), want)
+        assert np.array_equal(f(cache.key_rows(page)[:, pos % 64]), want)
         rot = O.apply_rope(want[None], f(cos), f(sin), "bf16", positions=np.array([pos]))[0]
-        assert np.array_equal(f(cache.kr_pages[page, :, pos % 64]), rot)
-        assert np.array_equal(f(cache.v_pages[page, :, :, pos % 64]), f(vn)[s])
+        assert np.array_equal(f(cache.key_rows(page, rotated=True)[:, pos % 64]), rot)
+        assert np.array_equal(f(cache.value_rows(page)[:, pos % 64]), f(vn)[s])
         kcs[s] = torch.cat([kcs[s], torch.from_numpy(want)[None].to(kcs[s])], 0)
     # a decode step after the append sees the appended token (keys, rotation, value)
     qd = torch.randn(2, 14, 64, generator=g).to(torch.bfloat16).to(dev)
@@ -690,6 +690,6 @@ def test_kv_append_and_page_summaries(dev):
         assert np.abs(f(out[s]) - ref).max() <= TOL["bf16"], s
     # the page that just filled (sequence 0, tokens 64..127) got its summary
     full = cache._table[0][127 // 64]
-    kpage = f(cache.kc_pages[full]).transpose(1, 0, 2)                    # [64, Hkv, d]
+    kpage = f(cache.key_rows(full)).transpose(1, 0, 2)                    # [64, Hkv, d]
     sref = O.summarize(kpage, f(x["probes"]), f(x["proj"]), 64)[:, 0]
     assert np.abs(f(cache.summ_pages[full]) - sref).max() <= 2 ** -7 * max(1, np.abs(sref).max())
