@@ -1278,13 +1278,51 @@ __global__ __launch_bounds__(256) void bwd_dkv_fin_kernel(
 
 using namespace hba;
 
+// Workspace of hba_attn_bwd: the query rows in the storage type (QKNorm'd,
+// rotated), LSE and D per (head, row), the fp32 sink accumulators
+// [B, Hkv, 2, 64, d]; on the bf16 path also the transposed keys kct, krt
+// [B, Hkv, d, n] and the fp32 dk / dv accumulators [B, Hkv, n, 3, d].
+namespace {
+struct BwdWs {
+    size_t qc, qr, lse, dd, sink, kct, krt, dkv, total;
+};
+size_t bw_align(size_t x) { return (x + 255) & ~(size_t)255; }
+BwdWs bwd_ws_layout(int dtype, int64_t B, int64_t n, int64_t Hq, int64_t Hkv, int64_t d) {
+    BwdWs L{};
+    size_t o = 0;
+    auto take = [&](size_t bytes) {
+        const size_t r = o;
+        o = bw_align(o + bytes);
+        return r;
+    };
+    const size_t qe = dtype == HBA_DTYPE_BF16 ? 2 : 4;
+    L.qc = take((size_t)(B * n * Hq * d) * qe);
+    L.qr = take((size_t)(B * n * Hq * d) * qe);
+    L.lse = take((size_t)(B * Hq * n) * 4);
+    L.dd = take((size_t)(B * Hq * n) * 4);
+    L.sink = take((size_t)(B * Hkv * 2 * 64 * d) * 4);
+    if (dtype == HBA_DTYPE_BF16) {
+        L.kct = take((size_t)(B * Hkv * d * n) * 2);
+        L.krt = take((size_t)(B * Hkv * d * n) * 2);
+        L.dkv = take((size_t)(B * Hkv * n * 3 * d) * 4);
+    }
+    L.total = o;
+    return L;
+}
+}  // namespace
+
+extern "C" int hba_attn_bwd_workspace_bytes(int dtype, int64_t B, int64_t n, int64_t Hq, int64_t Hkv, int64_t d,
+                                            size_t *bytes) {
+    if (!bytes || B <= 0 || n <= 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv || d <= 0) return HBA_ERR_INVALID_ARG;
+    if (dtype != HBA_DTYPE_F32 && dtype != HBA_DTYPE_BF16) return HBA_ERR_UNSUPPORTED;
+    *bytes = bwd_ws_layout(dtype, B, n, Hq, Hkv, d).total;
+    return HBA_OK;
+}
+
 extern "C" int hba_attn_bwd_workspace_size(int64_t B, int64_t n, int64_t Hq, int64_t d, size_t *bytes) {
     if (!bytes || B <= 0 || n <= 0 || Hq <= 0 || d <= 0) return HBA_ERR_INVALID_ARG;
-    // fp32: query rows (2), LSE and D, sink accumulators; bf16: transposed keys
-    // (2); fp32: the dk / dv accumulators of the MFMA path (Hkv <= Hq bounds
-    // the KV-head dimension of the last three)
-    *bytes = (size_t)(2 * B * n * Hq * d + 2 * B * Hq * n + B * Hq * 2 * 64 * d) * 4 + (size_t)(2 * B * Hq * n * d) * 2 +
-             (size_t)(B * Hq * n * 3 * d) * 4;
+    // an upper bound for either dtype and any Hkv <= Hq
+    *bytes = bwd_ws_layout(HBA_DTYPE_BF16, B, n, Hq, Hq, d).total + (size_t)(2 * B * n * Hq * d) * 2;
     return HBA_OK;
 }
 
@@ -1306,19 +1344,19 @@ extern "C" int hba_attn_bwd(int dtype, const void *q, const void *k, const void 
     if (Hq / Hkv > bw::BW_GMAX) return HBA_ERR_UNSUPPORTED;
     if (B * Hkv * n > 0x7fffffffLL * 4 || B * Hkv * (n / 64) > 0x7fffffffLL || n > 0x7fffffffLL)
         return HBA_ERR_UNSUPPORTED;
-    size_t need = 0;
-    hba_attn_bwd_workspace_size(B, n, Hq, d, &need);
-    if (ws_bytes < need || !abi::aligned16(workspace)) return HBA_ERR_INVALID_ARG;
-    float *qc_ws = (float *)workspace;
-    float *qr_ws = qc_ws + B * n * Hq * d;
-    bf16_t *qcb_ws = reinterpret_cast<bf16_t *>(qc_ws);            // the bf16 path's query rows (half the room)
-    bf16_t *qrb_ws = reinterpret_cast<bf16_t *>(qr_ws);
-    float *lse_ws = qr_ws + B * n * Hq * d;
-    float *dd_ws = lse_ws + B * Hq * n;
-    float *sink_acc = dd_ws + B * Hq * n;                          // [B, Hkv, 2, 64, d] (Hkv <= Hq)
-    bf16_t *kct = reinterpret_cast<bf16_t *>(sink_acc + B * Hq * 2 * 64 * d);   // [B, Hkv, d, n] (bf16 path)
-    bf16_t *krt = kct + B * Hkv * d * n;
-    float *dkv_acc = reinterpret_cast<float *>(kct + 2 * B * Hq * n * d);   // [B, Hkv, n, 3, d] (bf16 path)
+    const BwdWs L = bwd_ws_layout(dtype, B, n, Hq, Hkv, d);
+    if (ws_bytes < L.total || !abi::aligned16(workspace)) return HBA_ERR_INVALID_ARG;
+    char *wsb = (char *)workspace;
+    float *qc_ws = (float *)(wsb + L.qc);                          // fp32 path's query rows
+    float *qr_ws = (float *)(wsb + L.qr);
+    bf16_t *qcb_ws = (bf16_t *)(wsb + L.qc);                       // bf16 path's query rows
+    bf16_t *qrb_ws = (bf16_t *)(wsb + L.qr);
+    float *lse_ws = (float *)(wsb + L.lse);
+    float *dd_ws = (float *)(wsb + L.dd);
+    float *sink_acc = (float *)(wsb + L.sink);                     // [B, Hkv, 2, 64, d]
+    bf16_t *kct = (bf16_t *)(wsb + L.kct);                         // [B, Hkv, d, n] (bf16 path)
+    bf16_t *krt = (bf16_t *)(wsb + L.krt);
+    float *dkv_acc = (float *)(wsb + L.dkv);                       // [B, Hkv, n, 3, d] (bf16 path)
     hipStream_t s = (hipStream_t)stream;
     const int64_t nwaves = B * Hkv * n;
     const int64_t g1 = (nwaves + 3) / 4;

@@ -40,6 +40,7 @@ SIGNATURES = {
     "hba_attn_bwd": [_i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _f, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64,
                      _i64, _i64, _i64, _i64, _i64, _i64, _f, _vp, ctypes.c_size_t, _vp, _vp, _vp, _vp, _vp, _vp],
     "hba_attn_bwd_workspace_size": [_i64, _i64, _i64, _i64, ctypes.POINTER(ctypes.c_size_t)],
+    "hba_attn_bwd_workspace_bytes": [_i, _i64, _i64, _i64, _i64, _i64, ctypes.POINTER(ctypes.c_size_t)],
     "hba_kv_append": [_i, _vp, _vp, _vp, _f, _vp, _vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i64,
                       _vp, _vp, _vp, _vp],
     "hba_summarize_pages": [_i, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _vp],

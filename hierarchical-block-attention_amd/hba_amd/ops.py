@@ -384,7 +384,8 @@ def attn_bwd(q: Tensor, k: Tensor, v: Tensor, kc: Tensor, kr: Tensor, q_gain: Op
     dqg = torch.zeros(Hq, dtype=torch.float32, device=dev)
     dkg = torch.zeros(Hkv, dtype=torch.float32, device=dev)
     nbytes = ctypes.c_size_t(0)
-    check(lib().hba_attn_bwd_workspace_size(B, n, Hq, d, ctypes.byref(nbytes)), "hba_attn_bwd_workspace_size")
+    check(lib().hba_attn_bwd_workspace_bytes(_code(q), B, n, Hq, Hkv, d, ctypes.byref(nbytes)),
+          "hba_attn_bwd_workspace_bytes")
     ws = torch.empty(max(int(nbytes.value), 16), dtype=torch.uint8, device=dev)
     with torch.cuda.device(dev):
         st = lib().hba_attn_bwd(_code(q), _p(q), _p(k), _p(v), _p(kc), _p(kr), _p(qg), _p(kg), eps, _p(cos),

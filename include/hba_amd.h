@@ -315,12 +315,17 @@ int hba_attn_bwd(int dtype, const void *q, const void *k, const void *v,
                  void *workspace, size_t ws_bytes,
                  void *dq, void *dk, void *dv, float *dq_gain, float *dk_gain, void *stream);
 
-/* Scratch bytes hba_attn_bwd needs: the QKNorm'd and rotated query rows
- * (2*B*n*Hq*d fp32), the per-row LSE and <dout, out> (2*B*Hq*n fp32), the
- * sink-key accumulators (2*B*Hq*64*d fp32), the transposed prepared keys
- * (2*B*Hq*n*d bf16) and the dk/dv accumulators (3*B*Hq*n*d fp32); the last
- * two are used by the bf16 path only.  Hq bounds the KV-head count of the
- * last three. */
+/* Scratch bytes hba_attn_bwd needs for this dtype and Hkv: the QKNorm'd and
+ * rotated query rows (2*B*n*Hq*d in the storage type), the per-row LSE and
+ * <dout, out> (2*B*Hq*n fp32), the sink-key accumulators (2*B*Hkv*64*d
+ * fp32); on the bf16 path also the transposed prepared keys (2*B*Hkv*n*d
+ * bf16) and the dk/dv accumulators (3*B*Hkv*n*d fp32); each part rounded up
+ * to 256 bytes. */
+int hba_attn_bwd_workspace_bytes(int dtype, int64_t B, int64_t n, int64_t Hq, int64_t Hkv,
+                                 int64_t d, size_t *bytes);
+
+/* An upper bound of hba_attn_bwd_workspace_bytes over both dtypes and every
+ * Hkv <= Hq (for callers that size one workspace for any call). */
 int hba_attn_bwd_workspace_size(int64_t B, int64_t n, int64_t Hq, int64_t d, size_t *bytes);
 
 #ifdef __cplusplus

@@ -40,6 +40,27 @@ def test_static_queries_without_a_gpu():
     assert L.hba_decode_workspace_size(32, 14, 2, 64, 16, 32, 1024, 32768, ctypes.byref(n)) == -2
 
 
+def test_backward_workspace_is_sized_by_dtype_and_kv_heads():
+    """bf16 at 32K, 14/2 heads, d = 64: bf16 query rows (2 x n*Hq*d), LSE and
+    D (2 x Hq*n fp32), sink accumulators (2*Hkv*64*d fp32), transposed keys
+    (2 x Hkv*d*n bf16), dk/dv accumulators (3*Hkv*n*d fp32), each rounded up
+    to 256 bytes; within the all-dtype bound of hba_attn_bwd_workspace_size."""
+    L = _lib.lib()
+    B, n, Hq, Hkv, d = 1, 32768, 14, 2, 64
+    r = lambda x: (x + 255) // 256 * 256
+    want = (2 * r(n * Hq * d * 2) + 2 * r(Hq * n * 4) + r(Hkv * 2 * 64 * d * 4) + 2 * r(Hkv * d * n * 2)
+            + r(Hkv * n * 3 * d * 4))
+    got, bound = ctypes.c_size_t(0), ctypes.c_size_t(0)
+    assert L.hba_attn_bwd_workspace_bytes(1, B, n, Hq, Hkv, d, ctypes.byref(got)) == 0
+    assert got.value == want
+    assert L.hba_attn_bwd_workspace_size(B, n, Hq, d, ctypes.byref(bound)) == 0
+    assert got.value < bound.value
+    f32 = ctypes.c_size_t(0)
+    assert L.hba_attn_bwd_workspace_bytes(0, B, n, Hq, Hkv, d, ctypes.byref(f32)) == 0
+    assert f32.value == 2 * r(n * Hq * d * 4) + 2 * r(Hq * n * 4) + r(Hkv * 2 * 64 * d * 4) <= bound.value
+    assert L.hba_attn_bwd_workspace_bytes(1, B, n, Hq, 3, d, ctypes.byref(got)) == -1   # Hq % Hkv
+
+
 def test_ops_refuse_cpu_tensors():
     import torch
     q = torch.zeros(1, 64, 2, 64)

@@ -473,9 +473,23 @@ def test_equiv_rejects_ragged_length(dev):
 
 # -------------------------------------------------------------- backward -----
 # gates.py:247 holds input gradients to 2e-3 relative to their magnitude
-# (fp32); bf16 storage of q/k/v and of the forward's QKNorm/RoPE rows moves
-# the recomputed probabilities by about one bf16 ulp, hence 5e-2 there.
-GRAD_TOL = {"f32": 2e-3, "bf16": 5e-2}
+# (fp32).  bf16 storage of q/k/v and of the forward's QKNorm/RoPE rows moves
+# the recomputed probabilities by about one bf16 ulp.  Measured maxima over
+# the bf16 cases below (relative to each gradient's largest magnitude):
+# dq 7.7e-3, dk 5.8e-3, dv 4.1e-3; the gain gradients, sums over every row
+# and element of a head, 2.7e-2.  The bf16 gates are about twice those.
+GRAD_TOL = {"f32": {"dq": 2e-3, "dk": 2e-3, "dv": 2e-3, "gain": 2e-3},
+            "bf16": {"dq": 1.5e-2, "dk": 1.2e-2, "dv": 1e-2, "gain": 5.5e-2}}
+
+
+def check_grads(case, dt, got, ref):
+    """Relative max errors of dq, dk, dv (and the gain gradients) against the
+    oracle, printed (pytest -s) and held to GRAD_TOL."""
+    rel = {name: np.abs(a - b).max() / max(np.abs(b).max(), 1e-6)
+           for name, a, b in zip(["dq", "dk", "dv", "dq_gain", "dk_gain"], got, ref)}
+    print(case, {k: f"{v:.2e}" for k, v in rel.items()})
+    for name, e in rel.items():
+        assert e < GRAD_TOL[dt][name.split("_")[-1] if "_" in name else name], (case, name, e)
 
 
 @pytest.mark.parametrize("dt,qknorm,mode", [("f32", True, "dense"), ("f32", False, "eval"), ("bf16", True, "eval"),
@@ -517,9 +531,7 @@ def test_backward_matches_oracle(dev, dt, qknorm, mode):
     got = [f(q.grad)[0], f(k.grad)[0], f(v.grad)[0]]
     if qknorm:
         got += [f(gq.grad), f(gk.grad)]
-    for name, a, b in zip(["dq", "dk", "dv", "dq_gain", "dk_gain"], got, ref):
-        rel = np.abs(a - b).max() / max(np.abs(b).max(), 1e-6)
-        assert rel < GRAD_TOL[dt], (name, rel)
+    check_grads(f"{dt}-{qknorm}-{mode}", dt, got, ref)
 
 
 def test_backward_row_ranges_matches_oracle(dev):
@@ -544,9 +556,7 @@ def test_backward_row_ranges_matches_oracle(dev):
     ref = O.union_backward(f(x["q"])[0], f(x["k"])[0], f(x["v"])[0], f(cos), f(sin), scale, f(x["q_gain"]),
                            f(x["k_gain"]), 1e-6, idx, cnt, f(dout)[0], cfg.sinks, cfg.window, 64, True)
     got = [f(q.grad)[0], f(k.grad)[0], f(v.grad)[0], f(gq.grad), f(gk.grad)]
-    for name, a, b in zip(["dq", "dk", "dv", "dq_gain", "dk_gain"], got, ref):
-        rel = np.abs(a - b).max() / max(np.abs(b).max(), 1e-6)
-        assert rel < GRAD_TOL["bf16"], (name, rel)
+    check_grads("bf16", "bf16", got, ref)
 
 
 @pytest.mark.parametrize("Hq,Hkv,k,d", [(8, 2, 4, 64), (10, 2, 8, 64), (16, 1, 4, 64), (7, 1, 4, 128),
@@ -572,9 +582,62 @@ def test_backward_group_sizes_match_oracle(dev, Hq, Hkv, k, d):
     ref = O.union_backward(f(x["q"])[0], f(x["k"])[0], f(x["v"])[0], f(cos), f(sin), scale, f(x["q_gain"]),
                            f(x["k_gain"]), 1e-6, idx, cnt, f(dout)[0], cfg.sinks, cfg.window, 64, True)
     got = [f(q.grad)[0], f(k_.grad)[0], f(v.grad)[0], f(gq.grad), f(gk.grad)]
-    for name, a, b in zip(["dq", "dk", "dv", "dq_gain", "dk_gain"], got, ref):
-        rel = np.abs(a - b).max() / max(np.abs(b).max(), 1e-6)
-        assert rel < GRAD_TOL["bf16"], (name, rel)
+    check_grads("bf16", "bf16", got, ref)
+
+
+@pytest.mark.parametrize("case", ["B2", "S0", "S64", "equiv"])
+def test_backward_bf16_cases(dev, case):
+    """bf16 backward with two batch rows (the per-batch indexing of every
+    backward kernel), without sinks (the sink launch skipped), with a full
+    64-key sink block, and in equiv mode (W = n: every page staged).  The
+    relative errors are printed per gradient (pytest -s)."""
+    n, B, S, W, equiv = 512, 1, 4, 128, False
+    if case == "B2":
+        B = 2
+    elif case == "S0":
+        S = 0
+    elif case == "S64":
+        S = 64
+    else:
+        equiv = True
+    cfg, x, prm, cos, sin = make(dev, "bf16", n=n, B=B, W=W, k=4, S=S, needles=True, aux_w=0.0)
+    q, k, v = (x[t].clone().requires_grad_(True) for t in ("q", "k", "v"))
+    gq = x["q_gain"].clone().requires_grad_(True)
+    gk = x["k_gain"].clone().requires_grad_(True)
+    qkn = synth.Params(gq, gk, x["probes"], x["proj"])
+    out = hba_amd.hba_attention_eval(q, k, v, cos, sin, cfg, qkn, qkn, None, equiv=equiv)
+    dout = torch.randn(out.shape, generator=torch.Generator().manual_seed(13)).to(out.dtype).to(dev)
+    out.backward(dout)
+    torch.cuda.synchronize()
+    scale = hba_amd.union_scale(cfg, cfg.head_dim, n)
+    if not equiv:
+        with torch.no_grad():
+            r = hba_amd.forward_stages(x["q"], x["k"], x["v"], cos, sin, cfg, qkn, qkn)
+            assert torch.equal(r["out"], out.detach())
+    grads = {"dq": 0.0, "dk": 0.0, "dv": 0.0}
+    refs = {"dq": 0.0, "dk": 0.0, "dv": 0.0}
+    gain_ref = [np.zeros(cfg.n_heads), np.zeros(cfg.n_kv)]
+    for b in range(B):
+        if equiv:
+            idx = np.zeros((cfg.n_kv, n, 1), dtype=np.int32)
+            cnt = np.zeros((cfg.n_kv, n), dtype=np.int32)
+            Sb, Wb = 0, n
+        else:
+            idx, cnt = r["idx"][b].cpu().numpy(), r["cnt"][b].cpu().numpy()
+            Sb, Wb = S, W
+        ref = O.union_backward(f(x["q"])[b], f(x["k"])[b], f(x["v"])[b], f(cos), f(sin), scale, f(x["q_gain"]),
+                               f(x["k_gain"]), 1e-6, idx, cnt, f(dout)[b], Sb, Wb, 64, True)
+        for name, a, rb in zip(["dq", "dk", "dv"], [f(q.grad)[b], f(k.grad)[b], f(v.grad)[b]], ref[:3]):
+            grads[name] = max(grads[name], np.abs(a - rb).max())
+            refs[name] = max(refs[name], np.abs(rb).max())
+        gain_ref[0] = gain_ref[0] + ref[3]
+        gain_ref[1] = gain_ref[1] + ref[4]
+    rel = {name: grads[name] / max(refs[name], 1e-6) for name in grads}
+    for name, a, rb in (("dq_gain", f(gq.grad), gain_ref[0]), ("dk_gain", f(gk.grad), gain_ref[1])):
+        rel[name] = np.abs(a - rb).max() / max(np.abs(rb).max(), 1e-6)
+    print(case, {k_: f"{v_:.2e}" for k_, v_ in rel.items()})
+    for name, e in rel.items():
+        assert e < GRAD_TOL["bf16"][name.split("_")[-1] if "_" in name else name], (case, name, e)
 
 
 def test_backward_no_grad_inputs_stays_forward_only(dev):
