@@ -465,8 +465,11 @@ def bench_hier128k(dev):
 def bench_donor(dev, steps=64):
     """Donor-shaped layer: B=2, n=65536, 28/4 heads, d=128, 8 sinks, window
     1024, top-16, bf16, N(0,1) inputs from a seed: the prefill forward (stages
-    timed), then a 64-step batched decode continuation from that cache, each
-    step appending one new token per sequence and decoding its query."""
+    timed), then a batched decode continuation from that cache, each token
+    appending one new key/value per sequence and decoding its query: `steps`
+    tokens through cache.append + hba_decode_step, then `steps` through a
+    DecodeLoop (two launches per token straight through the C-ABI), then
+    `steps` replayed from a DecodeLoop's HIP graph."""
     import torch
     import hba_amd
     from hba_amd import ops, synth
@@ -476,7 +479,7 @@ def bench_donor(dev, steps=64):
     x = synth.layer_inputs(B, n, Hq, Hkv, d, m=m, dtype=torch.bfloat16, device=dev, seed=0, sharp=True,
                            needles=False, window=W)
     prm = synth.Params(x["q_gain"], x["k_gain"], x["probes"], x["proj"])
-    Lmax = n + steps
+    Lmax = n + 3 * steps + 3
     cos, sin = hba_amd.rope_tables(Lmax, d, cfg.rope_theta, dev)
     scale = union_scale(cfg, d, n)
     t_prep, (kc, kr, vt) = _timed(lambda: ops.prep_keys(x["k"], x["v"], prm.k.gain, 1e-6, cos, sin), reps=3)
@@ -496,6 +499,8 @@ def bench_donor(dev, steps=64):
     qs = torch.randn(steps, B, Hq, d, generator=g).to(torch.bfloat16).to(dev)
     ks = torch.randn(steps, B, Hkv, d, generator=g).to(torch.bfloat16).to(dev)
     vs = torch.randn(steps, B, Hkv, d, generator=g).to(torch.bfloat16).to(dev)
+    cache.append(ks[0], vs[0], prm, prm, cos, sin)          # first calls of the ops, one token
+    hba_amd.hba_decode_step(qs[0], cache, cfg, prm, cos, sin)
     torch.cuda.synchronize()
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
     t0 = torch.cuda.Event(enable_timing=True)
@@ -509,6 +514,19 @@ def bench_donor(dev, steps=64):
     t1.record()
     torch.cuda.synchronize()
     step_us = sorted(a.elapsed_time(b) * 1000.0 for a, b in ev)
+    loop_us = {}
+    for mode in ("direct", "graph"):
+        lp = hba_amd.DecodeLoop(cache, cfg, prm, prm, cos, sin, graph=(mode == "graph"))
+        lp.step(qs[0], ks[0], vs[0])                    # first call (graph upload), one token
+        torch.cuda.synchronize()
+        t2 = torch.cuda.Event(enable_timing=True)
+        t3 = torch.cuda.Event(enable_timing=True)
+        t2.record()
+        for st in range(steps):
+            lp.step(qs[st], ks[st], vs[st])
+        t3.record()
+        torch.cuda.synchronize()
+        loop_us[mode] = round(t2.elapsed_time(t3) * 1000.0 / steps, 2)
     return {"metric": "HBA donor-shaped layer: prefill tokens/s; decode continuation us/step",
             "config": {"workload": "hba_layer_fwd_donor_64k_d128", "batch": B, "seq_len": n, "q_heads": Hq,
                        "kv_heads": Hkv, "head_dim": d, "sinks": S, "window": W, "top_k": k, "decode_steps": steps},
@@ -519,7 +537,8 @@ def bench_donor(dev, steps=64):
             "decode": {"step_us_median": round(step_us[len(step_us) // 2], 2),
                        "step_us_min": round(step_us[0], 2),
                        "append_plus_step_us": round(t0.elapsed_time(t1) * 1000.0 / steps, 2),
-                       "lengths": [n + 1, n + steps]}}
+                       "loop_token_us": loop_us["direct"], "loop_graph_token_us": loop_us["graph"],
+                       "lengths": [n + 1, n + 3 * steps + 3]}}
 
 
 def main():

@@ -44,6 +44,9 @@ SIGNATURES = {
     "hba_kv_append": [_i, _vp, _vp, _vp, _f, _vp, _vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i64,
                       _vp, _vp, _vp, _vp],
     "hba_summarize_pages": [_i, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _vp],
+    "hba_kv_append_advance": [_i, _vp, _vp, _vp, _f, _vp, _vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i64,
+                              _vp, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp],
+    "hba_summarize_filled": [_i, _vp, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _vp],
     "hba_decode_workspace_size": [_i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                                   ctypes.POINTER(ctypes.c_size_t)],
     "hba_decode_fwd": [_i, _vp, _vp, _f, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _i64,

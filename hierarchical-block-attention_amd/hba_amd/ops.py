@@ -13,7 +13,10 @@ device.
     hba::attn_fwd         union attention forward (prefill)
     hba::attn_bwd         union attention backward (dq, dk, dv, QKNorm gain grads)
     hba::kv_append        paged-cache append (mutates the pages)
+    hba::kv_append_advance  the decode loop's append: token, filled-page summary,
+                          seq_lens += 1 and the new length's scale, one launch
     hba::summarize_pages  summaries of listed pages (mutates summ_pages)
+    hba::summarize_filled summaries of the pages the last append filled (mutates summ_pages)
     hba::decode_fwd       decode step over the paged cache
 """
 import ctypes
@@ -420,6 +423,37 @@ def kv_append(k_new: Tensor, v_new: Tensor, k_gain: Optional[Tensor], eps: float
     check(st, "hba_kv_append")
 
 
+@torch.library.custom_op("hba::kv_append_advance", mutates_args=("seq_lens", "kc_pages", "kr_pages", "v_pages",
+                                                               "summ_pages", "scales"), device_types="cuda")
+def kv_append_advance(k_new: Tensor, v_new: Tensor, k_gain: Optional[Tensor], eps: float, cos: Tensor,
+                      sin: Tensor, page_table: Tensor, seq_lens: Tensor, kc_pages: Tensor, kr_pages: Tensor,
+                      v_pages: Tensor, probes: Tensor, proj: Tensor, summ_pages: Tensor, scale_tab: Tensor,
+                      scales: Tensor) -> None:
+    """Append one token per sequence at position seq_lens[s], summarise a page
+    it fills, then seq_lens += 1 and scales[s] = scale_tab[seq_lens[s]], all on
+    the device (one launch)."""
+    dev = _dev(k_new)
+    Bd, Hkv, d = k_new.shape
+    kg = _f32c(k_gain, dev, Hkv, "k_gain")
+    cos, sin = _tables(cos, sin, 1, d, dev)
+    m = probes.shape[1]
+    pr = _f32c(probes, dev, Hkv * m * d, "probes")
+    pj = _f32c(proj, dev, Hkv * d * d, "proj")
+    for t, what, dt in ((page_table, "page_table", torch.int32), (seq_lens, "seq_lens", torch.int32),
+                        (scale_tab, "scale_tab", torch.float32), (scales, "scales", torch.float32)):
+        if t.dtype != dt or not t.is_contiguous() or t.device != dev:
+            raise ValueError(f"{what} must be a contiguous {dt} tensor on {dev}")
+    if seq_lens.numel() != Bd or scales.numel() != Bd:
+        raise ValueError(f"seq_lens and scales must hold {Bd} entries")
+    with torch.cuda.device(dev):
+        st = lib().hba_kv_append_advance(_code(k_new), _p(k_new.contiguous()), _p(v_new.contiguous()), _p(kg), eps,
+                                         _p(cos), _p(sin), cos.shape[0], _p(page_table), page_table.shape[1],
+                                         _p(seq_lens), Bd, Hkv, d, BLOCK, _p(kc_pages), _p(kr_pages), _p(v_pages),
+                                         _p(pr), _p(pj), m, _p(summ_pages), _p(scale_tab), scale_tab.numel(),
+                                         _p(scales), _stream(dev))
+    check(st, "hba_kv_append_advance")
+
+
 @torch.library.custom_op("hba::summarize_pages", mutates_args=("summ_pages",), device_types="cuda")
 def summarize_pages(kc_pages: Tensor, pages: Tensor, probes: Tensor, proj: Tensor,
                     summ_pages: Tensor) -> None:
@@ -436,6 +470,29 @@ def summarize_pages(kc_pages: Tensor, pages: Tensor, probes: Tensor, proj: Tenso
         st = lib().hba_summarize_pages(_code(kc_pages), _p(kc_pages), _p(pages), pages.numel(), Hkv, d, Bk,
                                        _p(pr), _p(pj), m, _p(summ_pages), _stream(dev))
     check(st, "hba_summarize_pages")
+
+
+@torch.library.custom_op("hba::summarize_filled", mutates_args=("summ_pages",), device_types="cuda")
+def summarize_filled(kc_pages: Tensor, page_table: Tensor, seq_lens: Tensor, probes: Tensor, proj: Tensor,
+                     summ_pages: Tensor) -> None:
+    """Summaries of the pages the last append filled (sequences whose
+    seq_lens is a positive multiple of 64), found on the device."""
+    dev = _dev(kc_pages)
+    Hkv = kc_pages.shape[1]
+    d = probes.shape[-1]
+    if kc_pages[0, 0].numel() != BLOCK * d:
+        raise ValueError(f"kc_pages: expected {BLOCK * d} elements per page and KV head")
+    for t, what in ((page_table, "page_table"), (seq_lens, "seq_lens")):
+        if t.dtype != torch.int32 or not t.is_contiguous() or t.device != dev:
+            raise ValueError(f"{what} must be a contiguous int32 tensor on {dev}")
+    m = probes.shape[1]
+    pr = _f32c(probes, dev, Hkv * m * d, "probes")
+    pj = _f32c(proj, dev, Hkv * d * d, "proj")
+    with torch.cuda.device(dev):
+        st = lib().hba_summarize_filled(_code(kc_pages), _p(kc_pages), _p(page_table), page_table.shape[1],
+                                        _p(seq_lens), seq_lens.numel(), Hkv, d, BLOCK, _p(pr), _p(pj), m,
+                                        _p(summ_pages), _stream(dev))
+    check(st, "hba_summarize_filled")
 
 
 def decode_workspace_bytes(Bd, Hq, Hkv, d, k, window, max_len):

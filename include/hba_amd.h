@@ -227,6 +227,27 @@ int hba_kv_append(int dtype, const void *k_new, const void *v_new, const float *
                   void *kr_pages, void *v_pages, void *stream);
 
 /*
+ * The decode loop's append, one launch: for each sequence s, the token goes
+ * to position pos = seq_lens[s] (QKNorm, rotation and writes as
+ * hba_kv_append); when it fills its page (pos % Bk == Bk-1) that page's slot
+ * summaries are written (as hba_summarize_pages); then seq_lens[s] becomes
+ * pos+1 and, when scales is not NULL, scales[s] = scale_tab[pos+1] (a table
+ * of the step scale by length, n_scale entries, the last one used past its
+ * end).  A position outside the page table or at/after n_tab appends nothing
+ * and leaves seq_lens[s] (scales[s] is still written).  seq_lens is read and
+ * written on the device, so a decode loop of this and hba_decode_fwd needs no
+ * host round trip per token and can be captured in a graph.  No counterpart
+ * in the reference, which has no KV cache.
+ */
+int hba_kv_append_advance(int dtype, const void *k_new, const void *v_new, const float *k_gain,
+                          float eps, const float *cos_tab, const float *sin_tab, int64_t n_tab,
+                          const int32_t *page_table, int64_t max_pages, int32_t *seq_lens,
+                          int64_t Bd, int64_t Hkv, int64_t d, int64_t Bk, void *kc_pages,
+                          void *kr_pages, void *v_pages, const float *probes, const float *proj,
+                          int64_t m, void *summ_pages, const float *scale_tab, int64_t n_scale,
+                          float *scales, void *stream);
+
+/*
  * Slot summaries of the listed physical pages (SlotSummarizer.summarize on
  * one block each): pages int32 [npages]; writes summ_pages[pages[i]].
  */
@@ -234,6 +255,20 @@ int hba_summarize_pages(int dtype, const void *kc_pages, const int32_t *pages,
                         int64_t npages, int64_t Hkv, int64_t d, int64_t Bk,
                         const float *probes, const float *proj, int64_t m,
                         void *summ_pages, void *stream);
+
+/*
+ * Slot summaries of the pages the last append filled, found on the device:
+ * for each sequence s whose seq_lens[s] is a positive multiple of Bk, the
+ * page page_table[s][seq_lens[s]/Bk - 1] (SlotSummarizer.summarize on that
+ * block, src/hba/summarizer.py:34-42); other sequences are left alone.  No
+ * host-side page list, so a decode loop that appends on the device (and a
+ * captured graph of it) needs no host round trip.  No counterpart in the
+ * reference, which has no KV cache.
+ */
+int hba_summarize_filled(int dtype, const void *kc_pages, const int32_t *page_table,
+                         int64_t max_pages, const int32_t *seq_lens, int64_t Bd, int64_t Hkv,
+                         int64_t d, int64_t Bk, const float *probes, const float *proj, int64_t m,
+                         void *summ_pages, void *stream);
 
 /*
  * Scratch bytes hba_decode_fwd needs for these sizes (max_len = max seq_len).

@@ -48,3 +48,26 @@ def test_value_operand_loads_are_contiguous():
                     assert torch.equal(chunk, chunk[0] + torch.arange(8))
                     run.append(int(chunk[0]))
                 assert run == [((dt * 2 + h) * 64) * 8 + 8 * lane for lane in range(64)]
+
+
+def test_scale_table_matches_union_scale():
+    """The cache's per-length scale table (gathered by seq_lens on the device)
+    holds union_scale(cfg, d, max(L, 1)) rounded to fp32 for every L: it is
+    evaluated only past n_cal, where the log-length temperature starts, and the
+    closed form 1/d * (1 + c * log(L / n_cal)) fixes a few entries."""
+    import math
+
+    import hba_amd
+    cfg = hba_amd.HBAConfig(native_ctx=1000, temp_c=0.1)
+    c = hba_amd.PagedKVCache(cfg, 2, 3000, torch.bfloat16, "cpu")
+    tab = c.scale_table()
+    want = torch.tensor([hba_amd.union_scale(cfg, 64, max(L, 1)) for L in range(3001)], dtype=torch.float32)
+    assert tab.shape == (3001,) and torch.equal(tab, want)
+    for L, v in ((0, 1 / 64), (1, 1 / 64), (1000, 1 / 64), (2000, (1 + 0.1 * math.log(2)) / 64),
+                 (3000, (1 + 0.1 * math.log(3)) / 64)):
+        assert tab[L].item() == torch.tensor(v, dtype=torch.float32).item(), L
+    assert c.scale_table() is tab                                # built once per scale setting
+    for other in (hba_amd.HBAConfig(temp_c=0.0), hba_amd.HBAConfig(qknorm=False, head_dim=128)):
+        t2 = c.scale_table(other)
+        assert torch.equal(t2, torch.full((3001,), hba_amd.union_scale(other, other.head_dim, 5),
+                                          dtype=torch.float32))

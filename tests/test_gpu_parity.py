@@ -726,33 +726,106 @@ def test_decode_equals_prefill_last_row(dev):
     assert (out[0].float() - r["out"][0, L - 1].float()).abs().max().item() <= 2e-2
 
 
-def test_kv_append_and_page_summaries(dev):
+@pytest.mark.parametrize("dt,d", [("bf16", 64), ("f32", 64), ("bf16", 128)])
+def test_kv_append_and_page_summaries(dev, dt, d):
+    """cache.append (hba_kv_append_advance, one launch): the appended key
+    (QKNorm), its rotation and the value bit-exact against the oracle, and
+    hba_kv_append writes the same rows; a decode step sees the token; the
+    page the token filled gets the oracle's summary, bit-identical to the
+    page-list summary kernel's; lengths and step scales move on the device."""
     lens = [127, 60]
-    cfg, x, prm, cos, sin, cache, kcs, qn = build_cache(dev, "bf16", lens, W=64, k=4, seed=5)
+    Hq, Hkv = (14, 2) if d == 64 else (28, 4)
+    cfg, x, prm, cos, sin, cache, kcs, qn = build_cache(dev, dt, lens, Hq=Hq, Hkv=Hkv, d=d, W=64, k=4, seed=5)
     g = torch.Generator().manual_seed(3)
-    kn = torch.randn(2, 2, 64, generator=g).to(torch.bfloat16).to(dev)
-    vn = torch.randn(2, 2, 64, generator=g).to(torch.bfloat16).to(dev)
+    kn = torch.randn(2, Hkv, d, generator=g).to(TDT[dt]).to(dev)
+    vn = torch.randn(2, Hkv, d, generator=g).to(TDT[dt]).to(dev)
     cache.append(kn, vn, prm, prm, cos, sin)
     torch.cuda.synchronize()
     assert cache.lens == [128, 61]
+    kc2, kr2, v2 = (torch.zeros_like(t_) for t_ in (cache.kc_pages, cache.kr_pages, cache.v_pages))
+    ops.kv_append(kn, vn, x["k_gain"], 1e-6, cos, sin, cache.page_table, cache.seq_lens, kc2, kr2, v2)
+    rows = lambda t_, page, off: t_[page][:, off].unflatten(-1, (64, d))                  # [Hkv, 64, d]
     for s, pos in enumerate([127, 60]):
         page = cache._table[s][pos // 64]
-        want = O.qknorm(f(kn)[s], f(x["k_gain"]), 1e-6, "bf16")
+        want = O.qknorm(f(kn)[s], f(x["k_gain"]), 1e-6, dt)
         assert np.array_equal(f(cache.key_rows(page)[:, pos % 64]), want)
-        rot = O.apply_rope(want[None], f(cos), f(sin), "bf16", positions=np.array([pos]))[0]
+        rot = O.apply_rope(want[None], f(cos), f(sin), dt, positions=np.array([pos]))[0]
         assert np.array_equal(f(cache.key_rows(page, rotated=True)[:, pos % 64]), rot)
         assert np.array_equal(f(cache.value_rows(page)[:, pos % 64]), f(vn)[s])
+        for a, b, off in ((kc2, cache.kc_pages, cache._koff), (kr2, cache.kr_pages, cache._koff),
+                          (v2, cache.v_pages, cache._voff)):
+            assert torch.equal(rows(a, page, off)[:, pos % 64], rows(b, page, off)[:, pos % 64]), s
         kcs[s] = torch.cat([kcs[s], torch.from_numpy(want)[None].to(kcs[s])], 0)
     # a decode step after the append sees the appended token (keys, rotation, value)
-    qd = torch.randn(2, 14, 64, generator=g).to(torch.bfloat16).to(dev)
+    qd = torch.randn(2, Hq, d, generator=g).to(TDT[dt]).to(dev)
     out, sidx, scnt = hba_amd.hba_decode_step(qd, cache, cfg, prm, cos, sin)
     for s, L in enumerate(cache.lens):
         vseq = np.concatenate([f(x["v"][s, :L - 1]), f(vn)[s][None]], 0)
         ref, _ = O.decode_row(f(qd[s]), f(kcs[s]), vseq, f(cos), f(sin), cfg, cache_summaries(cache, s, L // 64),
-                              f(x["q_gain"]), 1e-6, "bf16", hba_amd.union_scale(cfg, 64, L))
-        assert np.abs(f(out[s]) - ref).max() <= TOL["bf16"], s
+                              f(x["q_gain"]), 1e-6, dt, hba_amd.union_scale(cfg, d, L))
+        assert np.abs(f(out[s]) - ref).max() <= TOL[dt], s
     # the page that just filled (sequence 0, tokens 64..127) got its summary
     full = cache._table[0][127 // 64]
     kpage = f(cache.key_rows(full)).transpose(1, 0, 2)                    # [64, Hkv, d]
     sref = O.summarize(kpage, f(x["probes"]), f(x["proj"]), 64)[:, 0]
     assert np.abs(f(cache.summ_pages[full]) - sref).max() <= 2 ** -7 * max(1, np.abs(sref).max())
+    # the append's in-launch summary equals the page-list summary kernel's
+    again = cache.summ_pages.clone()
+    again[full].zero_()
+    ops.summarize_pages(cache.kc_pages, torch.tensor([full], dtype=torch.int32), x["probes"], x["proj"], again)
+    assert torch.equal(again[full], cache.summ_pages[full])
+    # hba_summarize_filled finds the same page from the page table and lengths
+    summ2 = torch.zeros_like(cache.summ_pages)
+    ops.summarize_filled(cache.kc_pages, cache.page_table, cache.seq_lens, x["probes"], x["proj"], summ2)
+    assert torch.equal(summ2[full], cache.summ_pages[full])
+    others = [p_ for p_ in range(summ2.shape[0]) if p_ != full]
+    assert summ2[others].abs().sum().item() == 0                        # sequence 1 (61 tokens) filled none
+    # and the device lengths / step scales moved with the host mirror
+    assert cache.seq_lens.cpu().tolist() == [128, 61]
+    assert torch.equal(cache._scales, torch.index_select(cache.scale_table(), 0, cache.seq_lens))
+
+
+@pytest.mark.parametrize("graph", [False, True], ids=["direct", "graph"])
+def test_decode_loop_matches_append_and_step(dev, graph):
+    """DecodeLoop (two launches per token straight through the C-ABI, or both
+    captured once as a HIP graph and replayed) against cache.append +
+    hba_decode_step on an identical cache, 60 tokens that fill pages of every
+    sequence (127 -> 128 at once, 60 -> 64, 2500 -> 2560, the cache's last full
+    page): each step's output, selection and counts equal the reference
+    path's bit for bit at the same launch size (max_len), and stay within
+    bf16 rounding of the step sized by the longest sequence; the filled
+    pages' summaries, the appended rows and the device lengths agree.  Work
+    of the other path runs between the replays."""
+    lens = [127, 60, 2500]
+    kw = dict(W=256, k=8, seed=6)
+    cfg, x, prm, cos, sin, ca, kcs, qn = build_cache(dev, "bf16", lens, **kw)
+    _, _, _, _, _, cb, _, _ = build_cache(dev, "bf16", lens, **kw)
+    loop = hba_amd.DecodeLoop(cb, cfg, prm, prm, cos, sin, graph=graph)
+    gen = torch.Generator().manual_seed(8)
+    B, Hkv, d = len(lens), cfg.n_kv, cfg.head_dim
+    for t in range(60):
+        kn = torch.randn(B, Hkv, d, generator=gen).to(torch.bfloat16).to(dev)
+        vn = torch.randn(B, Hkv, d, generator=gen).to(torch.bfloat16).to(dev)
+        qd = torch.randn(B, cfg.n_heads, d, generator=gen).to(torch.bfloat16).to(dev)
+        ca.append(kn, vn, prm, prm, cos, sin)
+        oe, ie, ne = hba_amd.hba_decode_step(qd, ca, cfg, prm, cos, sin, max_len=ca.max_len)
+        o2, _, _ = hba_amd.hba_decode_step(qd, ca, cfg, prm, cos, sin)
+        og, ig, ng = loop.step(qd, kn, vn)
+        torch.cuda.synchronize()
+        assert cb.lens == ca.lens, t
+        assert torch.equal(ng, ne) and torch.equal(ig, ie), t
+        assert torch.equal(og, oe), (t, (og.float() - oe.float()).abs().max().item())
+        assert (og.float() - o2.float()).abs().max().item() <= 2 ** -6, t
+    assert torch.equal(cb.seq_lens.cpu(), torch.tensor(ca.lens, dtype=torch.int32))
+    assert torch.equal(ca.seq_lens.cpu(), torch.tensor(ca.lens, dtype=torch.int32))
+    for s, L in enumerate(ca.lens):
+        pa = torch.tensor(ca._table[s][: (L + 63) // 64], dtype=torch.long)
+        pb = torch.tensor(cb._table[s][: (L + 63) // 64], dtype=torch.long)
+        assert torch.equal(ca.summ_pages[pa[: L // 64]], cb.summ_pages[pb[: L // 64]]), s
+        for rows in (lambda c, pg: c.key_rows(pg), lambda c, pg: c.key_rows(pg, rotated=True),
+                     lambda c, pg: c.value_rows(pg)):
+            assert torch.equal(rows(ca, pa[-2:])[..., : (L - 1) % 64 + 1, :],
+                               rows(cb, pb[-2:])[..., : (L - 1) % 64 + 1, :]), s
+    with pytest.raises(ValueError, match="at most"):
+        cb.lens[0] = cb.max_len
+        loop.step(qd, kn, vn)
