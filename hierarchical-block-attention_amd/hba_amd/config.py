@@ -82,6 +82,17 @@ def route_scale(cfg, dh):
     return content_scale(cfg, dh) if getattr(cfg, "qknorm", False) else dh ** -0.5
 
 
+def yarn_theta(cfg, n):
+    """attention.py:47-53: the RoPE base for the donor+YaRN eval baseline.
+    Up to native_ctx it is rope_theta; past it, with s = n / native_ctx,
+    NTK-aware rescaling gives rope_theta * s ** (d / (d - 2)), d the head dim
+    (the base whose lowest frequency stretches by s)."""
+    if n <= cfg.native_ctx:
+        return cfg.rope_theta
+    d = cfg.head_dim
+    return cfg.rope_theta * ((n / cfg.native_ctx) ** (d / (d - 2)))
+
+
 def rope_tables(n, head_dim, theta, device, dtype=torch.float32):
     """attention.py:27-32 (fp32 cos/sin [n, head_dim]); built with torch on `device`."""
     inv = 1.0 / (theta ** (torch.arange(0, head_dim, 2, device=device).float() / head_dim))

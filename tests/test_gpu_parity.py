@@ -464,6 +464,26 @@ def test_equiv_matches_oracle(dev, dt, qknorm, n):
     assert err <= TOL[dt], err
 
 
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_equiv_with_yarn_tables_matches_oracle(dev, dt):
+    """The donor+YaRN eval baseline (evals.py:194-197): equiv attention at
+    n = 4 x native_ctx with cos/sin built from yarn_theta, against the oracle
+    on the same tables (they differ from the native ones)."""
+    n = 2048
+    cfg, x, prm, cos, sin = make(dev, dt, n=n, native_ctx=512)
+    th = hba_amd.yarn_theta(cfg, n)
+    assert th > cfg.rope_theta
+    cy, sy = hba_amd.rope_tables(n, cfg.head_dim, th, dev)
+    assert not torch.equal(cy, cos)
+    out = hba_amd.hba_attention_eval(x["q"], x["k"], x["v"], cy, sy, cfg, prm, prm, None, equiv=True)
+    torch.cuda.synchronize()
+    rows = np.unique(np.concatenate([[0, 1, 63, 64, n // 2, n - 1], np.random.RandomState(1).randint(0, n, 16)]))
+    ref = O.forward_equiv(f(x["q"]), f(x["k"]), f(x["v"]), f(cy), f(sy), cfg, f(x["q_gain"]), f(x["k_gain"]),
+                          1e-6, dt, rows)
+    err = np.abs(f(out)[:, rows] - ref).max()
+    assert err <= TOL[dt], err
+
+
 def test_equiv_rejects_ragged_length(dev):
     cfg, x, prm, cos, sin = make(dev, "bf16", n=128)
     with pytest.raises(ValueError):
