@@ -252,6 +252,91 @@ def summarize(kc, probes, proj, Bk):
     return np.einsum("hcmd,hde->hcme", S, pj)
 
 
+def aux_teacher(qc, kc, n_kv, scale, Bk, W):
+    """The aux-KL teacher p* (attention.py:375-381; the chunked form
+    _teacher_chunk :478-495) in float64.  qc [B, n, Hq, d], kc [B, n, Hkv, d]
+    (content q/k) -> [B, Hkv, n, nb]: for each query head, the softmax of its
+    content logits (scale) over the keys of candidate blocks, summed per block,
+    averaged over the G heads of the KV group and renormalised; rows without a
+    candidate block are 0."""
+    B, n, Hq, d = qc.shape
+    G, nb = Hq // n_kv, n // Bk
+    cand = route_candidates(n, W, nb, Bk)
+    ckey = np.repeat(cand, Bk, axis=1)                                   # [n, n]
+    out = np.zeros((B, n_kv, n, nb))
+    for b in range(B):
+        for g in range(n_kv):
+            kg = kc[b, :, g].astype(np.float64)
+            acc = np.zeros((n, nb))
+            for h in range(g * G, (g + 1) * G):
+                s = (qc[b, :, h].astype(np.float64) @ kg.T) * scale
+                s = np.where(ckey, s, -np.inf)
+                mx = s.max(-1, keepdims=True)
+                e = np.where(ckey, np.exp(s - np.where(np.isfinite(mx), mx, 0.0)), 0.0)
+                z = e.sum(-1, keepdims=True)
+                w = np.divide(e, z, out=np.zeros_like(e), where=z > 0)
+                acc += w.reshape(n, nb, Bk).sum(-1)
+            acc /= G
+            out[b, g] = acc / np.maximum(acc.sum(-1, keepdims=True), 1e-9)
+    return out
+
+
+def aux_kl(qc, kc, probes, proj, n_kv, scale_u, scale_r, Bk, W):
+    """The summarizer auxiliary loss of hba_attention_dense (attention.py:
+    366-389) and its gradients, float64.  qc [B, n, Hq, d], kc [B, n, Hkv, d]
+    content q/k; scale_u the union (teacher) scale, scale_r the routing scale.
+
+      bsc = max over slots of (grouped query . summary) * scale_r, -inf off
+            the candidates (route_topk, attention.py:272-303)
+      aux = -mean over (B, Hkv, queries with a candidate) of
+            sum_b p*_b log softmax(bsc)_b   (terms with p*_b = 0 dropped)
+
+    Gradients reach only probes and proj (the routing runs on detached q/k):
+    d aux / d bsc_c = (softmax_c * sum_b p*_b - p*_c) / N, the max over slots
+    passes it evenly to the tied slots, and the summariser's einsums and
+    softmax are differentiated by hand.  Returns (aux, dprobes, dproj, pstar)."""
+    B, n, Hq, d = qc.shape
+    G, nb = Hq // n_kv, n // Bk
+    m = probes.shape[1]
+    cand = route_candidates(n, W, nb, Bk)
+    vq = cand.any(-1)
+    pstar = aux_teacher(qc, kc, n_kv, scale_u, Bk, W)
+    pr, pj = probes.astype(np.float64), proj.astype(np.float64)
+    qg = qc.astype(np.float64).reshape(B, n, n_kv, G, d).sum(3)            # [B, n, Hkv, d]
+    kb = kc[:, : nb * Bk].astype(np.float64).reshape(B, nb, Bk, n_kv, d)
+    logit = np.einsum("hmd,bckhd->bhcmk", pr, kb) * d ** -0.5               # [B,Hkv,nb,m,Bk]
+    att = np.exp(logit - logit.max(-1, keepdims=True))
+    att /= att.sum(-1, keepdims=True)
+    Sp = np.einsum("bhcmk,bckhd->bhcmd", att, kb)                           # pooled
+    S0 = np.einsum("bhcmd,hde->bhcme", Sp, pj)
+    raw = np.einsum("bihd,bhcmd->bhicm", qg, S0)                            # [B,Hkv,n,nb,m]
+    mx = raw.max(-1)
+    bsc = np.where(cand[None, None], mx * scale_r, -np.inf)
+    N = B * n_kv * int(vq.sum())
+    if N == 0:
+        return 0.0, np.zeros_like(pr), np.zeros_like(pj), pstar
+    cm = np.broadcast_to(cand[None, None], bsc.shape)
+    fin = np.where(cm, bsc, 0.0)                                            # finite stand-ins off the candidates
+    top = np.where(vq[None, None, :, None], fin.max(-1, keepdims=True, initial=-np.inf, where=cm), 0.0)
+    z = np.where(cm, np.exp(fin - top), 0.0).sum(-1, keepdims=True)
+    lse = top + np.log(np.where(z > 0, z, 1.0))
+    soft = np.where(cm, np.exp(fin - lse), 0.0)                             # softmax(bsc)
+    pos = (pstar > 0) & cm
+    term = np.where(pos, pstar * (fin - lse), 0.0).sum(-1)                  # [B,Hkv,n]
+    aux = -term[:, :, vq].sum() / N
+    P = np.where(pos, pstar, 0.0).sum(-1, keepdims=True)
+    dbsc = np.where(vq[None, None, :, None], soft * P - np.where(pos, pstar, 0.0), 0.0) / N
+    ties = raw == mx[..., None]
+    draw = (dbsc * scale_r)[..., None] * ties / ties.sum(-1, keepdims=True)   # [B,Hkv,n,nb,m]
+    dS0 = np.einsum("bhicm,bihd->bhcmd", draw, qg)
+    dproj = np.einsum("bhcmd,bhcme->hde", Sp, dS0)
+    dSp = np.einsum("bhcme,hde->bhcmd", dS0, pj)
+    datt = np.einsum("bhcmd,bckhd->bhcmk", dSp, kb)
+    dlog = att * (datt - (att * datt).sum(-1, keepdims=True))
+    dprobes = np.einsum("bhcmk,bckhd->hmd", dlog, kb) * d ** -0.5
+    return float(aux), dprobes, dproj, pstar
+
+
 # ---------------------------------------------------------------- routing -----
 def cand_bmax(i, Bk, W):
     """Largest candidate block for query i (0: none). attention.py:250-256"""

@@ -132,3 +132,61 @@ def test_build_super_and_hier_select_match_reference(name):
             assert np.allclose(np.sort(val[0, r, : cnt[0, r]]), np.sort(rv[np.isfinite(rv)]),
                                rtol=1e-6, atol=1e-7)
     assert int(z["hier_comp"]) == O.hier_comparisons(hn, Bk, cfg.fanout, cfg.beam)
+
+
+# ------------------------------------------------------------- aux-KL -------
+AUX = np.load(f"{MG.HERE}/golden_aux.npz")
+
+
+def _aux_oracle(name):
+    case = MG.CASES[name]
+    inp = MG.gen_inputs(case)
+    assert np.allclose(MG.checksum(inp["q"]), AUX[f"{name}_ck_q"]), "input generator changed"
+    cfg = O.Cfg(**case["cfg"])
+    c = case["cfg"]
+    qc, kc, su = O.content_qk(inp["q"], inp["k"], cfg, inp["q_gain"], inp["k_gain"], EPS, case["n"], "f32")
+    sr = O.route_scale(cfg, c["head_dim"])
+    return O.aux_kl(qc, kc, inp["probes"], inp["proj"], c["n_kv"], su, sr, c["block"], c["window"])
+
+
+@pytest.mark.parametrize("name", NAMES)
+def test_aux_kl_and_its_gradients_match_reference(name):
+    """aux (hba_attention_dense, attention.py:366-389) and d aux / d probes,
+    d proj from the reference's autograd, fp32; the chunked (fused-path)
+    teacher gives the same aux; the reference's aux sends exactly zero
+    gradient into q, k, v (gates.py:129-167)."""
+    aux, dprobes, dproj, pstar = _aux_oracle(name)
+    ga = float(AUX[f"{name}_aux"])
+    assert abs(aux - ga) <= 1e-6 * abs(ga)
+    assert abs(float(AUX[f"{name}_aux_chunked"]) - ga) <= 1e-6 * abs(ga)
+    for got, key in ((dprobes, "dprobes"), (dproj, "dproj")):
+        ref = AUX[f"{name}_{key}"]
+        assert np.abs(got - ref).max() <= 1e-5 * np.abs(ref).max(), key
+    assert float(AUX[f"{name}_grad_qkv_max"]) == 0.0
+    gp = AUX[f"{name}_pstar"]
+    p = pstar if gp.shape == pstar.shape else pstar[:, :, -gp.shape[2]:]
+    rows = np.isfinite(gp).all(-1)                          # the reference's rows without candidates are NaN
+    assert rows.any() and np.abs(p[rows] - gp[rows]).max() <= 1e-6
+    assert np.all(p[~rows] == 0.0)
+
+
+def test_aux_kl_is_a_cross_entropy_bounded_by_the_teacher_entropy():
+    """aux is a cross-entropy H(p*, softmax(bsc)) >= H(p*): equality needs the
+    router to reproduce the teacher, so the oracle's aux sits above the mean
+    teacher entropy; and a planted sign error in the teacher renormalisation
+    (a mistake the golden check must catch) moves aux off the golden value."""
+    name = "d64"
+    aux, _, _, pstar = _aux_oracle(name)
+    case = MG.CASES[name]
+    c = case["cfg"]
+    vq = O.route_candidates(case["n"], c["window"], case["n"] // c["block"], c["block"]).any(-1)
+    p = pstar[:, :, vq]
+    ent = -np.where(p > 0, p * np.log(np.where(p > 0, p, 1.0)), 0.0).sum(-1).mean()
+    assert aux > ent > 0
+    orig = O.aux_teacher
+    try:
+        O.aux_teacher = lambda *a: orig(*a) ** 1.01            # a planted mistake
+        bad, _, _, _ = _aux_oracle(name)
+    finally:
+        O.aux_teacher = orig
+    assert abs(bad - float(AUX[f"{name}_aux"])) > 1e-4
