@@ -1,0 +1,595 @@
+// The summarizer auxiliary loss (aux-KL) and its gradient into the slot
+// summarizer's probes and projection (hba_attention_dense
+// src/hba/attention.py:366-389; the chunked teacher of the fused path
+// :478-549).
+//
+//   aux = -mean over (batch, KV head g, query i with a candidate block) of
+//         sum_b p*_b log softmax_b(bsc)      (terms with p*_b = 0 dropped)
+//   bsc[i, b] = max over slots of (grouped query . S0[b, slot]) * scale_r
+//   p*[i, b]  = mean over the G heads of g of softmax_b(LSE of head h's
+//               content logits over the 64 keys of block b), renormalised;
+//               both softmaxes run over the candidate blocks of i only.
+//
+// Gradients reach only probes and proj (routing runs on detached q/k, the
+// teacher under no_grad): d aux / d bsc = (softmax(bsc) * sum p* - p*) / N,
+// the slot max passes it evenly to tied slots, and the summariser is
+// differentiated by hand.
+//
+// Launches, in order (one stream, no host synchronisation):
+//   aux_qc      content queries qc = QKNorm(q) rounded to the storage type
+//   aux_scores  grouped queries qg (fp32) and bsc with the tied-slot masks
+//   aux_teacher per (query, head, candidate block) the block LSE of the
+//               content logits, on MFMA (16 keys x 16 (query, head) columns)
+//   aux_rows    per (query, KV head): p*, the row's KL term, d aux / d bsc
+//   aux_sum     aux = -(sum of row terms) / N, one workgroup, fixed order
+//   aux_dsum    d aux / d S0 = sum over queries of d bsc * tie share * qg
+//   aux_sbwd    per block: the summariser's backward into per-block partial
+//               d probes / d proj
+//   aux_gsum    partials summed over blocks in a fixed order
+// Every reduction runs in a fixed order: the results are deterministic.
+#include "hba_common.h"
+#include "hba_abi.h"
+
+namespace hba {
+namespace aux {
+
+constexpr int BK = 64;
+constexpr int BT = 8;           // blocks per aux_dsum workgroup
+
+struct Ws {
+    size_t qc, qg, bsc, ties, L, rowt, dS0, pproj, pprb, total;
+};
+
+inline size_t up256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+inline Ws layout(int dtype, int64_t B, int64_t n, int64_t Hq, int64_t Hkv, int64_t d, int64_t m) {
+    const int64_t nb = n / BK, G = Hq / Hkv;
+    Ws w;
+    size_t o = 0;
+    w.qc = o;    o += up256((size_t)B * n * Hq * d * (dtype == HBA_DTYPE_BF16 ? 2 : 4));
+    w.qg = o;    o += up256((size_t)B * Hkv * n * d * 4);
+    w.bsc = o;   o += up256((size_t)B * Hkv * n * nb * 4);
+    w.ties = o;  o += up256((size_t)B * Hkv * n * nb);
+    w.L = o;     o += up256((size_t)B * Hkv * n * G * nb * 4);
+    w.rowt = o;  o += up256((size_t)B * Hkv * n * 4);
+    w.dS0 = o;   o += up256((size_t)B * Hkv * nb * m * d * 4);
+    w.pproj = o; o += up256((size_t)B * nb * Hkv * d * d * 4);
+    w.pprb = o;  o += up256((size_t)B * nb * Hkv * m * d * 4);
+    w.total = o;
+    return w;
+}
+
+// First query with a candidate block: cand_bmax(i) >= 1 <=> i >= 2*BK + W - 1.
+__host__ __device__ inline int64_t first_valid(int64_t W) { return 2 * BK + W - 1; }
+
+// ------------------------------------------------------------------ qc -----
+template <int DT, int D>
+__global__ __launch_bounds__(256) void aux_qc_kernel(const typename St<DT>::T *__restrict__ q, int64_t sb,
+                                                     int64_t sn, int64_t sh, const float *__restrict__ qgain,
+                                                     float eps, int64_t B, int64_t n, int64_t Hq,
+                                                     typename St<DT>::T *__restrict__ qc) {
+    const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (r >= B * n * Hq) return;
+    const int64_t h = r % Hq, i = (r / Hq) % n, b = r / (Hq * n);
+    const typename St<DT>::T *src = q + b * sb + i * sn + h * sh;
+    float x[D];
+#pragma unroll
+    for (int t = 0; t < D; ++t) x[t] = St<DT>::ld(src, t);
+    if (qgain) qknorm_row<DT, D>(x, qgain[h], eps);
+#pragma unroll
+    for (int t = 0; t < D; ++t) St<DT>::st(qc, r * D + t, x[t]);
+}
+
+// -------------------------------------------------------------- scores -----
+// Workgroup = (64 queries, KV head g, batch b).  qg rows (the G heads summed
+// in head order, rounded to the storage type, as grouped_query) go to LDS and
+// to the qg buffer; the summaries of CB blocks at a time are staged in LDS;
+// thread (query, block) takes the slot max of the fp32 dot products and the
+// mask of the slots that reach it.
+template <int DT, int D>
+__global__ __launch_bounds__(256) void aux_scores_kernel(const typename St<DT>::T *__restrict__ qc,
+                                                         const typename St<DT>::T *__restrict__ S0, int64_t n,
+                                                         int64_t Hq, int64_t Hkv, int m, int64_t W, float scale_r,
+                                                         float *__restrict__ qg_out, float *__restrict__ bsc,
+                                                         uint8_t *__restrict__ ties) {
+    constexpr int CB = (D == 64) ? 8 : 4;   // summary blocks staged per step (LDS under 64 KB)
+    __shared__ float qgs[64][D + 1];
+    __shared__ float s0[CB][8][D];
+    const int tid = threadIdx.x;
+    const int64_t i0 = (int64_t)blockIdx.x * 64, g = blockIdx.y, b = blockIdx.z;
+    const int64_t G = Hq / Hkv, nb = n / BK;
+    for (int e = tid; e < 64 * D; e += 256) {
+        const int qi = e / D, t = e % D;
+        const int64_t i = i0 + qi;
+        float s = 0.0f;
+        if (i < n) {
+            const typename St<DT>::T *row = qc + ((b * n + i) * Hq + g * G) * D + t;
+            s = St<DT>::ld(row, 0);
+            for (int64_t h = 1; h < G; ++h) s = s + St<DT>::ld(row, h * D);
+            s = St<DT>::rnd(s);
+            qg_out[((b * Hkv + g) * n + i) * D + t] = s;
+        }
+        qgs[qi][t] = s;
+    }
+    const int64_t ilast = (i0 + 63 < n) ? i0 + 63 : n - 1;
+    const int64_t bmax = cand_bmax(ilast, BK, W);
+    const typename St<DT>::T *sg = S0 + (b * Hkv + g) * nb * m * D;
+    for (int64_t c0 = 1; c0 <= bmax; c0 += CB) {
+        __syncthreads();   // qgs written / the previous chunk is used
+        for (int e = tid; e < CB * m * D; e += 256) {
+            const int cb = e / (m * D), rem = e % (m * D);
+            const int64_t c = c0 + cb;
+            s0[cb][rem / D][rem % D] = (c <= bmax) ? St<DT>::ld(sg, c * m * D + rem) : 0.0f;
+        }
+        __syncthreads();
+        for (int e = tid; e < 64 * CB; e += 256) {
+            const int qi = e % 64, cb = e / 64;
+            const int64_t i = i0 + qi, c = c0 + cb;
+            if (i >= n || c > cand_bmax(i, BK, W)) continue;
+            float best = -INFINITY;
+            uint32_t mask = 0;
+            for (int sl = 0; sl < m; ++sl) {
+                float acc = 0.0f;
+#pragma unroll 16
+                for (int t = 0; t < D; ++t) acc = fmaf(qgs[qi][t], s0[cb][sl][t], acc);
+                if (acc > best) {
+                    best = acc;
+                    mask = 1u << sl;
+                } else if (acc == best) {
+                    mask |= 1u << sl;
+                }
+            }
+            const int64_t o = ((b * Hkv + g) * n + i) * nb + c;
+            bsc[o] = best * scale_r;
+            ties[o] = (uint8_t)mask;
+        }
+    }
+}
+
+// ------------------------------------------------------------- teacher -----
+// Each wave owns 16 columns: QPW = 16/G queries x the G heads of KV head g
+// (column c -> query i0w + c/G, head g*G + c%G; columns past QPW*G idle).
+// For every candidate block of its last query it forms S^T = K_blk . Q^T as
+// four 16-key M-tiles, and per column the LSE over the block's 64 keys of the
+// content logits (scale_u); it writes the LSE of each (query, head, block)
+// that is a candidate.  Waves are independent (no LDS, no barriers).
+__device__ __forceinline__ f32x4 mfma_bf16(bf16x8 a, bf16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+template <int DT, int D>
+__global__ __launch_bounds__(256) void aux_teacher_kernel(const typename St<DT>::T *__restrict__ qc,
+                                                          const typename St<DT>::T *__restrict__ kc, int64_t n,
+                                                          int64_t Hq, int64_t Hkv, int64_t W, float scale_u,
+                                                          float *__restrict__ L) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int l16 = lane & 15, lg = lane >> 4;
+    const int64_t g = blockIdx.y, b = blockIdx.z;
+    const int G = (int)(Hq / Hkv), QPW = 16 / G;
+    const int64_t nb = n / BK;
+    const int64_t i0w = ((int64_t)blockIdx.x * 4 + w) * QPW;
+    if (i0w >= n) return;
+    const int cq = l16 / G, ch = l16 % G;
+    const int64_t iq = i0w + cq;
+    const bool col_ok = l16 < QPW * G && iq < n;
+    const int64_t ic = col_ok ? iq : i0w;
+    const int64_t col_bmax = col_ok ? cand_bmax(iq, BK, W) : 0;
+    const int64_t ilast = (i0w + QPW - 1 < n) ? i0w + QPW - 1 : n - 1;
+    const int64_t bmax = cand_bmax(ilast, BK, W);
+    const typename St<DT>::T *qrow = qc + ((b * n + ic) * Hq + g * G + ch) * D;
+    const typename St<DT>::T *kg = kc + (b * Hkv + g) * n * D;
+    float *Lrow = L + (((b * Hkv + g) * n + ic) * G + ch) * nb;
+    if constexpr (DT == 1) {
+        constexpr int NKS = D / 32;
+        bf16x8 qop[NKS];
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) {
+            const uint4 u = col_ok ? *reinterpret_cast<const uint4 *>(qrow + 32 * ks + 8 * lg) : make_uint4(0, 0, 0, 0);
+            qop[ks] = __builtin_bit_cast(bf16x8, u);
+        }
+        for (int64_t c = 1; c <= bmax; ++c) {
+            f32x4 acc[4];
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) {
+                acc[mt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                const typename St<DT>::T *krow = kg + (c * BK + mt * 16 + l16) * D + 8 * lg;
+#pragma unroll
+                for (int ks = 0; ks < NKS; ++ks) {
+                    const uint4 u = *reinterpret_cast<const uint4 *>(krow + 32 * ks);
+                    acc[mt] = mfma_bf16(__builtin_bit_cast(bf16x8, u), qop[ks], acc[mt]);
+                }
+            }
+            float mx = -INFINITY;
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) mx = fmaxf(mx, acc[mt][r] * scale_u);
+            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            float se = 0.0f;
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) se += expf(acc[mt][r] * scale_u - mx);
+            se += __shfl_xor(se, 16, 64);
+            se += __shfl_xor(se, 32, 64);
+            if (lg == 0 && col_ok && c <= col_bmax) Lrow[c] = mx + logf(se);
+        }
+    } else {
+        constexpr int NK4 = D / 4;
+        float qop[NK4];
+#pragma unroll
+        for (int ks = 0; ks < NK4; ++ks) qop[ks] = col_ok ? St<DT>::ld(qrow, 4 * ks + lg) : 0.0f;
+        for (int64_t c = 1; c <= bmax; ++c) {
+            f32x4 acc[4];
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) {
+                acc[mt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                const typename St<DT>::T *krow = kg + (c * BK + mt * 16 + l16) * D + lg;
+#pragma unroll
+                for (int ks = 0; ks < NK4; ++ks)
+                    acc[mt] = __builtin_amdgcn_mfma_f32_16x16x4f32(St<DT>::ld(krow, 4 * ks), qop[ks], acc[mt], 0,
+                                                                   0, 0);
+            }
+            float mx = -INFINITY;
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) mx = fmaxf(mx, acc[mt][r] * scale_u);
+            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            float se = 0.0f;
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) se += expf(acc[mt][r] * scale_u - mx);
+            se += __shfl_xor(se, 16, 64);
+            se += __shfl_xor(se, 32, 64);
+            if (lg == 0 && col_ok && c <= col_bmax) Lrow[c] = mx + logf(se);
+        }
+    }
+}
+
+// ---------------------------------------------------------------- rows -----
+// One wave per (b, g, i) with a candidate block: p* from the block LSEs, the
+// row's KL term (rowt), and d aux / d bsc written over bsc.  Head h's max and
+// sum of exponentials over the candidate blocks are kept by lane h.
+__global__ __launch_bounds__(256) void aux_rows_kernel(const float *__restrict__ L, int64_t B, int64_t n,
+                                                       int64_t Hkv, int G, int64_t W, float invN,
+                                                       float *__restrict__ bsc, float *__restrict__ rowt) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int64_t r = (int64_t)blockIdx.x * 4 + w;
+    if (r >= B * Hkv * n) return;
+    const int64_t i = r % n;
+    const int64_t nb = n / BK;
+    const int64_t nbm = cand_bmax(i, BK, W);
+    if (nbm < 1) {
+        if (lane == 0) rowt[r] = 0.0f;
+        return;
+    }
+    const float *Lr = L + r * G * nb;
+    float *br = bsc + r * nb;
+    float myM = 0.0f, myZ = 1.0f;
+    for (int h = 0; h < G; ++h) {
+        float mx = -INFINITY;
+        for (int64_t c = 1 + lane; c <= nbm; c += 64) mx = fmaxf(mx, Lr[h * nb + c]);
+        mx = wave_max(mx);
+        float z = 0.0f;
+        for (int64_t c = 1 + lane; c <= nbm; c += 64) z += expf(Lr[h * nb + c] - mx);
+        z = wave_sum(z);
+        if (lane == h) {
+            myM = mx;
+            myZ = z;
+        }
+    }
+    auto pmass = [&](int64_t c) {   // called by the whole wave
+        float p = 0.0f;
+        for (int h = 0; h < G; ++h) {
+            const float Mh = __shfl(myM, h, 64), Zh = __shfl(myZ, h, 64);
+            p += (c <= nbm) ? expf(Lr[h * nb + c] - Mh) / Zh : 0.0f;
+        }
+        return p / (float)G;
+    };
+    const int64_t cend = 1 + ((nbm + 63) / 64) * 64;   // uniform trip count for the shuffles
+    float p0 = 0.0f, top = -INFINITY;
+    for (int64_t c = 1 + lane; c < cend; c += 64) {
+        p0 += pmass(c);
+        if (c <= nbm) top = fmaxf(top, br[c]);
+    }
+    p0 = fmaxf(wave_sum(p0), 1e-9f);
+    top = wave_max(top);
+    float zb = 0.0f;
+    for (int64_t c = 1 + lane; c <= nbm; c += 64) zb += expf(br[c] - top);
+    const float lse = top + logf(wave_sum(zb));
+    float term = 0.0f, P = 0.0f;
+    for (int64_t c = 1 + lane; c < cend; c += 64) {
+        const float ps = pmass(c) / p0;
+        if (c <= nbm && ps > 0.0f) {
+            term += ps * (br[c] - lse);
+            P += ps;
+        }
+    }
+    term = wave_sum(term);
+    P = wave_sum(P);
+    for (int64_t c = 1 + lane; c < cend; c += 64) {
+        const float ps = pmass(c) / p0;
+        if (c <= nbm) {
+            const float soft = expf(br[c] - lse);
+            br[c] = (soft * P - (ps > 0.0f ? ps : 0.0f)) * invN;
+        }
+    }
+    if (lane == 0) rowt[r] = term;
+}
+
+// aux = -(sum of the row terms) / N: one workgroup, double accumulation in a
+// fixed order.
+__global__ __launch_bounds__(256) void aux_sum_kernel(const float *__restrict__ rowt, int64_t rows, float invN,
+                                                      float *__restrict__ aux) {
+    __shared__ double part[256];
+    double s = 0.0;
+    for (int64_t r = threadIdx.x; r < rows; r += 256) s += (double)rowt[r];
+    part[threadIdx.x] = s;
+    __syncthreads();
+    for (int o = 128; o >= 1; o >>= 1) {
+        if ((int)threadIdx.x < o) part[threadIdx.x] += part[threadIdx.x + o];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) aux[0] = (float)(-part[0] * (double)invN);
+}
+
+// ---------------------------------------------------------------- dS0 ------
+// Workgroup = (BT blocks, g, b): d aux / d S0[c, slot, :] = sum over the
+// candidate queries of c of d bsc[i, c] * scale_r * [slot ties the max] /
+// (number of tied slots) * qg[i, :], queries in ascending order.
+template <int D>
+__global__ __launch_bounds__(256) void aux_dsum_kernel(const float *__restrict__ dbsc,
+                                                       const uint8_t *__restrict__ ties,
+                                                       const float *__restrict__ qg, int64_t n, int64_t Hkv, int m,
+                                                       int64_t W, float scale_r, float *__restrict__ dS0) {
+    constexpr int OPT = BT * 8 * D / 256;          // outputs per thread, m <= 8
+    __shared__ float qgs[64][D];
+    __shared__ float coef[64][BT][8];
+    const int tid = threadIdx.x;
+    const int64_t c0 = (int64_t)blockIdx.x * BT, g = blockIdx.y, b = blockIdx.z;
+    const int64_t nb = n / BK;
+    const int64_t bg = b * Hkv + g;
+    float acc[OPT];
+#pragma unroll
+    for (int j = 0; j < OPT; ++j) acc[j] = 0.0f;
+    const int64_t ilo = (c0 + 1) * BK + W - 1;     // first candidate query of block c0
+    for (int64_t i0 = (ilo > 0 ? ilo : 0); i0 < n; i0 += 64) {
+        __syncthreads();   // the previous chunk is used
+        for (int e = tid; e < 64 * D; e += 256) {
+            const int64_t i = i0 + e / D;
+            qgs[e / D][e % D] = (i < n) ? qg[(bg * n + i) * D + e % D] : 0.0f;
+        }
+        for (int e = tid; e < 64 * BT; e += 256) {
+            const int qi = e / BT, bb = e % BT;
+            const int64_t i = i0 + qi, c = c0 + bb;
+            float cf = 0.0f;
+            uint32_t mask = 0;
+            if (i < n && c < nb && c >= 1 && c <= cand_bmax(i, BK, W)) {
+                const int64_t o = (bg * n + i) * nb + c;
+                mask = ties[o];
+                cf = dbsc[o] * scale_r / (float)__builtin_popcount(mask);
+            }
+#pragma unroll
+            for (int sl = 0; sl < 8; ++sl) coef[qi][bb][sl] = ((mask >> sl) & 1u) ? cf : 0.0f;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < OPT; ++j) {
+            const int o = tid + 256 * j;
+            const int bb = o / (8 * D), sl = (o / D) % 8, t = o % D;
+            float a = acc[j];
+            for (int qi = 0; qi < 64; ++qi) a = fmaf(coef[qi][bb][sl], qgs[qi][t], a);
+            acc[j] = a;
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < OPT; ++j) {
+        const int o = tid + 256 * j;
+        const int bb = o / (8 * D), sl = (o / D) % 8, t = o % D;
+        const int64_t c = c0 + bb;
+        if (c < nb && sl < m) dS0[((bg * nb + c) * m + sl) * D + t] = acc[j];
+    }
+}
+
+// -------------------------------------------------- summariser backward ----
+// Workgroup = (block c, g, b): recompute the block's slot attention (att) and
+// pooled rows (Sp) from its keys, then with dO = d aux / d S0[c]:
+//   d proj  += Sp^T dO                 (per-block partial)
+//   dSp      = dO proj^T
+//   datt     = dSp K^T,  dlogit = att * (datt - sum_k att * datt)
+//   d probes += dlogit K / sqrt(d)     (per-block partial)
+template <int DT, int D>
+__global__ __launch_bounds__(256) void aux_sbwd_kernel(const typename St<DT>::T *__restrict__ kc,
+                                                       const float *__restrict__ probes,
+                                                       const float *__restrict__ proj,
+                                                       const float *__restrict__ dS0, int64_t n, int64_t Hkv, int m,
+                                                       float *__restrict__ pproj, float *__restrict__ pprb) {
+    __shared__ float kb[BK][D + 1];
+    __shared__ float pr[8][D];
+    __shared__ float att[8][BK];
+    __shared__ float sp[8][D];
+    __shared__ float dO[8][D];
+    __shared__ float dsp[8][D];
+    const int tid = threadIdx.x;
+    const int64_t c = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
+    const int64_t nb = n / BK;
+    const float isd = 1.0f / sqrtf((float)D);
+    const typename St<DT>::T *src = kc + ((b * Hkv + g) * n + c * BK) * D;
+    for (int e = tid; e < BK * D; e += 256) kb[e / D][e % D] = St<DT>::ld(src, e);
+    for (int e = tid; e < m * D; e += 256) {
+        pr[e / D][e % D] = probes[g * m * D + e];
+        dO[e / D][e % D] = dS0[((b * Hkv + g) * nb + c) * m * D + e];
+    }
+    __syncthreads();
+    for (int e = tid; e < m * BK; e += 256) {
+        const int s = e / BK, k = e % BK;
+        float a = 0.0f;
+        for (int t = 0; t < D; ++t) a = fmaf(pr[s][t], kb[k][t], a);
+        att[s][k] = a * isd;
+    }
+    __syncthreads();
+    {   // softmax over the 64 keys of each slot, one wave per slot
+        const int wv = tid / 64, l = tid % 64;
+        for (int s = wv; s < m; s += 4) {
+            const float x = att[s][l];
+            const float mx = wave_max(x);
+            const float ex = expf(x - mx);
+            att[s][l] = ex / wave_sum(ex);
+        }
+    }
+    __syncthreads();
+    for (int e = tid; e < m * D; e += 256) {
+        const int s = e / D, t = e % D;
+        float a = 0.0f;
+        for (int k = 0; k < BK; ++k) a = fmaf(att[s][k], kb[k][t], a);
+        sp[s][t] = a;
+    }
+    __syncthreads();
+    float *pp = pproj + ((b * nb + c) * Hkv + g) * D * D;
+    for (int e = tid; e < D * D; e += 256) {
+        const int t = e / D, ee = e % D;
+        float a = 0.0f;
+        for (int s = 0; s < m; ++s) a = fmaf(sp[s][t], dO[s][ee], a);
+        pp[e] = a;
+    }
+    const float *pj = proj + g * D * D;
+    for (int e = tid; e < m * D; e += 256) {
+        const int s = e / D, t = e % D;
+        float a = 0.0f;
+        for (int ee = 0; ee < D; ++ee) a = fmaf(dO[s][ee], pj[t * D + ee], a);
+        dsp[s][t] = a;
+    }
+    __syncthreads();
+    {   // datt, then the softmax backward, one wave per slot (lane = key)
+        const int wv = tid / 64, l = tid % 64;
+        for (int s = wv; s < m; s += 4) {
+            float a = 0.0f;
+            for (int t = 0; t < D; ++t) a = fmaf(dsp[s][t], kb[l][t], a);
+            const float at = att[s][l];
+            const float dot = wave_sum(at * a);
+            att[s][l] = at * (a - dot);   // dlogit, in place
+        }
+    }
+    __syncthreads();
+    float *pb = pprb + ((b * nb + c) * Hkv + g) * m * D;
+    for (int e = tid; e < m * D; e += 256) {
+        const int s = e / D, t = e % D;
+        float a = 0.0f;
+        for (int k = 0; k < BK; ++k) a = fmaf(att[s][k], kb[k][t], a);
+        pb[e] = a * isd;
+    }
+}
+
+// Sum of per-block partials (count of them, each `len` floats apart) in block
+// order.
+__global__ __launch_bounds__(256) void aux_gsum_kernel(const float *__restrict__ part, int64_t count,
+                                                       int64_t len, float *__restrict__ out) {
+    const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (e >= len) return;
+    float s = 0.0f;
+    for (int64_t p = 0; p < count; ++p) s += part[p * len + e];
+    out[e] = s;
+}
+
+__global__ void aux_zero_kernel(float *__restrict__ p, int64_t len) {
+    const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (e < len) p[e] = 0.0f;
+}
+
+}  // namespace aux
+}  // namespace hba
+
+using namespace hba;
+
+extern "C" int hba_aux_kl_workspace_size(int dtype, int64_t B, int64_t n, int64_t Hq, int64_t Hkv, int64_t d,
+                                         int64_t m, int64_t Bk, size_t *bytes) {
+    int st = abi::check_dtype_dim(dtype, d);
+    if (st) return st;
+    if (!bytes || B <= 0 || n <= 0 || Hq <= 0 || Hkv <= 0 || m <= 0) return HBA_ERR_INVALID_ARG;
+    if (Hq % Hkv) return HBA_ERR_INVALID_ARG;
+    if (Bk != aux::BK || n % aux::BK || m > 8 || Hq / Hkv > 16) return HBA_ERR_UNSUPPORTED;
+    *bytes = aux::layout(dtype, B, n, Hq, Hkv, d, m).total;
+    return HBA_OK;
+}
+
+extern "C" int hba_aux_kl(int dtype, const void *q, const int64_t q_strides[3], const float *q_gain, float eps,
+                          const void *kc, const void *S0, const float *probes, const float *proj, int64_t B,
+                          int64_t n, int64_t Hq, int64_t Hkv, int64_t d, int64_t m, int64_t Bk, int64_t W,
+                          float scale_u, float scale_r, void *ws, size_t ws_bytes, float *aux, float *dprobes,
+                          float *dproj, void *stream) {
+    size_t need = 0;
+    int st = hba_aux_kl_workspace_size(dtype, B, n, Hq, Hkv, d, m, Bk, &need);
+    if (st) return st;
+    if (!q || !q_strides || !kc || !S0 || !probes || !proj || !ws || !aux || (!dprobes) != (!dproj) || W < 1)
+        return HBA_ERR_INVALID_ARG;
+    if (ws_bytes < need) return HBA_ERR_INVALID_ARG;
+    if (!abi::aligned16(ws) || !abi::aligned16(kc)) return HBA_ERR_UNSUPPORTED;
+    if (n / aux::BK > 0x7fffffff || Hkv > 65535 || B > 65535) return HBA_ERR_UNSUPPORTED;
+    const aux::Ws L = aux::layout(dtype, B, n, Hq, Hkv, d, m);
+    char *w = (char *)ws;
+    hipStream_t s = (hipStream_t)stream;
+    const int64_t nb = n / aux::BK, G = Hq / Hkv;
+    const int64_t nvalid = n > aux::first_valid(W) ? n - aux::first_valid(W) : 0;
+    const int64_t N = B * Hkv * nvalid;
+    const float invN = N ? (float)(1.0 / (double)N) : 0.0f;
+    float *qg = (float *)(w + L.qg), *bsc = (float *)(w + L.bsc), *Lb = (float *)(w + L.L);
+    float *rowt = (float *)(w + L.rowt), *dS0 = (float *)(w + L.dS0);
+    float *pproj = (float *)(w + L.pproj), *pprb = (float *)(w + L.pprb);
+    uint8_t *ties = (uint8_t *)(w + L.ties);
+    const int64_t rows = B * Hkv * n;
+    if (N == 0) {   // no query has a candidate block: aux and its gradients are zero
+        hipLaunchKernelGGL(aux::aux_zero_kernel, dim3(1), dim3(256), 0, s, aux, (int64_t)1);
+        if (dprobes) {
+            hipLaunchKernelGGL(aux::aux_zero_kernel, dim3((unsigned)((Hkv * m * d + 255) / 256)), dim3(256), 0, s,
+                               dprobes, Hkv * m * d);
+            hipLaunchKernelGGL(aux::aux_zero_kernel, dim3((unsigned)((Hkv * d * d + 255) / 256)), dim3(256), 0, s,
+                               dproj, Hkv * d * d);
+        }
+        HBA_LAUNCH_CHECK();
+        return HBA_OK;
+    }
+#define HBA_AUX_FWD(DT, D)                                                                               \
+    do {                                                                                                 \
+        typedef St<DT>::T T;                                                                             \
+        T *qc = (T *)(w + L.qc);                                                                         \
+        hipLaunchKernelGGL((aux::aux_qc_kernel<DT, D>), dim3((unsigned)((B * n * Hq + 255) / 256)),       \
+                           dim3(256), 0, s, (const T *)q, q_strides[0], q_strides[1], q_strides[2], q_gain, \
+                           eps, B, n, Hq, qc);                                                           \
+        hipLaunchKernelGGL((aux::aux_scores_kernel<DT, D>), dim3((unsigned)((n + 63) / 64), (unsigned)Hkv,  \
+                           (unsigned)B), dim3(256), 0, s, (const T *)qc, (const T *)S0, n, Hq, Hkv, (int)m, W, \
+                           scale_r, qg, bsc, ties);                                                      \
+        const int64_t qpw = 16 / G;                                                                      \
+        hipLaunchKernelGGL((aux::aux_teacher_kernel<DT, D>),                                             \
+                           dim3((unsigned)((n + 4 * qpw - 1) / (4 * qpw)), (unsigned)Hkv, (unsigned)B),      \
+                           dim3(256), 0, s, (const T *)qc, (const T *)kc, n, Hq, Hkv, W, scale_u, Lb);    \
+    } while (0)
+    HBA_DISPATCH_DT_D(dtype, d, HBA_AUX_FWD);
+#undef HBA_AUX_FWD
+    hipLaunchKernelGGL(aux::aux_rows_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, Lb, B, n, Hkv,
+                       (int)G, W, invN, bsc, rowt);
+    hipLaunchKernelGGL(aux::aux_sum_kernel, dim3(1), dim3(256), 0, s, rowt, rows, invN, aux);
+    if (dprobes) {
+#define HBA_AUX_BWD(DT, D)                                                                               \
+    do {                                                                                                 \
+        typedef St<DT>::T T;                                                                             \
+        hipLaunchKernelGGL((aux::aux_dsum_kernel<D>), dim3((unsigned)((nb + aux::BT - 1) / aux::BT),     \
+                           (unsigned)Hkv, (unsigned)B), dim3(256), 0, s, bsc, ties, qg, n, Hkv, (int)m, W, \
+                           scale_r, dS0);                                                                \
+        hipLaunchKernelGGL((aux::aux_sbwd_kernel<DT, D>), dim3((unsigned)nb, (unsigned)Hkv, (unsigned)B),  \
+                           dim3(256), 0, s, (const T *)kc, probes, proj, dS0, n, Hkv, (int)m, pproj, pprb); \
+    } while (0)
+        HBA_DISPATCH_DT_D(dtype, d, HBA_AUX_BWD);
+#undef HBA_AUX_BWD
+        const int64_t lp = Hkv * d * d, lb = Hkv * m * d;
+        hipLaunchKernelGGL(aux::aux_gsum_kernel, dim3((unsigned)((lp + 255) / 256)), dim3(256), 0, s, pproj, B * nb,
+                           lp, dproj);
+        hipLaunchKernelGGL(aux::aux_gsum_kernel, dim3((unsigned)((lb + 255) / 256)), dim3(256), 0, s, pprb, B * nb,
+                           lb, dprobes);
+    }
+    HBA_LAUNCH_CHECK();
+    return HBA_OK;
+}

@@ -3,17 +3,17 @@ HIP kernels (forward, and the backward through autograd).
 
   hba_attention_eval(q, k, v, cos, sin, cfg, summ, qkn, cap, hier=False, equiv=False)
       src/hba/attention.py:610-713 (equiv=True: :634-649)
-  hba_attention_dense(q, k, v, cos, sin, cfg, summ, qkn, equiv=False) -> (out, aux=0)
-      src/hba/attention.py:306-356 (forward; the aux-KL teacher is training-only;
-      equiv=True: :330-336)
-  hba_attention_fused(q, k, v, cos, sin, cfg, summ, qkn) -> (out, aux=0)
-      src/hba/attention.py:552-607 (forward: same math as dense)
+  hba_attention_dense(q, k, v, cos, sin, cfg, summ, qkn, equiv=False) -> (out, aux)
+      src/hba/attention.py:306-389 (equiv=True: :330-336)
+  hba_attention_fused(q, k, v, cos, sin, cfg, summ, qkn) -> (out, aux)
+      src/hba/attention.py:552-607 (the same math as dense)
 
 Gradients: when grad mode is on and q, k, v or the QKNorm gains require grad,
 the output carries an autograd node whose backward is the HIP backward
 (ops.attn_bwd): dq, dk, dv and the gain gradients, the selection held fixed
-(the reference routes on detached q/k, attention.py:288-303).  The aux-KL
-teacher is not provided (aux = 0).
+(the reference routes on detached q/k, attention.py:288-303).  aux (the
+summarizer's distillation loss, hba_aux_kl) has gradients into the
+summarizer's probes and proj only.
 
 Tensors: q [B, n, Hq, d], k, v [B, n, Hkv, d] (token-major views, last dim
 contiguous), cos/sin fp32 [n, d] from rope_tables.  `cfg` is read duck-typed
@@ -170,45 +170,65 @@ def hba_attention_eval(q, k, v, cos, sin, cfg, summ, qkn, cap=None, hier=False, 
     return forward_stages(q, k, v, cos, sin, cfg, summ, qkn, hier=hier)["out"]
 
 
-def _refuse_aux_training(q, k, v, cfg, summ, qkn):
-    """The reference returns the aux-KL distillation loss as `aux` whenever
-    cfg.aux_w != 0 (attention.py:363-389, 605-606); it is the summarizer's only
-    gradient.  This build does not compute it, so a training call (grad mode
-    on, something upstream requiring grad) with aux_w != 0 raises instead of
-    returning a zero that would leave the summarizer silently untrained.  The
-    reference's own frozen-summarizer stage sets aux_w = 0.0, and then aux is
-    a graph-free zero there too (:363-364)."""
-    if getattr(cfg, "aux_w", 1.0) == 0.0 or not torch.is_grad_enabled():
-        return
-    ts = [q, k, v, getattr(summ, "probes", None), getattr(summ, "proj", None)]
-    if getattr(cfg, "qknorm", False):
-        ts += [qkn.q.gain, qkn.k.gain]
-    if any(isinstance(t, torch.Tensor) and t.requires_grad for t in ts):
-        raise NotImplementedError(
-            "hba_attention_dense/fused: the aux-KL teacher (the summarizer's gradient, "
-            "attention.py:358-389) is not implemented by the HIP backend; train with cfg.aux_w = 0.0 "
-            "(frozen summarizers) or run under torch.no_grad()")
+class _AuxKL(torch.autograd.Function):
+    """The summarizer auxiliary loss as an autograd node whose only inputs
+    with a gradient are the summarizer's probes and proj (the routing and the
+    teacher run on detached q/k: attention.py:288-303, 372-381).  The HIP
+    entry point returns the loss and its gradient in one call; backward
+    scales the saved gradient."""
+
+    @staticmethod
+    def forward(ctx, probes, proj, q, k, v, q_gain, k_gain, cos, sin, cfg, qeps, keps, want):
+        B, n, Hq, dh = q.shape
+        kc, _, _ = ops.prep_keys(k, v, k_gain, keps, cos, sin)
+        S0 = ops.summarize(kc, probes.detach(), proj.detach())
+        aux, dpr, dpj = ops.aux_kl(q, q_gain, qeps, kc, S0, probes.detach(), proj.detach(), cfg.window,
+                                   union_scale(cfg, dh, n), route_scale(cfg, dh), want)
+        ctx.save_for_backward(dpr, dpj)
+        ctx.dtypes = (probes.dtype, proj.dtype)
+        return aux
+
+    @staticmethod
+    def backward(ctx, g):
+        dpr, dpj = ctx.saved_tensors
+        gpr = (g * dpr).to(ctx.dtypes[0]) if dpr is not None and ctx.needs_input_grad[0] else None
+        gpj = (g * dpj).to(ctx.dtypes[1]) if dpj is not None and ctx.needs_input_grad[1] else None
+        return gpr, gpj, None, None, None, None, None, None, None, None, None, None, None
+
+
+def aux_kl(q, k, v, cos, sin, cfg, summ, qkn):
+    """The aux-KL of the training paths (attention.py:366-389, 509-549): the
+    teacher p* (group-averaged content mass of the candidate blocks) against
+    log softmax of the summarizer's block scores, a 0-d fp32 tensor whose
+    gradient reaches only summ.probes and summ.proj."""
+    qg, kg, qeps, keps = _qk(cfg, qkn)
+    qg = None if qg is None else qg.detach()
+    kg = None if kg is None else kg.detach()
+    probes, proj = summ.probes, summ.proj
+    want = torch.is_grad_enabled() and (probes.requires_grad or proj.requires_grad)
+    return _AuxKL.apply(probes, proj, q.detach(), k.detach(), v.detach(), qg, kg, cos, sin, cfg, qeps, keps, want)
 
 
 def hba_attention_dense(q, k, v, cos, sin, cfg, summ, qkn, equiv=False):
-    """Forward of the reference's naive path: selection with route_topk's
-    scale (no temperature), attention with the union scale.  aux = 0: a
-    training call with cfg.aux_w != 0 raises NotImplementedError
-    (_refuse_aux_training).  equiv=True: dense uniform-RoPE causal attention
-    (equiv_attention)."""
-    if not equiv:
-        _refuse_aux_training(q, k, v, cfg, summ, qkn)
+    """The reference's naive training path: selection with route_topk's
+    scale (no temperature), attention with the union scale, and the aux-KL
+    (aux_kl) unless cfg.aux_w == 0 (then a zero, as the reference skips its
+    teacher, attention.py:363-364).  equiv=True: dense uniform-RoPE causal
+    attention (equiv_attention) and aux = 0."""
     out = _with_grad(q, k, v, cos, sin, cfg, summ, qkn, "equiv" if equiv else "dense")
-    if out is not None:
+    if out is None:
+        if equiv:
+            out = equiv_attention(q, k, v, cos, sin, cfg, qkn)
+        else:
+            out = forward_stages(q, k, v, cos, sin, cfg, summ, qkn, dense_route=True)["out"]
+    if equiv or getattr(cfg, "aux_w", 1.0) == 0.0:
         return out, q.new_zeros(())
-    if equiv:
-        return equiv_attention(q, k, v, cos, sin, cfg, qkn), q.new_zeros(())
-    out = forward_stages(q, k, v, cos, sin, cfg, summ, qkn, dense_route=True)["out"]
-    return out, q.new_zeros(())
+    return out, aux_kl(q, k, v, cos, sin, cfg, summ, qkn)
 
 
 def hba_attention_fused(q, k, v, cos, sin, cfg, summ, qkn):
-    """Forward of the reference's fused path (identical math to dense)."""
+    """The reference's fused training path (the same math as dense: outputs
+    agree to rounding, and its chunked teacher gives the same aux)."""
     return hba_attention_dense(q, k, v, cos, sin, cfg, summ, qkn)
 
 

@@ -271,6 +271,35 @@ int hba_summarize_filled(int dtype, const void *kc_pages, const int32_t *page_ta
                          void *summ_pages, void *stream);
 
 /*
+ * The summarizer auxiliary loss of the training path (aux-KL,
+ * hba_attention_dense src/hba/attention.py:366-389; the fused path's chunked
+ * teacher :478-549, the same value) and, when dprobes / dproj are given, its
+ * gradient with respect to the summarizer's probes [Hkv, m, d] and proj
+ * [Hkv, d, d] (fp32; the only gradient it has: the routing runs on detached
+ * q/k, so nothing flows into q, k or v).
+ *   q       [B, n, Hq, d] raw queries (element strides; QKNorm'd inside with
+ *           q_gain, NULL = qknorm off), kc [B, Hkv, n, d] content keys and
+ *           S0 [B, Hkv, n/Bk, m, d] their summaries (hba_prep_keys,
+ *           hba_summarize);
+ *   scale_u the union scale of the teacher's content logits (_content_qk),
+ *   scale_r route_topk's scale of the block scores;
+ *   aux     one fp32 on the device: -mean over (batch, KV head, queries with
+ *           a candidate block) of sum_b p*_b log softmax_b(bsc), 0 when no
+ *           query has a candidate.
+ * Work is O(n^2 d) (the teacher scores every candidate key).  ws: at least
+ * hba_aux_kl_workspace_size bytes, 16-byte aligned, no initial contents.
+ * Every reduction runs in a fixed order (deterministic).  Bk = 64, m <= 8,
+ * Hq / Hkv <= 16.
+ */
+int hba_aux_kl_workspace_size(int dtype, int64_t B, int64_t n, int64_t Hq, int64_t Hkv, int64_t d,
+                              int64_t m, int64_t Bk, size_t *bytes);
+int hba_aux_kl(int dtype, const void *q, const int64_t q_strides[3], const float *q_gain, float eps,
+               const void *kc, const void *S0, const float *probes, const float *proj, int64_t B,
+               int64_t n, int64_t Hq, int64_t Hkv, int64_t d, int64_t m, int64_t Bk, int64_t W,
+               float scale_u, float scale_r, void *ws, size_t ws_bytes, float *aux,
+               float *dprobes, float *dproj, void *stream);
+
+/*
  * Scratch bytes hba_decode_fwd needs for these sizes (max_len = max seq_len).
  * The workspace must be zero-filled before its first call: it opens with
  * per-(sequence, KV head) completion counters of the one-launch bf16 step,

@@ -281,7 +281,7 @@ def aux_teacher(qc, kc, n_kv, scale, Bk, W):
     return out
 
 
-def aux_kl(qc, kc, probes, proj, n_kv, scale_u, scale_r, Bk, W):
+def aux_kl(qc, kc, probes, proj, n_kv, scale_u, scale_r, Bk, W, S0_scores=None, dtype="f32"):
     """The summarizer auxiliary loss of hba_attention_dense (attention.py:
     366-389) and its gradients, float64.  qc [B, n, Hq, d], kc [B, n, Hkv, d]
     content q/k; scale_u the union (teacher) scale, scale_r the routing scale.
@@ -294,7 +294,11 @@ def aux_kl(qc, kc, probes, proj, n_kv, scale_u, scale_r, Bk, W):
     Gradients reach only probes and proj (the routing runs on detached q/k):
     d aux / d bsc_c = (softmax_c * sum_b p*_b - p*_c) / N, the max over slots
     passes it evenly to the tied slots, and the summariser's einsums and
-    softmax are differentiated by hand.  Returns (aux, dprobes, dproj, pstar)."""
+    softmax are differentiated by hand.  S0_scores: summaries [B, Hkv, nb, m, d]
+    to score the blocks with instead of the exact ones (a kernel's stored,
+    rounded summaries); the summarizer's backward always uses the exact
+    forward.  dtype "bf16": the grouped query is rounded to bf16 as
+    grouped_query does on bf16 tensors.  Returns (aux, dprobes, dproj, pstar)."""
     B, n, Hq, d = qc.shape
     G, nb = Hq // n_kv, n // Bk
     m = probes.shape[1]
@@ -302,14 +306,14 @@ def aux_kl(qc, kc, probes, proj, n_kv, scale_u, scale_r, Bk, W):
     vq = cand.any(-1)
     pstar = aux_teacher(qc, kc, n_kv, scale_u, Bk, W)
     pr, pj = probes.astype(np.float64), proj.astype(np.float64)
-    qg = qc.astype(np.float64).reshape(B, n, n_kv, G, d).sum(3)            # [B, n, Hkv, d]
+    qg = np.stack([grouped_query(qc[b], n_kv, dtype) for b in range(B)]).transpose(0, 2, 1, 3).astype(np.float64)
     kb = kc[:, : nb * Bk].astype(np.float64).reshape(B, nb, Bk, n_kv, d)
     logit = np.einsum("hmd,bckhd->bhcmk", pr, kb) * d ** -0.5               # [B,Hkv,nb,m,Bk]
     att = np.exp(logit - logit.max(-1, keepdims=True))
     att /= att.sum(-1, keepdims=True)
     Sp = np.einsum("bhcmk,bckhd->bhcmd", att, kb)                           # pooled
     S0 = np.einsum("bhcmd,hde->bhcme", Sp, pj)
-    raw = np.einsum("bihd,bhcmd->bhicm", qg, S0)                            # [B,Hkv,n,nb,m]
+    raw = np.einsum("bihd,bhcmd->bhicm", qg, S0 if S0_scores is None else S0_scores.astype(np.float64))
     mx = raw.max(-1)
     bsc = np.where(cand[None, None], mx * scale_r, -np.inf)
     N = B * n_kv * int(vq.sum())

@@ -491,6 +491,109 @@ def test_equiv_rejects_ragged_length(dev):
                                    prm, prm, None, equiv=True)
 
 
+# ---------------------------------------------------------------- aux-KL -----
+def _aux_setup(dev, case_cfg, inp, dt):
+    cfg = hba_amd.HBAConfig(**case_cfg, aux_w=1.0)
+    T = TDT[dt]
+    q, k, v = (torch.from_numpy(inp[x]).to(T).to(dev).requires_grad_(True) for x in ("q", "k", "v"))
+    summ = hba_amd.SlotSummarizer(cfg).to(dev)
+    qkn = hba_amd.QKNorm(cfg).to(dev)
+    with torch.no_grad():
+        summ.probes.copy_(torch.from_numpy(inp["probes"]))
+        summ.proj.copy_(torch.from_numpy(inp["proj"]))
+        qkn.q.gain.copy_(torch.from_numpy(inp["q_gain"]))
+        qkn.k.gain.copy_(torch.from_numpy(inp["k_gain"]))
+    cos, sin = hba_amd.rope_tables(q.shape[1], cfg.head_dim, cfg.rope_theta, dev)
+    return cfg, q, k, v, summ, qkn, cos, sin
+
+
+def test_aux_kl_matches_reference_golden(dev):
+    """The reference's own aux-KL and its gradients into probes and proj
+    (golden_aux.npz, written by the reference's hba_attention_dense and
+    autograd; d = 64, 64-key blocks, 4/2 heads, n = 1024, W = 128, fp32),
+    here from hba_attention_dense / _fused on the GPU; the gradient-isolation
+    rule (gates.py:129-167): aux reaches no q/k/v, the output reaches no
+    summarizer parameter."""
+    import make_golden as MG
+    z = np.load(f"{MG.HERE}/golden_aux.npz")
+    case = MG.CASES["d64"]
+    inp = MG.gen_inputs(case)
+    cfg, q, k, v, summ, qkn, cos, sin = _aux_setup(dev, case["cfg"], inp, "f32")
+    for fn in (hba_amd.hba_attention_dense, hba_amd.hba_attention_fused):
+        summ.zero_grad(set_to_none=True)
+        out, aux = fn(q, k, v, cos, sin, cfg, summ, qkn)
+        aux.backward()
+        torch.cuda.synchronize()
+        ga = float(z["d64_aux"])
+        assert abs(aux.item() - ga) <= 1e-5 * abs(ga), (aux.item(), ga)
+        for p_, key in ((summ.probes, "d64_dprobes"), (summ.proj, "d64_dproj")):
+            ref = z[key]
+            err = np.abs(f(p_.grad) - ref).max() / np.abs(ref).max()
+            assert err <= 1e-4, (key, err)
+        assert q.grad is None and k.grad is None and v.grad is None
+        summ.zero_grad(set_to_none=True)
+        out.sum().backward()
+        assert summ.probes.grad is None and summ.proj.grad is None
+        assert q.grad is not None and q.grad.abs().max().item() > 0
+        q.grad = k.grad = v.grad = None
+
+
+# (aux relative, gradient relative to its largest element).  Against the
+# oracle scoring blocks with the kernels' own summaries, both dtypes measured
+# <= 5e-8 (aux) and 1.4e-6 (gradients).  bf16 against the exact (unrounded)
+# summaries: bf16 storage of S0 moves the slot argmax of near-tied slots,
+# which moved the probe gradients by up to 4.9% and the proj gradients by
+# 1.4% (measured), the aux by 1.5e-6.
+AUX_TOL = {"f32": (1e-6, 2e-5), "bf16": (1e-6, 2e-5)}
+AUX_BF16_EXACT_S0_TOL = (2e-5, 8e-2)
+
+
+@pytest.mark.parametrize("dt,d,Hq,Hkv,qknorm,B", [("f32", 64, 14, 2, True, 2), ("bf16", 64, 14, 2, True, 1),
+                                                  ("f32", 128, 28, 4, False, 1), ("bf16", 128, 28, 4, True, 1)])
+def test_aux_kl_matches_oracle(dev, dt, d, Hq, Hkv, qknorm, B):
+    """hba_aux_kl at the kernels' geometries (G = 7, d = 64 and 128, qknorm
+    on and off, B = 2) against the oracle's float64 aux and gradients on the
+    same storage-rounded content q/k (n = 2048, W = 512: 1535 queries with
+    candidates, up to 23 candidate blocks)."""
+    n, W, m = 2048, 512, 4
+    rs = np.random.RandomState(7 + d + B)
+    inp = dict(q=rs.standard_normal((B, n, Hq, d)).astype(np.float32),
+               k=rs.standard_normal((B, n, Hkv, d)).astype(np.float32),
+               v=rs.standard_normal((B, n, Hkv, d)).astype(np.float32),
+               probes=(rs.standard_normal((Hkv, m, d)) * d ** -0.5).astype(np.float32),
+               proj=(np.eye(d)[None].repeat(Hkv, 0) + rs.standard_normal((Hkv, d, d)) * 0.02).astype(np.float32),
+               q_gain=(d ** 0.25 * rs.uniform(0.8, 1.2, Hq)).astype(np.float32),
+               k_gain=(d ** 0.25 * rs.uniform(0.8, 1.2, Hkv)).astype(np.float32))
+    ccfg = dict(n_heads=Hq, n_kv=Hkv, head_dim=d, window=W, sinks=4, k_blocks=8, slots=m, qknorm=qknorm,
+                native_ctx=1024)
+    cfg, q, k, v, summ, qkn, cos, sin = _aux_setup(dev, ccfg, inp, dt)
+    aux = hba_amd.aux_kl(q, k, v, cos, sin, cfg, summ, qkn)
+    aux.backward()
+    torch.cuda.synchronize()
+    ocfg = O.Cfg(**ccfg)
+    qc, kc, su = O.content_qk(f(q), f(k), ocfg, inp["q_gain"], inp["k_gain"], 1e-6, n, dt)
+    kch, _, _ = ops.prep_keys(k.detach(), v.detach(), qkn.k.gain if qknorm else None, 1e-6, cos, sin)
+    S0k = f(ops.summarize(kch, summ.probes.detach(), summ.proj.detach()))       # the kernels' summaries
+    for S0s, (ta, tg) in ((S0k, AUX_TOL[dt]), (None, AUX_BF16_EXACT_S0_TOL if dt == "bf16" else AUX_TOL[dt])):
+        ref, dpr, dpj, _ = O.aux_kl(qc, kc, inp["probes"], inp["proj"], Hkv, su, O.route_scale(ocfg, d), 64, W,
+                                    S0_scores=S0s, dtype=dt)
+        errs = (abs(aux.item() - ref) / abs(ref), np.abs(f(summ.probes.grad) - dpr).max() / np.abs(dpr).max(),
+                np.abs(f(summ.proj.grad) - dpj).max() / np.abs(dpj).max())
+        print(dt, d, qknorm, B, "kernel S0" if S0s is not None else "exact S0", [f"{e:.2e}" for e in errs])
+        assert errs[0] <= ta and errs[1] <= tg and errs[2] <= tg, errs
+
+
+def test_aux_kl_without_candidates_is_zero(dev):
+    """n <= W + 2*64 - 1: no query has a candidate block; aux and its
+    gradients are 0 (the reference's graph-free zero, attention.py:382-388)."""
+    cfg, x, prm, cos, sin = make(dev, "bf16", n=512, W=512, k=4)
+    summ = hba_amd.SlotSummarizer(cfg).to(dev)
+    aux = hba_amd.aux_kl(x["q"], x["k"], x["v"], cos, sin, cfg, summ, prm)
+    aux.backward()
+    assert aux.item() == 0.0
+    assert summ.probes.grad.abs().max().item() == 0.0 and summ.proj.grad.abs().max().item() == 0.0
+
+
 # -------------------------------------------------------------- backward -----
 # gates.py:247 holds input gradients to 2e-3 relative to their magnitude
 # (fp32).  bf16 storage of q/k/v and of the forward's QKNorm/RoPE rows moves
