@@ -594,6 +594,74 @@ def test_aux_kl_without_candidates_is_zero(dev):
     assert summ.probes.grad.abs().max().item() == 0.0 and summ.proj.grad.abs().max().item() == 0.0
 
 
+# ------------------------------------------------------------ model layer ----
+def test_model_layer_modes_match_cpu_reference(dev):
+    """HBAAttention (the attention branch of model.py:118-140: projections,
+    QKNorm, the mode switch) on the GPU in fp32 against the same layer on the
+    CPU over the oracle's torch restatements: "train" (hba_attention_dense,
+    attention.py:306-356) with its output, the gradients of every projection
+    weight and bias and of the QKNorm gains under autograd, and the aux-KL
+    against the oracle; "eval" / "eval_hier" / "equiv" outputs."""
+    import copy
+
+    from oracle import hba_cpu_torch as CT
+    cfg = hba_amd.HBAConfig(n_heads=4, n_kv=2, head_dim=64, window=256, sinks=4, k_blocks=4, slots=4,
+                            native_ctx=512, fanout=4, beam=2)
+    B, n, hidden, d = 1, 1024, 128, 64
+    torch.manual_seed(3)
+    cpu = hba_amd.HBAAttention(cfg, hidden)
+    with torch.no_grad():
+        cpu.qknorm.q.gain.copy_(d ** 0.25 * (0.8 + 0.4 * torch.rand(4)))
+        cpu.qknorm.k.gain.copy_(d ** 0.25 * (0.8 + 0.4 * torch.rand(2)))
+    gpu = copy.deepcopy(cpu).to(dev)
+    a = torch.randn(B, n, hidden)
+    cos, sin = hba_amd.rope_tables(n, d, cfg.rope_theta, "cpu")
+    cd, sd = cos.to(dev), sin.to(dev)
+    g = torch.randn(B, n, hidden)
+    og, aux = gpu(a.to(dev), cd, sd, mode="train")
+    ((og * g.to(dev)).sum() + aux).backward()          # aux reaches only the summarizer
+    q = cpu.q_proj(a).view(B, n, 4, d)
+    k = cpu.k_proj(a).view(B, n, 2, d)
+    v = cpu.v_proj(a).view(B, n, 2, d)
+    ref = CT.dense_forward(q, k, v, cos, sin, cfg, cpu.summarizer.probes.detach(), cpu.summarizer.proj.detach(),
+                           cpu.qknorm.q.gain, cpu.qknorm.k.gain, 1e-6)
+    oc = cpu.o_proj(ref.reshape(B, n, 4 * d))
+    (oc * g).sum().backward()
+    torch.cuda.synchronize()
+    assert (og.cpu() - oc).abs().max().item() <= 1e-4 * oc.abs().max().item()
+    for name, pc in cpu.named_parameters():
+        if "summarizer" in name:
+            continue
+        pg = dict(gpu.named_parameters())[name]
+        rel = (pg.grad.cpu() - pc.grad).abs().max().item() / pc.grad.abs().max().item()
+        assert rel <= 2e-3, (name, rel)
+    ocfg = O.Cfg(n_heads=4, n_kv=2, head_dim=64, window=256, sinks=4, k_blocks=4, slots=4, native_ctx=512)
+    qc, kc, su = O.content_qk(q.detach().numpy(), k.detach().numpy(), ocfg, f(cpu.qknorm.q.gain),
+                              f(cpu.qknorm.k.gain), 1e-6, n, "f32")
+    aref, dpr, _, _ = O.aux_kl(qc, kc, f(cpu.summarizer.probes), f(cpu.summarizer.proj), 2, su,
+                               O.route_scale(ocfg, d), 64, 256)
+    assert abs(aux.item() - aref) <= 1e-5 * abs(aref)
+    assert np.abs(f(gpu.summarizer.probes.grad) - dpr).max() <= 1e-4 * np.abs(dpr).max()
+    with torch.no_grad():
+        x = a.to(dev)
+        for mode in ("eval", "eval_hier", "equiv"):
+            o, none = gpu(x, cd, sd, mode=mode)
+            assert none is None
+            qg, kg, vg = (t.view(B, n, -1, d) for t in (gpu.q_proj(x), gpu.k_proj(x), gpu.v_proj(x)))
+            direct = hba_amd.hba_attention_eval(qg, kg, vg, cd, sd, cfg, gpu.summarizer, gpu.qknorm, None,
+                                                hier=mode == "eval_hier", equiv=mode == "equiv")
+            assert torch.equal(o, gpu.o_proj(direct.reshape(B, n, 4 * d))), mode
+        rows = np.array([0, 5, 300, 700, n - 1])
+        o_eval = gpu(x, cd, sd, mode="eval")[0]
+        r_eval = CT.gathered_forward(q.detach(), k.detach(), v.detach(), cos, sin, cfg,
+                                     cpu.summarizer.probes.detach(), cpu.summarizer.proj.detach(),
+                                     cpu.qknorm.q.gain.detach(), cpu.qknorm.k.gain.detach(), 1e-6)
+        r_eval = cpu.o_proj(r_eval.reshape(B, n, 4 * d))
+        assert (o_eval.cpu()[:, rows] - r_eval[:, rows]).abs().max().item() <= 1e-4 * r_eval.abs().max().item()
+    with pytest.raises(ValueError, match="unknown mode"):
+        gpu(x, cd, sd, mode="decode")
+
+
 # -------------------------------------------------------------- backward -----
 # gates.py:247 holds input gradients to 2e-3 relative to their magnitude
 # (fp32).  bf16 storage of q/k/v and of the forward's QKNorm/RoPE rows moves
