@@ -45,7 +45,7 @@ ATTN_KERNELS = "hba_attn_fwd = attn_win_kernel<64,2> + attn_routed_kernel<64,2>"
 # FETCH_SIZE and WRITE_SIZE summed over the two kernels, each divided by the
 # counter's reading per byte of a plain device copy (python bench.py
 # --copy-probe 1024); profiles/hba_attn_32k_traffic.md.
-ATTN_TRAFFIC_BYTES = 767784019
+ATTN_TRAFFIC_BYTES = 769909293
 
 
 def cpu_model():
@@ -373,7 +373,7 @@ def bench_bwd32k(dev, reps=5):
     import hba_amd
     from hba_amd import synth
     cfg, x, prm, cos, sin = layer_setup(dev)
-    cfg.aux_w = 0.0          # frozen summarizers: no aux-KL teacher (not provided by this backend)
+    cfg.aux_w = 0.0          # the attention backward alone; the aux-KL is timed below
     q, k, v = (x[t].clone().requires_grad_(True) for t in ("q", "k", "v"))
     gq = x["q_gain"].clone().requires_grad_(True)
     gk = x["k_gain"].clone().requires_grad_(True)
@@ -395,12 +395,34 @@ def bench_bwd32k(dev, reps=5):
     flop = 2.5 * synth.attention_flops(w["batch"], w["seq_len"], w["q_heads"], w["head_dim"], w["sinks"],
                                        w["window"], w["block"], w["top_k"])
     tflops = flop / (ms * 1e-3) / 1e12
+    # the summarizer's aux-KL (teacher, KL, gradients into probes and proj) at the same size
+    pr = x["probes"].clone().requires_grad_(True)
+    pj = x["proj"].clone().requires_grad_(True)
+    summ = synth.Params(gq, gk, pr, pj)
+    qd, kd, vd = x["q"], x["k"], x["v"]
+    for _ in range(2):
+        hba_amd.aux_kl(qd, kd, vd, cos, sin, cfg, summ, qkn)
+    torch.cuda.synchronize()
+    ea = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+    ea[0].record()
+    for r in range(3):
+        hba_amd.aux_kl(qd, kd, vd, cos, sin, cfg, summ, qkn)
+        ea[r + 1].record()
+    torch.cuda.synchronize()
+    aux_ms = float(sorted(ea[r].elapsed_time(ea[r + 1]) for r in range(3))[1])
+    n_, Bk_, W_ = w["seq_len"], w["block"], w["window"]
+    cand_keys = sum(max(0, (i - W_ + 1) // Bk_ - 1) * Bk_ for i in range(n_) if i - W_ + 1 >= 2 * Bk_)
+    teacher_flop = 2.0 * w["head_dim"] * w["q_heads"] * cand_keys * w["batch"]
     return {"metric": "HBA layer backward tokens/s at 32K (dq, dk, dv, QKNorm gain grads; selection fixed)",
             "config": {"workload": "hba_layer_bwd_32k", "batch": 1, "seq_len": w["seq_len"], "q_heads": w["q_heads"],
                        "kv_heads": w["kv_heads"], "head_dim": w["head_dim"], "top_k": w["top_k"]},
             "tokens_per_s": round(w["seq_len"] / (ms * 1e-3), 1), "ms": round(ms, 3), "flop": flop,
             "achieved_TFLOPs": round(tflops, 2), "mfma_frac": round(tflops / PEAK_BF16_TFLOPS, 5),
             "timing": f"median of {reps} backward calls",
+            "aux_kl": {"ms": round(aux_ms, 3), "teacher_flop": teacher_flop,
+                       "teacher_TFLOPs": round(teacher_flop / (aux_ms * 1e-3) / 1e12, 2),
+                       "what": "hba_aux_kl: QKNorm'd queries, block scores, the teacher's block LSEs on MFMA over "
+                               "every candidate key, the KL rows, d aux / d probes and d proj (median of 3)"},
             "kernels": "bwd_kt (transposed keys) + bwd_dq_mfma (16/G queries per wave, 64-key units on MFMA) + "
                        "bwd_dkv_mfma (one workgroup per KV head, 64-key block and 4096-row range, 64-pair tiles "
                        "on MFMA; a second launch for the sink keys) + bwd_dkv_fin (rope^T, QKNorm backward)"}

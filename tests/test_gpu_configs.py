@@ -103,7 +103,11 @@ def test_fp32_4096_selection_exact_and_every_row(dev, sharp):
     err = np.abs(f(r["out"])[0] - ref).max()
     assert err <= 1e-5, err
     # dense: route_topk's scale has no temperature; at n <= native_ctx it is the same selection
-    assert np.abs(f(out_d)[0] - ref).max() <= 1e-5 and float(aux) == 0.0
+    assert np.abs(f(out_d)[0] - ref).max() <= 1e-5
+    # and its aux-KL (aux_w = 1) against the oracle's, on the same summaries
+    aref = O.aux_kl(P.qc[None], P.kc[None], f(x["probes"]), f(x["proj"]), Hkv, r["scale"],
+                    hba_amd.route_scale(cfg, d), 64, cfg.window, S0_scores=S0[None], dtype="f32")[0]
+    assert abs(float(aux) - aref) <= 1e-5 * abs(aref), (float(aux), aref)
 
 
 # ---------------------------------------------------------- bf16 at 32K ----

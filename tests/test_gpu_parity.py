@@ -396,7 +396,11 @@ def test_end_to_end_eval_and_dense_vs_oracle(dev, dt):
     ref_d, _ = O.forward_dense(*args, rows=rows, S0=S0)
     assert np.abs(f(out_e)[0][rows] - ref_e[0]).max() <= TOL[dt]
     assert np.abs(f(out_d)[0][rows] - ref_d[0]).max() <= TOL[dt]
-    assert float(aux) == 0.0
+    # aux_w = 1 (the default): the summarizer's aux-KL comes back with the output
+    qc, kc, su = O.content_qk(f(x["q"]), f(x["k"]), cfg, f(x["q_gain"]), f(x["k_gain"]), 1e-6, 2048, dt)
+    aref = O.aux_kl(qc, kc, f(x["probes"]), f(x["proj"]), cfg.n_kv, su, O.route_scale(cfg, 64), 64, cfg.window,
+                    S0_scores=S0, dtype=dt)[0]
+    assert abs(float(aux) - aref) <= 1e-5 * abs(aref), (float(aux), aref)
 
 
 def test_strided_views_are_accepted(dev):
