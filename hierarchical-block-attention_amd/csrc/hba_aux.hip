@@ -19,10 +19,12 @@
 //   aux_qc      content queries qc = QKNorm(q) rounded to the storage type
 //   aux_scores  grouped queries qg (fp32) and bsc with the tied-slot masks
 //   aux_teacher per (query, head, candidate block) the block LSE of the
-//               content logits, on MFMA (16 keys x 16 (query, head) columns)
+//               content logits, on MFMA (16 keys x 16 (query, head) columns;
+//               bf16: 16 waves share each staged key block)
 //   aux_rows    per (query, KV head): p*, the row's KL term, d aux / d bsc
 //   aux_sum     aux = -(sum of row terms) / N, one workgroup, fixed order
 //   aux_dsum    d aux / d S0 = sum over queries of d bsc * tie share * qg
+//               (query segments, partials summed in order by aux_gsum)
 //   aux_sbwd    per block: the summariser's backward into per-block partial
 //               d probes / d proj
 //   aux_gsum    partials summed over blocks in a fixed order
@@ -34,10 +36,11 @@ namespace hba {
 namespace aux {
 
 constexpr int BK = 64;
-constexpr int BT = 8;           // blocks per aux_dsum workgroup
+
+constexpr int QS = 8;           // query segments of aux_dsum (partials summed in order)
 
 struct Ws {
-    size_t qc, qg, bsc, ties, L, rowt, dS0, pproj, pprb, total;
+    size_t qc, qg, bsc, ties, L, rowt, dS0, pdS0, pproj, pprb, total;
 };
 
 inline size_t up256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -53,6 +56,7 @@ inline Ws layout(int dtype, int64_t B, int64_t n, int64_t Hq, int64_t Hkv, int64
     w.L = o;     o += up256((size_t)B * Hkv * n * G * nb * 4);
     w.rowt = o;  o += up256((size_t)B * Hkv * n * 4);
     w.dS0 = o;   o += up256((size_t)B * Hkv * nb * m * d * 4);
+    w.pdS0 = o;  o += up256((size_t)QS * B * Hkv * nb * m * d * 4);
     w.pproj = o; o += up256((size_t)B * nb * Hkv * d * d * 4);
     w.pprb = o;  o += up256((size_t)B * nb * Hkv * m * d * 4);
     w.total = o;
@@ -250,6 +254,87 @@ __global__ __launch_bounds__(256) void aux_teacher_kernel(const typename St<DT>:
     }
 }
 
+// bf16 teacher with the key blocks shared: a workgroup of 16 waves covers
+// 16 * QPW consecutive queries (each wave its 16 columns, as above) and
+// streams the candidate blocks of its last query once through a two-slot
+// LDS buffer (rows padded to D + 8 bf16, so the 16 rows of an A-fragment
+// read fall in distinct banks); the next block's 16-byte chunks are loaded
+// into registers while the current one is used.  A wave skips the blocks
+// past its own last query's candidates but meets every barrier.  Logits go
+// through exp2 with scale * log2(e) folded into one multiply.
+template <int D>
+__global__ __launch_bounds__(1024) void aux_teacher_bf16_kernel(const bf16_t *__restrict__ qc,
+                                                                const bf16_t *__restrict__ kc, int64_t n,
+                                                                int64_t Hq, int64_t Hkv, int64_t W, float scale_u,
+                                                                float *__restrict__ L) {
+    constexpr int NW = 16, NKS = D / 32, ROW = D + 8, CH = BK * D / 8;   // CH 16-byte chunks per block
+    static_assert(CH <= NW * 64, "one chunk per thread");
+    __shared__ __align__(16) bf16_t kb[2][BK * ROW];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int l16 = lane & 15, lg = lane >> 4;
+    const int64_t g = blockIdx.y, b = blockIdx.z;
+    const int G = (int)(Hq / Hkv), QPW = 16 / G;
+    const int64_t nb = n / BK;
+    const int64_t i0 = (int64_t)blockIdx.x * NW * QPW;
+    const int64_t ilast = (i0 + NW * QPW - 1 < n) ? i0 + NW * QPW - 1 : n - 1;
+    const int64_t bmax = cand_bmax(ilast, BK, W);          // uniform over the workgroup
+    if (bmax < 1) return;
+    const int64_t i0w = i0 + (int64_t)w * QPW;
+    const int64_t wlast = (i0w + QPW - 1 < n) ? i0w + QPW - 1 : n - 1;
+    const int64_t wmax = (i0w < n) ? cand_bmax(wlast, BK, W) : 0;
+    const int cq = l16 / G, ch = l16 % G;
+    const int64_t iq = i0w + cq;
+    const bool col_ok = l16 < QPW * G && iq < n;
+    const int64_t ic = col_ok ? iq : i0;
+    const int64_t col_bmax = col_ok ? cand_bmax(iq, BK, W) : 0;
+    const bf16_t *qrow = qc + ((b * n + ic) * Hq + g * G + ch) * D;
+    float *Lrow = L + (((b * Hkv + g) * n + ic) * G + ch) * nb;
+    bf16x8 qop[NKS];
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+        const uint4 u = col_ok ? *reinterpret_cast<const uint4 *>(qrow + 32 * ks + 8 * lg) : make_uint4(0, 0, 0, 0);
+        qop[ks] = __builtin_bit_cast(bf16x8, u);
+    }
+    const bf16_t *kg = kc + (b * Hkv + g) * n * D;
+    const bool ld = tid < CH;
+    const int r = tid / (D / 8), cc = tid % (D / 8);
+    uint4 reg = ld ? *reinterpret_cast<const uint4 *>(kg + (BK + r) * D + 8 * cc) : make_uint4(0, 0, 0, 0);
+    const float s2 = scale_u * 1.4426950408889634f;       // logits in log2 units
+    for (int64_t c = 1; c <= bmax; ++c) {
+        bf16_t *slot = kb[c & 1];
+        if (ld) *reinterpret_cast<uint4 *>(slot + r * ROW + 8 * cc) = reg;
+        __syncthreads();   // this block staged; every wave is past block c - 2, which used this slot
+        if (ld && c + 1 <= bmax) reg = *reinterpret_cast<const uint4 *>(kg + ((c + 1) * BK + r) * D + 8 * cc);
+        if (c > wmax) continue;
+        f32x4 acc[4];
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+            acc[mt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            const bf16_t *krow = slot + (mt * 16 + l16) * ROW + 8 * lg;
+#pragma unroll
+            for (int ks = 0; ks < NKS; ++ks)
+                acc[mt] = mfma_bf16(__builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4 *>(krow + 32 * ks)),
+                                    qop[ks], acc[mt]);
+        }
+        float mx = -INFINITY;
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) mx = fmaxf(mx, acc[mt][e]);
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float off = mx * s2;
+        float se = 0.0f;
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) se += __builtin_amdgcn_exp2f(fmaf(acc[mt][e], s2, -off));
+        se += __shfl_xor(se, 16, 64);
+        se += __shfl_xor(se, 32, 64);
+        if (lg == 0 && col_ok && c <= col_bmax) Lrow[c] = (off + __log2f(se)) * 0.6931471805599453f;
+    }
+}
+
 // ---------------------------------------------------------------- rows -----
 // One wave per (b, g, i) with a candidate block: p* from the block LSEs, the
 // row's KL term (rowt), and d aux / d bsc written over bsc.  Head h's max and
@@ -338,60 +423,75 @@ __global__ __launch_bounds__(256) void aux_sum_kernel(const float *__restrict__ 
 }
 
 // ---------------------------------------------------------------- dS0 ------
-// Workgroup = (BT blocks, g, b): d aux / d S0[c, slot, :] = sum over the
-// candidate queries of c of d bsc[i, c] * scale_r * [slot ties the max] /
-// (number of tied slots) * qg[i, :], queries in ascending order.
+// d aux / d S0[c, slot, :] = sum over the candidate queries i of c of
+// d bsc[i, c] * scale_r / (number of tied slots) * qg[i, :], over the slots
+// that tie the max -- in practice one slot per (i, c).  Workgroup = (group
+// of 16/m blocks, query segment qs of QS, KV head g, batch b), 16 waves: wave
+// (bb, slot) owns that block's slot row, lane t its dims t and t + 64.  Per
+// chunk of 64 queries the grouped queries and the (coefficient, tie mask)
+// pairs are staged in LDS; a wave adds a query only when its slot is tied at
+// the max (a wave-uniform branch), in ascending query order.  The segment's
+// partial goes to pdS0[qs]; aux_gsum adds the QS partials in order.
 template <int D>
-__global__ __launch_bounds__(256) void aux_dsum_kernel(const float *__restrict__ dbsc,
-                                                       const uint8_t *__restrict__ ties,
-                                                       const float *__restrict__ qg, int64_t n, int64_t Hkv, int m,
-                                                       int64_t W, float scale_r, float *__restrict__ dS0) {
-    constexpr int OPT = BT * 8 * D / 256;          // outputs per thread, m <= 8
+__global__ __launch_bounds__(1024) void aux_dsum_kernel(const float *__restrict__ dbsc,
+                                                        const uint8_t *__restrict__ ties,
+                                                        const float *__restrict__ qg, int64_t n, int64_t Hkv, int m,
+                                                        int64_t W, float scale_r, float *__restrict__ pdS0) {
+    constexpr int DL = D / 64;                     // dims per lane
     __shared__ float qgs[64][D];
-    __shared__ float coef[64][BT][8];
-    const int tid = threadIdx.x;
-    const int64_t c0 = (int64_t)blockIdx.x * BT, g = blockIdx.y, b = blockIdx.z;
+    __shared__ float coef[64][16];
+    __shared__ uint8_t msk[64][16];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int bt = 16 / m;                         // blocks per workgroup
+    const int bb = w / m, sl = w % m;              // this wave's (block, slot); waves past bt*m idle
+    const int64_t c0 = (int64_t)blockIdx.x * bt, qs = blockIdx.y % QS, g = blockIdx.y / QS, b = blockIdx.z;
     const int64_t nb = n / BK;
     const int64_t bg = b * Hkv + g;
-    float acc[OPT];
+    const int64_t c = c0 + bb;
+    float acc[DL];
 #pragma unroll
-    for (int j = 0; j < OPT; ++j) acc[j] = 0.0f;
-    const int64_t ilo = (c0 + 1) * BK + W - 1;     // first candidate query of block c0
-    for (int64_t i0 = (ilo > 0 ? ilo : 0); i0 < n; i0 += 64) {
+    for (int u = 0; u < DL; ++u) acc[u] = 0.0f;
+    // this segment's 64-query chunks of the group's candidate queries
+    const int64_t ilo = (c0 + 1) * BK + W - 1;
+    const int64_t nch = (ilo < n) ? (n - ilo + 63) / 64 : 0;
+    const int64_t per = (nch + QS - 1) / QS;
+    const int64_t k0 = qs * per, k1 = (k0 + per < nch) ? k0 + per : nch;
+    for (int64_t kc_ = k0; kc_ < k1; ++kc_) {
+        const int64_t i0 = ilo + kc_ * 64;
         __syncthreads();   // the previous chunk is used
-        for (int e = tid; e < 64 * D; e += 256) {
+        for (int e = tid; e < 64 * D; e += 1024) {
             const int64_t i = i0 + e / D;
             qgs[e / D][e % D] = (i < n) ? qg[(bg * n + i) * D + e % D] : 0.0f;
         }
-        for (int e = tid; e < 64 * BT; e += 256) {
-            const int qi = e / BT, bb = e % BT;
-            const int64_t i = i0 + qi, c = c0 + bb;
+        for (int e = tid; e < 64 * bt; e += 1024) {
+            const int qi = e / bt, j = e % bt;
+            const int64_t i = i0 + qi, cj = c0 + j;
             float cf = 0.0f;
-            uint32_t mask = 0;
-            if (i < n && c < nb && c >= 1 && c <= cand_bmax(i, BK, W)) {
-                const int64_t o = (bg * n + i) * nb + c;
-                mask = ties[o];
-                cf = dbsc[o] * scale_r / (float)__builtin_popcount(mask);
+            uint32_t mk = 0;
+            if (i < n && cj < nb && cj >= 1 && cj <= cand_bmax(i, BK, W)) {
+                const int64_t o = (bg * n + i) * nb + cj;
+                mk = ties[o];
+                cf = dbsc[o] * scale_r / (float)__builtin_popcount(mk);
             }
-#pragma unroll
-            for (int sl = 0; sl < 8; ++sl) coef[qi][bb][sl] = ((mask >> sl) & 1u) ? cf : 0.0f;
+            coef[qi][j] = cf;
+            msk[qi][j] = (uint8_t)mk;
         }
         __syncthreads();
+        if (bb < bt) {
+            for (int qi = 0; qi < 64; ++qi) {
+                if ((msk[qi][bb] >> sl) & 1u) {   // uniform over the wave
+                    const float cf = coef[qi][bb];
 #pragma unroll
-        for (int j = 0; j < OPT; ++j) {
-            const int o = tid + 256 * j;
-            const int bb = o / (8 * D), sl = (o / D) % 8, t = o % D;
-            float a = acc[j];
-            for (int qi = 0; qi < 64; ++qi) a = fmaf(coef[qi][bb][sl], qgs[qi][t], a);
-            acc[j] = a;
+                    for (int u = 0; u < DL; ++u) acc[u] = fmaf(cf, qgs[qi][lane + 64 * u], acc[u]);
+                }
+            }
         }
     }
+    if (bb < bt && c < nb) {
+        float *dst = pdS0 + ((qs * Hkv * gridDim.z + bg) * nb + c) * m * D + sl * D;
+        // (pdS0 is [QS][B*Hkv][nb][m][D]; gridDim.z = B)
 #pragma unroll
-    for (int j = 0; j < OPT; ++j) {
-        const int o = tid + 256 * j;
-        const int bb = o / (8 * D), sl = (o / D) % 8, t = o % D;
-        const int64_t c = c0 + bb;
-        if (c < nb && sl < m) dS0[((bg * nb + c) * m + sl) * D + t] = acc[j];
+        for (int u = 0; u < DL; ++u) dst[lane + 64 * u] = acc[u];
     }
 }
 
@@ -537,7 +637,7 @@ extern "C" int hba_aux_kl(int dtype, const void *q, const int64_t q_strides[3], 
     const int64_t N = B * Hkv * nvalid;
     const float invN = N ? (float)(1.0 / (double)N) : 0.0f;
     float *qg = (float *)(w + L.qg), *bsc = (float *)(w + L.bsc), *Lb = (float *)(w + L.L);
-    float *rowt = (float *)(w + L.rowt), *dS0 = (float *)(w + L.dS0);
+    float *rowt = (float *)(w + L.rowt), *dS0 = (float *)(w + L.dS0), *pdS0 = (float *)(w + L.pdS0);
     float *pproj = (float *)(w + L.pproj), *pprb = (float *)(w + L.pprb);
     uint8_t *ties = (uint8_t *)(w + L.ties);
     const int64_t rows = B * Hkv * n;
@@ -563,9 +663,16 @@ extern "C" int hba_aux_kl(int dtype, const void *q, const int64_t q_strides[3], 
                            (unsigned)B), dim3(256), 0, s, (const T *)qc, (const T *)S0, n, Hq, Hkv, (int)m, W, \
                            scale_r, qg, bsc, ties);                                                      \
         const int64_t qpw = 16 / G;                                                                      \
-        hipLaunchKernelGGL((aux::aux_teacher_kernel<DT, D>),                                             \
-                           dim3((unsigned)((n + 4 * qpw - 1) / (4 * qpw)), (unsigned)Hkv, (unsigned)B),      \
-                           dim3(256), 0, s, (const T *)qc, (const T *)kc, n, Hq, Hkv, W, scale_u, Lb);    \
+        if (DT == 1)                                                                                     \
+            hipLaunchKernelGGL((aux::aux_teacher_bf16_kernel<D>),                                        \
+                               dim3((unsigned)((n + 16 * qpw - 1) / (16 * qpw)), (unsigned)Hkv,           \
+                               (unsigned)B), dim3(1024), 0, s, (const bf16_t *)qc, (const bf16_t *)kc, n,  \
+                               Hq, Hkv, W, scale_u, Lb);                                                 \
+        else                                                                                             \
+            hipLaunchKernelGGL((aux::aux_teacher_kernel<DT, D>),                                         \
+                               dim3((unsigned)((n + 4 * qpw - 1) / (4 * qpw)), (unsigned)Hkv,             \
+                               (unsigned)B), dim3(256), 0, s, (const T *)qc, (const T *)kc, n, Hq, Hkv, W, \
+                               scale_u, Lb);                                                             \
     } while (0)
     HBA_DISPATCH_DT_D(dtype, d, HBA_AUX_FWD);
 #undef HBA_AUX_FWD
@@ -576,9 +683,11 @@ extern "C" int hba_aux_kl(int dtype, const void *q, const int64_t q_strides[3], 
 #define HBA_AUX_BWD(DT, D)                                                                               \
     do {                                                                                                 \
         typedef St<DT>::T T;                                                                             \
-        hipLaunchKernelGGL((aux::aux_dsum_kernel<D>), dim3((unsigned)((nb + aux::BT - 1) / aux::BT),     \
-                           (unsigned)Hkv, (unsigned)B), dim3(256), 0, s, bsc, ties, qg, n, Hkv, (int)m, W, \
-                           scale_r, dS0);                                                                \
+        hipLaunchKernelGGL((aux::aux_dsum_kernel<D>), dim3((unsigned)((nb + 16 / m - 1) / (16 / m)),     \
+                           (unsigned)(Hkv * aux::QS), (unsigned)B), dim3(1024), 0, s, bsc, ties, qg, n, Hkv, \
+                           (int)m, W, scale_r, pdS0);                                                    \
+        hipLaunchKernelGGL(aux::aux_gsum_kernel, dim3((unsigned)((B * Hkv * nb * m * d + 255) / 256)),   \
+                           dim3(256), 0, s, pdS0, (int64_t)aux::QS, B * Hkv * nb * m * d, dS0);          \
         hipLaunchKernelGGL((aux::aux_sbwd_kernel<DT, D>), dim3((unsigned)nb, (unsigned)Hkv, (unsigned)B),  \
                            dim3(256), 0, s, (const T *)kc, probes, proj, dS0, n, Hkv, (int)m, pproj, pprb); \
     } while (0)
