@@ -255,17 +255,22 @@ __global__ __launch_bounds__(256) void aux_teacher_kernel(const typename St<DT>:
 }
 
 // bf16 teacher with the key blocks shared: a workgroup of 16 waves covers
-// 16 * QPW consecutive queries (each wave its 16 columns, as above) and
-// streams the candidate blocks of its last query once through a two-slot
-// LDS buffer (rows padded to D + 8 bf16, so the 16 rows of an A-fragment
-// read fall in distinct banks); the next block's 16-byte chunks are loaded
-// into registers while the current one is used.  A wave skips the blocks
-// past its own last query's candidates but meets every barrier.  Logits go
-// through exp2 with scale * log2(e) folded into one multiply.
+// 16 * CT * QPW consecutive queries (each wave CT column tiles of 16 columns,
+// QPW = 16/G queries x G heads each, so every A fragment read from LDS feeds
+// CT MFMAs) and streams the candidate blocks of its last query once through
+// a two-slot LDS buffer (rows padded to D + 8 bf16, so the 16 rows of an
+// A-fragment read fall in distinct banks); the next block's 16-byte chunks
+// are loaded into registers while the current one is used.  A wave skips the
+// blocks past its own last query's candidates but meets every barrier.
+// Logits go through exp2 with scale * log2(e) folded into one multiply.
+constexpr int TCT = 2;   // column tiles per teacher wave
+
 template <int D>
 __global__ __launch_bounds__(1024) void aux_teacher_bf16_kernel(const bf16_t *__restrict__ qc,
                                                                 const bf16_t *__restrict__ kc, int64_t n,
                                                                 int64_t Hq, int64_t Hkv, int64_t W, float scale_u,
+                                                                const float *__restrict__ qgain,
+                                                                const float *__restrict__ kgain,
                                                                 float *__restrict__ L) {
     constexpr int NW = 16, NKS = D / 32, ROW = D + 8, CH = BK * D / 8;   // CH 16-byte chunks per block
     static_assert(CH <= NW * 64, "one chunk per thread");
@@ -275,63 +280,86 @@ __global__ __launch_bounds__(1024) void aux_teacher_bf16_kernel(const bf16_t *__
     const int64_t g = blockIdx.y, b = blockIdx.z;
     const int G = (int)(Hq / Hkv), QPW = 16 / G;
     const int64_t nb = n / BK;
-    const int64_t i0 = (int64_t)blockIdx.x * NW * QPW;
-    const int64_t ilast = (i0 + NW * QPW - 1 < n) ? i0 + NW * QPW - 1 : n - 1;
+    const int64_t i0 = (int64_t)blockIdx.x * NW * TCT * QPW;
+    const int64_t ilast = (i0 + NW * TCT * QPW - 1 < n) ? i0 + NW * TCT * QPW - 1 : n - 1;
     const int64_t bmax = cand_bmax(ilast, BK, W);          // uniform over the workgroup
     if (bmax < 1) return;
-    const int64_t i0w = i0 + (int64_t)w * QPW;
-    const int64_t wlast = (i0w + QPW - 1 < n) ? i0w + QPW - 1 : n - 1;
+    const int64_t i0w = i0 + (int64_t)w * TCT * QPW;
+    const int64_t wlast = (i0w + TCT * QPW - 1 < n) ? i0w + TCT * QPW - 1 : n - 1;
     const int64_t wmax = (i0w < n) ? cand_bmax(wlast, BK, W) : 0;
     const int cq = l16 / G, ch = l16 % G;
-    const int64_t iq = i0w + cq;
-    const bool col_ok = l16 < QPW * G && iq < n;
-    const int64_t ic = col_ok ? iq : i0;
-    const int64_t col_bmax = col_ok ? cand_bmax(iq, BK, W) : 0;
-    const bf16_t *qrow = qc + ((b * n + ic) * Hq + g * G + ch) * D;
-    float *Lrow = L + (((b * Hkv + g) * n + ic) * G + ch) * nb;
-    bf16x8 qop[NKS];
+    const float s2 = scale_u * 1.4426950408889634f;       // logits in log2 units
+    // QKNorm bounds a column's logits by D * |gq| * |gk| * scale (the rows'
+    // norms are gain * sqrt(D)); when that bound is at most 60 in log2 units
+    // for every column of the wave, it is the column's shift (exp2 of the
+    // lowest logit stays a normal float) and no per-block max is needed
+    const float bcol = (qgain && kgain) ? (float)D * fabsf(qgain[g * G + ch]) * fabsf(kgain[g]) * s2 : INFINITY;
+    const bool fixed = __builtin_amdgcn_readfirstlane(
+                           (int)(__builtin_amdgcn_ballot_w64(!(bcol <= 60.0f)) == 0ull)) != 0;
+    bf16x8 qop[TCT][NKS];
+    bool col_ok[TCT];
+    int64_t col_bmax[TCT];
+    float *Lrow[TCT];
 #pragma unroll
-    for (int ks = 0; ks < NKS; ++ks) {
-        const uint4 u = col_ok ? *reinterpret_cast<const uint4 *>(qrow + 32 * ks + 8 * lg) : make_uint4(0, 0, 0, 0);
-        qop[ks] = __builtin_bit_cast(bf16x8, u);
+    for (int t = 0; t < TCT; ++t) {
+        const int64_t iq = i0w + t * QPW + cq;
+        col_ok[t] = l16 < QPW * G && iq < n;
+        const int64_t ic = col_ok[t] ? iq : i0;
+        col_bmax[t] = col_ok[t] ? cand_bmax(iq, BK, W) : 0;
+        const bf16_t *qrow = qc + ((b * n + ic) * Hq + g * G + ch) * D;
+        Lrow[t] = L + (((b * Hkv + g) * n + ic) * G + ch) * nb;
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) {
+            const uint4 u =
+                col_ok[t] ? *reinterpret_cast<const uint4 *>(qrow + 32 * ks + 8 * lg) : make_uint4(0, 0, 0, 0);
+            qop[t][ks] = __builtin_bit_cast(bf16x8, u);
+        }
     }
     const bf16_t *kg = kc + (b * Hkv + g) * n * D;
     const bool ld = tid < CH;
     const int r = tid / (D / 8), cc = tid % (D / 8);
     uint4 reg = ld ? *reinterpret_cast<const uint4 *>(kg + (BK + r) * D + 8 * cc) : make_uint4(0, 0, 0, 0);
-    const float s2 = scale_u * 1.4426950408889634f;       // logits in log2 units
     for (int64_t c = 1; c <= bmax; ++c) {
         bf16_t *slot = kb[c & 1];
         if (ld) *reinterpret_cast<uint4 *>(slot + r * ROW + 8 * cc) = reg;
         __syncthreads();   // this block staged; every wave is past block c - 2, which used this slot
         if (ld && c + 1 <= bmax) reg = *reinterpret_cast<const uint4 *>(kg + ((c + 1) * BK + r) * D + 8 * cc);
         if (c > wmax) continue;
-        f32x4 acc[4];
+        f32x4 acc[TCT][4];
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) {
-            acc[mt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int t = 0; t < TCT; ++t) acc[t][mt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
             const bf16_t *krow = slot + (mt * 16 + l16) * ROW + 8 * lg;
 #pragma unroll
-            for (int ks = 0; ks < NKS; ++ks)
-                acc[mt] = mfma_bf16(__builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4 *>(krow + 32 * ks)),
-                                    qop[ks], acc[mt]);
+            for (int ks = 0; ks < NKS; ++ks) {
+                const bf16x8 a = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4 *>(krow + 32 * ks));
+#pragma unroll
+                for (int t = 0; t < TCT; ++t) acc[t][mt] = mfma_bf16(a, qop[t][ks], acc[t][mt]);
+            }
         }
-        float mx = -INFINITY;
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
+        for (int t = 0; t < TCT; ++t) {
+            float off = bcol;
+            if (!fixed) {
+                float mx = -INFINITY;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) mx = fmaxf(mx, acc[mt][e]);
-        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        const float off = mx * s2;
-        float se = 0.0f;
+                for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
+                    for (int e = 0; e < 4; ++e) mx = fmaxf(mx, acc[t][mt][e]);
+                mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+                mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+                off = mx * s2;
+            }
+            float se = 0.0f;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) se += __builtin_amdgcn_exp2f(fmaf(acc[mt][e], s2, -off));
-        se += __shfl_xor(se, 16, 64);
-        se += __shfl_xor(se, 32, 64);
-        if (lg == 0 && col_ok && c <= col_bmax) Lrow[c] = (off + __log2f(se)) * 0.6931471805599453f;
+            for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) se += __builtin_amdgcn_exp2f(fmaf(acc[t][mt][e], s2, -off));
+            se += __shfl_xor(se, 16, 64);
+            se += __shfl_xor(se, 32, 64);
+            if (lg == 0 && col_ok[t] && c <= col_bmax[t]) Lrow[t][c] = (off + __log2f(se)) * 0.6931471805599453f;
+        }
     }
 }
 
@@ -339,7 +367,7 @@ __global__ __launch_bounds__(1024) void aux_teacher_bf16_kernel(const bf16_t *__
 // One wave per (b, g, i) with a candidate block: p* from the block LSEs, the
 // row's KL term (rowt), and d aux / d bsc written over bsc.  Head h's max and
 // sum of exponentials over the candidate blocks are kept by lane h.
-__global__ __launch_bounds__(256) void aux_rows_kernel(const float *__restrict__ L, int64_t B, int64_t n,
+__global__ __launch_bounds__(256) void aux_rows_kernel(float *__restrict__ L, int64_t B, int64_t n,
                                                        int64_t Hkv, int G, int64_t W, float invN,
                                                        float *__restrict__ bsc, float *__restrict__ rowt) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -352,34 +380,43 @@ __global__ __launch_bounds__(256) void aux_rows_kernel(const float *__restrict__
         if (lane == 0) rowt[r] = 0.0f;
         return;
     }
-    const float *Lr = L + r * G * nb;
+    float *Lr = L + r * G * nb;
     float *br = bsc + r * nb;
     float myM = 0.0f, myZ = 1.0f;
-    for (int h = 0; h < G; ++h) {
-        float mx = -INFINITY;
-        for (int64_t c = 1 + lane; c <= nbm; c += 64) mx = fmaxf(mx, Lr[h * nb + c]);
-        mx = wave_max(mx);
-        float z = 0.0f;
-        for (int64_t c = 1 + lane; c <= nbm; c += 64) z += expf(Lr[h * nb + c] - mx);
-        z = wave_sum(z);
+    for (int h = 0; h < G; ++h) {   // one pass per head: running max and sum of exponentials
+        float mx = -INFINITY, z = 0.0f;
+        for (int64_t c = 1 + lane; c <= nbm; c += 64) {
+            const float v = Lr[h * nb + c];
+            if (v > mx) {
+                z = z * expf(mx - v) + 1.0f;
+                mx = v;
+            } else {
+                z += expf(v - mx);
+            }
+        }
+        const float M = wave_max(mx);
+        const float Z = wave_sum((mx == -INFINITY) ? 0.0f : z * expf(mx - M));
         if (lane == h) {
-            myM = mx;
-            myZ = z;
+            myM = M;
+            myZ = Z;
         }
     }
-    auto pmass = [&](int64_t c) {   // called by the whole wave
+    // p(c), the group mean of the heads' block probabilities, replaces L[head 0][c]
+    // (each lane reads and writes only its own blocks c)
+    const int64_t cend = 1 + ((nbm + 63) / 64) * 64;   // uniform trip count for the shuffles
+    float p0 = 0.0f, top = -INFINITY;
+    for (int64_t c = 1 + lane; c < cend; c += 64) {
         float p = 0.0f;
         for (int h = 0; h < G; ++h) {
             const float Mh = __shfl(myM, h, 64), Zh = __shfl(myZ, h, 64);
             p += (c <= nbm) ? expf(Lr[h * nb + c] - Mh) / Zh : 0.0f;
         }
-        return p / (float)G;
-    };
-    const int64_t cend = 1 + ((nbm + 63) / 64) * 64;   // uniform trip count for the shuffles
-    float p0 = 0.0f, top = -INFINITY;
-    for (int64_t c = 1 + lane; c < cend; c += 64) {
-        p0 += pmass(c);
-        if (c <= nbm) top = fmaxf(top, br[c]);
+        if (c <= nbm) {
+            p /= (float)G;
+            Lr[c] = p;
+            p0 += p;
+            top = fmaxf(top, br[c]);
+        }
     }
     p0 = fmaxf(wave_sum(p0), 1e-9f);
     top = wave_max(top);
@@ -387,21 +424,19 @@ __global__ __launch_bounds__(256) void aux_rows_kernel(const float *__restrict__
     for (int64_t c = 1 + lane; c <= nbm; c += 64) zb += expf(br[c] - top);
     const float lse = top + logf(wave_sum(zb));
     float term = 0.0f, P = 0.0f;
-    for (int64_t c = 1 + lane; c < cend; c += 64) {
-        const float ps = pmass(c) / p0;
-        if (c <= nbm && ps > 0.0f) {
+    for (int64_t c = 1 + lane; c <= nbm; c += 64) {
+        const float ps = Lr[c] / p0;
+        if (ps > 0.0f) {
             term += ps * (br[c] - lse);
             P += ps;
         }
     }
     term = wave_sum(term);
     P = wave_sum(P);
-    for (int64_t c = 1 + lane; c < cend; c += 64) {
-        const float ps = pmass(c) / p0;
-        if (c <= nbm) {
-            const float soft = expf(br[c] - lse);
-            br[c] = (soft * P - (ps > 0.0f ? ps : 0.0f)) * invN;
-        }
+    for (int64_t c = 1 + lane; c <= nbm; c += 64) {
+        const float ps = Lr[c] / p0;
+        const float soft = expf(br[c] - lse);
+        br[c] = (soft * P - (ps > 0.0f ? ps : 0.0f)) * invN;
     }
     if (lane == 0) rowt[r] = term;
 }
@@ -616,7 +651,8 @@ extern "C" int hba_aux_kl_workspace_size(int dtype, int64_t B, int64_t n, int64_
     return HBA_OK;
 }
 
-extern "C" int hba_aux_kl(int dtype, const void *q, const int64_t q_strides[3], const float *q_gain, float eps,
+extern "C" int hba_aux_kl(int dtype, const void *q, const int64_t q_strides[3], const float *q_gain,
+                          const float *k_gain, float eps,
                           const void *kc, const void *S0, const float *probes, const float *proj, int64_t B,
                           int64_t n, int64_t Hq, int64_t Hkv, int64_t d, int64_t m, int64_t Bk, int64_t W,
                           float scale_u, float scale_r, void *ws, size_t ws_bytes, float *aux, float *dprobes,
@@ -665,9 +701,10 @@ extern "C" int hba_aux_kl(int dtype, const void *q, const int64_t q_strides[3], 
         const int64_t qpw = 16 / G;                                                                      \
         if (DT == 1)                                                                                     \
             hipLaunchKernelGGL((aux::aux_teacher_bf16_kernel<D>),                                        \
-                               dim3((unsigned)((n + 16 * qpw - 1) / (16 * qpw)), (unsigned)Hkv,           \
+                               dim3((unsigned)((n + 16 * aux::TCT * qpw - 1) / (16 * aux::TCT * qpw)),    \
+                                    (unsigned)Hkv,                                                       \
                                (unsigned)B), dim3(1024), 0, s, (const bf16_t *)qc, (const bf16_t *)kc, n,  \
-                               Hq, Hkv, W, scale_u, Lb);                                                 \
+                               Hq, Hkv, W, scale_u, q_gain, k_gain, Lb);                                 \
         else                                                                                             \
             hipLaunchKernelGGL((aux::aux_teacher_kernel<DT, D>),                                         \
                                dim3((unsigned)((n + 4 * qpw - 1) / (4 * qpw)), (unsigned)Hkv,             \

@@ -47,7 +47,7 @@ SIGNATURES = {
     "hba_kv_append_advance": [_i, _vp, _vp, _vp, _f, _vp, _vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i64,
                               _vp, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp],
     "hba_aux_kl_workspace_size": [_i, _i64, _i64, _i64, _i64, _i64, _i64, _i64, ctypes.POINTER(ctypes.c_size_t)],
-    "hba_aux_kl": [_i, _vp, _vp, _vp, _f, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+    "hba_aux_kl": [_i, _vp, _vp, _vp, _vp, _f, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                    _f, _f, _vp, ctypes.c_size_t, _vp, _vp, _vp, _vp],
     "hba_summarize_filled": [_i, _vp, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _vp],
     "hba_decode_workspace_size": [_i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,

@@ -182,7 +182,7 @@ class _AuxKL(torch.autograd.Function):
         B, n, Hq, dh = q.shape
         kc, _, _ = ops.prep_keys(k, v, k_gain, keps, cos, sin)
         S0 = ops.summarize(kc, probes.detach(), proj.detach())
-        aux, dpr, dpj = ops.aux_kl(q, q_gain, qeps, kc, S0, probes.detach(), proj.detach(), cfg.window,
+        aux, dpr, dpj = ops.aux_kl(q, q_gain, k_gain, qeps, kc, S0, probes.detach(), proj.detach(), cfg.window,
                                    union_scale(cfg, dh, n), route_scale(cfg, dh), want)
         ctx.save_for_backward(dpr, dpj)
         ctx.dtypes = (probes.dtype, proj.dtype)

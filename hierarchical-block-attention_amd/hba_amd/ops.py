@@ -495,7 +495,7 @@ def summarize_filled(kc_pages: Tensor, page_table: Tensor, seq_lens: Tensor, pro
     check(st, "hba_summarize_filled")
 
 
-def aux_kl(q, q_gain, eps, kc, S0, probes, proj, window, scale_u, scale_r, want_grad):
+def aux_kl(q, q_gain, k_gain, eps, kc, S0, probes, proj, window, scale_u, scale_r, want_grad):
     """The summarizer auxiliary loss (hba_aux_kl): returns (aux as a 0-d fp32
     tensor, d aux / d probes, d aux / d proj), the gradients None unless
     want_grad.  q [B, n, Hq, d] raw, kc [B, Hkv, n, d], S0 [B, Hkv, nb, m, d]."""
@@ -507,6 +507,7 @@ def aux_kl(q, q_gain, eps, kc, S0, probes, proj, window, scale_u, scale_r, want_
     if kc.shape != (B, Hkv, n, d) or kc.dtype != q.dtype or S0.dtype != q.dtype or S0.shape[2] != n // BLOCK:
         raise ValueError(f"kc {tuple(kc.shape)} / S0 {tuple(S0.shape)} do not match q {tuple(q.shape)}")
     qg = _f32c(q_gain, dev, Hq, "q_gain")
+    kg = _f32c(k_gain, dev, Hkv, "k_gain")
     pr = _f32c(probes, dev, Hkv * m * d, "probes")
     pj = _f32c(proj, dev, Hkv * d * d, "proj")
     nbytes = ctypes.c_size_t(0)
@@ -517,9 +518,9 @@ def aux_kl(q, q_gain, eps, kc, S0, probes, proj, window, scale_u, scale_r, want_
     dpr = torch.empty(Hkv, m, d, dtype=torch.float32, device=dev) if want_grad else None
     dpj = torch.empty(Hkv, d, d, dtype=torch.float32, device=dev) if want_grad else None
     with torch.cuda.device(dev):
-        st = lib().hba_aux_kl(_code(q), _p(q), strides3(q), _p(qg), eps, _p(kc), _p(S0), _p(pr), _p(pj), B, n, Hq,
-                              Hkv, d, m, BLOCK, window, scale_u, scale_r, _p(ws), ws.numel(), _p(aux), _p(dpr),
-                              _p(dpj), _stream(dev))
+        st = lib().hba_aux_kl(_code(q), _p(q), strides3(q), _p(qg), _p(kg), eps, _p(kc), _p(S0), _p(pr), _p(pj), B,
+                              n, Hq, Hkv, d, m, BLOCK, window, scale_u, scale_r, _p(ws), ws.numel(), _p(aux),
+                              _p(dpr), _p(dpj), _stream(dev))
     check(st, "hba_aux_kl")
     return aux[0], dpr, dpj
 

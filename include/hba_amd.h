@@ -278,7 +278,8 @@ int hba_summarize_filled(int dtype, const void *kc_pages, const int32_t *page_ta
  * [Hkv, d, d] (fp32; the only gradient it has: the routing runs on detached
  * q/k, so nothing flows into q, k or v).
  *   q       [B, n, Hq, d] raw queries (element strides; QKNorm'd inside with
- *           q_gain, NULL = qknorm off), kc [B, Hkv, n, d] content keys and
+ *           q_gain, NULL = qknorm off); k_gain the keys' QKNorm gains (NULL
+ *           when off: they bound the logits); kc [B, Hkv, n, d] content keys and
  *           S0 [B, Hkv, n/Bk, m, d] their summaries (hba_prep_keys,
  *           hba_summarize);
  *   scale_u the union scale of the teacher's content logits (_content_qk),
@@ -293,7 +294,8 @@ int hba_summarize_filled(int dtype, const void *kc_pages, const int32_t *page_ta
  */
 int hba_aux_kl_workspace_size(int dtype, int64_t B, int64_t n, int64_t Hq, int64_t Hkv, int64_t d,
                               int64_t m, int64_t Bk, size_t *bytes);
-int hba_aux_kl(int dtype, const void *q, const int64_t q_strides[3], const float *q_gain, float eps,
+int hba_aux_kl(int dtype, const void *q, const int64_t q_strides[3], const float *q_gain,
+               const float *k_gain, float eps,
                const void *kc, const void *S0, const float *probes, const float *proj, int64_t B,
                int64_t n, int64_t Hq, int64_t Hkv, int64_t d, int64_t m, int64_t Bk, int64_t W,
                float scale_u, float scale_r, void *ws, size_t ws_bytes, float *aux,
