@@ -42,9 +42,9 @@ class HBAConfig:
 
 def resolve_backend(cfg):
     """Backend name for the attention call (config.py:187-194).  'hip' and the
-    reference's 'fused'/'naive' train backends all map to the HIP kernels
-    (forward, and the backward of the attention output through autograd; the
-    aux-KL teacher is not provided, so training needs aux_w = 0)."""
+    reference's 'fused'/'naive' train backends all map to the HIP kernels:
+    the forward, the backward of the attention output through autograd, and
+    the aux-KL with its gradient into the summarizer."""
     b = getattr(cfg, "attn_backend", "hip")
     if b in ("hip", "fused", "naive"):
         return "hip"
