@@ -348,18 +348,9 @@ __device__ __forceinline__ void routing_queries_tile(const bf16_t *q, int64_t qs
             rr[j] = sqrtf(ms);
         }
     };
-    if (qgain) {
-        if (G <= 8) chains(std::integral_constant<int, 2>());
-        else chains(std::integral_constant<int, 4>());
-    }
     const bf16_t *base = row0 + part * DP;
     float acc[DP];
-#pragma unroll
-    for (int h = 0; h < GMAX; ++h) {
-        if (h >= G) break;   // uniform
-        uint4 raw[NC];
-#pragma unroll
-        for (int c = 0; c < NC; ++c) raw[c] = reinterpret_cast<const uint4 *>(base + (int64_t)h * qsh)[c];
+    auto head = [&](int h, const uint4 (&raw)[NC]) {
         float x[DP];
 #pragma unroll
         for (int e = 0; e < DP; ++e) x[e] = unpack(raw[e >> 3], e & 7);
@@ -380,6 +371,31 @@ __device__ __forceinline__ void routing_queries_tile(const bf16_t *q, int64_t qs
         }
 #pragma unroll
         for (int e = 0; e < DP; ++e) acc[e] = (h == 0) ? x[e] : acc[e] + x[e];
+    };
+    if (G <= 8) {
+        // every load first: the quarter rows of all heads (past G: head G-1
+        // again, unused), then the full rows of the sums of squares
+        uint4 rq[8][NC];
+#pragma unroll
+        for (int h = 0; h < 8; ++h) {
+            const int hc = h < G ? h : G - 1;
+#pragma unroll
+            for (int c = 0; c < NC; ++c) rq[h][c] = reinterpret_cast<const uint4 *>(base + (int64_t)hc * qsh)[c];
+        }
+        if (qgain) chains(std::integral_constant<int, 2>());
+#pragma unroll
+        for (int h = 0; h < 8; ++h)
+            if (h < G) head(h, rq[h]);
+    } else {
+        if (qgain) chains(std::integral_constant<int, 4>());
+#pragma unroll
+        for (int h = 0; h < GMAX; ++h) {
+            if (h >= G) break;   // uniform
+            uint4 raw[NC];
+#pragma unroll
+            for (int c = 0; c < NC; ++c) raw[c] = reinterpret_cast<const uint4 *>(base + (int64_t)h * qsh)[c];
+            head(h, raw);
+        }
     }
 #pragma unroll
     for (int e = 0; e < DP; ++e) qgs[qq * ROWQ + part * DP + e] = f2bf(acc[e]);
@@ -391,17 +407,76 @@ __device__ __forceinline__ void routing_queries_tile(const bf16_t *q, int64_t qs
 // then inserts only children of those supers.  On a GPU tile of 64 queries
 // the kept supers cover nearly every super, so the children are scored as the
 // flat GEMM and filtered, not gathered.
+// (score, block) as one unsigned key ordered like (score desc, block asc):
+// the score's bits mapped to an order-preserving unsigned (a zero score
+// taken as +0, which the float comparison treats as equal to -0), then the
+// complement of the block.
+__device__ __forceinline__ uint64_t sel_key(float v, int blk) {
+    const uint32_t u = __float_as_uint(v + 0.0f);
+    const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((uint64_t)ord << 32) | (uint32_t)(0xffffffffu - (uint32_t)blk);
+}
+__device__ __forceinline__ float sel_key_score(uint64_t key) {
+    const uint32_t ord = (uint32_t)(key >> 32);
+    return __uint_as_float((ord & 0x80000000u) ? (ord & 0x7fffffffu) : ~ord);
+}
+__device__ __forceinline__ int sel_key_block(uint64_t key) { return (int)(0xffffffffu - (uint32_t)key); }
+
+// Position of the r-th (0-based) set bit of m; m must hold more than r.
+__device__ __forceinline__ int nth_set_bit64(uint64_t m, int r) {
+    int pos = 0;
+#pragma unroll
+    for (int wdt = 32; wdt >= 1; wdt >>= 1) {
+        const uint64_t low = m & ((1ull << wdt) - 1ull);
+        const int c = __popcll(low);
+        if (r >= c) {
+            r -= c;
+            m >>= wdt;
+            pos += wdt;
+        } else {
+            m = low;
+        }
+    }
+    return pos;
+}
+
+// Orders one wave's LDS writes before its later reads of them (other lanes'
+// included): LDS operations of a wave are performed in issue order, so only
+// the compiler needs holding back.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t x, int o) {
+    const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)x, o, 64);
+    const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(x >> 32), o, 64);
+    return ((uint64_t)hi << 32) | lo;
+}
+
 constexpr int SEL_PMW = 64;   // most words of the per-query super bitmask: ns <= 2048
 constexpr int32_t SEL_OVERFLOW = -2;   // cnt marker: the threshold kernel left this query to the exact pass
+constexpr int SEL_GMAXE = 256;   // gather path: most child positions per query (beam * F)
+constexpr int SEL_GCAP = 64;     // gather path: most children at or above the threshold per query
+// Dynamic LDS of the HIER kernel: the parent bitmask [64][nwp] (nwp = nw | 1,
+// an odd row stride: the per-super ballot reads one word of every query
+// without bank conflicts); for the gather path also the kept supers' prefix
+// counts [64][nwp] (bytes), the kept supers ascending [64][16] and the
+// children's scores [64][beam * F].
+__host__ __device__ inline int sel_nwp(int64_t ns) { return (int)(((ns + 31) / 32) | 1); }
+__host__ __device__ inline size_t sel_pre_off(int nwp) { return (size_t)64 * nwp * 4; }
+__host__ __device__ inline size_t sel_ksup_off(int nwp) { return (sel_pre_off(nwp) + (size_t)64 * nwp + 15) & ~(size_t)15; }
+__host__ __device__ inline size_t sel_cs_off(int nwp) { return sel_ksup_off(nwp) + (size_t)64 * 16 * 2; }
 // marked_only: run only for a 64-query tile holding a query whose cnt is
 // SEL_OVERFLOW (the threshold kernel's overflow), and recompute the tile.
-template <int D, int KMAX, bool HIER>
-__global__ __launch_bounds__(256) void score_select_mfma_kernel(
+template <int D, int KMAX, bool HIER, int BEAMMAX = 16>
+__global__ __launch_bounds__(256, (D == 64) ? 2 : 1) void score_select_mfma_kernel(
     const bf16_t *__restrict__ q, int64_t qsb, int64_t qsn, int64_t qsh, const float *__restrict__ qgain,
     float eps, const bf16_t *__restrict__ S0, int64_t n, int Hq, int Hkv, int64_t nb, int64_t W, int kk,
     float scale, int32_t *__restrict__ idx, float *__restrict__ val, int32_t *__restrict__ cnt,
     float *__restrict__ scores, const bf16_t *__restrict__ S1, int F, int beam, float *__restrict__ sup_scores,
-    int marked_only) {
+    int marked_only, int gather) {
     if (marked_only) {
         __shared__ int marked;
         const int64_t ib = (int64_t)blockIdx.x * 64 + threadIdx.x;
@@ -418,7 +493,6 @@ __global__ __launch_bounds__(256) void score_select_mfma_kernel(
     constexpr int ROWQ = D + 8;                        // padded LDS row of the routing queries
     constexpr int SROWS = CB * 4;                      // rows per stage
     constexpr int PPW = SROWS * D * 2 / 1024 / 4;      // 1 KB DMA parts per wave per stage
-    constexpr int BEAMMAX = 16;
     // LDS: the routing queries; the stage ring
     constexpr int RING_BYTES = NSS * SROWS * D * 2;
     __shared__ __align__(16) bf16_t qgs[64 * ROWQ];
@@ -496,7 +570,7 @@ __global__ __launch_bounds__(256) void score_select_mfma_kernel(
         last = fmaxf(last, lane_xor(last, 16));
         return fmaxf(last, lane_xor(last, 32));
     };
-    const int nw = HIER ? (int)(((nb + F - 1) / F + 31) / 32) : 0;
+    const int nw = HIER ? sel_nwp((nb + F - 1) / F) : 0;   // row stride of pmask
     int kout = kk;
     if constexpr (HIER) {
         // ---- level 1: supers holding at least one candidate child
@@ -527,6 +601,273 @@ __global__ __launch_bounds__(256) void score_select_mfma_kernel(
             if (lg == 0) pmask[qcol * nw + (p >> 5)] |= 1u << (p & 31);
         });
         __syncthreads();
+        if (gather) {
+            // ---- level 2 by super (F = 4, 8 or 16; beff * F <= SEL_GMAXE):
+            // each kept super's F children are scored against only the
+            // queries of the tile that kept it, 16 to an MFMA column group,
+            // with the operands and order of the flat scan (the same scores).
+            // Child c of the query's r-th kept super (ascending) has list
+            // position r * F + c; a position no child fills stays -inf.
+            const int E = beff * F;
+            const int NMT = F / 4;
+            uint8_t *pre = reinterpret_cast<uint8_t *>(reinterpret_cast<char *>(pmask) + sel_pre_off(nw));
+            uint16_t *ksup = reinterpret_cast<uint16_t *>(reinterpret_cast<char *>(pmask) + sel_ksup_off(nw));
+            float *cs = reinterpret_cast<float *>(reinterpret_cast<char *>(pmask) + sel_cs_off(nw));
+            const int nwu = (int)((ns + 31) / 32);        // words in use
+            for (int e = tid; e < 64 * E; e += 256) cs[e] = -INFINITY;
+            if (tid < 64) {   // per query: kept supers before each word, and the kept supers ascending
+                int c = 0;
+                for (int wd = 0; wd < nwu; ++wd) {
+                    pre[tid * nw + wd] = (uint8_t)c;
+                    uint32_t m = pmask[tid * nw + wd];
+                    while (m) {
+                        const int bit = __ffs(m) - 1;
+                        if (c < 16) ksup[tid * 16 + c] = (uint16_t)(wd * 32 + bit);
+                        ++c;
+                        m &= m - 1u;
+                    }
+                }
+            }
+            __syncthreads();
+            const bf16_t *Sg = S0 + (b * Hkv + g) * nb * 4 * D;
+            auto loadA = [&](int64_t sp, bf16x8 (&af)[4][NKS]) {
+#pragma unroll
+                for (int mt = 0; mt < 4; ++mt) {
+                    if (mt >= NMT) break;   // uniform
+                    int64_t blk = sp * F + 4 * mt + (l16 >> 2);
+                    blk = (blk < nb) ? blk : nb - 1;   // rows past the last block: never stored
+                    const bf16_t *src = Sg + (blk * 4 + (l16 & 3)) * D + 8 * lg;
+#pragma unroll
+                    for (int ks = 0; ks < NKS; ++ks) af[mt][ks] = ldb8(src + 32 * ks);
+                }
+            };
+            auto unit = [&](int64_t sp, const bf16x8 (&af)[4][NKS]) {
+                const int wd = (int)(sp >> 5);
+                const uint32_t bit = 1u << (sp & 31);
+                const uint64_t qm = __ballot((pmask[lane * nw + wd] & bit) != 0u);   // lane = query
+                const int nq = __popcll(qm);
+                for (int j0 = 0; j0 < nq; j0 += 16) {
+                    const int r = j0 + l16;
+                    const bool cv = r < nq;
+                    const int qc = cv ? nth_set_bit64(qm, r) : 0;
+                    bf16x8 qv[NKS];
+#pragma unroll
+                    for (int ks = 0; ks < NKS; ++ks) qv[ks] = ldb8(qgs + qc * ROWQ + 32 * ks + 8 * lg);
+                    f32x4 acc[4];
+#pragma unroll
+                    for (int mt = 0; mt < 4; ++mt) {
+                        if (mt >= NMT) break;
+                        acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                        for (int ks = 0; ks < NKS; ++ks)
+                            acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[mt][ks], qv[ks], acc[mt], 0, 0, 0);
+                    }
+                    const int rk = pre[qc * nw + wd] + __popc(pmask[qc * nw + wd] & (bit - 1u));
+                    const int64_t qi = i0 + qc;
+                    const int64_t bm = (qi < n) ? cand_bmax(qi, 64, W) : 0;
+                    float *dst = cs + qc * E + rk * F;
+#pragma unroll
+                    for (int mt = 0; mt < 4; ++mt) {
+                        if (mt >= NMT) break;
+                        const int ch = 4 * mt + lg;
+                        const int64_t blk = sp * F + ch;
+                        float best = acc[mt][0];
+                        best = (acc[mt][1] > best) ? acc[mt][1] : best;
+                        best = (acc[mt][2] > best) ? acc[mt][2] : best;
+                        best = (acc[mt][3] > best) ? acc[mt][3] : best;
+                        const float v = best * scale;
+                        const bool ok = cv && blk >= 1 && blk <= bm;
+                        if (cv) dst[ch] = ok ? v : -INFINITY;
+                        if (ok && scores) scores[((b * Hkv + g) * n + qi) * nb + blk] = v;
+                    }
+                }
+            };
+            // Two supers at a time, so that the two dependent chains (ballot,
+            // column queries, operand loads, MFMAs, stores) overlap; the
+            // general unit where either has more than 16 queries.
+            auto pair = [&](int64_t sa, const bf16x8 (&fa)[4][NKS], int64_t sb, const bf16x8 (&fb)[4][NKS]) {
+                if (sb >= nsup) {
+                    unit(sa, fa);
+                    return;
+                }
+                const int wa = (int)(sa >> 5), wb = (int)(sb >> 5);
+                const uint32_t ba = 1u << (sa & 31), bb = 1u << (sb & 31);
+                const uint32_t ma = pmask[lane * nw + wa], mb = pmask[lane * nw + wb];
+                const uint64_t qa = __ballot((ma & ba) != 0u), qb2 = __ballot((mb & bb) != 0u);
+                const int na = __popcll(qa), nb2 = __popcll(qb2);
+                if (na > 16 || nb2 > 16) {   // uniform
+                    unit(sa, fa);
+                    unit(sb, fb);
+                    return;
+                }
+                const bool ca = l16 < na, cb = l16 < nb2;
+                const int qca = ca ? nth_set_bit64(qa, l16) : 0;
+                const int qcb = cb ? nth_set_bit64(qb2, l16) : 0;
+                bf16x8 va[NKS], vb[NKS];
+#pragma unroll
+                for (int ks = 0; ks < NKS; ++ks) {
+                    va[ks] = ldb8(qgs + qca * ROWQ + 32 * ks + 8 * lg);
+                    vb[ks] = ldb8(qgs + qcb * ROWQ + 32 * ks + 8 * lg);
+                }
+                const int rka = pre[qca * nw + wa] + __popc(pmask[qca * nw + wa] & (ba - 1u));
+                const int rkb = pre[qcb * nw + wb] + __popc(pmask[qcb * nw + wb] & (bb - 1u));
+                f32x4 xa[4], xb[4];
+#pragma unroll
+                for (int mt = 0; mt < 4; ++mt) {
+                    if (mt >= NMT) break;
+                    xa[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+                    xb[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int ks = 0; ks < NKS; ++ks) {
+                        xa[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[mt][ks], va[ks], xa[mt], 0, 0, 0);
+                        xb[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[mt][ks], vb[ks], xb[mt], 0, 0, 0);
+                    }
+                }
+                const int64_t qia = i0 + qca, qib = i0 + qcb;
+                const int64_t bma = (qia < n) ? cand_bmax(qia, 64, W) : 0;
+                const int64_t bmb = (qib < n) ? cand_bmax(qib, 64, W) : 0;
+                float *da = cs + qca * E + rka * F;
+                float *db = cs + qcb * E + rkb * F;
+#pragma unroll
+                for (int mt = 0; mt < 4; ++mt) {
+                    if (mt >= NMT) break;
+                    const int ch = 4 * mt + lg;
+                    const int64_t blka = sa * F + ch, blkb = sb * F + ch;
+                    float ma4 = xa[mt][0], mb4 = xb[mt][0];   // as in unit: the same result, zeros included
+#pragma unroll
+                    for (int e = 1; e < 4; ++e) {
+                        ma4 = (xa[mt][e] > ma4) ? xa[mt][e] : ma4;
+                        mb4 = (xb[mt][e] > mb4) ? xb[mt][e] : mb4;
+                    }
+                    const float va4 = ma4 * scale, vb4 = mb4 * scale;
+                    const bool oka = ca && blka >= 1 && blka <= bma;
+                    const bool okb = cb && blkb >= 1 && blkb <= bmb;
+                    if (ca) da[ch] = oka ? va4 : -INFINITY;
+                    if (cb) db[ch] = okb ? vb4 : -INFINITY;
+                    if (scores) {
+                        if (oka) scores[((b * Hkv + g) * n + qia) * nb + blka] = va4;
+                        if (okb) scores[((b * Hkv + g) * n + qib) * nb + blkb] = vb4;
+                    }
+                }
+            };
+            {   // this wave's supers w, w + 4, ... in pairs, their A fragments one pair ahead
+                bf16x8 a0[4][NKS], a1[4][NKS], a2[4][NKS], a3[4][NKS];
+                int64_t sp = w;
+                if (sp < nsup) loadA(sp, a0);
+                if (sp + 4 < nsup) loadA(sp + 4, a1);
+                if (sp + 8 < nsup) loadA(sp + 8, a2);
+                if (sp + 12 < nsup) loadA(sp + 12, a3);
+                while (sp < nsup) {
+                    pair(sp, a0, sp + 4, a1);
+                    if (sp + 16 < nsup) loadA(sp + 16, a0);
+                    if (sp + 20 < nsup) loadA(sp + 20, a1);
+                    sp += 8;
+                    if (sp >= nsup) break;
+                    pair(sp, a2, sp + 4, a3);
+                    if (sp + 16 < nsup) loadA(sp + 16, a2);
+                    if (sp + 20 < nsup) loadA(sp + 20, a3);
+                    sp += 8;
+                }
+            }
+            __syncthreads();
+            // ---- per query, 16 lanes: the kout best listed children.  Each
+            // lane keeps its 2 best keys; the kout-th best key tau of the 32 is
+            // a lower bound of the query's kout-th (or 0: every valid key
+            // qualifies); the keys >= tau are listed and ranked by count.
+            // the wave's own LDS (no other wave touches it: wave-level syncs)
+            uint64_t *tk = reinterpret_cast<uint64_t *>(pool) + w * (4 * 32 + 4 * SEL_GCAP);
+            uint64_t *lst = tk + 4 * 32;
+            const int qq = lane >> 4, sl = lane & 15;
+            constexpr int EL = SEL_GMAXE / 16;   // positions per lane
+            const int j0 = sl / F, jstep = 16 / F, ch0 = sl % F;
+            for (int r4 = 0; r4 < 4; ++r4) {
+                const int qc = 16 * w + 4 * r4 + qq;
+                const int64_t qi = i0 + qc;
+                const float *cq = cs + qc * E;
+                const uint16_t *kq = ksup + qc * 16;
+                // this lane's keys: positions sl + 16 t, child sl % F of the
+                // query's (sl / F + t * 16 / F)-th kept super (0 where no child)
+                float cv[EL];
+                int kb[EL];
+#pragma unroll
+                for (int t = 0; t < EL; ++t) {
+                    const int p = sl + 16 * t;
+                    const int jr = j0 + t * jstep;
+                    cv[t] = (p < E) ? cq[p] : -INFINITY;
+                    kb[t] = kq[jr < 16 ? jr : 15];
+                }
+                uint64_t ky[EL];
+#pragma unroll
+                for (int t = 0; t < EL; ++t) ky[t] = (cv[t] == -INFINITY) ? 0ull : sel_key(cv[t], kb[t] * F + ch0);
+                uint64_t t0 = 0ull, t1 = 0ull;
+#pragma unroll
+                for (int t = 0; t < EL; ++t) {
+                    const uint64_t key = ky[t];
+                    t1 = (key > t0) ? t0 : ((key > t1) ? key : t1);
+                    t0 = (key > t0) ? key : t0;
+                }
+                tk[qq * 32 + 2 * sl] = t0;
+                tk[qq * 32 + 2 * sl + 1] = t1;
+                wave_lds_sync();
+                int g0 = 0, g1 = 0;
+                for (int j = 0; j < 32; ++j) {
+                    const uint64_t x = tk[qq * 32 + j];
+                    g0 += (x > t0) ? 1 : 0;
+                    g1 += (x > t1) ? 1 : 0;
+                }
+                uint64_t tau = ~0ull;
+                if (g0 < kout) tau = t0;
+                if (g1 < kout && t1 < tau) tau = t1;
+#pragma unroll
+                for (int o = 1; o < 16; o <<= 1) {
+                    const uint64_t ot = shfl_xor_u64(tau, o);
+                    tau = (ot < tau) ? ot : tau;
+                }
+                int mine = 0;
+#pragma unroll
+                for (int t = 0; t < EL; ++t) mine += (ky[t] != 0ull && ky[t] >= tau) ? 1 : 0;
+                int incl = mine;
+#pragma unroll
+                for (int o = 1; o < 16; o <<= 1) {
+                    const int t = __shfl_up(incl, o, 16);
+                    if (sl >= o) incl += t;
+                }
+                const int total = __shfl(incl, 15, 16);
+                if (total <= SEL_GCAP) {
+                    int pos = incl - mine;
+#pragma unroll
+                    for (int t = 0; t < EL; ++t)
+                        if (ky[t] != 0ull && ky[t] >= tau) lst[qq * SEL_GCAP + pos++] = ky[t];
+                }
+                wave_lds_sync();
+                if (qi < n) {
+                    const int64_t o = ((b * Hkv + g) * n + qi) * kk;
+                    if (total > SEL_GCAP) {   // too many ties at tau: the exact pass recomputes the tile
+                        if (sl == 0) cnt[(b * Hkv + g) * n + qi] = SEL_OVERFLOW;
+                    } else {
+                        const uint64_t *lq = lst + qq * SEL_GCAP;
+                        for (int j = sl; j < total; j += 16) {
+                            const uint64_t key = lq[j];
+                            int rank = 0;
+#pragma unroll 8
+                            for (int j2 = 0; j2 < total; ++j2) rank += (lq[j2] > key) ? 1 : 0;
+                            if (rank < kout) {
+                                idx[o + rank] = sel_key_block(key);
+                                val[o + rank] = sel_key_score(key);
+                            }
+                        }
+                        const int taken = (total < kout) ? total : kout;
+                        for (int j = taken + sl; j < kk; j += 16) {
+                            idx[o + j] = -1;
+                            val[o + j] = -INFINITY;
+                        }
+                        if (sl == 0) cnt[(b * Hkv + g) * n + qi] = taken;
+                    }
+                }
+                wave_lds_sync();   // tk and lst are reused by the next four queries
+            }
+            return;
+        }
     }
     // ---- blocks (children of the kept supers, for HIER)
     float vals[KMAX];
@@ -598,20 +939,6 @@ struct Cfg {
 };
 }  // namespace thr
 
-// (score, block) as one unsigned key ordered like (score desc, block asc):
-// the score's bits mapped to an order-preserving unsigned (a zero score
-// taken as +0, which the float comparison treats as equal to -0), then the
-// complement of the block.
-__device__ __forceinline__ uint64_t sel_key(float v, int blk) {
-    const uint32_t u = __float_as_uint(v + 0.0f);
-    const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-    return ((uint64_t)ord << 32) | (uint32_t)(0xffffffffu - (uint32_t)blk);
-}
-__device__ __forceinline__ float sel_key_score(uint64_t key) {
-    const uint32_t ord = (uint32_t)(key >> 32);
-    return __uint_as_float((ord & 0x80000000u) ? (ord & 0x7fffffffu) : ~ord);
-}
-__device__ __forceinline__ int sel_key_block(uint64_t key) { return (int)(0xffffffffu - (uint32_t)key); }
 
 template <int D, int KMAX>
 __global__ __launch_bounds__(256, (D == 64) ? 2 : 1) void score_select_thr_kernel(
@@ -940,7 +1267,7 @@ void launch_flat(const void *q, const int64_t *qs, const float *qgain, float eps
                                (int)Hkv, n / 64, W, (int)k, scale, idx, val, cnt, scores, ntiles);
             hipLaunchKernelGGL((score_select_mfma_kernel<D, KMAX, false>), grid, dim3(256), 0, s,
                                (const bf16_t *)q, qs[0], qs[1], qs[2], qgain, eps, (const bf16_t *)S0, n, (int)Hq,
-                               (int)Hkv, n / 64, W, (int)k, scale, idx, val, cnt, scores, nullptr, 1, 1, nullptr, 1);
+                               (int)Hkv, n / 64, W, (int)k, scale, idx, val, cnt, scores, nullptr, 1, 1, nullptr, 1, 0);
             return;
         }
     }
@@ -959,11 +1286,28 @@ void launch_hier(const void *q, const int64_t *qs, const float *qgain, float eps
     if constexpr (DT == 1 && M == 4 && KMAX <= 32) {
         if (ns <= 32 * SEL_PMW && Hq / Hkv <= 16) {
             dim3 grid((unsigned)((n + 63) / 64), (unsigned)Hkv, (unsigned)B);
-            const size_t pm = (size_t)64 * ((ns + 31) / 32) * sizeof(uint32_t);
-            hipLaunchKernelGGL((score_select_mfma_kernel<D, KMAX, true>), grid, dim3(256), pm, s, (const bf16_t *)q,
-                               qs[0], qs[1], qs[2], qgain, eps, (const bf16_t *)S0, n, (int)Hq, (int)Hkv, n / 64,
-                               W, (int)k, scale, idx, val, cnt, scores, (const bf16_t *)S1, (int)F, (int)beam,
-                               sup_scores, 0);
+            const int nwp = sel_nwp(ns);
+            const int64_t beff = (beam < ns) ? beam : ns;
+            // level 2 by super where its lists fit; the exact kernel then
+            // recomputes any tile holding a query whose list overflowed
+            const bool gather = F >= 4 && 16 % F == 0 && beff * F <= SEL_GMAXE;
+            const size_t pm = (size_t)64 * nwp * sizeof(uint32_t);
+            const size_t pmg = sel_cs_off(nwp) + (size_t)64 * beff * F * sizeof(float);
+            // level 1 keeps beam-sized lists per lane (insertion cost grows with the length)
+            auto kfn = (beam <= 8) ? score_select_mfma_kernel<D, KMAX, true, 8>
+                                   : score_select_mfma_kernel<D, KMAX, true, 16>;
+            if (gather && pmg > 65536 &&
+                hipFuncSetAttribute(reinterpret_cast<const void *>(kfn), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    (int)pmg) != hipSuccess)
+                return;   // the error stays as hipGetLastError's, which the entry point reports
+            hipLaunchKernelGGL(kfn, grid, dim3(256), gather ? pmg : pm, s, (const bf16_t *)q, qs[0], qs[1], qs[2],
+                               qgain, eps, (const bf16_t *)S0, n, (int)Hq, (int)Hkv, n / 64, W, (int)k, scale, idx,
+                               val, cnt, scores, (const bf16_t *)S1, (int)F, (int)beam, sup_scores, 0,
+                               gather ? 1 : 0);
+            if (gather)
+                hipLaunchKernelGGL(kfn, grid, dim3(256), pm, s, (const bf16_t *)q, qs[0], qs[1], qs[2], qgain, eps,
+                                   (const bf16_t *)S0, n, (int)Hq, (int)Hkv, n / 64, W, (int)k, scale, idx, val,
+                                   cnt, scores, (const bf16_t *)S1, (int)F, (int)beam, sup_scores, 1, 0);
             return;
         }
     }

@@ -327,6 +327,35 @@ def test_hier_select_adversarial(dev, pattern):
                          sup[0, g].cpu().numpy())
 
 
+def test_hier_select_threshold_overflow(dev):
+    """A layout on which the by-super path's threshold admits more children
+    than its 64-entry list: child c < 8 of super j scores 255 - 32 c - j
+    (times the query's first routing element), child c >= 8 scores 0, so for
+    a query with a positive first element the 2 best children per child slot
+    put the 16th-best key low and children 0..6 of all 16 kept supers (112)
+    clear it; the exact kernel then recomputes those tiles.  Every value is
+    exact in bf16 and in the products, so the picks are fixed; beam and
+    fanout are the largest that path takes."""
+    torch.manual_seed(11)
+    n, Hkv, Hq, d, m, W, kk, F, beam = 32768, 2, 14, 64, 4, 1024, 16, 16, 16
+    nb = n // 64
+    blk = torch.arange(nb)
+    a = torch.where(blk % 16 < 8, 255 - 32 * (blk % 16) - blk // 16, torch.zeros_like(blk)).float()
+    q = torch.randn(1, n, Hq, d, device=dev).to(torch.bfloat16)
+    gq = torch.full((Hq,), d ** 0.25, device=dev)
+    S0 = torch.zeros(1, Hkv, nb, m, d)
+    S0[..., 0] = a[None, None, :, None]
+    S0 = S0.to(torch.bfloat16).to(dev)
+    S1 = ops.build_super(S0, F)
+    idx, val, cnt, scores, sup = ops.hier_select_with_scores(q, gq, 1e-6, S0, S1, W, kk, F, beam, 0.125)
+    torch.cuda.synchronize()
+    qg = O.grouped_query(O.qknorm(f(q)[0], f(gq), 1e-6, "bf16"), Hkv, "bf16")
+    for g in range(Hkv):
+        check_hier_dumps(qg[g], f(S0)[0, g], f(S1)[0, g], F, beam, kk, 0.125, W, idx[0, g].cpu().numpy(),
+                         val[0, g].cpu().numpy(), cnt[0, g].cpu().numpy(), scores[0, g].cpu().numpy(),
+                         sup[0, g].cpu().numpy())
+
+
 # ------------------------------------------------------------- attention -----
 ATTN_CASES = [
     dict(dt="f32", n=2048, W=512, k=8),
