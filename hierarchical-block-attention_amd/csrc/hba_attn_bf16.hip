@@ -156,7 +156,10 @@ __device__ __forceinline__ void qoperand(const bf16_t *q, int64_t qsb, int64_t q
 
 // Workgroup -> (batch*KV head combo, query tile).  Workgroup i runs on XCD
 // i % 8; xmap 1 (8 % Cn == 0) and 2 (Cn % 8 == 0) give each XCD one combo's
-// keys at a time, so the blocks it gathers share that XCD's L2.
+// keys at a time, so the blocks it gathers share that XCD's L2.  Tiles go
+// deepest first: a tile's union of routed blocks grows with its candidate
+// count, and starting the longest workgroups first leaves the short ones to
+// fill the end.
 __device__ __forceinline__ void xcd_map(int i, int Cn, int ntiles, int xmap, int &combo, int &tile) {
     if (xmap == 1) {
         combo = (i & 7) % Cn;
@@ -168,6 +171,7 @@ __device__ __forceinline__ void xcd_map(int i, int Cn, int ntiles, int xmap, int
         combo = i / ntiles;
         tile = i % ntiles;
     }
+    if (tile < ntiles) tile = ntiles - 1 - tile;   // padding workgroups (xmap 1) keep tile >= ntiles
 }
 
 // ======================================================== tile staging ====

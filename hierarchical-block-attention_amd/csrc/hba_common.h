@@ -37,6 +37,24 @@ __device__ __forceinline__ bf16_t f2bf(float x) {
 
 __device__ __forceinline__ float rnd_bf16(float x) { return bf2f(f2bf(x)); }
 
+// Two values rounded to bf16 (nearest even) at once by v_cvt_pk_bf16_f32 and
+// widened back: the same results as rnd_bf16 for every non-NaN input.
+__device__ __forceinline__ void rnd_bf16_pair(float &a, float &b) {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    typedef float f32x2_t __attribute__((ext_vector_type(2)));
+    const uint32_t u = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
+    a = __uint_as_float(u << 16);
+    b = __uint_as_float(u & 0xffff0000u);
+}
+
+// Two values as packed bf16 (nearest even; a in the low half), the same bits
+// as f2bf for every non-NaN input.
+__device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    typedef float f32x2_t __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
+}
+
 // Storage-type traits: DT 0 = fp32, 1 = bf16.
 template <int DT> struct St;
 template <> struct St<0> {

@@ -363,7 +363,9 @@ __device__ __forceinline__ void routing_queries_tile(const bf16_t *q, int64_t qs
             if (!__any(slow)) {
                 const float inv = 1.0f / r;
 #pragma unroll
-                for (int e = 0; e < DP; ++e) x[e] = rnd_bf16(div_rn_fast(x[e], r, inv) * gn);
+                for (int e = 0; e < DP; ++e) x[e] = div_rn_fast(x[e], r, inv) * gn;
+#pragma unroll
+                for (int e = 0; e < DP; e += 2) rnd_bf16_pair(x[e], x[e + 1]);
             } else {
 #pragma unroll
                 for (int e = 0; e < DP; ++e) x[e] = rnd_bf16((x[e] / r) * gn);
@@ -398,7 +400,8 @@ __device__ __forceinline__ void routing_queries_tile(const bf16_t *q, int64_t qs
         }
     }
 #pragma unroll
-    for (int e = 0; e < DP; ++e) qgs[qq * ROWQ + part * DP + e] = f2bf(acc[e]);
+    for (int e = 0; e < DP; e += 2)
+        *reinterpret_cast<uint32_t *>(qgs + qq * ROWQ + part * DP + e) = pk_bf16(acc[e], acc[e + 1]);
 }
 
 // HIER: the two-level beam descent (hier_select) on the same machinery.  A
@@ -455,6 +458,19 @@ __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t x, int o) {
     return ((uint64_t)hi << 32) | lo;
 }
 
+// Workgroup -> (64-query tile, KV head, batch) of a 1-D grid, the deepest
+// tiles first: a tile's work grows with its candidate count, and starting the
+// longest workgroups first leaves the short ones to fill the end (longest-
+// first list scheduling).  The KV heads and batches of one depth are adjacent.
+__device__ __forceinline__ void sel_deep_first(int ntiles, int Hkv, int &tile, int &g, int64_t &b) {
+    const int64_t i = blockIdx.x;
+    const int64_t per = (int64_t)Hkv * (gridDim.x / ((int64_t)ntiles * Hkv));   // Hkv * B
+    const int64_t j = i / per, r = i % per;
+    tile = ntiles - 1 - (int)j;
+    g = (int)(r % Hkv);
+    b = r / Hkv;
+}
+
 constexpr int SEL_PMW = 64;   // most words of the per-query super bitmask: ns <= 2048
 constexpr int32_t SEL_OVERFLOW = -2;   // cnt marker: the threshold kernel left this query to the exact pass
 constexpr int SEL_GMAXE = 256;   // gather path: most child positions per query (beam * F)
@@ -477,13 +493,15 @@ __global__ __launch_bounds__(256, (D == 64) ? 2 : 1) void score_select_mfma_kern
     float scale, int32_t *__restrict__ idx, float *__restrict__ val, int32_t *__restrict__ cnt,
     float *__restrict__ scores, const bf16_t *__restrict__ S1, int F, int beam, float *__restrict__ sup_scores,
     int marked_only, int gather) {
+    int tile_, g_;
+    int64_t b_;
+    sel_deep_first((int)((n + 63) / 64), Hkv, tile_, g_, b_);
     if (marked_only) {
         __shared__ int marked;
-        const int64_t ib = (int64_t)blockIdx.x * 64 + threadIdx.x;
+        const int64_t ib = (int64_t)tile_ * 64 + threadIdx.x;
         if (threadIdx.x == 0) marked = 0;
         __syncthreads();
-        if (threadIdx.x < 64 && ib < n && cnt[((int64_t)blockIdx.z * Hkv + blockIdx.y) * n + ib] == SEL_OVERFLOW)
-            marked = 1;
+        if (threadIdx.x < 64 && ib < n && cnt[(b_ * Hkv + g_) * n + ib] == SEL_OVERFLOW) marked = 1;
         __syncthreads();
         if (!marked) return;   // workgroup-uniform
     }
@@ -502,10 +520,10 @@ __global__ __launch_bounds__(256, (D == 64) ? 2 : 1) void score_select_mfma_kern
 
     const int tid = threadIdx.x;
     const int w = tid >> 6, lane = tid & 63, l16 = lane & 15, lg = lane >> 4;
-    const int g = blockIdx.y;
-    const int64_t b = blockIdx.z;
+    const int g = g_;
+    const int64_t b = b_;
     const int G = Hq / Hkv;
-    const int64_t i0 = (int64_t)blockIdx.x * 64;
+    const int64_t i0 = (int64_t)tile_ * 64;
     routing_queries_tile<D, ROWQ>(q, qsb, qsn, qsh, qgain, eps, b, i0, n, g, G, qgs, tid);
     __syncthreads();
     const int qcol = 16 * w + l16;
@@ -963,12 +981,10 @@ __global__ __launch_bounds__(256, (D == 64) ? 2 : 1) void score_select_thr_kerne
 
     const int tid = threadIdx.x;
     const int w = tid >> 6, lane = tid & 63, l16 = lane & 15, lg = lane >> 4;
-    const int g = blockIdx.y;
-    const int64_t b = blockIdx.z;
+    int tile, g;
+    int64_t b;
+    sel_deep_first(ntiles, Hkv, tile, g, b);
     const int G = Hq / Hkv;
-    // deep and shallow tiles alternate in launch order
-    const int bx = blockIdx.x;
-    const int tile = (bx & 1) ? ntiles - 1 - (bx >> 1) : (bx >> 1);
     const int64_t i0 = (int64_t)tile * QW;
     routing_queries_tile<D, ROWQ>(q, qsb, qsn, qsh, qgain, eps, b, i0, n, g, G, qgs, tid);
     __syncthreads();
@@ -1248,7 +1264,7 @@ int select_checks(int dtype, const void *q, const int64_t *qs, const void *S0, i
     if (k > 64 || !(m == 1 || m == 2 || m == 4 || m == 8)) return HBA_ERR_UNSUPPORTED;
     if (m * d > SEL_LDS_FLOATS) return HBA_ERR_UNSUPPORTED;
     if (!abi::rows_aligned(dtype, q, qs)) return HBA_ERR_UNSUPPORTED;
-    if (B > 65535 || Hkv > 65535 || (n + SEL_WG - 1) / SEL_WG > 0x7fffffff) return HBA_ERR_UNSUPPORTED;
+    if (B > 65535 || Hkv > 65535 || (n + SEL_WG - 1) / SEL_WG * Hkv * B > 0x7fffffff) return HBA_ERR_UNSUPPORTED;
     return HBA_OK;
 }
 
@@ -1261,11 +1277,11 @@ void launch_flat(const void *q, const int64_t *qs, const float *qgain, float eps
         if (Hq / Hkv <= 16) {   // the routing-query tile takes up to 16 heads per KV head
             // threshold top-k, then the exact kernel on the tiles it marked
             const int ntiles = (int)((n + thr::QW - 1) / thr::QW);
-            hipLaunchKernelGGL((score_select_thr_kernel<D, KMAX>),
-                               dim3((unsigned)ntiles, (unsigned)Hkv, (unsigned)B), dim3(256), 0, s,
+            const dim3 g1((unsigned)(ntiles * Hkv * B));
+            hipLaunchKernelGGL((score_select_thr_kernel<D, KMAX>), g1, dim3(256), 0, s,
                                (const bf16_t *)q, qs[0], qs[1], qs[2], qgain, eps, (const bf16_t *)S0, n, (int)Hq,
                                (int)Hkv, n / 64, W, (int)k, scale, idx, val, cnt, scores, ntiles);
-            hipLaunchKernelGGL((score_select_mfma_kernel<D, KMAX, false>), grid, dim3(256), 0, s,
+            hipLaunchKernelGGL((score_select_mfma_kernel<D, KMAX, false>), g1, dim3(256), 0, s,
                                (const bf16_t *)q, qs[0], qs[1], qs[2], qgain, eps, (const bf16_t *)S0, n, (int)Hq,
                                (int)Hkv, n / 64, W, (int)k, scale, idx, val, cnt, scores, nullptr, 1, 1, nullptr, 1, 0);
             return;
@@ -1285,7 +1301,7 @@ void launch_hier(const void *q, const int64_t *qs, const float *qgain, float eps
     const int64_t ns = (n / 64 + F - 1) / F;
     if constexpr (DT == 1 && M == 4 && KMAX <= 32) {
         if (ns <= 32 * SEL_PMW && Hq / Hkv <= 16) {
-            dim3 grid((unsigned)((n + 63) / 64), (unsigned)Hkv, (unsigned)B);
+            const dim3 grid((unsigned)(((n + 63) / 64) * Hkv * B));
             const int nwp = sel_nwp(ns);
             const int64_t beff = (beam < ns) ? beam : ns;
             // level 2 by super where its lists fit; the exact kernel then
