@@ -193,11 +193,14 @@ def decode_bytes(lens, Hkv, d, m, S, W, k, Hq, esize=2):
     return tot
 
 
-def bench_decode(dev, iters=200):
+DECODE_PAIR_MIN = 128   # (sequence, KV head) pairs from which the library runs decode_pair_kernel
+
+
+def bench_decode(dev, iters=200, batch=None):
     import torch
     import hba_amd
     from hba_amd import ops, synth
-    Bd = DECODE["batch"]
+    Bd = batch or DECODE["batch"]
     Hq, Hkv, d, m, S, W, k = 14, 2, 64, 4, 4, 1024, 16
     cfg = hba_amd.HBAConfig(n_heads=Hq, n_kv=Hkv, head_dim=d, slots=m, sinks=S, window=W, k_blocks=k)
     lens = synth.decode_lengths(Bd, DECODE["len_lo"], DECODE["len_hi"], seed=DECODE["seed"])
@@ -246,13 +249,16 @@ def bench_decode(dev, iters=200):
     ok = ok and bool(torch.equal(gout, eager))
     nbytes = decode_bytes(lens, Hkv, d, m, S, W, k, Hq)
     gbs = nbytes / (us * 1e-6) / 1e9
+    pair = Bd * Hkv >= DECODE_PAIR_MIN and os.environ.get("HBA_DECODE_KERNEL") != "fused"
+    kern = ("decode_pair_kernel: one launch, one workgroup per (sequence, KV head) (scores, top-k in "
+            "LDS, window, sink and routed pages, LSE merge), replayed from a HIP graph") if pair else (
+           "decode_fused_kernel: one launch (page scores and chunk top-k with the window "
+           "and sink pages; the last score workgroup of a (sequence, KV head) merges the lists "
+           "and runs the routed pages; the last workgroup merges the partial states), "
+           "replayed from a HIP graph")
     return dict(us_per_step=round(us, 3), algorithmic_bytes=nbytes, achieved_GBs=round(gbs, 1),
                 hbm_frac=round(gbs / PEAK_HBM_GBS, 4), graph_replay_matches_eager=ok,
-                batch=Bd, context="L ~ U[16384, 32768], paged bf16, shuffled page table",
-                kernels="decode_fused_kernel: one launch (page scores and chunk top-k with the window "
-                        "and sink pages; the last score workgroup of a (sequence, KV head) merges the lists "
-                        "and runs the routed pages; the last workgroup merges the partial states), "
-                        "replayed from a HIP graph")
+                batch=Bd, context="L ~ U[16384, 32768], paged bf16, shuffled page table", kernels=kern)
 
 
 CPU_WORKLOAD = dict(batch=1, seq_len=4096, q_heads=14, kv_heads=2, head_dim=64, sinks=4, window=1024, block=64,
@@ -574,10 +580,12 @@ def main():
                     help="internal: run only the CPU baseline (no GPU use) and print its JSON")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run 3 plain device copies of MIB MiB (counter calibration) and exit")
-    ap.add_argument("--config", choices=["layer32k", "hier128k", "donor", "equiv32k", "bwd32k", "decode32k"],
+    ap.add_argument("--config", choices=["layer32k", "hier128k", "donor", "equiv32k", "bwd32k", "decode32k",
+                                         "decode32k_b128"],
                     default="layer32k",
                     help="layer32k: the headline line (default); hier128k / donor / equiv32k / bwd32k / "
-                         "decode32k: the other measured workloads, one JSON line each")
+                         "decode32k / decode32k_b128 (the decode step at 128 sequences): the other "
+                         "measured workloads, one JSON line each")
     a = ap.parse_args()
     if a.cpu_leg:
         cpu_leg()
@@ -603,7 +611,9 @@ def main():
         line = {"hier128k": bench_hier128k, "donor": bench_donor, "equiv32k": bench_equiv32k,
                 "bwd32k": bench_bwd32k,
                 "decode32k": lambda d: {"metric": "HBA decode step µs (B=32, 16-32K paged bf16 cache)",
-                                        **bench_decode(d)}}[a.config](dev)
+                                        **bench_decode(d)},
+                "decode32k_b128": lambda d: {"metric": "HBA decode step µs (B=128, 16-32K paged bf16 cache)",
+                                             **bench_decode(d, iters=100, batch=128)}}[a.config](dev)
         line.update({"n_gpus": 1, "dtype": "bf16", "data": "synthetic"})
         print(json.dumps(line))
         return

@@ -33,6 +33,8 @@
 //   D2  every attention unit: window and sink units directly; routed units
 //       first merge the chunk top-k lists and take their pick;
 //   D3  LSE merge of the partial states, one wave per (sequence, head).
+#include <cstdlib>
+#include <cstring>
 #include <mutex>
 
 #include "hba_common.h"
@@ -173,6 +175,13 @@ __device__ __forceinline__ void dec_query(const typename St<DT>::T *q, const flo
     }
 }
 
+// 1 if entry (u, iu) ranks before (v, iv) under score desc, index asc; 0
+// otherwise.  Bitwise, so that it compiles to selects (the short-circuit form
+// becomes a branch per comparison).
+__device__ __forceinline__ int rank_before(float u, int iu, float v, int iv) {
+    return (int)(u > v) | ((int)(u == v) & (int)(iu < iv));
+}
+
 // ---------------------------------------------------------- bf16 units ----
 __device__ __forceinline__ bf16x8 dld_b8(const bf16_t *p) {
     return __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4d *>(p));
@@ -212,19 +221,19 @@ __device__ __forceinline__ void dec_unit_load(const bf16_t *kpage, const bf16_t 
         for (int h = 0; h < 2; ++h) va[dt][h] = dld_b8(vpage + ((dt * 2 + h) * 64 + lane) * 8);
 }
 
-// Zero the V^T values of the keys outside [lo, hi] (cache rows past the
-// sequence end may hold anything, and 0 * NaN would poison P.V).  Lane
-// (l16, lg) holds keys kbase + 32*h + 8*lg .. +7 in va[dt][h].
+// Zero the V^T values of the keys outside page offsets [rlo, rhi] (cache
+// rows past the sequence end may hold anything, and 0 * NaN would poison
+// P.V).  Lane (l16, lg) holds page offsets 32*h + 8*lg .. +7 in va[dt][h].
 template <int D>
-__device__ __forceinline__ void dec_mask_v(bf16x8 (&va)[D / 16][2], int64_t kbase, int64_t lo, int64_t hi) {
+__device__ __forceinline__ void dec_mask_v(bf16x8 (&va)[D / 16][2], int rlo, int rhi) {
     const int lg = (threadIdx.x & 63) >> 4;
     uint32_t m[2][4];
 #pragma unroll
     for (int h = 0; h < 2; ++h)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            const int64_t a = kbase + 32 * h + 8 * lg + 2 * e;
-            m[h][e] = ((a >= lo && a <= hi) ? 0x0000ffffu : 0u) | ((a + 1 >= lo && a + 1 <= hi) ? 0xffff0000u : 0u);
+            const int a = 32 * h + 8 * lg + 2 * e;   // key offset within the page
+            m[h][e] = ((a >= rlo && a <= rhi) ? 0x0000ffffu : 0u) | ((a + 1 >= rlo && a + 1 <= rhi) ? 0xffff0000u : 0u);
         }
 #pragma unroll
     for (int dt = 0; dt < D / 16; ++dt)
@@ -258,14 +267,16 @@ __device__ __forceinline__ void dec_unit_core(const bf16x8 (&ka)[4][D / 32], bf1
         for (int ks = 0; ks < NKS; ++ks)
             Sa[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[mt][ks], qop[ks], Sa[mt], 0, 0, 0);
     }
-    // Sa[mt][e] of lane (l16, lg): head l16, key kbase + 32*(mt>>1) + 8*lg + 4*(mt&1) + e
+    // Sa[mt][e] of lane (l16, lg): head l16, key kbase + 32*(mt>>1) + 8*lg + 4*(mt&1) + e;
+    // the valid keys are page offsets rlo..rhi (a unit lies within one page)
+    const int rlo = (int)(lo - kbase), rhi = (int)(hi - kbase);
     float tmax = -INFINITY;
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            const int64_t jj = kbase + 32 * (mt >> 1) + 8 * lg + 4 * (mt & 1) + e;
-            if (jj >= lo && jj <= hi) tmax = fmaxf(tmax, Sa[mt][e]);
+            const int jj = 32 * (mt >> 1) + 8 * lg + 4 * (mt & 1) + e;
+            if (jj >= rlo && jj <= rhi) tmax = fmaxf(tmax, Sa[mt][e]);
         }
     tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
@@ -277,8 +288,8 @@ __device__ __forceinline__ void dec_unit_core(const bf16x8 (&ka)[4][D / 32], bf1
     for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            const int64_t jj = kbase + 32 * (mt >> 1) + 8 * lg + 4 * (mt & 1) + e;
-            float p = (jj >= lo && jj <= hi) ? __builtin_amdgcn_exp2f(fmaf(Sa[mt][e], sl2, -ml2)) : 0.0f;
+            const int jj = 32 * (mt >> 1) + 8 * lg + 4 * (mt & 1) + e;
+            float p = (jj >= rlo && jj <= rhi) ? __builtin_amdgcn_exp2f(fmaf(Sa[mt][e], sl2, -ml2)) : 0.0f;
             p = rnd_bf16(p);                           // the weight P.V uses
             pk[mt >> 1][(mt & 1) * 4 + e] = p;
             psum += p;
@@ -286,7 +297,7 @@ __device__ __forceinline__ void dec_unit_core(const bf16x8 (&ka)[4][D / 32], bf1
     psum += __shfl_xor(psum, 16, 64);
     psum += __shfl_xor(psum, 32, 64);
     const bf16x8 pb0 = dpack_b8(pk[0]), pb1 = dpack_b8(pk[1]);
-    if (lo > kbase || hi < kbase + 63) dec_mask_v<D>(va, kbase, lo, hi);   // wave-uniform
+    if (rlo > 0 || rhi < 63) dec_mask_v<D>(va, rlo, rhi);   // wave-uniform
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) {
         O[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -486,7 +497,7 @@ __global__ __launch_bounds__(DEC_WG) void decode_d1_kernel(
 #pragma unroll 16
         for (int o = 0; o < DEC_CP; ++o) {
             const float vo = sc[o];
-            rank += ((vo > vv) || (vo == vv && o < tid)) ? 1 : 0;
+            rank += rank_before(vo, o, vv, tid);
         }
         if (rank < K) {
             const int64_t o = (((int64_t)s * Hkv + g) * gm.nsc + z) * K + rank;
@@ -582,7 +593,7 @@ __global__ __launch_bounds__(DEC_WG) void decode_d2_kernel(
                 const int mid = (lo + hi) >> 1;
                 const float vo = ev[c * K + mid];
                 const int io = ei[c * K + mid];
-                const bool before = vo != -INFINITY && ((vo > v) || (vo == v && io < id));
+                const bool before = (int)(vo != -INFINITY) & rank_before(vo, io, v, id);
                 if (before) lo = mid + 1;
                 else hi = mid;
             }
@@ -1055,10 +1066,10 @@ __global__ __launch_bounds__(DF_NT) void decode_fused_kernel(
 #pragma unroll
                     for (int i = 0; i < 8; ++i) {
                         const int o = o0 + 4 * i;
-                        rank += ((v4[i].x > vv) || (v4[i].x == vv && o < tid)) ? 1 : 0;
-                        rank += ((v4[i].y > vv) || (v4[i].y == vv && o + 1 < tid)) ? 1 : 0;
-                        rank += ((v4[i].z > vv) || (v4[i].z == vv && o + 2 < tid)) ? 1 : 0;
-                        rank += ((v4[i].w > vv) || (v4[i].w == vv && o + 3 < tid)) ? 1 : 0;
+                        rank += rank_before(v4[i].x, o, vv, tid);
+                        rank += rank_before(v4[i].y, o + 1, vv, tid);
+                        rank += rank_before(v4[i].z, o + 2, vv, tid);
+                        rank += rank_before(v4[i].w, o + 3, vv, tid);
                     }
                 }
                 if (rank < K) {
@@ -1132,7 +1143,7 @@ __global__ __launch_bounds__(DF_NT) void decode_fused_kernel(
             for (int o = part; o < E; o += 8) {
                 const float vo = ev[o];
                 const int io = ei[o];
-                cnt += (vo != -INFINITY && ((vo > v) || (vo == v && io < id))) ? 1 : 0;
+                cnt += (int)(vo != -INFINITY) & rank_before(vo, io, v, id);
             }
             cnt += __shfl_xor(cnt, 1, 64);
             cnt += __shfl_xor(cnt, 2, 64);
@@ -1232,6 +1243,369 @@ __global__ __launch_bounds__(DF_NT) void decode_fused_kernel(
     }
 }
 
+// ============================================================================
+// bf16: one workgroup per (sequence, KV head).
+//
+// Grid (Bd, Hkv), DP_NT threads, no workspace.  The workgroup scores every
+// candidate page of its (s, g) (the declared-order slot scores of
+// decode_fused_kernel), ranks them in LDS (64-page chunks, one wave each,
+// then the chunk lists: an entry's rank is the number of live entries ordered
+// before it), and runs the window, sink and routed page units on MFMA: wave w
+// takes units w, w + DP_NW, ... of the list (window pages, the sinks, the k
+// routed pages), loading the next unit while it computes one, and folds them
+// into one partial state per head; the waves' states merge by LSE, in wave
+// order, into out.  Every dependent step stays inside the workgroup, so the
+// step needs no cross-workgroup hand-off: page table; summaries (and, at
+// d = 64, the first window page); routed pages; out.
+// ============================================================================
+constexpr int DP_NT = 512;
+constexpr int DP_NW = DP_NT / 64;
+constexpr int DP_PMAX = 2048;                      // candidate pages ranked in LDS
+constexpr int DP_LMAX = DP_PMAX / 64 * DEC_KMAX;   // chunk-list entries
+constexpr int DP_WMAX = 256;                       // window + sink units
+
+template <int D>
+struct DpSmem {
+    float qc[DF_GMAX * D];
+    float qr[DF_GMAX * D];
+    float qx[D];
+    float sc[DP_PMAX];
+    int phys[DP_PMAX];
+    int wph[DP_WMAX];
+    int pick[DEC_KMAX], pickp[DEC_KMAX];
+    int nvalid;
+    union {
+        struct {
+            float v[DP_LMAX];
+            int p[DP_LMAX];
+        } ls;
+        float pbuf[DP_NW * DF_HB * dec_prow(D)];
+    } un;
+};
+
+// A page unit of the pair kernel: its key and value pages, first key,
+// valid key range and operand (rotated or not); ok false if it has no key.
+struct DpUnit {
+    const bf16_t *kp, *vp;
+    int64_t kbase, lo, hi;
+    bool ok, rope;
+};
+
+template <int D, int M>
+__global__ __launch_bounds__(DP_NT) void decode_pair_kernel(
+    const bf16_t *__restrict__ q, const float *__restrict__ qgain, float eps, const bf16_t *__restrict__ kcp,
+    const bf16_t *__restrict__ krp, const bf16_t *__restrict__ vp, const bf16_t *__restrict__ sp,
+    const int32_t *__restrict__ ptab, int64_t maxp, const int32_t *__restrict__ lens,
+    const float *__restrict__ cosT, const float *__restrict__ sinT, const float *__restrict__ scales, int Hq,
+    int Hkv, int S, int64_t W, int K, int nwp, int64_t gbmax, int64_t lmax, bf16_t *__restrict__ out,
+    int32_t *__restrict__ sel_idx, int32_t *__restrict__ sel_cnt) {
+    constexpr int BK = 64;
+    constexpr int NKS = D / 32, NDT = D / 16, PR = dec_prow(D);
+    constexpr int CPP = DP_NT / M;        // candidate pages per scoring pass
+    constexpr bool PREF = D == 64;        // the first window unit loads during the scoring
+    constexpr bool DBUF = D == 64;        // the next unit loads while one computes
+    __shared__ DpSmem<D> sm;
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, lg = lane >> 4;
+    const int64_t s = blockIdx.x;
+    const int g = blockIdx.y;
+    const int G = Hq / Hkv;
+    const int64_t sg = s * Hkv + g;
+    const int32_t *pt = ptab + s * maxp;
+
+    // Loads in the order of their use (see decode_fused_kernel): query
+    // elements and gain, length and scale, page-table entries of every page
+    // that can be a candidate at any length up to lmax (gbmax < maxp).
+    const int e0 = 8 * tid;
+    const bool hx = e0 < G * D;
+    const int ec = hx ? e0 : G * D - 8;
+    const u32x4d xr = *reinterpret_cast<const u32x4d *>(q + (s * Hq + (int64_t)g * G) * D + ec);
+    const float graw = *(qgain ? qgain + g * G + ec / D : scales + s);
+    const float gn = qgain ? graw : 1.0f;
+    int ph[DP_PMAX / DP_NT];
+#pragma unroll
+    for (int r = 0; r < DP_PMAX / DP_NT; ++r) {
+        const int64_t blk = 1 + tid + r * DP_NT;
+        ph[r] = pt[blk <= gbmax ? blk : 0];
+    }
+    const int64_t L = min(min((int64_t)lens[s], maxp * BK), lmax);
+    const float scale = scales[s];
+    const int64_t bmax = (L >= 1) ? cand_bmax(L - 1, BK, W) : 0;   // candidate pages 1..bmax
+    const int npass = (int)((bmax + CPP - 1) / CPP);
+    // window and sink units: their pages' table entries; cos/sin at L-1
+    int64_t ulo = 0, uhi = -1, upage = 0;
+    const bool uany = tid <= nwp && dec_unit_range(tid, L, S, W, nwp, ulo, uhi, upage);
+    const int uph = pt[uany ? upage : 0];
+    const int64_t crow = ((L >= 1) ? L - 1 : 0) * D + ec % D;
+    float cs[8], sn[8];
+    ld8<0>(cosT + crow, cs);
+    ld8<0>(sinT + crow, sn);
+#pragma unroll
+    for (int r = 0; r < DP_PMAX / DP_NT; ++r) sm.phys[tid + r * DP_NT] = ph[r];
+    if (tid <= nwp) sm.wph[tid] = uph;
+    float x[8];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        x[2 * e] = hx ? __uint_as_float(xr[e] << 16) : 0.0f;
+        x[2 * e + 1] = hx ? __uint_as_float(xr[e] & 0xffff0000u) : 0.0f;
+    }
+    df_query<D>(x, hx, qgain != nullptr, gn, eps, sm.qc, sm.qr, cs, sn);   // ends with a barrier
+    if (tid < D) {   // routing query: sequential head sum, rounded (summarizer.py:50-54)
+        float a = sm.qc[tid];
+        for (int h = 1; h < G; ++h) a = a + sm.qc[h * D + tid];
+        sm.qx[tid] = rnd_bf16(a);
+    }
+    if (tid == 0) sm.nvalid = 0;
+    if (tid < K) {
+        sm.pick[tid] = -1;
+        sm.pickp[tid] = -1;
+    }
+    __syncthreads();
+
+    // ------------------------------------------------ unit list of wave w --
+    const int nwin = (w <= nwp) ? (nwp - w) / DP_NW + 1 : 0;   // window and sink units
+    const int nrt = (w < K) ? (K - 1 - w) / DP_NW + 1 : 0;      // routed pages
+    const int nj = nwin + nrt;
+    auto unit = [&](int j) {
+        DpUnit U{kcp, vp, 0, 0, -1, false, false};
+        if (j < nwin) {
+            const int u = w + DP_NW * j;
+            int64_t lo, hi, page;
+            if (dec_unit_range(u, L, S, W, nwp, lo, hi, page)) {
+                const int64_t phy = sm.wph[u];
+                U.ok = true;
+                U.rope = u < nwp;
+                U.kbase = 64 * page;
+                U.lo = lo;
+                U.hi = hi;
+                U.kp = (U.rope ? krp : kcp) + (phy * Hkv + g) * BK * D;
+                U.vp = vp + (phy * Hkv + g) * D * BK;
+            }
+        } else if (j < nj) {
+            const int r = w + DP_NW * (j - nwin);
+            const int pb = sm.pick[r];
+            const int64_t phy = sm.pickp[r];
+            if (pb >= 1 && (int64_t)pb < maxp && phy >= 0) {
+                U.ok = true;
+                U.kbase = 64 * (int64_t)pb;
+                U.lo = U.kbase;
+                U.hi = U.kbase + 63;
+                U.kp = kcp + (phy * Hkv + g) * BK * D;
+                U.vp = vp + (phy * Hkv + g) * D * BK;
+            }
+        }
+        return U;
+    };
+    bf16x8 ka0[4][NKS], va0[NDT][2];
+    DpUnit cur{kcp, vp, 0, 0, -1, false, false};
+    const bool pre = PREF && nwin > 0;   // wave-uniform
+    if (pre) {
+        cur = unit(0);
+        dec_unit_load<D>(cur.kp, cur.vp, ka0, va0);
+    }
+
+    // ------------------------------------------------ candidate scores ----
+    const int p = tid / M, sl = tid % M;
+    auto srow_load = [&](int ps, u32x4d (&sr)[D / 8]) {
+        const int64_t blk = 1 + (int64_t)ps * CPP + p;
+        const bf16_t *src = (blk <= bmax) ? sp + (((int64_t)sm.phys[blk - 1] * Hkv + g) * M + sl) * D : sp;
+#pragma unroll
+        for (int c = 0; c < D / 8; ++c) sr[c] = *reinterpret_cast<const u32x4d *>(src + 8 * c);
+    };
+    auto score = [&](int ps, const u32x4d (&sr)[D / 8]) {
+        const int64_t blk = 1 + (int64_t)ps * CPP + p;
+        float acc = 0.0f;   // declared order: sequential FMA over the elements
+#pragma unroll
+        for (int c0 = 0; c0 < D / 8; c0 += 4) {
+            float4 qv[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) qv[i] = *reinterpret_cast<const float4 *>(&sm.qx[8 * c0 + 4 * i]);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const uint32_t *r32 = reinterpret_cast<const uint32_t *>(&sr[c0 + c]);
+                const float4 a = qv[2 * c], b = qv[2 * c + 1];
+                acc = fmaf(a.x, __uint_as_float(r32[0] << 16), acc);
+                acc = fmaf(a.y, __uint_as_float(r32[0] & 0xffff0000u), acc);
+                acc = fmaf(a.z, __uint_as_float(r32[1] << 16), acc);
+                acc = fmaf(a.w, __uint_as_float(r32[1] & 0xffff0000u), acc);
+                acc = fmaf(b.x, __uint_as_float(r32[2] << 16), acc);
+                acc = fmaf(b.y, __uint_as_float(r32[2] & 0xffff0000u), acc);
+                acc = fmaf(b.z, __uint_as_float(r32[3] << 16), acc);
+                acc = fmaf(b.w, __uint_as_float(r32[3] & 0xffff0000u), acc);
+            }
+        }
+        float best = (acc > -INFINITY) ? acc : -INFINITY;
+#pragma unroll
+        for (int o = 1; o < M; o <<= 1) {   // max over a page's slots: exact in any order
+            const float ot = __shfl_xor(best, o, 64);
+            best = (ot > best) ? ot : best;
+        }
+        if (sl == 0 && blk <= bmax) sm.sc[blk - 1] = best * scale;
+    };
+    {
+        u32x4d sa[D / 8], sb[D / 8];
+        srow_load(0, sa);
+        srow_load(1, sb);
+        for (int ps = 0; ps < npass; ps += 2) {
+            score(ps, sa);
+            srow_load(ps + 2, sa);
+            score(ps + 1, sb);
+            srow_load(ps + 3, sb);
+        }
+    }
+    __syncthreads();
+
+    // -------------------------------------- top-K: 64-page chunk lists ----
+    // (rolled loops in this single-pass code: every workgroup runs it once,
+    // so its length is instruction fetch time)
+    const int nb = (int)bmax;   // <= DP_PMAX
+    const int nch = (nb + 63) / 64;
+    float *lv = sm.un.ls.v;
+    int *lp = sm.un.ls.p;
+#pragma unroll 1
+    for (int c = w; c < nch; c += DP_NW) {
+        const int cb = 64 * c;
+        const int pg = cb + lane;
+        const float vr = sm.sc[pg];   // inside sc (pg < DP_PMAX); masked below
+        const float v = (pg < nb) ? vr : -INFINITY;
+        const int lim = nb - cb;   // valid entries of the chunk
+        int rank = 0;   // score desc, page asc
+#pragma unroll 1
+        for (int o = 0; o < 64; o += 8) {
+            const float4 va4 = *reinterpret_cast<const float4 *>(&sm.sc[cb + o]);
+            const float4 vb4 = *reinterpret_cast<const float4 *>(&sm.sc[cb + o + 4]);
+            const float vo[8] = {va4.x, va4.y, va4.z, va4.w, vb4.x, vb4.y, vb4.z, vb4.w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float u = (o + e < lim) ? vo[e] : -INFINITY;
+                rank += rank_before(u, o + e, v, lane);
+            }
+        }
+        if (rank < K) {   // the ranks are a permutation: every list entry is written
+            lv[c * K + rank] = v;
+            lp[c * K + rank] = pg + 1;
+        }
+    }
+    __syncthreads();
+    // merge: an entry's global rank is the number of live entries of all
+    // lists ordered before it (the lists hold distinct pages); 8 threads
+    // count an eighth of the entries each
+    const int E = nch * K;
+#pragma unroll 1
+    for (int f0 = 0; f0 < E; f0 += DP_NT / 8) {
+        const int e = f0 + tid / 8, part = tid % 8;
+        const float v = (e < E) ? lv[e] : -INFINITY;
+        const int id = (e < E) ? lp[e] : 0;
+        int cnt = 0;
+#pragma unroll 4
+        for (int o = part; o < E; o += 8) {
+            const float vo = lv[o];
+            const int io = lp[o];
+            cnt += (int)(vo != -INFINITY) & rank_before(vo, io, v, id);
+        }
+        cnt += __shfl_xor(cnt, 1, 64);
+        cnt += __shfl_xor(cnt, 2, 64);
+        cnt += __shfl_xor(cnt, 4, 64);
+        if (part == 0 && v != -INFINITY && cnt < K) {
+            sm.pick[cnt] = id;
+            sm.pickp[cnt] = sm.phys[id - 1];
+            atomicAdd(&sm.nvalid, 1);
+        }
+    }
+    __syncthreads();
+
+    // ------------------------------------------------------- page units ----
+    bf16x8 qr_op[NKS], qc_op[NKS];
+    df_qop<D>(sm.qr, G, qr_op);
+    df_qop<D>(sm.qc, G, qc_op);
+    f32x4 Oa[NDT];
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) Oa[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float ma = -INFINITY, la = 0.0f;
+    auto run = [&](const DpUnit &U, const bf16x8 (&ka)[4][NKS], bf16x8 (&va)[NDT][2]) {
+        if (!U.ok) return;
+        f32x4 O[NDT];
+        float mu, lu;
+        dec_unit_core<D>(ka, va, U.rope ? qr_op : qc_op, U.kbase, U.lo, U.hi, scale, O, mu, lu);
+        dec_fold<NDT>(Oa, ma, la, O, mu, lu);
+    };
+    if (!pre && nj > 0) {
+        cur = unit(0);
+        dec_unit_load<D>(cur.kp, cur.vp, ka0, va0);
+    }
+    if constexpr (DBUF) {
+        // the next unit's loads are in flight while this one computes; one
+        // copy of the unit code (the operands move between the buffers)
+#pragma unroll 1
+        for (int j = 0; j < nj; ++j) {
+            const DpUnit nx = unit(j + 1);
+            bf16x8 ka1[4][NKS], va1[NDT][2];
+            dec_unit_load<D>(nx.kp, nx.vp, ka1, va1);
+            run(cur, ka0, va0);
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+                for (int ks = 0; ks < NKS; ++ks) ka0[mt][ks] = ka1[mt][ks];
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt) {
+                va0[dt][0] = va1[dt][0];
+                va0[dt][1] = va1[dt][1];
+            }
+            cur = nx;
+        }
+    } else {
+#pragma unroll 1
+        for (int j = 0; j < nj; ++j) {
+            if (j > 0) {
+                cur = unit(j);
+                dec_unit_load<D>(cur.kp, cur.vp, ka0, va0);
+            }
+            run(cur, ka0, va0);
+        }
+    }
+
+    // --------------------------- the waves' states, merged by LSE, to out ---
+    float *pbuf = sm.un.pbuf;
+#pragma unroll 1
+    for (int hc = 0; hc < G; hc += DF_HB) {
+        __syncthreads();   // the region's earlier readers (the lists, the last pass) are done
+        const int hh = l16 - hc;
+        if (l16 < G && hh >= 0 && hh < DF_HB) {
+            float *dst = pbuf + (w * DF_HB + hh) * PR;
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt)
+                *reinterpret_cast<float4 *>(dst + 16 * dt + 4 * lg) = float4{Oa[dt][0], Oa[dt][1], Oa[dt][2], Oa[dt][3]};
+            if (lg == 0) {
+                dst[D] = ma;
+                dst[D + 1] = la;
+            }
+        }
+        __syncthreads();
+        for (int e = tid; e < DF_HB * D; e += DP_NT) {
+            const int hb = e / D, t = e % D, h = hc + hb;
+            if (h >= G) continue;
+            float mx = -INFINITY;
+#pragma unroll
+            for (int ww = 0; ww < DP_NW; ++ww) mx = fmaxf(mx, pbuf[(ww * DF_HB + hb) * PR + D]);
+            float o = 0.0f, l = 0.0f;
+            if (mx != -INFINITY) {
+#pragma unroll
+                for (int ww = 0; ww < DP_NW; ++ww) {
+                    const float *src = pbuf + (ww * DF_HB + hb) * PR;
+                    const float mw = src[D];
+                    if (mw == -INFINITY) continue;
+                    const float a = exp2f((mw - mx) * DEC_LOG2E);
+                    o = fmaf(src[t], a, o);
+                    l = fmaf(src[D + 1], a, l);
+                }
+            }
+            out[(s * Hq + (int64_t)g * G + h) * D + t] = f2bf(l > 0.0f ? o / l : 0.0f);
+        }
+    }
+    const int nv = sm.nvalid;
+    if (sel_idx && tid < K) sel_idx[sg * K + tid] = (tid < nv) ? sm.pick[tid] : -1;
+    if (sel_cnt && tid == 0) sel_cnt[sg] = nv < K ? nv : K;
+}
+
 // Clears n 16-byte words (the no-allocation scratch, once per device).
 __global__ void dec_zero_kernel(uint4 *p, size_t n) {
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
@@ -1291,6 +1665,23 @@ extern "C" int hba_decode_workspace_size(int64_t Bd, int64_t Hq, int64_t Hkv, in
     return HBA_OK;
 }
 
+// The bf16 step's kernel.  decode_pair_kernel (one workgroup per (sequence,
+// KV head), no hand-off between workgroups) when there are at least
+// DP_MIN_PAIRS pairs and its LDS holds the candidate and window pages of the
+// longest sequence; decode_fused_kernel (the scoring split over workgroups)
+// otherwise.  Measured at 16-32K tokens, 14/2 heads, d = 64 (graph replay):
+// 32 sequences fused 30.7 / pair 38.1 us, 128 sequences 69.2 / 47.8 us, 256
+// sequences 143.5 / 95.7 us.  HBA_DECODE_KERNEL=pair or =fused in the
+// environment overrides the pair count (the LDS bounds still hold).
+constexpr int64_t DP_MIN_PAIRS = 128;
+static bool dec_use_pair(int64_t Bd, int64_t Hkv, int64_t gbmax, int nwp) {
+    if (gbmax > DP_PMAX || nwp + 1 > DP_WMAX) return false;
+    const char *e = getenv("HBA_DECODE_KERNEL");
+    if (e && !strcmp(e, "fused")) return false;
+    if (e && !strcmp(e, "pair")) return true;
+    return Bd * Hkv >= DP_MIN_PAIRS;
+}
+
 // The decode step on a given workspace; scratch_max > 0 marks the
 // no-allocation entry point, whose workspace is the fixed scratch array
 // (a request that does not fit it is HBA_ERR_SCRATCH).
@@ -1329,6 +1720,28 @@ static int decode_fwd_ws(int dtype, const void *q, const float *q_gain, float ep
         ws_layout_fused(Bd, Hq, Hkv, d, k, fg, &ov, &oi, &oph, &op, &total);
         if (scratch_max && total > scratch_max) return HBA_ERR_SCRATCH;
         if (ws_bytes < total) return HBA_ERR_INVALID_ARG;
+        const int64_t gbmax = cand_bmax(max_len - 1, 64, W);
+        if (dec_use_pair(Bd, Hkv, gbmax, fg.nwp)) {
+#define HBA_DP(D, M)                                                                                          \
+    hipLaunchKernelGGL((decode_pair_kernel<D, M>), dim3((unsigned)Bd, (unsigned)Hkv), dim3(DP_NT), 0, s,        \
+                       (const bf16_t *)q, q_gain, eps, (const bf16_t *)kc_pages, (const bf16_t *)kr_pages,     \
+                       (const bf16_t *)v_pages, (const bf16_t *)summ_pages, page_table, max_pages, seq_lens,   \
+                       cos_tab, sin_tab, scales, (int)Hq, (int)Hkv, (int)S, W, (int)k, fg.nwp, gbmax, max_len, \
+                       (bf16_t *)out, sel_idx, sel_cnt)
+#define HBA_DPM(D)                     \
+    do {                               \
+        if (m == 1) HBA_DP(D, 1);      \
+        else if (m == 2) HBA_DP(D, 2); \
+        else if (m == 4) HBA_DP(D, 4); \
+        else HBA_DP(D, 8);             \
+    } while (0)
+            if (d == 64) HBA_DPM(64);
+            else HBA_DPM(128);
+#undef HBA_DP
+#undef HBA_DPM
+            HBA_LAUNCH_CHECK();
+            return HBA_OK;
+        }
         dim3 grid((unsigned)Bd, (unsigned)Hkv, (unsigned)fg.nz);
 #define HBA_DF(D, M)                                                                                   \
     hipLaunchKernelGGL((decode_fused_kernel<D, M>), grid, dim3(DF_NT), 0, s, (const bf16_t *)q, q_gain, eps, \

@@ -193,11 +193,13 @@ def check_decode(cache, cfg, prm, cos, sin, kcs, vs, qd, dt, out, sidx, scnt):
         assert err <= TOL[dt], (s, L, err)
 
 
-@pytest.mark.parametrize("dt", ["bf16", "f32"])
-def test_decode_16k_32k_batch(dev, dt):
+@pytest.mark.parametrize("dt,kern", [("bf16", "fused"), ("bf16", "pair"), ("f32", "fused")])
+def test_decode_16k_32k_batch(dev, dt, kern, monkeypatch):
     """The decode workload's lengths (L ~ U[16384, 32768], seed 0) plus one
     sequence of exactly 32768 tokens (8 score chunks of 64 candidate pages)
-    and two short ones, whose chunks past their last candidate are empty."""
+    and two short ones, whose chunks past their last candidate are empty; in
+    bf16 on both kernels."""
+    monkeypatch.setenv("HBA_DECODE_KERNEL", kern)
     lens = synth.decode_lengths(6, 16384, 32768, seed=0) + [32768, 70, 1500]
     cfg, cache, prm, cos, sin, kcs, vs, g = lean_cache(dev, dt, lens)
     qd = torch.randn(len(lens), 14, 64, generator=g).to(TDT[dt]).to(dev)
@@ -206,12 +208,15 @@ def test_decode_16k_32k_batch(dev, dt):
     check_decode(cache, cfg, prm, cos, sin, kcs, vs, qd, dt, out, sidx, scnt)
 
 
-def test_decode_d128_continuation_over_a_page_boundary(dev):
+@pytest.mark.parametrize("kern", ["fused", "pair"])
+def test_decode_d128_continuation_over_a_page_boundary(dev, kern, monkeypatch):
     """The donor shape's decode continuation: 28/4 heads, d = 128, 8 sinks,
     two sequences loaded at ~6000 tokens (2 score chunks), then 70 steps that
     each append one token per sequence (kv_append, bit-exact) and decode a
     new query against the oracle; the pages that fill get their summaries.
-    native_ctx = 4096 makes the log-length temperature differ per sequence."""
+    native_ctx = 4096 makes the log-length temperature differ per sequence.
+    On both bf16 decode kernels."""
+    monkeypatch.setenv("HBA_DECODE_KERNEL", kern)
     lens = [6000, 5950]
     cfg, cache, prm, cos, sin, kcs, vs, g = lean_cache(dev, "bf16", lens, Hq=28, Hkv=4, d=128, S=8, extra=80,
                                                        native_ctx=4096)

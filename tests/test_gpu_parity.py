@@ -954,15 +954,26 @@ def _decode_vs_oracle(dev, dt, lens, **kw):
         assert np.abs(f(out[s]) - ref).max() <= TOL[dt], (s, np.abs(f(out[s]) - ref).max())
 
 
-@pytest.mark.parametrize("dt", ["f32", "bf16"])
-def test_decode_matches_oracle(dev, dt):
+def use_decode_kernel(monkeypatch, kern):
+    """Pick the bf16 decode kernel (decode_pair_kernel or decode_fused_kernel)
+    whatever the batch size, through the library's HBA_DECODE_KERNEL switch."""
+    monkeypatch.setenv("HBA_DECODE_KERNEL", kern)
+
+
+@pytest.mark.parametrize("dt,kern", [("f32", "fused"), ("bf16", "fused"), ("bf16", "pair")])
+def test_decode_matches_oracle(dev, dt, kern, monkeypatch):
+    use_decode_kernel(monkeypatch, kern)
     _decode_vs_oracle(dev, dt, [1, 3, 70, 1100, 1200, 2500, 2049, 4096, 3333], W=1024, k=16)
 
 
-@pytest.mark.parametrize("d,k,Hq,Hkv,S", [(128, 16, 28, 4, 8), (64, 40, 14, 2, 4), (64, 64, 8, 1, 0)])
-def test_decode_bf16_shapes(dev, d, k, Hq, Hkv, S):
-    """bf16 decode at d = 128 (8-wave routed/merge workgroups), and with more
-    picks than waves (k = 40, 64: each wave runs several routed pages)."""
+@pytest.mark.parametrize("kern", ["fused", "pair"])
+@pytest.mark.parametrize("d,k,Hq,Hkv,S", [(128, 16, 28, 4, 8), (64, 40, 14, 2, 4), (64, 64, 8, 1, 0),
+                                          (64, 16, 32, 2, 4), (128, 8, 16, 1, 64)])
+def test_decode_bf16_shapes(dev, d, k, Hq, Hkv, S, kern, monkeypatch):
+    """bf16 decode at d = 128, with more picks than waves (k = 40, 64: each
+    wave runs several routed pages), 16 heads per KV head and a full sink
+    page, on both bf16 kernels."""
+    use_decode_kernel(monkeypatch, kern)
     _decode_vs_oracle(dev, "bf16", [70, 700, 2500, 4096], Hq=Hq, Hkv=Hkv, d=d, S=S, W=512, k=k)
 
 
@@ -1036,9 +1047,10 @@ def test_kv_append_and_page_summaries(dev, dt, d):
     assert torch.equal(cache._scales, torch.index_select(cache.scale_table(), 0, cache.seq_lens))
 
 
-@pytest.mark.parametrize("dt,graph", [("bf16", False), ("bf16", True), ("f32", False)],
-                         ids=["bf16-direct", "bf16-graph", "f32-direct"])
-def test_decode_loop_matches_append_and_step(dev, dt, graph):
+@pytest.mark.parametrize("dt,graph,kern", [("bf16", False, "fused"), ("bf16", True, "fused"), ("f32", False, "fused"),
+                                            ("bf16", False, "pair"), ("bf16", True, "pair")],
+                         ids=["bf16-direct", "bf16-graph", "f32-direct", "bf16-direct-pair", "bf16-graph-pair"])
+def test_decode_loop_matches_append_and_step(dev, dt, graph, kern, monkeypatch):
     """DecodeLoop (two launches per token straight through the C-ABI, or both
     captured once as a HIP graph and replayed) against cache.append +
     hba_decode_step on an identical cache, 60 tokens that fill pages of every
@@ -1048,6 +1060,7 @@ def test_decode_loop_matches_append_and_step(dev, dt, graph):
     the dtype's rounding of the step sized by the longest sequence; the filled
     pages' summaries, the appended rows and the device lengths agree.  Work
     of the other path runs between the replays."""
+    use_decode_kernel(monkeypatch, kern)
     lens = [127, 60, 2500]
     kw = dict(W=256, k=8, seed=6)
     cfg, x, prm, cos, sin, ca, kcs, qn = build_cache(dev, dt, lens, **kw)

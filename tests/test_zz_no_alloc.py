@@ -40,8 +40,9 @@ def _cache(dev, dt, lens, seed, Hq=14, Hkv=2, d=64, m=4, W=1024, S=4, k=16):
     return cfg, cache, prm, cos, sin, q
 
 
-@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
-def test_noalloc_decode_equals_decode_on_two_calls(dev, dt):
+@pytest.mark.parametrize("dt,kern", [(torch.bfloat16, "fused"), (torch.bfloat16, "pair"), (torch.float32, "fused")])
+def test_noalloc_decode_equals_decode_on_two_calls(dev, dt, kern, monkeypatch):
+    monkeypatch.setenv("HBA_DECODE_KERNEL", kern)   # either bf16 kernel, whatever the batch size
     for lens, seed in (([9000, 4100, 12000, 300, 7777, 20000], 0), ([5000, 130, 2600], 1)):
         cfg, cache, prm, cos, sin, q = _cache(dev, dt, lens, seed)
         scales = cache.scales(cfg)
