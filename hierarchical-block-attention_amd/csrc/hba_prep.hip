@@ -65,35 +65,135 @@ __device__ __forceinline__ void store_row(typename St<DT>::T *p, const float (&x
     }
 }
 
+// 8 consecutive elements (16 bytes of bf16, 32 of fp32; 16-byte aligned)
+template <int DT>
+__device__ __forceinline__ void load8(const typename St<DT>::T *p, float (&x)[8]) {
+    if constexpr (DT == 1) {
+        const uint4 u = *reinterpret_cast<const uint4 *>(p);
+        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            x[2 * e] = __uint_as_float(w[e] << 16);
+            x[2 * e + 1] = __uint_as_float(w[e] & 0xffff0000u);
+        }
+    } else {
+        const float4 a = reinterpret_cast<const float4 *>(p)[0], c = reinterpret_cast<const float4 *>(p)[1];
+        x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+        x[4] = c.x; x[5] = c.y; x[6] = c.z; x[7] = c.w;
+    }
+}
+
+template <int DT>
+__device__ __forceinline__ void store8(typename St<DT>::T *p, const float (&x)[8]) {
+    if constexpr (DT == 1) {
+        uint32_t w[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) w[e] = (uint32_t)f2bf(x[2 * e]) | ((uint32_t)f2bf(x[2 * e + 1]) << 16);
+        *reinterpret_cast<uint4 *>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+    } else {
+        float4 *q = reinterpret_cast<float4 *>(p);
+        q[0] = make_float4(x[0], x[1], x[2], x[3]);
+        q[1] = make_float4(x[4], x[5], x[6], x[7]);
+    }
+}
+
 // --------------------------------------------------------------- kernels ----
+// One workgroup per (batch, KV head, 64-key tile); D/8 lanes per key row, 8
+// elements each, so that every row load and store is one coalesced 16-byte
+// access per lane.  QKNorm's sum of squares runs in the declared order
+// (sequential FMA over the row, as qknorm_row) as a chain through the row's
+// lanes: lane c continues the sum of lane c-1 (row_shr:1 DPP move); the
+// rotation's partner elements (rotate-half) come from lane c ^ (D/16).  The
+// values are transposed through LDS, so that vt rows are written as 8
+// consecutive keys per lane.
 template <int DT, int D>
 __global__ __launch_bounds__(256) void prep_keys_kernel(
     const typename St<DT>::T *__restrict__ k, int64_t ksb, int64_t ksn, int64_t ksh,
     const typename St<DT>::T *__restrict__ v, int64_t vsb, int64_t vsn, int64_t vsh,
     const float *__restrict__ kgain, float eps, const float *__restrict__ cosT,
-    const float *__restrict__ sinT, int64_t B, int64_t n, int64_t Hkv,
+    const float *__restrict__ sinT, int64_t n, int64_t Hkv, int64_t ntile,
     typename St<DT>::T *__restrict__ kc, typename St<DT>::T *__restrict__ kr,
     typename St<DT>::T *__restrict__ vt) {
-    int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (gid >= B * Hkv * n) return;
-    int64_t j = gid % n;
-    int64_t g = (gid / n) % Hkv;
-    int64_t b = gid / (n * Hkv);
-    float x[D];
-    load_row<DT, D>(k + b * ksb + j * ksn + g * ksh, x);
-    if (kgain) qknorm_row<DT, D>(x, kgain[g], eps);
-    int64_t row = ((b * Hkv + g) * n + j) * D;
-    store_row<DT, D>(kc + row, x);
-    if (kr) {
-        float y[D];
-        rope_row<DT, D>(x, y, cosT + j * D, sinT + j * D);
-        store_row<DT, D>(kr + row, y);
-    }
-    if (vt) {
-        load_row<DT, D>(v + b * vsb + j * vsn + g * vsh, x);
-        typename St<DT>::T *o = vt + (b * Hkv + g) * D * n + j;
+    using T = typename St<DT>::T;
+    constexpr int TPH = D / 8;          // lanes per key row
+    constexpr int RPP = 256 / TPH;      // rows per pass
+    __shared__ float vs[D][65];         // the tile's values (exact in fp32), key-minor
+    const int tid = threadIdx.x;
+    const int64_t tile = blockIdx.x % ntile;
+    const int64_t bg = blockIdx.x / ntile;   // b * Hkv + g
+    const int64_t b = bg / Hkv, g = bg % Hkv;
+    const int jl = tid % TPH, t0 = 8 * jl;
+    const bool lo = t0 < D / 2;
+    const float gn = kgain ? kgain[g] : 0.0f;
+#pragma unroll 1
+    for (int pass = 0; pass < 64 / RPP; ++pass) {
+        const int r = pass * RPP + tid / TPH;
+        const int64_t j = tile * 64 + r;
+        const bool act = j < n;
+        const int64_t jj = act ? j : 0;
+        float x[8];
+        load8<DT>(k + b * ksb + jj * ksn + g * ksh + t0, x);
+        if (kgain) {
+            float run = 0.0f;
 #pragma unroll
-        for (int t = 0; t < D; ++t) St<DT>::st(o, (int64_t)t * n, x[t]);
+            for (int step = 0; step < TPH; ++step) {
+                const float in = __builtin_bit_cast(
+                    float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, run), 0x111, 0xf, 0xf, false));
+                if (jl == step) {
+                    float a = (jl == 0) ? 0.0f : in;
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) a = fmaf(x[u], x[u], a);
+                    run = a;
+                }
+            }
+            const float ss = __shfl(run, (tid & 63) | (TPH - 1), 64);   // the row's last lane
+            float ms = ss / (float)D;
+            if (ms < eps) ms = eps;
+            const float rr = sqrtf(ms);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) x[u] = St<DT>::rnd((x[u] / rr) * gn);
+        }
+        const int64_t row = (bg * n + jj) * D + t0;
+        if (act) store8<DT>(kc + row, x);
+        if (kr) {
+            float cs[8], sn[8], y[8];
+            load8<0>(cosT + jj * D + t0, cs);
+            load8<0>(sinT + jj * D + t0, sn);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const float part = __shfl_xor(x[u], TPH / 2, 64);
+                const float rot = lo ? -part : part;
+                y[u] = St<DT>::rnd(St<DT>::rnd(x[u] * St<DT>::rnd(cs[u])) + St<DT>::rnd(rot * St<DT>::rnd(sn[u])));
+            }
+            if (act) store8<DT>(kr + row, y);
+        }
+        if (vt) {
+            float vv[8];
+            load8<DT>(v + b * vsb + jj * vsn + g * vsh + t0, vv);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) vs[t0 + u][r] = vv[u];
+        }
+    }
+    if (!vt) return;
+    __syncthreads();
+    // vt[bg][t][tile*64 + 8c' .. +7]: 8 consecutive keys of one row per thread
+    T *vrow = vt + bg * D * n;
+    const int64_t k0 = tile * 64;
+    const bool vec = ((reinterpret_cast<uintptr_t>(vt) & 15) == 0) && (n % 8 == 0);   // uniform
+#pragma unroll 1
+    for (int c = tid; c < D * 8; c += 256) {
+        const int t = c / 8, j8 = 8 * (c % 8);
+        float o[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) o[u] = vs[t][j8 + u];
+        const int64_t jo = k0 + j8;
+        if (vec && jo + 8 <= n) {
+            store8<DT>(vrow + (int64_t)t * n + jo, o);
+        } else {
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                if (jo + u < n) St<DT>::st(vrow, (int64_t)t * n + jo + u, o[u]);
+        }
     }
 }
 
@@ -244,7 +344,13 @@ __global__ __launch_bounds__(256) void summarize_kernel(
     } else {
         src = kc + ((b * Hkv + g) * n + c * BK) * D;
         dst = out + ((b * Hkv + g) * nb + c) * m * D;
-        for (int e = tid; e < BK * D; e += 256) kb[e / D][e % D] = St<DT>::ld(src, e);
+        for (int c8 = tid; c8 < BK * D / 8; c8 += 256) {   // 16-byte loads, 8 elements of one row
+            float x[8];
+            load8<DT>(src + 8 * c8, x);
+            const int r = (8 * c8) / D, t0 = (8 * c8) % D;
+#pragma unroll
+            for (int u = 0; u < 8; ++u) kb[r][t0 + u] = x[u];
+        }
     }
     __syncthreads();
     summarize_staged<DT, D, LONE>(sm, probes + g * m * D, proj + g * D * D, m, att_scale, dst, tid);
@@ -472,18 +578,20 @@ extern "C" int hba_prep_keys(int dtype, const void *k, const int64_t k_strides[3
     if (!k || !k_strides || !kc || B <= 0 || n <= 0 || Hkv <= 0) return HBA_ERR_INVALID_ARG;
     if (kr && (!cos_tab || !sin_tab)) return HBA_ERR_INVALID_ARG;
     if (vt && (!v || !v_strides)) return HBA_ERR_INVALID_ARG;
+    if (kr && (!abi::aligned16(cos_tab) || !abi::aligned16(sin_tab))) return HBA_ERR_UNSUPPORTED;
     if (!abi::rows_aligned(dtype, k, k_strides) || (vt && !abi::rows_aligned(dtype, v, v_strides)) ||
         !abi::aligned16(kc) || (kr && !abi::aligned16(kr)))
         return HBA_ERR_UNSUPPORTED;
     hipStream_t s = (hipStream_t)stream;
-    int64_t total = B * Hkv * n;
-    dim3 grid((unsigned)((total + 255) / 256));
+    const int64_t ntile = (n + 63) / 64;
+    if (B * Hkv * ntile > 0x7fffffff) return HBA_ERR_UNSUPPORTED;
+    dim3 grid((unsigned)(B * Hkv * ntile));
     const int64_t *vs = v_strides ? v_strides : k_strides;
 #define HBA_PREP(DT, D)                                                                            \
     hipLaunchKernelGGL((prep_keys_kernel<DT, D>), grid, dim3(256), 0, s,                           \
                        (const St<DT>::T *)k, k_strides[0], k_strides[1], k_strides[2],             \
-                       (const St<DT>::T *)v, vs[0], vs[1], vs[2], k_gain, eps, cos_tab, sin_tab, B, n, \
-                       Hkv, (St<DT>::T *)kc, (St<DT>::T *)kr, (St<DT>::T *)vt)
+                       (const St<DT>::T *)v, vs[0], vs[1], vs[2], k_gain, eps, cos_tab, sin_tab, n, \
+                       Hkv, ntile, (St<DT>::T *)kc, (St<DT>::T *)kr, (St<DT>::T *)vt)
     HBA_DISPATCH_DT_D(dtype, d, HBA_PREP);
 #undef HBA_PREP
     HBA_LAUNCH_CHECK();
@@ -501,6 +609,7 @@ static int summarize_common(int dtype, const void *kc, int64_t B, int64_t Hkv, i
     if (m < 1 || m > 8) return HBA_ERR_UNSUPPORTED;
     if (nblocks <= 0) return HBA_OK;
     if (nblocks > 0x7fffffff || Hkv > 65535 || B > 65535) return HBA_ERR_UNSUPPORTED;
+    if (!abi::aligned16(kc)) return HBA_ERR_UNSUPPORTED;
     hipStream_t s = (hipStream_t)stream;
     dim3 grid((unsigned)nblocks, (unsigned)Hkv, (unsigned)B);
     float att_scale = (float)(1.0 / __builtin_sqrt((double)d));
