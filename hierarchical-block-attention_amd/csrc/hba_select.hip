@@ -1387,3 +1387,163 @@ extern "C" int hba_hier_select(int dtype, const void *q, const int64_t q_strides
     HBA_LAUNCH_CHECK();
     return HBA_OK;
 }
+
+// ---------------------------------------------------------------------------
+// hier_select with an arbitrary candidate mask: the reference function as
+// hba_attention_eval and evals.hier_fidelity call it (src/hba/attention.py:
+// 217-246, src/hba/evals.py:314).  One workgroup per (batch row, query row).
+// Scores in fp32 in the declared order (dot over d in index order, slot max,
+// times scale); a super is scored if one of its children is a candidate;
+// the top b_eff = min(beam, ns) supers, then the top min(kk, b_eff * F)
+// candidate children, each by block-wide argmax rounds under (score desc,
+// block asc).
+namespace hr {
+constexpr int NT = 256;
+constexpr int DMAX = 256, NSMAX = 4096, BEAMMAX = 64, CMAX = 1024;
+
+template <int DT>
+__device__ __forceinline__ float score(const float *q, const typename St<DT>::T *S, int m, int d, float scale) {
+    float best = 0.0f;
+    for (int s = 0; s < m; ++s) {
+        float acc = 0.0f;
+        for (int t = 0; t < d; ++t) acc = fmaf(q[t], St<DT>::ld(S, (int64_t)s * d + t), acc);
+        best = (s == 0 || acc > best) ? acc : best;
+    }
+    return best * scale;
+}
+
+// Position of the best finite entry of vals[0..len) (ids: its block, null =
+// the position), -1 if none; the same answer in every thread.  Ends with a
+// barrier.
+__device__ int argmax(const float *vals, const int *ids, int len, float *wv, int *wi, int *wj) {
+    float bv = -INFINITY;
+    int bi = 0, bj = -1;
+    for (int j = threadIdx.x; j < len; j += NT) {
+        const float v = vals[j];
+        const int id = ids ? ids[j] : j;
+        if (v != -INFINITY && v == v && (bj < 0 || better(v, id, bv, bi))) {
+            bv = v;
+            bi = id;
+            bj = j;
+        }
+    }
+    for (int o = 32; o >= 1; o >>= 1) {
+        const float ov = __shfl_xor(bv, o, 64);
+        const int oi = __shfl_xor(bi, o, 64), oj = __shfl_xor(bj, o, 64);
+        if (oj >= 0 && (bj < 0 || better(ov, oi, bv, bi))) {
+            bv = ov;
+            bi = oi;
+            bj = oj;
+        }
+    }
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+        wv[w] = bv;
+        wi[w] = bi;
+        wj[w] = bj;
+    }
+    __syncthreads();
+    float rv = wv[0];
+    int ri = wi[0], rj = wj[0];
+    for (int x = 1; x < NT / 64; ++x)
+        if (wj[x] >= 0 && (rj < 0 || better(wv[x], wi[x], rv, ri))) {
+            rv = wv[x];
+            ri = wi[x];
+            rj = wj[x];
+        }
+    __syncthreads();
+    return rj;
+}
+}  // namespace hr
+
+template <int DT>
+__global__ __launch_bounds__(hr::NT) void hier_rows_kernel(
+    const typename St<DT>::T *__restrict__ qn, const typename St<DT>::T *__restrict__ S0,
+    const typename St<DT>::T *__restrict__ S1, const uint8_t *__restrict__ cand, int64_t c, int nb, int ns,
+    int m, int d, int F, int beff, int kke, float scale, int64_t *__restrict__ top_idx,
+    float *__restrict__ top_val) {
+    using namespace hr;
+    __shared__ float q[DMAX];
+    __shared__ float ssc[NSMAX];
+    __shared__ float csc[CMAX];
+    __shared__ int cid[CMAX];
+    __shared__ int par[BEAMMAX];
+    __shared__ float wv[NT / 64];
+    __shared__ int wi[NT / 64], wj[NT / 64];
+    const int tid = threadIdx.x;
+    const int64_t row = blockIdx.x, b = blockIdx.y;
+    for (int t = tid; t < d; t += NT) q[t] = St<DT>::ld(qn, (b * c + row) * d + t);
+    const uint8_t *cr = cand + row * nb;
+    const typename St<DT>::T *S0b = S0 + b * nb * m * d;
+    const typename St<DT>::T *S1b = S1 + b * ns * m * d;
+    __syncthreads();
+    for (int p = tid; p < ns; p += NT) {
+        bool has = false;
+        for (int j = 0; j < F && p * F + j < nb; ++j) has = has || cr[p * F + j] != 0;
+        ssc[p] = has ? score<DT>(q, S1b + (int64_t)p * m * d, m, d, scale) : -INFINITY;
+    }
+    __syncthreads();
+    int np = 0;
+    for (int a = 0; a < beff; ++a) {
+        const int j = argmax(ssc, nullptr, ns, wv, wi, wj);
+        if (j < 0) break;   // uniform
+        if (tid == 0) {
+            par[a] = j;
+            ssc[j] = -INFINITY;
+        }
+        np = a + 1;
+        __syncthreads();
+    }
+    const int nc = np * F;   // children in parent rank order
+    for (int j = tid; j < nc; j += NT) {
+        const int blk = par[j / F] * F + j % F;
+        cid[j] = blk;
+        csc[j] = (blk < nb && cr[blk]) ? score<DT>(q, S0b + (int64_t)blk * m * d, m, d, scale) : -INFINITY;
+    }
+    __syncthreads();
+    int64_t *oi = top_idx + (b * c + row) * kke;
+    float *ov = top_val + (b * c + row) * kke;
+    for (int r = 0; r < kke; ++r) {
+        const int j = argmax(csc, cid, nc, wv, wi, wj);
+        if (j < 0) {   // uniform: no candidate child left
+            for (int rr = r + tid; rr < kke; rr += NT) {
+                oi[rr] = -1;
+                ov[rr] = -INFINITY;
+            }
+            break;
+        }
+        if (tid == 0) {
+            oi[r] = cid[j];
+            ov[r] = csc[j];
+            csc[j] = -INFINITY;
+        }
+        __syncthreads();
+    }
+}
+
+extern "C" int hba_hier_select_rows(int dtype, const void *qn, const void *S0, const void *S1,
+                                    const uint8_t *cand, int64_t B, int64_t c, int64_t nb, int64_t m,
+                                    int64_t d, int64_t fanout, int64_t beam, int64_t kk, float scale,
+                                    int64_t *top_idx, float *top_val, void *stream) {
+    if (dtype != HBA_DTYPE_F32 && dtype != HBA_DTYPE_BF16) return HBA_ERR_UNSUPPORTED;
+    if (!qn || !S0 || !S1 || !cand || !top_idx || !top_val) return HBA_ERR_INVALID_ARG;
+    if (B < 1 || c < 0 || nb < 1 || m < 1 || d < 1 || fanout < 1 || beam < 1 || kk < 1) return HBA_ERR_INVALID_ARG;
+    const int64_t ns = (nb + fanout - 1) / fanout;
+    const int64_t beff = beam < ns ? beam : ns;
+    if (d > hr::DMAX || ns > hr::NSMAX || beff > hr::BEAMMAX || beff * fanout > hr::CMAX) return HBA_ERR_UNSUPPORTED;
+    if (c > 0x7fffffff || B > 65535) return HBA_ERR_UNSUPPORTED;
+    if (c == 0) return HBA_OK;
+    const int64_t kke = kk < beff * fanout ? kk : beff * fanout;
+    dim3 grid((unsigned)c, (unsigned)B);
+    hipStream_t s = (hipStream_t)stream;
+    if (dtype == HBA_DTYPE_F32)
+        hipLaunchKernelGGL(hier_rows_kernel<0>, grid, dim3(hr::NT), 0, s, (const float *)qn, (const float *)S0,
+                           (const float *)S1, cand, c, (int)nb, (int)ns, (int)m, (int)d, (int)fanout, (int)beff,
+                           (int)kke, scale, top_idx, top_val);
+    else
+        hipLaunchKernelGGL(hier_rows_kernel<1>, grid, dim3(hr::NT), 0, s, (const bf16_t *)qn, (const bf16_t *)S0,
+                           (const bf16_t *)S1, cand, c, (int)nb, (int)ns, (int)m, (int)d, (int)fanout, (int)beff,
+                           (int)kke, scale, top_idx, top_val);
+    HBA_LAUNCH_CHECK();
+    return HBA_OK;
+}

@@ -241,6 +241,19 @@ def build_super(S0, fanout):
     return (S1.squeeze(1) if squeeze else S1), S1.shape[2]
 
 
+def hier_select(qn, S0, S1, fanout, beam, kk, cand, scale):
+    """attention.py:217-246 with the reference's signature: qn [B, c, dh],
+    S0 [B, nb, m, dh], S1 [B, ns, m, dh], cand bool [c, nb].  Returns
+    (top_idx [B, c, kk_eff], top_val [B, c, kk_eff], n_comparisons) with
+    kk_eff = min(kk, min(beam, ns) * fanout); a pick is valid iff top_val is
+    finite (the reference's rule), and an invalid one has index -1.  Scores
+    are fp32 (declared order) for fp32 and bf16 inputs alike; ties go to the
+    lowest block index."""
+    ns = S1.shape[1]
+    idx, val = ops.hier_select_rows(qn, S0, S1, int(fanout), int(beam), int(kk), cand, float(scale))
+    return idx, val, ns + min(beam, ns) * fanout
+
+
 def selected_mask(idx, cnt, nb):
     """Boolean selection mask [B, Hkv, n, nb] (route_topk's `sel`) from idx/cnt."""
     B, Hkv, n, kk = idx.shape

@@ -244,6 +244,42 @@ def _(q, q_gain, eps, S0, S1, window, k, fanout, beam, scale):
             q.new_empty(B, Hkv, n, dtype=torch.int32))
 
 
+@torch.library.custom_op("hba::hier_select_rows", mutates_args=(), device_types="cuda")
+def hier_select_rows(qn: Tensor, S0: Tensor, S1: Tensor, fanout: int, beam: int, kk: int, cand: Tensor,
+                     scale: float) -> Tuple[Tensor, Tensor]:
+    """hier_select (attention.py:217-246) on routing queries qn [B, c, d] with
+    a candidate mask cand [c, nb] (any rule): top_idx int64 / top_val fp32
+    [B, c, min(kk, min(beam, ns) * fanout)], -1 / -inf past the picks."""
+    dev = _dev(qn)
+    qn = qn.contiguous()
+    S0 = S0.to(qn.dtype).contiguous()
+    S1 = S1.to(qn.dtype).contiguous()
+    B, c, d = qn.shape
+    nb, m = S0.shape[1], S0.shape[2]
+    ns = (nb + fanout - 1) // fanout
+    if S0.shape[0] != B or S0.shape[3] != d or tuple(S1.shape) != (B, ns, m, d):
+        raise ValueError("S0 [B, nb, m, d] / S1 [B, ceil(nb / fanout), m, d] do not match qn [B, c, d]")
+    if tuple(cand.shape) != (c, nb):
+        raise ValueError(f"cand must be [c, nb] = [{c}, {nb}], got {tuple(cand.shape)}")
+    cm = cand.to(device=dev, dtype=torch.uint8).contiguous()
+    kke = min(kk, min(beam, ns) * fanout)
+    idx = torch.empty(B, c, kke, dtype=torch.int64, device=dev)
+    val = torch.empty(B, c, kke, dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        st = lib().hba_hier_select_rows(_code(qn), _p(qn), _p(S0), _p(S1), _p(cm), B, c, nb, m, d, fanout, beam,
+                                        kk, scale, _p(idx), _p(val), _stream(dev))
+    check(st, "hba_hier_select_rows")
+    return idx, val
+
+
+@hier_select_rows.register_fake
+def _(qn, S0, S1, fanout, beam, kk, cand, scale):
+    B, c = qn.shape[0], qn.shape[1]
+    ns = (S0.shape[1] + fanout - 1) // fanout
+    kke = min(kk, min(beam, ns) * fanout)
+    return (qn.new_empty(B, c, kke, dtype=torch.int64), qn.new_empty(B, c, kke, dtype=torch.float32))
+
+
 # ------------------------------------------------------------- attention ----
 @torch.library.custom_op("hba::attn_fwd", mutates_args=(), device_types="cuda")
 def attn_fwd(q: Tensor, q_gain: Optional[Tensor], k_gain: Optional[Tensor], eps: float, kc: Tensor,

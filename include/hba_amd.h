@@ -136,6 +136,24 @@ int hba_hier_select(int dtype, const void *q, const int64_t q_strides[3],
                     float *scores, float *sup_scores, void *stream);
 
 /*
+ * hier_select with the reference's own signature and an arbitrary candidate
+ * mask: qn [B, c, d] routing queries (already grouped and QKNorm'd, as the
+ * reference's eval path passes them), S0 [B, nb, m, d], S1 [B, ns, m, d] with
+ * ns = ceil(nb / fanout), cand uint8 [c, nb] (nonzero = candidate).  Writes
+ * top_idx int64 / top_val fp32 [B, c, kk_eff], kk_eff = min(kk, min(beam, ns)
+ * * fanout): the picks in order (score desc, block asc), then -1 / -inf.
+ * Scores are fp32 in the declared order (dot in index order, slot max, times
+ * scale), also for bf16 inputs.
+ *   replaces: hier_select  src/hba/attention.py:217-246 (called by
+ *             evals.hier_fidelity, src/hba/evals.py:314)
+ * d <= 256, ns <= 4096, min(beam, ns) <= 64, min(beam, ns) * fanout <= 1024.
+ */
+int hba_hier_select_rows(int dtype, const void *qn, const void *S0, const void *S1,
+                         const uint8_t *cand, int64_t B, int64_t c, int64_t nb, int64_t m,
+                         int64_t d, int64_t fanout, int64_t beam, int64_t kk, float scale,
+                         int64_t *top_idx, float *top_val, void *stream);
+
+/*
  * Union attention forward: one softmax per (query, head) over the NoPE sinks
  * j < min(S, i+1), the RoPE window max(S, i-W+1) <= j <= i, and the NoPE keys
  * of the valid selected blocks idx[b, h/G, i, 0..cnt).

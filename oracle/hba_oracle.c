@@ -37,6 +37,7 @@
  * and the oracle-vs-kernel agreement bit-exactly.
  */
 #include <math.h>
+#include <stdlib.h>
 #include <stdint.h>
 #include <string.h>
 
@@ -247,4 +248,53 @@ void hba_oracle_hier_select(const float *qg, const float *S0, const float *S1,
             val[r * kk + j] = -INFINITY;
         }
     }
+}
+
+/* hier_select with an arbitrary candidate mask, for one batch row: qn [r, d]
+ * (the routing queries), cand [r, nb] (1 = candidate).  A super is scored if
+ * any of its children is a candidate (cand_sup); the children of the top
+ * b_eff = min(beam, ns) supers are scored if they are candidates, and the
+ * top min(kk, b_eff*F) children are the picks.  attention.py:217-246 */
+void hba_oracle_hier_select_mask(const float *qn, const float *S0, const float *S1,
+                                 const uint8_t *cand, int64_t nrows, int nb, int m, int d,
+                                 int F, int beam, int kk, float scale,
+                                 int32_t *idx, float *val, int32_t *cnt)
+{
+    int ns = (nb + F - 1) / F;
+    int beff = beam < ns ? beam : ns;
+    int kke = kk < beff * F ? kk : beff * F;
+    float *ssc = (float *)malloc(sizeof(float) * (size_t)ns);
+    int32_t *pidx = (int32_t *)malloc(sizeof(int32_t) * (size_t)beff);
+    float *pval = (float *)malloc(sizeof(float) * (size_t)beff);
+    float *csc = (float *)malloc(sizeof(float) * (size_t)beff * F);
+    int *cid = (int *)malloc(sizeof(int) * (size_t)beff * F);
+    for (int64_t r = 0; r < nrows; ++r) {
+        const float *q = qn + r * d;
+        const uint8_t *cr = cand + r * nb;
+        for (int p = 0; p < ns; ++p) {
+            int has = 0;
+            for (int c = 0; c < F && p * F + c < nb; ++c) has |= cr[p * F + c] != 0;
+            ssc[p] = has ? slot_score(q, S1 + (int64_t)p * m * d, m, d, scale) : -INFINITY;
+        }
+        int np = topk_row(ssc, 0, ns, beff, pidx, pval);
+        int nc = 0;
+        for (int a = 0; a < np; ++a)
+            for (int c = 0; c < F; ++c) {
+                int b = pidx[a] * F + c;
+                if (b >= nb) continue;
+                csc[nc] = cr[b] ? slot_score(q, S0 + (int64_t)b * m * d, m, d, scale) : -INFINITY;
+                cid[nc] = b;
+                ++nc;
+            }
+        cnt[r] = topk_row(csc, cid, nc, kke, idx + r * kke, val + r * kke);
+        for (int j = cnt[r]; j < kke; ++j) {
+            idx[r * kke + j] = -1;
+            val[r * kke + j] = -INFINITY;
+        }
+    }
+    free(ssc);
+    free(pidx);
+    free(pval);
+    free(csc);
+    free(cid);
 }

@@ -80,6 +80,9 @@ def lib():
         L.hba_oracle_hier_select.argtypes = [f32p, f32p, f32p, i64p, c_i64, c_int, c_int, c_int,
                                              c_int, c_int, c_int, c_f, c_int, c_int,
                                              i32p, f32p, i32p]
+        L.hba_oracle_hier_select_mask.argtypes = [f32p, f32p, f32p, ctypes.POINTER(ctypes.c_uint8), c_i64,
+                                                  c_int, c_int, c_int, c_int, c_int, c_int, c_f,
+                                                  i32p, f32p, i32p]
         _LIB = L
     return _LIB
 
@@ -429,6 +432,28 @@ def hier_select(qg, S0, S1, F, beam, kk, scale, Bk, W, pos=None):
         lib().hba_oracle_hier_select(_p(qgg), _p(s0), _p(s1), _p(pos, ctypes.c_int64), r, nb, m, d,
                                      F, beam, kk, np.float32(scale), Bk, W,
                                      _p(ig, ctypes.c_int32), _p(vg), _p(cg, ctypes.c_int32))
+    return idx, val, cnt
+
+
+def hier_select_mask(qn, S0, S1, F, beam, kk, cand, scale):
+    """hier_select (attention.py:217-246) as the reference states it, with an
+    arbitrary candidate mask, for one batch row.  qn [r, d] routing queries,
+    S0 [nb, m, d], S1 [ns, m, d], cand bool [r, nb] -> idx, val
+    [r, min(kk, min(beam, ns) * F)] (value desc, block asc; -1 / -inf past the
+    picks), cnt [r].  Scores: declared-order fp32 dots, slot max, times scale."""
+    qn, S0, S1 = _f32(qn), _f32(S0), _f32(S1)
+    r, d = qn.shape
+    nb, m = S0.shape[0], S0.shape[1]
+    ns = S1.shape[0]
+    assert ns == (nb + F - 1) // F
+    kke = min(kk, min(beam, ns) * F)
+    cm = np.ascontiguousarray(cand, dtype=np.uint8)
+    assert cm.shape == (r, nb)
+    idx = np.empty((r, kke), dtype=np.int32)
+    val = np.empty((r, kke), dtype=np.float32)
+    cnt = np.empty((r,), dtype=np.int32)
+    lib().hba_oracle_hier_select_mask(_p(qn), _p(S0), _p(S1), _p(cm, ctypes.c_uint8), r, nb, m, d, F, beam, kk,
+                                      np.float32(scale), _p(idx, ctypes.c_int32), _p(val), _p(cnt, ctypes.c_int32))
     return idx, val, cnt
 
 

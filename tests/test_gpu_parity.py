@@ -327,6 +327,38 @@ def test_hier_select_adversarial(dev, pattern):
                          sup[0, g].cpu().numpy())
 
 
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+@pytest.mark.parametrize("nb,F,beam,kk", [(37, 4, 3, 8), (64, 16, 2, 40), (200, 8, 30, 16), (1000, 16, 8, 16)])
+def test_hier_select_drop_in_any_mask(dev, dt, nb, F, beam, kk):
+    """hba_amd.hier_select, the reference's hier_select(qn, S0, S1, fanout,
+    beam, kk, cand, scale) with an arbitrary candidate mask (hba_hier_select_rows),
+    against the oracle's masked form: picks and scores bit-exact in fp32 and
+    bf16 (fp32 declared-order scores of the stored values), over ragged last
+    supers, beam > ns, kk > beam * fanout, rows without a candidate, an
+    all-candidate row and tied summaries; the comparison count as the
+    reference returns it."""
+    g = torch.Generator().manual_seed(nb + F)
+    B, c, m, d = 2, 50, 4, 64
+    qn = torch.randn(B, c, d, generator=g).to(TDT[dt]).to(dev)
+    S0 = torch.randn(B, nb, m, d, generator=g)
+    S0[:, 9] = S0[:, 5]                                   # tied blocks
+    S0 = S0.to(TDT[dt]).to(dev)
+    S1, ns = hba_amd.build_super(S0, F)
+    cand = torch.rand(c, nb, generator=g) < 0.3
+    cand[:, 5] = cand[:, 9] = True
+    cand[4] = False
+    cand[7] = True
+    scale = 0.125
+    idx, val, ncomp = hba_amd.hier_select(qn, S0, S1, F, beam, kk, cand.to(dev), scale)
+    torch.cuda.synchronize()
+    assert ncomp == ns + min(beam, ns) * F
+    for b in range(B):
+        oi, ov, oc = O.hier_select_mask(f(qn[b]), f(S0[b]), f(S1[b]), F, beam, kk, cand.numpy(), scale)
+        assert np.array_equal(idx[b].cpu().numpy(), oi), b
+        assert np.array_equal(val[b].cpu().numpy(), ov), b
+    assert (idx[:, 4] == -1).all()
+
+
 def test_hier_select_threshold_overflow(dev):
     """A layout on which the by-super path's threshold admits more children
     than its 64-entry list: child c < 8 of super j scores 255 - 32 c - j

@@ -505,3 +505,51 @@ def test_planted_mistakes_are_caught(monkeypatch):
     caught["tau_dropped"] = O.union_scale(cfg_t, 8, 131072) != pytest.approx(
         O.content_scale(cfg_t, 8))
     assert all(caught.values()), caught
+
+
+# ------------------------------------------------ hier_select, any mask -----
+def _hier_case(seed, nb=37, m=4, d=16, F=4):
+    rng = np.random.default_rng(seed)
+    S0 = rng.standard_normal((nb, m, d)).astype(np.float32)
+    S1 = O.build_super(S0, F, "f32")
+    return rng, S0, S1
+
+
+def test_hier_select_mask_equals_the_causal_form():
+    """On the causal candidate rule the masked hier_select is the row-position
+    one (pinned to the reference's hier_select goldens) bit for bit."""
+    rng, S0, S1 = _hier_case(1)
+    nb, d, F, W, Bk = S0.shape[0], S0.shape[2], 4, 128, 64
+    qg = rng.standard_normal((nb * Bk, d)).astype(np.float32)
+    pos = np.arange(0, nb * Bk, 29)
+    for beam, kk in ((3, 8), (2, 16), (16, 5)):
+        i1, v1, c1 = O.hier_select(qg[None], S0[None], S1[None], F, beam, kk, 0.25, Bk, W, pos=pos)
+        bmax = np.array([O.cand_bmax(int(i), Bk, W) for i in pos])
+        blk = np.arange(nb)
+        cand = (blk[None] >= 1) & (blk[None] <= bmax[:, None])
+        i2, v2, c2 = O.hier_select_mask(qg[pos], S0, S1, F, beam, kk, cand, 0.25)
+        ke = i2.shape[1]
+        assert np.array_equal(i1[0][:, :ke], i2) and np.array_equal(v1[0][:, :ke], v2)
+        assert np.array_equal(c1[0], c2)
+
+
+def test_hier_select_mask_with_every_super_expanded_is_the_flat_top_k():
+    """beam >= ns expands every super holding a candidate, so the picks are the
+    flat top-k of the masked block scores, for any mask (ragged last super)."""
+    rng, S0, S1 = _hier_case(2)
+    nb, d, F = S0.shape[0], S0.shape[2], 4
+    ns = S1.shape[0]
+    q = rng.standard_normal((40, d)).astype(np.float32)
+    cand = rng.random((40, nb)) < 0.3
+    cand[:, 0] = False                                  # block 0 is never a routed candidate
+    cand[3] = False                                     # a row with no candidate
+    idx, val, cnt = O.hier_select_mask(q, S0, S1, F, ns, 12, cand, 0.5)
+    # declared-order scores of blocks 1..nb-1 for rows 0..39 (a window reaching
+    # back past the sequence start makes every such block a candidate)
+    full = O.block_scores(q, S0, np.arange(40), 0.5, 64, -10 ** 6)
+    assert np.isfinite(full[:, 1:]).all()
+    ti, tv, tc = O.topk(np.where(cand, full, -np.inf).astype(np.float32), 12)
+    fin = np.isfinite(tv)
+    assert np.array_equal(cnt, tc) and cnt[3] == 0
+    assert np.array_equal(np.where(fin, ti, -1), idx)
+    assert np.array_equal(np.where(fin, tv, -np.inf), val)
