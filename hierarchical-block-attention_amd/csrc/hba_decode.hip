@@ -999,6 +999,11 @@ __global__ __launch_bounds__(DF_NT) void decode_fused_kernel(
     for (int c = 0; c < D / 8; ++c) srow[c] = *reinterpret_cast<const u32x4d *>(src + 8 * c);
     const bf16_t *wk = any ? (rope ? krp : kcp) + (wph * Hkv + g) * BK * D : kcp;
     const bf16_t *wv = any ? vp + (wph * Hkv + g) * D * BK : vp;
+    // the window page's operands, in flight during the scoring (ready when
+    // the routing workgroup computes its window unit while its chunk-list
+    // loads are in flight)
+    bf16x8 ka[4][NKS], va[NDT][2];
+    dec_unit_load<D>(wk, wv, ka, va);
     float x[8];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -1092,9 +1097,8 @@ __global__ __launch_bounds__(DF_NT) void decode_fused_kernel(
     // ------------------------------------------- the score counter ------
     asm volatile("" ::"v"(pub_v), "v"(pub_i), "v"(pub_p), "v"(pub_iv), "v"(pub_pv), "v"(pub_vv));
     const bool router = scorer && dec_arrive(ctr + sg, gm.nsg, &sm.flag);   // workgroup-uniform
-    // Loads in the order of their use: the routing workgroup's chunk lists,
-    // then every workgroup's window page (so that the arrival above waited
-    // for the list stores only).
+    // The routing workgroup's chunk-list loads go out first; the window unit
+    // computes while they are in flight.
     const int E = router ? nsc_s * K : 0;
     const int64_t lb = sg * gm.nsc * K;
     float lv[4];
@@ -1109,8 +1113,21 @@ __global__ __launch_bounds__(DF_NT) void decode_fused_kernel(
             lp[r] = ld_dev(ws_phys + o);
         }
     }
-    bf16x8 ka[4][NKS], va[NDT][2];
-    dec_unit_load<D>(wk, wv, ka, va);
+    // --------------------------------------------- window / sink unit ------
+    f32x4 Oa[NDT];
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) Oa[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float ma = -INFINITY, la = 0.0f;
+    if (any) {
+        bf16x8 qop[NKS];
+        df_qop<D>(rope ? sm.qr : sm.qc, G, qop);
+        f32x4 O[NDT];
+        float mu, lu;
+        dec_unit_core<D>(ka, va, qop, 64 * page, lo, hi, scale, O, mu, lu);
+        dec_fold<NDT>(Oa, ma, la, O, mu, lu);
+    }
+    df_fold_slot<D>(Oa, ma, la, reinterpret_cast<float *>(sm.un), G, slots + (int64_t)z * G * PR);
+    __syncthreads();   // the fold's LDS readers are done before the lists are staged there
     if (router) {
         // ---------------------------- merge of the chunk lists of (s, g) -----
         // The lists (sorted; ties by page) hold distinct pages, so an entry's
@@ -1157,20 +1174,6 @@ __global__ __launch_bounds__(DF_NT) void decode_fused_kernel(
         __syncthreads();
     }
 
-    // --------------------------------------------- window / sink unit ------
-    f32x4 Oa[NDT];
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) Oa[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    float ma = -INFINITY, la = 0.0f;
-    if (any) {
-        bf16x8 qop[NKS];
-        df_qop<D>(rope ? sm.qr : sm.qc, G, qop);
-        f32x4 O[NDT];
-        float mu, lu;
-        dec_unit_core<D>(ka, va, qop, 64 * page, lo, hi, scale, O, mu, lu);
-        dec_fold<NDT>(Oa, ma, la, O, mu, lu);
-    }
-    df_fold_slot<D>(Oa, ma, la, reinterpret_cast<float *>(sm.un), G, slots + (int64_t)z * G * PR);
 
     if (router) {
         // ------------------------------------ routed pages of (s, g) ---------
