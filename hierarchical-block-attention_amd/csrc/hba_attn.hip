@@ -11,6 +11,7 @@
 //   products and a two-pass softmax; the fp32 parity path.
 #include "hba_common.h"
 #include "hba_abi.h"
+#include "hba_generic.h"
 #include "hba_attn_bf16.h"
 
 namespace hba {
@@ -139,6 +140,19 @@ extern "C" int hba_attn_fwd(int dtype, const void *q, const int64_t q_strides[3]
                             int64_t d, int64_t S, int64_t W, int64_t Bk, int64_t k, float scale,
                             void *workspace, size_t ws_bytes, void *out, const int64_t out_strides[3],
                             void *stream) {
+    if (dtype == HBA_DTYPE_F32 && !tuned_shape(d, Bk)) {   // fp32, other geometry: the generic kernel
+        if (!q || !q_strides || !kc || !kr || !vt || !cos_tab || !sin_tab || !idx || !cnt || !out ||
+            !out_strides)
+            return HBA_ERR_INVALID_ARG;
+        if (B <= 0 || n <= 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv != 0 || W < 1 || S < 0 || k < 1)
+            return HBA_ERR_INVALID_ARG;
+        if (!gen_shape_ok(d, Bk)) return HBA_ERR_UNSUPPORTED;
+        if (n % Bk != 0 || S > Bk) return HBA_ERR_INVALID_ARG;
+        if (B > 65535 || Hq > 65535) return HBA_ERR_UNSUPPORTED;
+        return gen_attn((const float *)q, q_strides, q_gain, eps, (const float *)kc, (const float *)kr,
+                        (const float *)vt, cos_tab, sin_tab, idx, cnt, B, n, Hq, Hkv, d, S, W, Bk, k, scale,
+                        (float *)out, out_strides, (hipStream_t)stream);
+    }
     int st = abi::check_dtype_dim(dtype, d);
     if (st) return st;
     if (!q || !q_strides || !kc || !kr || !vt || !cos_tab || !sin_tab || !idx || !cnt || !out ||

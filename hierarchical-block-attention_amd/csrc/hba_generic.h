@@ -1,0 +1,29 @@
+// fp32 forward for geometry outside the tuned kernels (hba_generic.hip): the
+// entry points call these when an fp32 call's head dim is not 64 / 128, its
+// block size is not 64, or (selection) k > 64 or the slot count is not 1, 2,
+// 4 or 8.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <cstdint>
+
+namespace hba {
+
+// an even head dim <= 256 and a block size 1..256
+bool gen_shape_ok(int64_t d, int64_t Bk);
+// the tuned kernels' geometry (they refuse anything else)
+inline bool tuned_shape(int64_t d, int64_t Bk) { return (d == 64 || d == 128) && Bk == 64; }
+
+int gen_prep_keys(const float *k, const int64_t *ks, const float *v, const int64_t *vs, const float *kgain,
+                  float eps, const float *cosT, const float *sinT, int64_t B, int64_t n, int64_t Hkv, int64_t d,
+                  float *kc, float *kr, float *vt, hipStream_t s);
+int gen_summarize(const float *kc, int64_t B, int64_t Hkv, int64_t n, int64_t d, int64_t Bk, int64_t nblocks,
+                  const float *probes, const float *proj, int64_t m, float *out, hipStream_t s);
+int gen_score_select(const float *q, const int64_t *qs, const float *qgain, float eps, const float *S0, int64_t B,
+                     int64_t n, int64_t Hq, int64_t Hkv, int64_t d, int64_t m, int64_t Bk, int64_t W, int64_t k,
+                     float scale, int32_t *idx, float *val, int32_t *cnt, float *scores, hipStream_t s);
+int gen_attn(const float *q, const int64_t *qs, const float *qgain, float eps, const float *kc, const float *kr,
+             const float *vt, const float *cosT, const float *sinT, const int32_t *idx, const int32_t *cnt, int64_t B,
+             int64_t n, int64_t Hq, int64_t Hkv, int64_t d, int64_t S, int64_t W, int64_t Bk, int64_t k, float scale,
+             float *out, const int64_t *os, hipStream_t s);
+
+}  // namespace hba

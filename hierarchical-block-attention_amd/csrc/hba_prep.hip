@@ -14,6 +14,7 @@
 // (summaries).
 #include "hba_common.h"
 #include "hba_abi.h"
+#include "hba_generic.h"
 
 namespace hba {
 
@@ -573,6 +574,14 @@ extern "C" int hba_prep_keys(int dtype, const void *k, const int64_t k_strides[3
                              const int64_t v_strides[3], const float *k_gain, float eps,
                              const float *cos_tab, const float *sin_tab, int64_t B, int64_t n,
                              int64_t Hkv, int64_t d, void *kc, void *kr, void *vt, void *stream) {
+    if (dtype == HBA_DTYPE_F32 && d != 64 && d != 128) {   // fp32, another head dim: the generic kernel
+        if (!gen_shape_ok(d, 1)) return HBA_ERR_UNSUPPORTED;
+        if (!k || !k_strides || !kc || B <= 0 || n <= 0 || Hkv <= 0) return HBA_ERR_INVALID_ARG;
+        if ((kr && (!cos_tab || !sin_tab)) || (vt && (!v || !v_strides))) return HBA_ERR_INVALID_ARG;
+        return gen_prep_keys((const float *)k, k_strides, (const float *)v, v_strides ? v_strides : k_strides,
+                             k_gain, eps, cos_tab, sin_tab, B, n, Hkv, d, (float *)kc, (float *)kr, (float *)vt,
+                             (hipStream_t)stream);
+    }
     int st = abi::check_dtype_dim(dtype, d);
     if (st) return st;
     if (!k || !k_strides || !kc || B <= 0 || n <= 0 || Hkv <= 0) return HBA_ERR_INVALID_ARG;
@@ -602,6 +611,14 @@ static int summarize_common(int dtype, const void *kc, int64_t B, int64_t Hkv, i
                             int64_t Bk, const int32_t *pages, const int32_t *ptab, int64_t maxp,
                             const int32_t *lens, int64_t nblocks, const float *probes,
                             const float *proj, int64_t m, void *out, void *stream) {
+    if (dtype == HBA_DTYPE_F32 && !pages && !ptab && !tuned_shape(d, Bk)) {   // fp32 prefill, other geometry
+        if (!kc || !probes || !proj || !out || B <= 0 || Hkv <= 0) return HBA_ERR_INVALID_ARG;
+        if (!gen_shape_ok(d, Bk) || m < 1 || m > 8) return HBA_ERR_UNSUPPORTED;
+        if (nblocks <= 0) return HBA_OK;
+        if (nblocks > 0x7fffffff || Hkv > 65535 || B > 65535) return HBA_ERR_UNSUPPORTED;
+        return gen_summarize((const float *)kc, B, Hkv, n, d, Bk, nblocks, probes, proj, m, (float *)out,
+                             (hipStream_t)stream);
+    }
     int st = abi::check_dtype_dim(dtype, d);
     if (st) return st;
     if (!kc || !probes || !proj || !out || B <= 0 || Hkv <= 0) return HBA_ERR_INVALID_ARG;

@@ -12,6 +12,7 @@
 
 #include "hba_common.h"
 #include "hba_abi.h"
+#include "hba_generic.h"
 #include "hba_dma.h"
 
 namespace hba {
@@ -1356,6 +1357,18 @@ extern "C" int hba_score_select(int dtype, const void *q, const int64_t q_stride
                                 int64_t Hq, int64_t Hkv, int64_t d, int64_t m, int64_t Bk, int64_t W,
                                 int64_t k, float scale, int32_t *idx, float *val, int32_t *cnt,
                                 float *scores, void *stream) {
+    if (dtype == HBA_DTYPE_F32 &&
+        (!tuned_shape(d, Bk) || k > 64 || !(m == 1 || m == 2 || m == 4 || m == 8) || m * d > SEL_LDS_FLOATS)) {
+        // fp32 with another geometry, k or slot count: the generic kernel
+        if (!q || !q_strides || !S0 || !idx || !val || !cnt) return HBA_ERR_INVALID_ARG;
+        if (B <= 0 || n <= 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv != 0 || W < 1 || k < 1 || m < 1)
+            return HBA_ERR_INVALID_ARG;
+        if (!gen_shape_ok(d, Bk)) return HBA_ERR_UNSUPPORTED;
+        if (n % Bk != 0) return HBA_ERR_INVALID_ARG;
+        if (B > 65535 || Hkv > 65535) return HBA_ERR_UNSUPPORTED;
+        return gen_score_select((const float *)q, q_strides, q_gain, eps, (const float *)S0, B, n, Hq, Hkv, d, m,
+                                Bk, W, k, scale, idx, val, cnt, scores, (hipStream_t)stream);
+    }
     int st = select_checks(dtype, q, q_strides, S0, B, n, Hq, Hkv, d, m, Bk, W, k, idx, val, cnt);
     if (st) return st;
     hipStream_t s = (hipStream_t)stream;

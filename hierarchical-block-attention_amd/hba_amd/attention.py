@@ -42,8 +42,9 @@ def forward_stages(q, k, v, cos, sin, cfg, summ, qkn, hier=False, dense_route=Fa
     (kc, kr, vt, S0, [S1], idx, val, cnt, out) and the scales used."""
     B, n, Hq, dh = q.shape
     assert n % cfg.block == 0, (n, cfg.block)
-    if cfg.block != ops.BLOCK:
-        raise ValueError(f"block {cfg.block} unsupported: the kernels use {ops.BLOCK}-key blocks")
+    if cfg.block != ops.BLOCK and (q.dtype != torch.float32 or hier):
+        raise ValueError(f"block {cfg.block}: the bf16 and hierarchical kernels use {ops.BLOCK}-key blocks "
+                         "(fp32 with flat selection takes any block size)")
     qg, kg, qeps, keps = _qk(cfg, qkn)
     scale = union_scale(cfg, dh, n)
     sel_scale = route_scale(cfg, dh) if dense_route else scale
@@ -62,20 +63,21 @@ def forward_stages(q, k, v, cos, sin, cfg, summ, qkn, hier=False, dense_route=Fa
             ops.attn_window_(q, qg, kg, qeps, r["kr"], r["vt"], cos, sin, cfg.sinks, cfg.window, scale, out, ws)
         for t in (out, ws, r["kr"], r["vt"]):
             t.record_stream(side)
-    r["S0"] = ops.summarize(r["kc"], summ.probes, summ.proj)
+    r["S0"] = ops.summarize(r["kc"], summ.probes, summ.proj, cfg.block)
     if hier:
         r["S1"] = ops.build_super(r["S0"], cfg.fanout)
         r["idx"], r["val"], r["cnt"] = ops.hier_select(q, qg, qeps, r["S0"], r["S1"], cfg.window, kk,
                                                        cfg.fanout, cfg.beam, sel_scale)
     else:
-        r["idx"], r["val"], r["cnt"] = ops.score_select(q, qg, qeps, r["S0"], cfg.window, kk, sel_scale)
+        r["idx"], r["val"], r["cnt"] = ops.score_select(q, qg, qeps, r["S0"], cfg.window, kk, sel_scale,
+                                                        cfg.block)
     if split:
         main.wait_stream(side)
         r["out"] = ops.attn_routed_(q, qg, kg, qeps, r["kc"], r["vt"], r["idx"], r["cnt"], cfg.sinks, scale,
                                     out, ws)
     else:
         r["out"] = ops.attn_fwd(q, qg, kg, qeps, r["kc"], r["kr"], r["vt"], cos, sin, r["idx"], r["cnt"],
-                                cfg.sinks, cfg.window, scale)
+                                cfg.sinks, cfg.window, scale, cfg.block)
     return r
 
 
@@ -133,6 +135,10 @@ def _with_grad(q, k, v, cos, sin, cfg, summ, qkn, mode):
         return None
     if qg is not None and qeps != keps:
         raise NotImplementedError("the backward takes one QKNorm eps for q and k")
+    if cfg.block != ops.BLOCK or q.shape[-1] not in (64, 128):
+        raise NotImplementedError(f"the backward runs at {ops.BLOCK}-key blocks and head dims 64 / 128 "
+                                  f"(got block {cfg.block}, head dim {q.shape[-1]}); the forward takes "
+                                  "other geometry in fp32 under torch.no_grad()")
     return _UnionAttention.apply(q, k, v, qg, kg, cos, sin, cfg, summ, qeps, keps, mode)
 
 

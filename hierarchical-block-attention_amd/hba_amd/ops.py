@@ -109,7 +109,7 @@ def _(k, v, k_gain, eps, cos, sin):
 
 
 @torch.library.custom_op("hba::summarize", mutates_args=(), device_types="cuda")
-def summarize(kc: Tensor, probes: Tensor, proj: Tensor) -> Tensor:
+def summarize(kc: Tensor, probes: Tensor, proj: Tensor, block: int = 64) -> Tensor:
     dev = _dev(kc)
     B, Hkv, n, d = kc.shape
     if not kc.is_contiguous():
@@ -117,18 +117,18 @@ def summarize(kc: Tensor, probes: Tensor, proj: Tensor) -> Tensor:
     m = probes.shape[1]
     pr = _f32c(probes, dev, Hkv * m * d, "probes")
     pj = _f32c(proj, dev, Hkv * d * d, "proj")
-    out = torch.empty(B, Hkv, n // BLOCK, m, d, dtype=kc.dtype, device=dev)
+    out = torch.empty(B, Hkv, n // block, m, d, dtype=kc.dtype, device=dev)
     with torch.cuda.device(dev):
-        st = lib().hba_summarize(_code(kc), _p(kc), B, Hkv, n, d, BLOCK, _p(pr), _p(pj), m, _p(out),
+        st = lib().hba_summarize(_code(kc), _p(kc), B, Hkv, n, d, block, _p(pr), _p(pj), m, _p(out),
                                  _stream(dev))
     check(st, "hba_summarize")
     return out
 
 
 @summarize.register_fake
-def _(kc, probes, proj):
+def _(kc, probes, proj, block=64):
     B, Hkv, n, d = kc.shape
-    return kc.new_empty(B, Hkv, n // BLOCK, probes.shape[1], d)
+    return kc.new_empty(B, Hkv, n // block, probes.shape[1], d)
 
 
 @torch.library.custom_op("hba::build_super", mutates_args=(), device_types="cuda")
@@ -160,39 +160,39 @@ def _sel_out(q, Hkv, k):
 
 @torch.library.custom_op("hba::score_select", mutates_args=(), device_types="cuda")
 def score_select(q: Tensor, q_gain: Optional[Tensor], eps: float, S0: Tensor, window: int, k: int,
-                 scale: float) -> Tuple[Tensor, Tensor, Tensor]:
-    return _score_select(q, q_gain, eps, S0, window, k, scale, None)
+                 scale: float, block: int = 64) -> Tuple[Tensor, Tensor, Tensor]:
+    return _score_select(q, q_gain, eps, S0, window, k, scale, None, block)
 
 
-def score_select_with_scores(q, q_gain, eps, S0, window, k, scale):
+def score_select_with_scores(q, q_gain, eps, S0, window, k, scale, block=64):
     """score_select that also returns every ranked candidate's fp32 score
     [B, Hkv, n, nb] (-inf elsewhere): the verification form, not a torch op."""
     B, n = q.shape[0], q.shape[1]
     scores = torch.full((B, S0.shape[1], n, S0.shape[2]), float("-inf"), dtype=torch.float32,
                         device=q.device)
-    return (*_score_select(q, q_gain, eps, S0, window, k, scale, scores), scores)
+    return (*_score_select(q, q_gain, eps, S0, window, k, scale, scores, block), scores)
 
 
-def _score_select(q, q_gain, eps, S0, window, k, scale, scores):
+def _score_select(q, q_gain, eps, S0, window, k, scale, scores, block=64):
     dev = _dev(q)
     _rows(q, "q")
     B, n, Hq, d = q.shape
     S0 = S0.contiguous()
     Hkv, nb, m = S0.shape[1], S0.shape[2], S0.shape[3]
-    if S0.shape[0] != B or S0.shape[4] != d or S0.dtype != q.dtype or nb != n // BLOCK:
+    if S0.shape[0] != B or S0.shape[4] != d or S0.dtype != q.dtype or nb != n // block:
         raise ValueError(f"S0 {tuple(S0.shape)} does not match q {tuple(q.shape)}")
     qg = _f32c(q_gain, dev, Hq, "q_gain")
     idx, val, cnt = _sel_out(q, Hkv, k)
     with torch.cuda.device(dev):
         st = lib().hba_score_select(_code(q), _p(q), strides3(q), _p(qg), eps, _p(S0), B, n, Hq, Hkv, d,
-                                    m, BLOCK, window, k, scale, _p(idx), _p(val), _p(cnt), _p(scores),
+                                    m, block, window, k, scale, _p(idx), _p(val), _p(cnt), _p(scores),
                                     _stream(dev))
     check(st, "hba_score_select")
     return idx, val, cnt
 
 
 @score_select.register_fake
-def _(q, q_gain, eps, S0, window, k, scale):
+def _(q, q_gain, eps, S0, window, k, scale, block=64):
     B, n = q.shape[0], q.shape[1]
     Hkv = S0.shape[1]
     return (q.new_empty(B, Hkv, n, k, dtype=torch.int32), q.new_empty(B, Hkv, n, k, dtype=torch.float32),
@@ -284,7 +284,7 @@ def _(qn, S0, S1, fanout, beam, kk, cand, scale):
 @torch.library.custom_op("hba::attn_fwd", mutates_args=(), device_types="cuda")
 def attn_fwd(q: Tensor, q_gain: Optional[Tensor], k_gain: Optional[Tensor], eps: float, kc: Tensor,
              kr: Tensor, vt: Tensor, cos: Tensor, sin: Tensor, idx: Tensor, cnt: Tensor, sinks: int,
-             window: int, scale: float) -> Tensor:
+             window: int, scale: float, block: int = 64) -> Tensor:
     dev = _dev(q)
     _rows(q, "q")
     B, n, Hq, d = q.shape
@@ -307,7 +307,7 @@ def attn_fwd(q: Tensor, q_gain: Optional[Tensor], k_gain: Optional[Tensor], eps:
     with torch.cuda.device(dev):
         st = lib().hba_attn_fwd(_code(q), _p(q), strides3(q), _p(qg), _p(kg), eps, _p(kc.contiguous()),
                                 _p(kr.contiguous()), _p(vt.contiguous()), _p(cos), _p(sin), _p(idx),
-                                _p(cnt), B, n, Hq, Hkv, d, sinks, window, BLOCK, idx.shape[3], scale,
+                                _p(cnt), B, n, Hq, Hkv, d, sinks, window, block, idx.shape[3], scale,
                                 _p(ws), int(nbytes.value), _p(out), strides3(out), _stream(dev))
     check(st, "hba_attn_fwd")
     return out
@@ -385,7 +385,7 @@ def side_stream(dev):
 
 
 @attn_fwd.register_fake
-def _(q, q_gain, k_gain, eps, kc, kr, vt, cos, sin, idx, cnt, sinks, window, scale):
+def _(q, q_gain, k_gain, eps, kc, kr, vt, cos, sin, idx, cnt, sinks, window, scale, block=64):
     return q.new_empty(q.shape)
 
 

@@ -352,3 +352,52 @@ def test_fp32_path_matches_reference_outputs(dev):
     for got, key in ((out_d, "out_dense"), (out_e, "out_eval"), (out_h, "out_hier")):
         err = np.abs(f(got)[:, rows] - z[key]).max()
         assert err <= 1e-5, (key, err)
+
+
+# ------------------------------------------- geometry outside the tuned path ----
+@pytest.mark.parametrize("Bk,d,Hq,Hkv,n,W,S,k,m", [
+    (16, 8, 4, 2, 512, 64, 4, 8, 4),          # the reference's own test geometry (tests/test_qknorm.py:28-35)
+    (32, 96, 6, 2, 1024, 128, 8, 6, 2),       # a head dim and block size the tuned kernels do not take
+    (64, 64, 14, 2, 8192, 1024, 4, 128, 4),   # k = n / block > 64 (the select-all gate, gates.py:211)
+], ids=["block16-d8", "block32-d96", "k128"])
+def test_fp32_generic_geometry_vs_oracle(dev, Bk, d, Hq, Hkv, n, W, S, k, m):
+    """fp32 forward at geometry outside the tuned kernels (hba_generic.hip
+    behind the same entry points): keys bit-exact, summaries within fp32
+    rounding of the float64 restatement, the flat selection bit-exact against
+    the oracle's declared order on the kernel's own summaries, and the union
+    softmax within 1e-5 of the oracle's float64 rows; the eval drop-in gives
+    the same output; off the tuned geometry a gradient request and bf16
+    refuse with a clear error."""
+    cfg = hba_amd.HBAConfig(n_heads=Hq, n_kv=Hkv, head_dim=d, window=W, sinks=S, k_blocks=k, slots=m, block=Bk)
+    x = synth.layer_inputs(1, n, Hq, Hkv, d, m=m, dtype=torch.float32, device=dev, seed=1, sharp=True)
+    prm = synth.Params(x["q_gain"], x["k_gain"], x["probes"], x["proj"])
+    cos, sin = hba_amd.rope_tables(n, d, cfg.rope_theta, dev)
+    with torch.no_grad():
+        r = hba_amd.forward_stages(x["q"], x["k"], x["v"], cos, sin, cfg, prm, prm)
+        out_e = hba_amd.hba_attention_eval(x["q"], x["k"], x["v"], cos, sin, cfg, prm, prm)
+    torch.cuda.synchronize()
+    S0 = f(r["S0"])[0]
+    P = O.prepare(f(x["q"])[0], f(x["k"])[0], f(x["v"])[0], f(cos), f(sin), cfg, f(x["probes"]), f(x["proj"]),
+                  f(x["q_gain"]), f(x["k_gain"]), 1e-6, "f32", S0=S0)
+    assert np.array_equal(f(r["kc"])[0].transpose(1, 0, 2), P.kc)
+    assert np.array_equal(f(r["kr"])[0].transpose(1, 0, 2), P.kr)
+    assert np.array_equal(f(r["vt"])[0].transpose(2, 0, 1), P.v)
+    ref_S0 = O.summarize(P.kc, f(x["probes"]), f(x["proj"]), Bk)
+    assert np.abs(S0 - ref_S0).max() <= 2e-5 * max(1.0, np.abs(ref_S0).max())
+    kk = min(k, n // Bk)
+    o_idx, o_val, o_cnt = O.flat_select(P.qg, P.S0, r["sel_scale"], kk, Bk, W)
+    for key, want in (("idx", o_idx), ("val", o_val), ("cnt", o_cnt)):
+        assert np.array_equal(r[key][0].cpu().numpy(), want), key
+    assert int(o_cnt.max()) > 0
+    rows = np.arange(n) if n <= 1024 else np.concatenate([np.arange(0, n, 41), np.arange(n - 64, n)])
+    ref = O.attn_rows(P.qc, P.qr, P.kc, P.kr, P.v, o_idx, o_cnt, r["scale"], S, W, Bk, rows)
+    assert np.abs(f(r["out"])[0][rows] - ref).max() <= 1e-5
+    assert torch.equal(out_e, r["out"])
+    if Bk != 64 or d not in (64, 128):
+        q = x["q"].clone().requires_grad_(True)
+        with pytest.raises(NotImplementedError, match="backward"):
+            hba_amd.hba_attention_eval(q, x["k"], x["v"], cos, sin, cfg, prm, prm)
+    if Bk != 64:
+        with pytest.raises(ValueError, match="block"):
+            hba_amd.hba_attention_eval(x["q"].bfloat16(), x["k"].bfloat16(), x["v"].bfloat16(), cos, sin, cfg,
+                                       prm, prm)
