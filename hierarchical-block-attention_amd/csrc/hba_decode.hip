@@ -45,7 +45,7 @@ namespace hba {
 constexpr int DEC_WG = 256;
 constexpr int DEC_CP = 64;    // candidate pages per score chunk
 constexpr int DEC_KMAX = 64;  // largest k
-constexpr int DEC_GMAX = 8;   // largest group size
+constexpr int DEC_GMAX = 16;  // largest group size (fp32 three-launch path)
 constexpr int DEC_PMAX = 128; // largest number of partial states
 constexpr int DEC_QROWS = 16; // query operand rows per (seq, KV head) and kind
 constexpr float DEC_LOG2E = 1.4426950408889634f;

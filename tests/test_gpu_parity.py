@@ -1009,6 +1009,13 @@ def test_decode_bf16_shapes(dev, d, k, Hq, Hkv, S, kern, monkeypatch):
     _decode_vs_oracle(dev, "bf16", [70, 700, 2500, 4096], Hq=Hq, Hkv=Hkv, d=d, S=S, W=512, k=k)
 
 
+@pytest.mark.parametrize("d,Hq,Hkv", [(64, 32, 2), (128, 16, 1)])
+def test_decode_f32_sixteen_heads_per_kv_head(dev, d, Hq, Hkv):
+    """The fp32 three-launch decode at 16 query heads per KV head (its
+    largest group), against the oracle."""
+    _decode_vs_oracle(dev, "f32", [70, 1100, 2500], Hq=Hq, Hkv=Hkv, d=d, S=4, W=512, k=8)
+
+
 def test_decode_equals_prefill_last_row(dev):
     """The decode step of a length-L sequence equals row L-1 of the prefill
     kernel on the same tokens (bf16, selection identical)."""
