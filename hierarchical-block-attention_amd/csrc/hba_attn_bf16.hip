@@ -365,30 +365,34 @@ __device__ __forceinline__ void win_body(
                 for (int rt = 0; rt < RT; ++rt) allact = allact && act[rt];
                 if (FIXED && RT > 1 && allact) {
                     // edge tile needed by every row tile: as the interior
-                    // path, with the keys outside a column's window masked
-                    // in the exponent
+                    // path (every row tile's S^T first, so that one row
+                    // tile's exponentials overlap another's MFMAs), with the
+                    // keys outside a column's window masked in the exponent
+                    f32x4 Sa[RT][4];
+#pragma unroll
+                    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+                        for (int mt = 0; mt < 4; ++mt) {
+                            Sa[rt][mt] = f32x4{-bl2, -bl2, -bl2, -bl2};
+#pragma unroll
+                            for (int ks = 0; ks < C::NKS; ++ks) Sa[rt][mt] = mma(kf[mt][ks], qop[rt][ks], Sa[rt][mt]);
+                        }
                     bf16x8 pf[RT][2];
 #pragma unroll
                     for (int rt = 0; rt < RT; ++rt) {
-                        f32x4 Sa1[4];
-#pragma unroll
-                        for (int mt = 0; mt < 4; ++mt) {
-                            Sa1[mt] = f32x4{-bl2, -bl2, -bl2, -bl2};
-#pragma unroll
-                            for (int ks = 0; ks < C::NKS; ++ks) Sa1[mt] = mma(kf[mt][ks], qop[rt][ks], Sa1[mt]);
-                        }
                         const int i = q0 + 16 * rt + l16;
-                        const int jlo = ((S > i - W + 1) ? S : i - W + 1) - kb;
-                        const int jhi = i - kb;
-                        const bool fullt = full[rt];
+                        // this lane's valid key offsets, relative to its own kl
+                        const int rlo = ((S > i - W + 1) ? S : i - W + 1) - kb - kl;
+                        const int rhi = full[rt] ? 63 : i - kb - kl;
+                        const int rl = full[rt] ? -64 : rlo;
                         float p[2][8];
 #pragma unroll
                         for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
                             for (int e = 0; e < 4; ++e) {
-                                const int j = kl + 32 * (mt >> 1) + 4 * (mt & 1) + e;
-                                const bool ok = fullt | ((j >= jlo) & (j <= jhi));
-                                p[mt >> 1][(mt & 1) * 4 + e] = ex2(ok ? Sa1[mt][e] : -INFINITY);
+                                const int j = 32 * (mt >> 1) + 4 * (mt & 1) + e;
+                                const bool ok = (j >= rl) & (j <= rhi);
+                                p[mt >> 1][(mt & 1) * 4 + e] = ex2(ok ? Sa[rt][mt][e] : -INFINITY);
                             }
                         pf[rt][0] = pack8(p[0]);
                         pf[rt][1] = pack8(p[1]);
