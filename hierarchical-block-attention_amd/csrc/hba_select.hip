@@ -1560,3 +1560,84 @@ extern "C" int hba_hier_select_rows(int dtype, const void *qn, const void *S0, c
     HBA_LAUNCH_CHECK();
     return HBA_OK;
 }
+
+// ---------------------------------------------------------------------------
+// The routing queries alone: qg[b, i, g, :] = the sum over the G heads of KV
+// group g of QKNorm(q[b, i, h, :]), in the declared order and storage roundings
+// of the selection kernels (grouped_query src/hba/summarizer.py:50-54 on
+// _HeadRMSNorm's output src/hba/attention.py:88-94).  qg [B, n, Hkv, d] is a
+// valid q for hba_score_select / hba_hier_select with Hq = Hkv and no gain:
+// their routing query of a one-head group without QKNorm is the row itself,
+// so precomputed and inline routing queries select identically.
+// bf16: one 256-thread workgroup per (64 queries, KV head, batch), the
+// selection kernels' routing_queries_tile; fp32: one thread per (query, KV
+// head), routing_query.
+template <int D>
+__global__ __launch_bounds__(256) void route_queries_bf16_kernel(const bf16_t *__restrict__ q, int64_t qsb,
+                                                                 int64_t qsn, int64_t qsh,
+                                                                 const float *__restrict__ qgain, float eps,
+                                                                 int64_t n, int Hq, int Hkv,
+                                                                 bf16_t *__restrict__ qg) {
+    __shared__ __align__(16) bf16_t rows[64 * D];
+    const int tid = threadIdx.x;
+    const int64_t i0 = (int64_t)blockIdx.x * 64;
+    const int g = blockIdx.y;
+    const int64_t b = blockIdx.z;
+    routing_queries_tile<D, D>(q, qsb, qsn, qsh, qgain, eps, b, i0, n, g, Hq / Hkv, rows, tid);
+    __syncthreads();
+    for (int c = tid; c < 64 * D / 8; c += 256) {   // 16-byte chunks of the tile's rows
+        const int r = c / (D / 8), k = c % (D / 8);
+        const int64_t i = i0 + r;
+        if (i < n)
+            *reinterpret_cast<uint4 *>(qg + ((b * n + i) * Hkv + g) * D + 8 * k) =
+                *reinterpret_cast<const uint4 *>(rows + r * D + 8 * k);
+    }
+}
+
+template <int D>
+__global__ __launch_bounds__(64) void route_queries_f32_kernel(const float *__restrict__ q, int64_t qsb,
+                                                               int64_t qsn, int64_t qsh,
+                                                               const float *__restrict__ qgain, float eps,
+                                                               int64_t n, int Hq, int Hkv, float *__restrict__ qg) {
+    const int64_t i = (int64_t)blockIdx.x * 64 + threadIdx.x;
+    const int g = blockIdx.y;
+    const int64_t b = blockIdx.z;
+    if (i >= n) return;
+    float x[D];
+    routing_query<0, D>(q, qsb, qsn, qsh, qgain, eps, b, i, g, Hq / Hkv, x);
+    float *dst = qg + ((b * n + i) * Hkv + g) * D;
+#pragma unroll
+    for (int t = 0; t < D; ++t) dst[t] = x[t];
+}
+
+extern "C" int hba_route_queries(int dtype, const void *q, const int64_t q_strides[3], const float *q_gain,
+                                 float eps, int64_t B, int64_t n, int64_t Hq, int64_t Hkv, int64_t d, void *qg,
+                                 void *stream) {
+    int st = abi::check_dtype_dim(dtype, d);
+    if (st) return st;
+    if (!q || !q_strides || !qg || B <= 0 || n <= 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv != 0)
+        return HBA_ERR_INVALID_ARG;
+    if (Hq / Hkv > 16) return HBA_ERR_UNSUPPORTED;
+    if (!abi::rows_aligned(dtype, q, q_strides) || !abi::aligned16(qg)) return HBA_ERR_UNSUPPORTED;
+    if (B > 65535 || Hkv > 65535 || (n + 63) / 64 > 0x7fffffff) return HBA_ERR_UNSUPPORTED;
+    dim3 grid((unsigned)((n + 63) / 64), (unsigned)Hkv, (unsigned)B);
+    hipStream_t s = (hipStream_t)stream;
+    if (dtype == HBA_DTYPE_BF16) {
+        if (d == 64)
+            hipLaunchKernelGGL(route_queries_bf16_kernel<64>, grid, dim3(256), 0, s, (const bf16_t *)q, q_strides[0],
+                               q_strides[1], q_strides[2], q_gain, eps, n, (int)Hq, (int)Hkv, (bf16_t *)qg);
+        else
+            hipLaunchKernelGGL(route_queries_bf16_kernel<128>, grid, dim3(256), 0, s, (const bf16_t *)q,
+                               q_strides[0], q_strides[1], q_strides[2], q_gain, eps, n, (int)Hq, (int)Hkv,
+                               (bf16_t *)qg);
+    } else {
+        if (d == 64)
+            hipLaunchKernelGGL(route_queries_f32_kernel<64>, grid, dim3(64), 0, s, (const float *)q, q_strides[0],
+                               q_strides[1], q_strides[2], q_gain, eps, n, (int)Hq, (int)Hkv, (float *)qg);
+        else
+            hipLaunchKernelGGL(route_queries_f32_kernel<128>, grid, dim3(64), 0, s, (const float *)q, q_strides[0],
+                               q_strides[1], q_strides[2], q_gain, eps, n, (int)Hq, (int)Hkv, (float *)qg);
+    }
+    HBA_LAUNCH_CHECK();
+    return HBA_OK;
+}

@@ -8,7 +8,7 @@ here through ctypes and registered as torch.library ops (namespace `hba`).
 """
 from . import ops
 from .attention import (aux_kl, build_super, equiv_attention, forward_stages, hba_attention_dense,
-                        hba_attention_eval, hba_attention_fused, hier_select, selected_mask)
+                        grouped_query, hba_attention_eval, hba_attention_fused, hier_select, selected_mask)
 from .config import (HBAConfig, content_scale, log_len_tau, resolve_backend, rope_tables,
                      route_scale, union_scale, yarn_theta)
 from .decode import DecodeLoop, PagedKVCache, hba_decode_step
@@ -18,6 +18,6 @@ from .modules import QKNorm, SlotSummarizer
 __all__ = [
     "ops", "HBAConfig", "resolve_backend", "content_scale", "log_len_tau", "union_scale",
     "route_scale", "rope_tables", "yarn_theta", "QKNorm", "SlotSummarizer", "hba_attention_eval",
-    "hba_attention_dense", "hba_attention_fused", "build_super", "hier_select", "forward_stages",
+    "hba_attention_dense", "hba_attention_fused", "build_super", "hier_select", "grouped_query", "forward_stages",
     "selected_mask", "equiv_attention", "aux_kl", "PagedKVCache", "hba_decode_step", "DecodeLoop", "HBAAttention", "attention_by_mode",
 ]

@@ -30,6 +30,7 @@ SIGNATURES = {
                          _i64, _i64, _f, _vp, _vp, _vp, _vp, _vp],
     "hba_hier_select": [_i, _vp, _c_i64p, _vp, _f, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
                         _i64, _i64, _i64, _i64, _i64, _f, _vp, _vp, _vp, _vp, _vp, _vp],
+    "hba_route_queries": [_i, _vp, _c_i64p, _vp, _f, _i64, _i64, _i64, _i64, _i64, _vp, _vp],
     "hba_hier_select_rows": [_i, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _f,
                              _vp, _vp, _vp],
     "hba_attn_fwd": [_i, _vp, _c_i64p, _vp, _vp, _f, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64,

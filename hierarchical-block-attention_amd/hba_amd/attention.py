@@ -247,6 +247,14 @@ def build_super(S0, fanout):
     return (S1.squeeze(1) if squeeze else S1), S1.shape[2]
 
 
+def grouped_query(qc, cfg):
+    """summarizer.py:50-54: the routing query of each KV group, the sum of its
+    heads' content queries qc [B, n, Hq, dh] (already QKNorm'd, as the
+    reference's callers pass them) in the declared order and qc's storage
+    rounding -> [B, Hkv, n, dh]."""
+    return ops.route_queries(qc, None, 1e-6, cfg.n_kv).transpose(1, 2)
+
+
 def hier_select(qn, S0, S1, fanout, beam, kk, cand, scale):
     """attention.py:217-246 with the reference's signature: qn [B, c, dh],
     S0 [B, nb, m, dh], S1 [B, ns, m, dh], cand bool [c, nb].  Returns

@@ -158,6 +158,29 @@ def _sel_out(q, Hkv, k):
             torch.empty(B, Hkv, n, dtype=torch.int32, device=q.device))
 
 
+@torch.library.custom_op("hba::route_queries", mutates_args=(), device_types="cuda")
+def route_queries(q: Tensor, q_gain: Optional[Tensor], eps: float, n_kv: int) -> Tensor:
+    """grouped_query (summarizer.py:50-54) of the QKNorm'd queries: [B, n, Hkv, d]
+    in q's dtype, a valid one-head-per-group q for score_select / hier_select
+    (q_gain None), which then select exactly as on q."""
+    dev = _dev(q)
+    _rows(q, "q")
+    B, n, Hq, d = q.shape
+    qg = _f32c(q_gain, dev, Hq, "q_gain")
+    out = torch.empty(B, n, n_kv, d, dtype=q.dtype, device=dev)
+    with torch.cuda.device(dev):
+        st = lib().hba_route_queries(_code(q), _p(q), strides3(q), _p(qg), eps, B, n, Hq, n_kv, d, _p(out),
+                                     _stream(dev))
+    check(st, "hba_route_queries")
+    return out
+
+
+@route_queries.register_fake
+def _(q, q_gain, eps, n_kv):
+    B, n, Hq, d = q.shape
+    return q.new_empty(B, n, n_kv, d)
+
+
 @torch.library.custom_op("hba::score_select", mutates_args=(), device_types="cuda")
 def score_select(q: Tensor, q_gain: Optional[Tensor], eps: float, S0: Tensor, window: int, k: int,
                  scale: float, block: int = 64) -> Tuple[Tensor, Tensor, Tensor]:

@@ -136,6 +136,20 @@ int hba_hier_select(int dtype, const void *q, const int64_t q_strides[3],
                     float *scores, float *sup_scores, void *stream);
 
 /*
+ * Routing queries: qg [B, n, Hkv, d] (contiguous, storage dtype) = per KV
+ * group, the sum of QKNorm(q) over its Hq/Hkv heads, in the declared order
+ * and storage roundings the selection kernels use (QKNorm skipped when q_gain
+ * is NULL).  qg is a valid q for hba_score_select / hba_hier_select with
+ * Hq = Hkv and q_gain = NULL, which then select exactly as on q itself.
+ *   replaces: grouped_query  src/hba/summarizer.py:50-54 applied to the
+ *             QKNorm'd queries (_HeadRMSNorm, src/hba/attention.py:88-94)
+ * d 64 or 128, Hq/Hkv <= 16.
+ */
+int hba_route_queries(int dtype, const void *q, const int64_t q_strides[3], const float *q_gain,
+                      float eps, int64_t B, int64_t n, int64_t Hq, int64_t Hkv, int64_t d, void *qg,
+                      void *stream);
+
+/*
  * hier_select with the reference's own signature and an arbitrary candidate
  * mask: qn [B, c, d] routing queries (already grouped and QKNorm'd, as the
  * reference's eval path passes them), S0 [B, nb, m, d], S1 [B, ns, m, d] with

@@ -174,6 +174,46 @@ def test_flat_select(dev, case):
             assert flips <= max(2, n // 1000), flips
 
 
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+@pytest.mark.parametrize("d,Hq,Hkv,qknorm", [(64, 14, 2, True), (128, 16, 1, True), (64, 4, 4, False),
+                                             (128, 28, 4, False)])
+def test_route_queries_bit_exact(dev, dt, d, Hq, Hkv, qknorm):
+    """hba_route_queries: grouped_query of the QKNorm'd heads (declared order,
+    storage roundings) against the oracle, bit for bit."""
+    cfg, x, prm, cos, sin = make(dev, dt, n=384, d=d, Hq=Hq, Hkv=Hkv, qknorm=qknorm)
+    gain = x["q_gain"] if qknorm else None
+    rq = ops.route_queries(x["q"], gain, 1e-6, Hkv)
+    torch.cuda.synchronize()
+    qc = O.qknorm(f(x["q"])[0], f(x["q_gain"]), 1e-6, dt) if qknorm else f(x["q"])[0]
+    want = O.grouped_query(qc, Hkv, dt)                                   # [Hkv, n, d]
+    assert np.array_equal(f(rq)[0].transpose(1, 0, 2), want)
+    if not qknorm:   # the grouped_query drop-in (summarizer.py:50-54): [B, Hkv, n, d]
+        assert np.array_equal(f(hba_amd.grouped_query(x["q"], cfg))[0], want)
+
+
+@pytest.mark.parametrize("dt,hier", [("bf16", False), ("f32", False), ("bf16", True), ("f32", True)])
+def test_selection_on_routed_queries_equals_selection_on_q(dev, dt, hier):
+    """The selection kernels on the precomputed routing queries (one head per
+    KV group, no gain) pick exactly what they pick on q: idx, val and cnt
+    bit-identical, flat and hierarchical."""
+    n = 4096
+    cfg, x, prm, cos, sin = make(dev, dt, n=n, W=512, k=16, needles=True)
+    kc, _, _ = ops.prep_keys(x["k"], x["v"], x["k_gain"], 1e-6, cos, sin)
+    S0 = ops.summarize(kc, x["probes"], x["proj"])
+    rq = ops.route_queries(x["q"], x["q_gain"], 1e-6, cfg.n_kv)
+    scale = hba_amd.union_scale(cfg, 64, n)
+    if hier:
+        S1 = ops.build_super(S0, 8)
+        a = ops.hier_select(x["q"], x["q_gain"], 1e-6, S0, S1, cfg.window, 16, 8, 4, scale)
+        b = ops.hier_select(rq, None, 1e-6, S0, S1, cfg.window, 16, 8, 4, scale)
+    else:
+        a = ops.score_select(x["q"], x["q_gain"], 1e-6, S0, cfg.window, 16, scale)
+        b = ops.score_select(rq, None, 1e-6, S0, cfg.window, 16, scale)
+    torch.cuda.synchronize()
+    for ta, tb in zip(a, b):
+        assert torch.equal(ta, tb)
+
+
 @pytest.mark.parametrize("dt", ["bf16", "f32"])
 @pytest.mark.parametrize("pattern", ["lane0", "ties", "zero_q"])
 def test_flat_select_adversarial(dev, pattern, dt):
