@@ -37,9 +37,13 @@ def _qk(cfg, qkn):
     return None, None, 1e-6, 1e-6
 
 
-def forward_stages(q, k, v, cos, sin, cfg, summ, qkn, hier=False, dense_route=False):
+def forward_stages(q, k, v, cos, sin, cfg, summ, qkn, hier=False, dense_route=False, overlap=False):
     """The forward path stage by stage; returns a dict with every intermediate
-    (kc, kr, vt, S0, [S1], idx, val, cnt, out) and the scales used."""
+    (kc, kr, vt, S0, [S1], idx, val, cnt, out) and the scales used.  The
+    stages run in sequence on the current stream; overlap=True (bf16) starts
+    the attention's window launch on a second stream while the summaries and
+    the selection run (the same bits, but measured no faster: the window
+    launch fills the GPU first)."""
     B, n, Hq, dh = q.shape
     assert n % cfg.block == 0, (n, cfg.block)
     if cfg.block != ops.BLOCK and (q.dtype != torch.float32 or hier):
@@ -51,9 +55,9 @@ def forward_stages(q, k, v, cos, sin, cfg, summ, qkn, hier=False, dense_route=Fa
     r = {"scale": scale, "sel_scale": sel_scale}
     r["kc"], r["kr"], r["vt"] = ops.prep_keys(k, v, kg, keps, cos, sin)
     kk = min(cfg.k_blocks, n // cfg.block)
-    # bf16: the window launch needs no selection, so it runs on a second
-    # stream while the summaries and the selection run on this one
-    split = q.dtype == torch.bfloat16
+    # bf16, overlap: the window launch needs no selection, so it can run on a
+    # second stream while the summaries and the selection run on this one
+    split = overlap and q.dtype == torch.bfloat16
     if split:
         main = torch.cuda.current_stream(q.device)
         side = ops.side_stream(q.device)
