@@ -540,12 +540,12 @@ def test_invalid_arguments_raise(dev):
 
 
 def test_overlapped_schedule_equals_one_stream(dev):
-    """forward_stages(overlap=True) runs the bf16 window launch on a second
-    stream while the selection runs; its output must be bit-identical to
-    hba_attn_fwd (both launches on one stream) on the same selection, and to
-    the default one-stream schedule."""
+    """forward_stages (overlap=True, the default) runs the bf16 window launch
+    on a second stream while the selection runs; its output must be
+    bit-identical to hba_attn_fwd (both launches on one stream) on the same
+    selection, and to the one-stream schedule (overlap=False)."""
     cfg, x, prm, cos, sin = make(dev, "bf16", n=4096, W=1024, k=16, needles=True)
-    seq = hba_amd.forward_stages(x["q"], x["k"], x["v"], cos, sin, cfg, prm, prm)["out"]
+    seq = hba_amd.forward_stages(x["q"], x["k"], x["v"], cos, sin, cfg, prm, prm, overlap=False)["out"]
     for _ in range(3):   # repeated calls reuse the side stream and the allocator's blocks
         r = hba_amd.forward_stages(x["q"], x["k"], x["v"], cos, sin, cfg, prm, prm, overlap=True)
         assert torch.equal(r["out"], seq)
