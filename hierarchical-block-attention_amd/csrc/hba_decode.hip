@@ -1622,9 +1622,20 @@ using namespace hba;
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 // Workspace.  Both layouts start with the counters of the one-launch bf16
-// step, two per (s, g): zero before the first call on a workspace, and left
-// zero by every call.
-static size_t ws_ctr_bytes(int64_t Bd, int64_t Hkv) { return align256((size_t)2 * Bd * Hkv * 4); }
+// step, two per (s, g) of one launch: zero before the first call on a
+// workspace, and left zero by every call.  The counter region has one fixed
+// size whatever the call's batch, so that the other regions of an earlier
+// call on the same workspace (fp32, or a smaller or larger batch) never lie
+// under a later call's counters; a bf16 step of more than DEC_CTR_PAIRS
+// (sequence, KV head) pairs runs as several launches over slices of the
+// batch, one after another on the stream.
+constexpr int64_t DEC_CTR_PAIRS = 4096;
+static size_t ws_ctr_bytes() { return align256((size_t)2 * DEC_CTR_PAIRS * 4); }
+// Sequences per bf16 fused launch.
+static int64_t dec_fused_chunk(int64_t Bd, int64_t Hkv) {
+    const int64_t c = DEC_CTR_PAIRS / Hkv;
+    return Bd < c ? Bd : c;
+}
 
 // fp32 (three launches): chunk top-k (values, pages, physical pages), query
 // operands, partial states.
@@ -1633,7 +1644,7 @@ static void ws_layout(int64_t Bd, int64_t Hq, int64_t Hkv, int64_t d, int64_t k,
                       size_t *off_part, size_t *total) {
     size_t nsel = (size_t)Bd * Hkv * (gm.nsc > 0 ? gm.nsc : 1) * k;
     size_t G = (size_t)(Hq / Hkv);
-    *off_val = ws_ctr_bytes(Bd, Hkv);
+    *off_val = ws_ctr_bytes();
     *off_idx = *off_val + align256(nsel * 4);
     *off_phys = *off_idx + align256(nsel * 4);
     *off_q = *off_phys + align256(nsel * 4);
@@ -1641,25 +1652,27 @@ static void ws_layout(int64_t Bd, int64_t Hq, int64_t Hkv, int64_t d, int64_t k,
     *total = *off_part + align256((size_t)Bd * Hkv * gm.npart * G * dec_prow((int)d) * 4);
 }
 
-// bf16 (one launch): chunk top-k (values, pages, physical pages), one
-// partial-state slot per contributing workgroup.
+// bf16 (one launch per slice of dec_fused_chunk sequences): chunk top-k
+// (values, pages, physical pages), one partial-state slot per contributing
+// workgroup, for one slice (the slices run in turn and reuse them).
 static void ws_layout_fused(int64_t Bd, int64_t Hq, int64_t Hkv, int64_t d, int64_t k, const DecFGeom &gm,
                             size_t *off_val, size_t *off_idx, size_t *off_phys, size_t *off_part,
                             size_t *total) {
-    size_t nsel = (size_t)Bd * Hkv * (gm.nsc > 0 ? gm.nsc : 1) * k;
+    const int64_t Bc = dec_fused_chunk(Bd, Hkv);
+    size_t nsel = (size_t)Bc * Hkv * (gm.nsc > 0 ? gm.nsc : 1) * k;
     size_t G = (size_t)(Hq / Hkv);
-    *off_val = ws_ctr_bytes(Bd, Hkv);
+    *off_val = ws_ctr_bytes();
     *off_idx = *off_val + align256(nsel * 4);
     *off_phys = *off_idx + align256(nsel * 4);
     *off_part = *off_phys + align256(nsel * 4);
-    *total = *off_part + align256((size_t)Bd * Hkv * (gm.nz + 1) * G * dec_prow((int)d) * 4);
+    *total = *off_part + align256((size_t)Bc * Hkv * (gm.nz + 1) * G * dec_prow((int)d) * 4);
 }
 
 extern "C" int hba_decode_workspace_size(int64_t Bd, int64_t Hq, int64_t Hkv, int64_t d, int64_t k,
                                          int64_t Bk, int64_t W, int64_t max_len, size_t *bytes) {
     if (!bytes || Bd <= 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv || k < 1 || W < 1 || max_len < 1)
         return HBA_ERR_INVALID_ARG;
-    if (Bk != 64 || k > DEC_KMAX) return HBA_ERR_UNSUPPORTED;
+    if (Bk != 64 || k > DEC_KMAX || Hkv > DEC_CTR_PAIRS) return HBA_ERR_UNSUPPORTED;
     size_t a, b, c, e, f, t32, t16;
     ws_layout(Bd, Hq, Hkv, d, k, dec_geom(W, k, max_len), &a, &b, &c, &e, &f, &t32);
     // the bf16 layout at m = 8, which has the most score chunks
@@ -1708,7 +1721,7 @@ static int decode_fwd_ws(int dtype, const void *q, const float *q_gain, float ep
     if (Hq / Hkv > (mf ? DF_GMAX : DEC_GMAX) || k > DEC_KMAX || !(m == 1 || m == 2 || m == 4 || m == 8))
         return HBA_ERR_UNSUPPORTED;
     if ((max_len + Bk - 1) / Bk > max_pages) return HBA_ERR_INVALID_ARG;
-    if (Bd > 65535 || Hkv > 65535) return HBA_ERR_UNSUPPORTED;
+    if (Bd > 65535 || Hkv > DEC_CTR_PAIRS) return HBA_ERR_UNSUPPORTED;
     if (!abi::aligned16(q) || !abi::aligned16(kc_pages) || !abi::aligned16(kr_pages) ||
         !abi::aligned16(v_pages) || !abi::aligned16(summ_pages) || !abi::aligned16(cos_tab) ||
         !abi::aligned16(sin_tab))
@@ -1745,14 +1758,22 @@ static int decode_fwd_ws(int dtype, const void *q, const float *q_gain, float ep
             HBA_LAUNCH_CHECK();
             return HBA_OK;
         }
-        dim3 grid((unsigned)Bd, (unsigned)Hkv, (unsigned)fg.nz);
-#define HBA_DF(D, M)                                                                                   \
-    hipLaunchKernelGGL((decode_fused_kernel<D, M>), grid, dim3(DF_NT), 0, s, (const bf16_t *)q, q_gain, eps, \
-                       (const bf16_t *)kc_pages, (const bf16_t *)kr_pages, (const bf16_t *)v_pages,          \
-                       (const bf16_t *)summ_pages, page_table, max_pages, seq_lens, cos_tab, sin_tab, scales, \
-                       (int)Hq, (int)Hkv, (int)S, W, (int)k, fg, (int *)ws, (float *)(ws + ov),              \
-                       (int32_t *)(ws + oi), (int32_t *)(ws + oph), (float *)(ws + op), (bf16_t *)out,       \
-                       sel_idx, sel_cnt)
+        // slices of Bc sequences, so that one launch's counters fit their region
+        const int64_t Bc = dec_fused_chunk(Bd, Hkv);
+        for (int64_t c0 = 0; c0 < Bd; c0 += Bc) {
+            const int64_t nc = (Bd - c0 < Bc) ? Bd - c0 : Bc;
+            dim3 grid((unsigned)nc, (unsigned)Hkv, (unsigned)fg.nz);
+            const bf16_t *qc0 = (const bf16_t *)q + c0 * Hq * d;
+            bf16_t *oc0 = (bf16_t *)out + c0 * Hq * d;
+            int32_t *si0 = sel_idx ? sel_idx + c0 * Hkv * k : nullptr;
+            int32_t *sc0 = sel_cnt ? sel_cnt + c0 * Hkv : nullptr;
+#define HBA_DF(D, M)                                                                                            \
+    hipLaunchKernelGGL((decode_fused_kernel<D, M>), grid, dim3(DF_NT), 0, s, qc0, q_gain, eps,                  \
+                       (const bf16_t *)kc_pages, (const bf16_t *)kr_pages, (const bf16_t *)v_pages,             \
+                       (const bf16_t *)summ_pages, page_table + c0 * max_pages, max_pages, seq_lens + c0,       \
+                       cos_tab, sin_tab, scales + c0, (int)Hq, (int)Hkv, (int)S, W, (int)k, fg, (int *)ws,      \
+                       (float *)(ws + ov), (int32_t *)(ws + oi), (int32_t *)(ws + oph), (float *)(ws + op), oc0, \
+                       si0, sc0)
 #define HBA_DFM(D)                     \
     do {                               \
         if (m == 1) HBA_DF(D, 1);      \
@@ -1760,11 +1781,12 @@ static int decode_fwd_ws(int dtype, const void *q, const float *q_gain, float ep
         else if (m == 4) HBA_DF(D, 4); \
         else HBA_DF(D, 8);             \
     } while (0)
-        if (d == 64) HBA_DFM(64);
-        else HBA_DFM(128);
+            if (d == 64) HBA_DFM(64);
+            else HBA_DFM(128);
 #undef HBA_DF
 #undef HBA_DFM
-        HBA_LAUNCH_CHECK();
+            HBA_LAUNCH_CHECK();
+        }
         return HBA_OK;
     }
     DecGeom gm = dec_geom(W, k, max_len);

@@ -211,6 +211,9 @@ def aux_kl(q, k, v, cos, sin, cfg, summ, qkn):
     teacher p* (group-averaged content mass of the candidate blocks) against
     log softmax of the summarizer's block scores, a 0-d fp32 tensor whose
     gradient reaches only summ.probes and summ.proj."""
+    if cfg.block != ops.BLOCK:
+        raise NotImplementedError(f"the aux-KL runs at {ops.BLOCK}-key blocks (got block {cfg.block}); set "
+                                  "cfg.aux_w = 0 to run the forward at other block sizes")
     qg, kg, qeps, keps = _qk(cfg, qkn)
     qg = None if qg is None else qg.detach()
     kg = None if kg is None else kg.detach()

@@ -584,6 +584,30 @@ def aux_kl(q, q_gain, k_gain, eps, kc, S0, probes, proj, window, scale_u, scale_
     return aux[0], dpr, dpj
 
 
+def _check_decode_cache(q, kc_pages, kr_pages, v_pages, summ_pages, page_table, seq_lens):
+    """The decode step's cache arguments: pages in q's dtype on q's device,
+    [P, Hkv, 64 * d] key/value pages and [P, Hkv, m, d] summaries, a
+    contiguous int32 page table [Bd, max_pages] and seq_lens [Bd]."""
+    dev = q.device
+    Bd, Hq, d = q.shape
+    P, Hkv = summ_pages.shape[:2]
+    for t, what in ((kc_pages, "kc_pages"), (kr_pages, "kr_pages"), (v_pages, "v_pages"),
+                    (summ_pages, "summ_pages")):
+        if t.dtype != q.dtype or t.device != dev or not t.is_contiguous():
+            raise ValueError(f"{what} must be a contiguous {q.dtype} tensor on {dev}")
+        if t.shape[:2] != (P, Hkv):
+            raise ValueError(f"{what}: expected {P} pages of {Hkv} KV heads, got {list(t.shape[:2])}")
+        if t is not summ_pages and t[0, 0].numel() != BLOCK * d:
+            raise ValueError(f"{what}: expected {BLOCK * d} elements per page and KV head")
+    if summ_pages.dim() != 4 or summ_pages.shape[3] != d:
+        raise ValueError(f"summ_pages: expected [pages, {Hkv}, m, {d}]")
+    for t, what in ((page_table, "page_table"), (seq_lens, "seq_lens")):
+        if t.dtype != torch.int32 or t.device != dev or not t.is_contiguous():
+            raise ValueError(f"{what} must be a contiguous int32 tensor on {dev}")
+    if page_table.dim() != 2 or page_table.shape[0] != Bd or seq_lens.shape != (Bd,):
+        raise ValueError(f"page_table [{Bd}, max_pages] and seq_lens [{Bd}] expected")
+
+
 def decode_workspace_bytes(Bd, Hq, Hkv, d, k, window, max_len):
     n = ctypes.c_size_t(0)
     check(lib().hba_decode_workspace_size(Bd, Hq, Hkv, d, k, BLOCK, window, max_len, ctypes.byref(n)),
@@ -617,6 +641,7 @@ def decode_fwd(q: Tensor, q_gain: Optional[Tensor], eps: float, kc_pages: Tensor
     dev = _dev(q)
     Bd, Hq, d = q.shape
     Hkv, m = summ_pages.shape[1], summ_pages.shape[2]
+    _check_decode_cache(q, kc_pages, kr_pages, v_pages, summ_pages, page_table, seq_lens)
     cos, sin = _tables(cos, sin, max_len, d, dev)
     qg = _f32c(q_gain, dev, Hq, "q_gain")
     sc = _f32c(scales, dev, Bd, "scales")
@@ -657,6 +682,14 @@ def decode_fwd_noalloc(q, q_gain, eps, kc_pages, kr_pages, v_pages, summ_pages, 
         raise TypeError("q_gain must be a contiguous float32 tensor")
     if cos.shape[0] < max_len or cos.shape[1] != d or sin.shape != cos.shape:
         raise ValueError(f"cos/sin: expected [>= {max_len}, {d}] tables")
+    _check_decode_cache(q, kc_pages, kr_pages, v_pages, summ_pages, page_table, seq_lens)
+    if scales.shape != (Bd,):
+        raise ValueError(f"scales: expected [{Bd}]")
+    for t, what, shape in ((sel_idx, "sel_idx", (Bd, Hkv, k)), (sel_cnt, "sel_cnt", (Bd, Hkv))):
+        if t is None:
+            continue
+        if t.dtype != torch.int32 or t.device != dev or not t.is_contiguous() or tuple(t.shape) != shape:
+            raise ValueError(f"{what}: expected a contiguous int32 tensor {list(shape)} on {dev}")
     with torch.cuda.device(dev):
         st = lib().hba_decode_fwd_noalloc(_code(q), _p(q), _p(q_gain), eps, _p(kc_pages), _p(kr_pages),
                                           _p(v_pages), _p(summ_pages), _p(page_table), page_table.shape[1],

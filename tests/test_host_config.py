@@ -1,4 +1,5 @@
-"""Host-side config helpers without a GPU: yarn_theta (attention.py:47-53)."""
+"""Host-side config helpers and checks without a GPU: yarn_theta
+(attention.py:47-53), the aux-KL's block-size guard."""
 import math
 
 import pytest
@@ -25,3 +26,20 @@ def test_yarn_theta_stretches_the_lowest_frequency_by_the_context_ratio(d):
         cos, sin = hba_amd.rope_tables(8, d, th, "cpu")
         assert torch.allclose(cos[:, 0], torch.cos(torch.arange(8.0)))
         assert torch.allclose(sin[:, d // 2 - 1], torch.sin(torch.arange(8.0) * low(th)), atol=1e-7)
+
+
+def test_aux_kl_refuses_other_block_sizes():
+    """The aux-KL kernel scores 64-key blocks: at the reference's block-16
+    test geometry it raises instead of training the summarizer on 64-key
+    blocks (checked before any tensor is touched, so CPU tensors do)."""
+    from hba_amd import attention as A
+    cfg = hba_amd.HBAConfig(block=16, head_dim=64, n_heads=4, n_kv=2, window=32, k_blocks=2)
+    q = torch.zeros(1, 64, 4, 64)
+    k = torch.zeros(1, 64, 2, 64)
+
+    class Summ:
+        probes = torch.zeros(2, 4, 64, requires_grad=True)
+        proj = torch.zeros(2, 64, 64, requires_grad=True)
+
+    with pytest.raises(NotImplementedError, match="64-key blocks"):
+        A.aux_kl(q, k, k, None, None, cfg, Summ(), None)
