@@ -68,10 +68,12 @@ __global__ __launch_bounds__(64) void attn_f32_kernel(
     float mx = -INFINITY;
     for (int64_t j = 0; j < s_end; ++j) mx = fmaxf(mx, dot_row<D>(qc, KC + j * D) * scale);
     for (int64_t j = w_beg; j <= i; ++j) mx = fmaxf(mx, dot_row<D>(qr, KR + j * D) * scale);
+    // a routed block's keys below S are sinks, counted once (the union mask
+    // of attention.py:351-352; with S <= 64 no routed block holds one)
     for (int r = 0; r < c; ++r) {
         if (ix[r] < 1 || ix[r] >= nb) continue;   // block 0 is never routed (sinks, window)
-        int64_t j0 = (int64_t)ix[r] * 64;
-        for (int64_t j = j0; j < j0 + 64; ++j) mx = fmaxf(mx, dot_row<D>(qc, KC + j * D) * scale);
+        const int64_t j0 = (int64_t)ix[r] * 64;
+        for (int64_t j = (j0 > S ? j0 : S); j < j0 + 64; ++j) mx = fmaxf(mx, dot_row<D>(qc, KC + j * D) * scale);
     }
     float acc[D];
 #pragma unroll
@@ -91,8 +93,8 @@ __global__ __launch_bounds__(64) void attn_f32_kernel(
     }
     for (int r = 0; r < c; ++r) {
         if (ix[r] < 1 || ix[r] >= nb) continue;   // block 0 is never routed (sinks, window)
-        int64_t j0 = (int64_t)ix[r] * 64;
-        for (int64_t j = j0; j < j0 + 64; ++j) {
+        const int64_t j0 = (int64_t)ix[r] * 64;
+        for (int64_t j = (j0 > S ? j0 : S); j < j0 + 64; ++j) {
             float p = expf(dot_row<D>(qc, KC + j * D) * scale - mx);
             l += p;
 #pragma unroll
@@ -147,7 +149,7 @@ extern "C" int hba_attn_fwd(int dtype, const void *q, const int64_t q_strides[3]
         if (B <= 0 || n <= 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv != 0 || W < 1 || S < 0 || k < 1)
             return HBA_ERR_INVALID_ARG;
         if (!gen_shape_ok(d, Bk)) return HBA_ERR_UNSUPPORTED;
-        if (n % Bk != 0 || S > Bk) return HBA_ERR_INVALID_ARG;
+        if (n % Bk != 0) return HBA_ERR_INVALID_ARG;
         if (B > 65535 || Hq > 65535) return HBA_ERR_UNSUPPORTED;
         return gen_attn((const float *)q, q_strides, q_gain, eps, (const float *)kc, (const float *)kr,
                         (const float *)vt, cos_tab, sin_tab, idx, cnt, B, n, Hq, Hkv, d, S, W, Bk, k, scale,
@@ -161,7 +163,8 @@ extern "C" int hba_attn_fwd(int dtype, const void *q, const int64_t q_strides[3]
     if (B <= 0 || n <= 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv != 0 || W < 1 || S < 0 || k < 1)
         return HBA_ERR_INVALID_ARG;
     if (Bk != 64) return HBA_ERR_UNSUPPORTED;
-    if (n % Bk != 0 || S > Bk) return HBA_ERR_INVALID_ARG;
+    if (n % Bk != 0) return HBA_ERR_INVALID_ARG;
+    if (dtype == HBA_DTYPE_BF16 && S > 2 * Bk) return HBA_ERR_UNSUPPORTED;   // the MFMA path stages 2 sink blocks
     if (!abi::rows_aligned(dtype, q, q_strides) || !abi::rows_aligned(dtype, out, out_strides) ||
         !abi::aligned16(kc) || !abi::aligned16(kr) || !abi::aligned16(vt))
         return HBA_ERR_UNSUPPORTED;
@@ -199,7 +202,8 @@ static int attn_split_checks(const void *q, const int64_t *q_strides, int64_t B,
     if (!q || !q_strides || !out || !out_strides) return HBA_ERR_INVALID_ARG;
     if (B <= 0 || n <= 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv != 0 || S < 0) return HBA_ERR_INVALID_ARG;
     if (Bk != 64) return HBA_ERR_UNSUPPORTED;
-    if (n % Bk != 0 || S > Bk) return HBA_ERR_INVALID_ARG;
+    if (n % Bk != 0) return HBA_ERR_INVALID_ARG;
+    if (S > 2 * Bk) return HBA_ERR_UNSUPPORTED;   // the MFMA path stages 2 sink blocks
     if (!abi::rows_aligned(HBA_DTYPE_BF16, q, q_strides) || !abi::rows_aligned(HBA_DTYPE_BF16, out, out_strides))
         return HBA_ERR_UNSUPPORTED;
     if (B > 65535 || Hq > 65535) return HBA_ERR_UNSUPPORTED;

@@ -547,13 +547,15 @@ __global__ __launch_bounds__(256, 3) void attn_win_kernel(
 enum { RM_SINK = 0, RM_COL = 1 };
 
 // One staged block against one 16-row tile.  mode RM_SINK: keys j < S and
-// j <= i are valid (nmt M-tiles can hold them); RM_COL: the whole block is
-// valid for the columns whose query picked it (colok).
+// j <= i are valid (nmt M-tiles can hold them); RM_COL: the block's keys j >=
+// kfloor are valid for the columns whose query picked it (colok) -- kfloor is
+// 0 except for routed block 1 when S > 64, whose keys below S are sinks.  S,
+// kfloor and icol count from the block's first key.
 template <int D, bool FIXED>
 __device__ __forceinline__ void rt_update(const bf16_t *Ks, const bf16_t *Vs, const bf16x8 (&qop)[D / 32],
                                           f32x4 (&O)[D / 16], float &mrun, float &lsum, int mode,
                                           int64_t icol, bool colok, int S, int nmt, float sl2, float bl2,
-                                          int l16, int lg) {
+                                          int l16, int lg, int kfloor = 0) {
     constexpr int NKS = D / 32, NDT = D / 16;
     // fixed shift, block columns: the query operand carries scale*log2(e), so
     // S^T starts at -shift (a column whose query did not pick the block at
@@ -571,6 +573,13 @@ __device__ __forceinline__ void rt_update(const bf16_t *Ks, const bf16_t *Vs, co
 #pragma unroll
             for (int ks = 0; ks < NKS; ++ks) Sa[mt] = mma(ldb8(kp + 8 * ((4 * ks + lg) ^ sw)), qop[ks], Sa[mt]);
         }
+    }
+    if (kfloor > 0) {   // wave-uniform and rare: keys below the floor out
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (32 * (mt >> 1) + 8 * lg + 4 * (mt & 1) + e < kfloor) Sa[mt][e] = -INFINITY;
     }
     float p[2][8];
     float shift = bl2;
@@ -631,7 +640,7 @@ __device__ __forceinline__ void rt_update(const bf16_t *Ks, const bf16_t *Vs, co
     }
 }
 
-template <int D, int PTW, bool FIXED>
+template <int D, int PTW, bool FIXED, bool S2>
 __device__ __forceinline__ void routed_body(
     const bf16_t *__restrict__ q, int64_t qsb, int64_t qsn, int64_t qsh, const float *__restrict__ qgain,
     float eps, const bf16_t *__restrict__ kc, const bf16_t *__restrict__ vt,
@@ -690,9 +699,10 @@ __device__ __forceinline__ void routed_body(
             dma16(dsrc[pp] + (int64_t)blk * dstr[pp],
                   ring_lds + (uint32_t)(slot * C::SLOT * 2) + (uint32_t)(w + C::WAVES * pp) * 1024u);
     };
-    // sinks: block 0 into the last ring slot (free until the first refill),
-    // landing during the set-up
+    // sinks: block 0 into the last ring slot and (S > 64) block 1 into the
+    // one before (both free until the first refill), landing during the set-up
     if (S > 0) fill(0, C::NS - 1);
+    if (S2) fill(1, C::NS - 2);
 
     // ----------------------------------------------------- per-row state --
     // (first, so that the query loads overlap the selection set-up)
@@ -779,16 +789,22 @@ __device__ __forceinline__ void routed_body(
     for (int e = 0; e < npro; ++e) fill(list[e], e);
     if (S > 0) {
         wait_vm_n(npro * C::DPW);
-        __syncthreads();   // every share of block 0 landed
-        const bf16_t *Ks = ring + (C::NS - 1) * C::SLOT;
-        const int nmt = (S <= 4) ? 1 : (S <= 32 ? 2 : 4);   // M-tiles holding keys 0..S-1
+        __syncthreads();   // every share of the sink blocks landed
+        for (int sb = 0; sb < (S2 ? 2 : 1); ++sb) {
+            const bf16_t *Ks = ring + (C::NS - 1 - sb) * C::SLOT;
+            const int Sb = min(S - 64 * sb, 64);            // sink keys of this block
+            const int nmt = (Sb <= 4) ? 1 : (Sb <= 32 ? 2 : 4);   // M-tiles holding keys 0..Sb-1
 #pragma unroll
-        for (int tt = 0; tt < PTW; ++tt) {
-            if (i0 + (int64_t)(w * PTW + tt) * QPT >= n) break;
-            rt_update<D, FIXED>(Ks, Ks + 64 * D, qop[tt], O[tt], mrun[tt], lsum[tt], RM_SINK, icol[tt], cok[tt], S,
-                                nmt, FIXED ? 1.0f : sl2, bl2, l16, lg);
+            for (int tt = 0; tt < PTW; ++tt) {
+                if (i0 + (int64_t)(w * PTW + tt) * QPT >= n) break;
+                rt_update<D, FIXED>(Ks, Ks + 64 * D, qop[tt], O[tt], mrun[tt], lsum[tt], RM_SINK, icol[tt] - 64 * sb,
+                                    cok[tt], Sb, nmt, FIXED ? 1.0f : sl2, bl2, l16, lg);
+            }
         }
     }
+    // with S > 64 the keys 64..S-1 are sinks: routed block 1 (union entry 0
+    // if picked) counts only its keys from S on
+    const bool b1 = S2 && ne > 0 && list[0] == 1;
     uint32_t qw[PTW], ww[PTW];   // this lane's query's / this row tile's bits of the current word
     for (int e0 = 0; e0 < ne; e0 += P) {
         // this wave's shares of entries e0..e0+P-1 have landed once at most
@@ -822,7 +838,7 @@ __device__ __forceinline__ void routed_body(
                 const bf16_t *Ks = ring + (e % C::NS) * C::SLOT;
                 const bool hit = (qw[tt] >> (sh + j)) & 1u;
                 rt_update<D, FIXED>(Ks, Ks + 64 * D, qop[tt], O[tt], mrun[tt], lsum[tt], RM_COL, icol[tt], hit, S,
-                                    4, FIXED ? 1.0f : sl2, bl2, l16, lg);
+                                    4, FIXED ? 1.0f : sl2, bl2, l16, lg, (S2 && b1 && e == 0) ? S - 64 : 0);
             }
         }
     }
@@ -859,7 +875,9 @@ __device__ __forceinline__ void routed_body(
     }
 }
 
-template <int D, int PTW>
+// S2: sinks beyond the first block (64 < S <= 128), a separate instantiation
+// so that the common case carries none of its code.
+template <int D, int PTW, bool S2>
 __global__ __launch_bounds__(RtCfg<D>::NTHR, RtCfg<D>::NTHR / 256) void attn_routed_kernel(
     const bf16_t *__restrict__ q, int64_t qsb, int64_t qsn, int64_t qsh, const float *__restrict__ qgain,
     const float *__restrict__ kgain, float eps, const bf16_t *__restrict__ kc, const bf16_t *__restrict__ vt,
@@ -875,10 +893,10 @@ __global__ __launch_bounds__(RtCfg<D>::NTHR, RtCfg<D>::NTHR / 256) void attn_rou
     const float sl2 = scale * LOG2E;
     float bl2;
     if (group_bound(qgain, kgain, combo % Hkv, G, sl2, D, bl2))
-        routed_body<D, PTW, true>(q, qsb, qsn, qsh, qgain, eps, kc, vt, idx, cnt, n, Hq, Hkv, S, kk, sl2, bl2,
+        routed_body<D, PTW, true, S2>(q, qsb, qsn, qsh, qgain, eps, kc, vt, idx, cnt, n, Hq, Hkv, S, kk, sl2, bl2,
                                   combo, tile, out, osb, osn, osh, lse, smem, nlist);
     else
-        routed_body<D, PTW, false>(q, qsb, qsn, qsh, qgain, eps, kc, vt, idx, cnt, n, Hq, Hkv, S, kk, sl2, bl2,
+        routed_body<D, PTW, false, S2>(q, qsb, qsn, qsh, qgain, eps, kc, vt, idx, cnt, n, Hq, Hkv, S, kk, sl2, bl2,
                                    combo, tile, out, osb, osn, osh, lse, smem, nlist);
 }
 
@@ -953,14 +971,17 @@ static int launch_routed_t(const void *q, const int64_t *qs, const float *qgain,
     int64_t grid;
     grid_map(B * Hkv, ntiles, xmap, grid);
     if (grid > 0x7fffffff) return HBA_ERR_UNSUPPORTED;
-    if (hipFuncSetAttribute(reinterpret_cast<const void *>(&attn_routed_kernel<D, PTW>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
-        return HBA_ERR_LAUNCH;
-    hipLaunchKernelGGL((attn_routed_kernel<D, PTW>), dim3((unsigned)grid), dim3(C::NTHR), lds, s,
-                       (const bf16_t *)q, qs[0], qs[1], qs[2], qgain, kgain, eps, (const bf16_t *)kc,
-                       (const bf16_t *)vt, idx, cnt, n, (int)Hq, (int)Hkv, (int)S, (int)k, scale, (int)ntiles,
-                       (int)(B * Hkv), xmap, (bf16_t *)out, os[0], os[1], os[2], lse);
-    return HBA_OK;
+    auto go = [&](auto kern) -> int {
+        if (hipFuncSetAttribute(reinterpret_cast<const void *>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)lds) != hipSuccess)
+            return HBA_ERR_LAUNCH;
+        hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(C::NTHR), lds, s, (const bf16_t *)q, qs[0], qs[1],
+                           qs[2], qgain, kgain, eps, (const bf16_t *)kc, (const bf16_t *)vt, idx, cnt, n, (int)Hq,
+                           (int)Hkv, (int)S, (int)k, scale, (int)ntiles, (int)(B * Hkv), xmap, (bf16_t *)out,
+                           os[0], os[1], os[2], lse);
+        return HBA_OK;
+    };
+    return (S > 64) ? go(&attn_routed_kernel<D, PTW, true>) : go(&attn_routed_kernel<D, PTW, false>);
 }
 
 // PTW row tiles per wave when the selection lists fit LDS beside the ring, else one

@@ -1,7 +1,7 @@
 // fp32 forward for geometry outside the tuned kernels (hba_generic.hip): the
 // entry points call these when an fp32 call's head dim is not 64 / 128, its
-// block size is not 64, or (selection) k > 64 or the slot count is not 1, 2,
-// 4 or 8.
+// block size is not 64, (selection) k > 64 or the slot count is not 1, 2, 4
+// or 8, or (routing queries) more than 16 query heads share a KV head.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <cstdint>
@@ -21,6 +21,8 @@ int gen_summarize(const float *kc, int64_t B, int64_t Hkv, int64_t n, int64_t d,
 int gen_score_select(const float *q, const int64_t *qs, const float *qgain, float eps, const float *S0, int64_t B,
                      int64_t n, int64_t Hq, int64_t Hkv, int64_t d, int64_t m, int64_t Bk, int64_t W, int64_t k,
                      float scale, int32_t *idx, float *val, int32_t *cnt, float *scores, hipStream_t s);
+int gen_route_queries(const float *q, const int64_t *qs, const float *qgain, float eps, int64_t B, int64_t n,
+                      int64_t Hq, int64_t Hkv, int64_t d, float *qg, hipStream_t s);
 int gen_attn(const float *q, const int64_t *qs, const float *qgain, float eps, const float *kc, const float *kr,
              const float *vt, const float *cosT, const float *sinT, const int32_t *idx, const int32_t *cnt, int64_t B,
              int64_t n, int64_t Hq, int64_t Hkv, int64_t d, int64_t S, int64_t W, int64_t Bk, int64_t k, float scale,

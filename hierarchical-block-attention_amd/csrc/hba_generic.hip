@@ -268,8 +268,8 @@ __global__ __launch_bounds__(64) void attn_kernel(const float *__restrict__ q, i
     for (int64_t j = w_beg; j <= i; ++j) mx = fmaxf(mx, dot_n(qr, KR + j * d, d) * scale);
     for (int r = 0; r < c; ++r) {
         if (ix[r] < 1 || ix[r] >= nb) continue;   // block 0 is never routed (sinks, window)
-        const int64_t j0 = (int64_t)ix[r] * Bk;
-        for (int64_t j = j0; j < j0 + Bk; ++j) mx = fmaxf(mx, dot_n(qc, KC + j * d, d) * scale);
+        const int64_t j0 = (int64_t)ix[r] * Bk;   // keys below S are sinks, counted once
+        for (int64_t j = (j0 > S ? j0 : S); j < j0 + Bk; ++j) mx = fmaxf(mx, dot_n(qc, KC + j * d, d) * scale);
     }
     for (int t = 0; t < d; ++t) acc[t] = 0.0f;
     float l = 0.0f;
@@ -283,11 +283,34 @@ __global__ __launch_bounds__(64) void attn_kernel(const float *__restrict__ q, i
     for (int r = 0; r < c; ++r) {
         if (ix[r] < 1 || ix[r] >= nb) continue;
         const int64_t j0 = (int64_t)ix[r] * Bk;
-        for (int64_t j = j0; j < j0 + Bk; ++j) add(qc, KC, j);
+        for (int64_t j = (j0 > S ? j0 : S); j < j0 + Bk; ++j) add(qc, KC, j);
     }
     float *orow = out + b * osb + i * osn + (int64_t)h * osh;
     const float inv = 1.0f / l;
     for (int t = 0; t < d; ++t) orow[t] = acc[t] * inv;
+}
+
+// ------------------------------------------------------- routing query ----
+// One thread per (query, KV head): the QKNorm'd rows of the group's G heads
+// summed in head order (grouped_query, summarizer.py:50-54), any G.
+__global__ __launch_bounds__(NT) void route_queries_kernel(const float *__restrict__ q, int64_t qsb, int64_t qsn,
+                                                           int64_t qsh, const float *__restrict__ qgain, float eps,
+                                                           int64_t B, int64_t n, int Hq, int Hkv, int d,
+                                                           float *__restrict__ qg) {
+    const int64_t gid = (int64_t)blockIdx.x * NT + threadIdx.x;
+    if (gid >= B * n * Hkv) return;
+    const int g = (int)(gid % Hkv);
+    const int64_t i = (gid / Hkv) % n, b = gid / (Hkv * n);
+    const int G = Hq / Hkv;
+    float acc[DMAX], x[DMAX];
+    for (int h = 0; h < G; ++h) {
+        const float *row = q + b * qsb + i * qsn + (int64_t)(g * G + h) * qsh;
+        for (int t = 0; t < d; ++t) x[t] = row[t];
+        if (qgain) qknorm_n(x, d, qgain[g * G + h], eps);
+        for (int t = 0; t < d; ++t) acc[t] = (h == 0) ? x[t] : acc[t] + x[t];
+    }
+    float *dst = qg + ((b * n + i) * Hkv + g) * d;
+    for (int t = 0; t < d; ++t) dst[t] = acc[t];
 }
 
 }  // namespace gen
@@ -338,6 +361,15 @@ int gen_attn(const float *q, const int64_t *qs, const float *qgain, float eps, c
     hipLaunchKernelGGL(gen::attn_kernel, dim3((unsigned)((n + 63) / 64), (unsigned)Hq, (unsigned)B), dim3(64), 0, s, q,
                        qs[0], qs[1], qs[2], qgain, eps, kc, kr, vt, cosT, sinT, idx, cnt, n, (int)Hq, (int)Hkv,
                        (int)S, W, (int)Bk, (int)k, (int)d, scale, out, os[0], os[1], os[2]);
+    HBA_LAUNCH_CHECK();
+    return HBA_OK;
+}
+
+int gen_route_queries(const float *q, const int64_t *qs, const float *qgain, float eps, int64_t B, int64_t n,
+                      int64_t Hq, int64_t Hkv, int64_t d, float *qg, hipStream_t s) {
+    const int64_t total = B * n * Hkv;
+    hipLaunchKernelGGL(gen::route_queries_kernel, dim3((unsigned)((total + gen::NT - 1) / gen::NT)), dim3(gen::NT), 0,
+                       s, q, qs[0], qs[1], qs[2], qgain, eps, B, n, (int)Hq, (int)Hkv, (int)d, qg);
     HBA_LAUNCH_CHECK();
     return HBA_OK;
 }

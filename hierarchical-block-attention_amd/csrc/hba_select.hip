@@ -1613,6 +1613,14 @@ __global__ __launch_bounds__(64) void route_queries_f32_kernel(const float *__re
 extern "C" int hba_route_queries(int dtype, const void *q, const int64_t q_strides[3], const float *q_gain,
                                  float eps, int64_t B, int64_t n, int64_t Hq, int64_t Hkv, int64_t d, void *qg,
                                  void *stream) {
+    if (dtype == HBA_DTYPE_F32 && (!(d == 64 || d == 128) || (Hkv > 0 && Hq / Hkv > 16))) {
+        // fp32, another head dim or group size: the generic kernel
+        if (!q || !q_strides || !qg || B <= 0 || n <= 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv != 0)
+            return HBA_ERR_INVALID_ARG;
+        if (!gen_shape_ok(d, 1)) return HBA_ERR_UNSUPPORTED;
+        return gen_route_queries((const float *)q, q_strides, q_gain, eps, B, n, Hq, Hkv, d, (float *)qg,
+                                 (hipStream_t)stream);
+    }
     int st = abi::check_dtype_dim(dtype, d);
     if (st) return st;
     if (!q || !q_strides || !qg || B <= 0 || n <= 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv != 0)

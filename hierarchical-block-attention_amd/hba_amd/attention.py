@@ -37,18 +37,89 @@ def _qk(cfg, qkn):
     return None, None, 1e-6, 1e-6
 
 
+def _tuned(q, k, cfg, summ, hier):
+    """Whether the tuned kernels take this forward: 64-key blocks, head dim 64
+    or 128, k <= 64, 1/2/4/8 slots; in bf16 also at most 16 query heads per KV
+    head and S <= 128; hierarchical also beam <= 16, fanout <= 64, G <= 16."""
+    B, n, Hq, dh = q.shape
+    G = Hq // k.shape[2]
+    kk = min(cfg.k_blocks, n // cfg.block)
+    ok = cfg.block == ops.BLOCK and dh in (64, 128) and kk <= 64 and summ.probes.shape[1] in (1, 2, 4, 8)
+    if q.dtype != torch.float32:
+        ok = ok and G <= 16 and cfg.sinks <= 2 * ops.BLOCK
+    if hier:
+        ok = ok and G <= 16 and cfg.beam <= 16 and cfg.fanout <= 64
+    return ok
+
+
+def _hier_generic(qf, qg, qeps, S0, S1, cfg, kk, scale):
+    """Hierarchical selection on the generic kernels (fp32): the routing
+    queries (hba_route_queries), then hba_hier_select_rows per KV head with
+    the routing candidate mask (attention.py:250-256), in chunks of rows that
+    bound the mask.  Returns idx, val [B, Hkv, n, kk] (-1 / -inf past the
+    picks) and cnt [B, Hkv, n]."""
+    B, n, Hq, d = qf.shape
+    Hkv, nb = S0.shape[1], S0.shape[2]
+    ns = S1.shape[2]
+    keff = min(kk, min(cfg.beam, ns) * cfg.fanout)
+    dev = qf.device
+    qn = ops.route_queries(qf, qg, qeps, Hkv)
+    idx = torch.full((B, Hkv, n, kk), -1, dtype=torch.int32, device=dev)
+    val = torch.full((B, Hkv, n, kk), float("-inf"), dtype=torch.float32, device=dev)
+    blk = torch.arange(nb, device=dev)
+    chunk = max(1, (1 << 26) // max(nb, 1))
+    for i0 in range(0, n, chunk):
+        i1 = min(n, i0 + chunk)
+        i = torch.arange(i0, i1, device=dev)
+        cand = (blk[None, :] >= 1) & ((blk[None, :] + 1) * cfg.block <= (i[:, None] - cfg.window + 1))
+        for g in range(Hkv):
+            ti, tv = ops.hier_select_rows(qn[:, i0:i1, g], S0[:, g], S1[:, g], cfg.fanout, cfg.beam, kk, cand,
+                                          scale)
+            idx[:, g, i0:i1, :keff] = ti.to(torch.int32)
+            val[:, g, i0:i1, :keff] = tv
+    cnt = torch.isfinite(val).sum(-1).to(torch.int32)
+    return idx, val, cnt
+
+
+def _forward_generic(q, k, v, cos, sin, cfg, summ, qkn, hier, dense_route):
+    """forward_stages off the tuned geometry: every stage on the generic fp32
+    kernels (bf16 inputs widened to fp32; the output back in q's dtype) --
+    any block size, even head dim <= 256, k, slot count, group size, sink
+    count, beam and fanout.  A correctness path, slower than the tuned one."""
+    B, n, Hq, dh = q.shape
+    qg, kg, qeps, keps = _qk(cfg, qkn)
+    qf, kf, vf = q.float(), k.float(), v.float()
+    scale = union_scale(cfg, dh, n)
+    sel_scale = route_scale(cfg, dh) if dense_route else scale
+    r = {"scale": scale, "sel_scale": sel_scale}
+    r["kc"], r["kr"], r["vt"] = ops.prep_keys(kf, vf, kg, keps, cos, sin)
+    kk = min(cfg.k_blocks, n // cfg.block)
+    r["S0"] = ops.summarize(r["kc"], summ.probes, summ.proj, cfg.block)
+    if hier:
+        r["S1"] = ops.build_super(r["S0"], cfg.fanout)
+        r["idx"], r["val"], r["cnt"] = _hier_generic(qf, qg, qeps, r["S0"], r["S1"], cfg, kk, sel_scale)
+    else:
+        r["idx"], r["val"], r["cnt"] = ops.score_select(qf, qg, qeps, r["S0"], cfg.window, kk, sel_scale,
+                                                        cfg.block)
+    out = ops.attn_fwd(qf, qg, kg, qeps, r["kc"], r["kr"], r["vt"], cos, sin, r["idx"], r["cnt"], cfg.sinks,
+                       cfg.window, scale, cfg.block)
+    r["out"] = out.to(q.dtype)
+    return r
+
+
 def forward_stages(q, k, v, cos, sin, cfg, summ, qkn, hier=False, dense_route=False, overlap=True):
     """The forward path stage by stage; returns a dict with every intermediate
     (kc, kr, vt, S0, [S1], idx, val, cnt, out) and the scales used.  In
     bf16 with overlap=True (the default) the attention's window launch runs on
     a second stream while the summaries and the selection run on the current
     one (0.4-1.5 % faster at 32K); overlap=False runs every stage in sequence
-    on the current stream.  Both give the same bits."""
+    on the current stream.  Both give the same bits.  Geometry the tuned
+    kernels do not take (_tuned) runs on the generic fp32 kernels
+    (_forward_generic)."""
     B, n, Hq, dh = q.shape
     assert n % cfg.block == 0, (n, cfg.block)
-    if cfg.block != ops.BLOCK and (q.dtype != torch.float32 or hier):
-        raise ValueError(f"block {cfg.block}: the bf16 and hierarchical kernels use {ops.BLOCK}-key blocks "
-                         "(fp32 with flat selection takes any block size)")
+    if not _tuned(q, k, cfg, summ, hier):
+        return _forward_generic(q, k, v, cos, sin, cfg, summ, qkn, hier, dense_route)
     qg, kg, qeps, keps = _qk(cfg, qkn)
     scale = union_scale(cfg, dh, n)
     sel_scale = route_scale(cfg, dh) if dense_route else scale
@@ -139,10 +210,12 @@ def _with_grad(q, k, v, cos, sin, cfg, summ, qkn, mode):
         return None
     if qg is not None and qeps != keps:
         raise NotImplementedError("the backward takes one QKNorm eps for q and k")
-    if cfg.block != ops.BLOCK or q.shape[-1] not in (64, 128):
-        raise NotImplementedError(f"the backward runs at {ops.BLOCK}-key blocks and head dims 64 / 128 "
-                                  f"(got block {cfg.block}, head dim {q.shape[-1]}); the forward takes "
-                                  "other geometry in fp32 under torch.no_grad()")
+    G = q.shape[2] // k.shape[2]
+    if cfg.block != ops.BLOCK or q.shape[-1] not in (64, 128) or cfg.sinks > ops.BLOCK or G > 16:
+        raise NotImplementedError(f"the backward runs at {ops.BLOCK}-key blocks, head dims 64 / 128, at most "
+                                  f"{ops.BLOCK} sinks and 16 query heads per KV head (got block {cfg.block}, "
+                                  f"head dim {q.shape[-1]}, {cfg.sinks} sinks, {G} heads per KV head); the "
+                                  "forward takes other geometry under torch.no_grad()")
     return _UnionAttention.apply(q, k, v, qg, kg, cos, sin, cfg, summ, qeps, keps, mode)
 
 

@@ -143,7 +143,9 @@ int hba_hier_select(int dtype, const void *q, const int64_t q_strides[3],
  * Hq = Hkv and q_gain = NULL, which then select exactly as on q itself.
  *   replaces: grouped_query  src/hba/summarizer.py:50-54 applied to the
  *             QKNorm'd queries (_HeadRMSNorm, src/hba/attention.py:88-94)
- * d 64 or 128, Hq/Hkv <= 16.
+ * bf16: d 64 or 128, Hq/Hkv <= 16; fp32: any even d <= 256, any Hq/Hkv
+ * (other than d 64 / 128 with Hq/Hkv <= 16: a generic one-thread-per-row
+ * kernel, same order).
  */
 int hba_route_queries(int dtype, const void *q, const int64_t q_strides[3], const float *q_gain,
                       float eps, int64_t B, int64_t n, int64_t Hq, int64_t Hkv, int64_t d, void *qg,
@@ -179,7 +181,11 @@ int hba_hier_select_rows(int dtype, const void *qn, const void *S0, const void *
  * the log-length temperature).  k_gain (the gains hba_prep_keys applied; NULL
  * if none) lets the kernel bound the logits by d*max(q_gain)*k_gain*scale
  * and use that bound as the softmax shift.  out [B, n, Hq, d] with
- * out_strides.  Requires S <= Bk and n % Bk == 0; Bk == 64 and d in {64, 128}.
+ * out_strides.  Requires n % Bk == 0.  A routed block's keys below S are
+ * sinks and count once, as the union mask of hba_attention_dense counts
+ * them (src/hba/attention.py:351-352).  bf16: Bk == 64, d in {64, 128},
+ * S <= 128.  fp32: any S; d 64 / 128 with Bk 64 on the tuned kernel,
+ * otherwise any even d <= 256 and Bk <= 256 on the generic one.
  */
 int hba_attn_fwd(int dtype, const void *q, const int64_t q_strides[3],
                  const float *q_gain, const float *k_gain, float eps,

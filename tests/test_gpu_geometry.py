@@ -1,0 +1,158 @@
+"""Geometry the tuned kernels reach only partly, against the oracle:
+
+  sinks > 64    S = 100 / 128 (the fused path's limit, attention.py:452): the
+                tuned bf16 kernel stages two sink blocks, and a routed block 1
+                counts only its keys from S on; compared with the oracle's
+                dense_rows, the reference's union mask (attention.py:342-356),
+                which counts a sink key once even when its block is routed
+  generic path  geometry off the tuned kernels runs on the generic fp32
+                kernels, bf16 inputs widened (forward_stages -> _forward_
+                generic): the reference's block-16 test geometry with
+                hierarchical selection (tests/test_qknorm.py:28-35, attention.py:
+                690-693), beam > 16, k > 64, more than 16 query heads per KV
+                head.  Selection bit-exact against the oracle's fp32 selection
+                on the same (storage-rounded) inputs, outputs within 1e-5 of
+                its float64 rows before the output rounding, and within the
+                bf16 bar of the oracle's bf16 emulation.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle.hba_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+hba_amd = pytest.importorskip("hba_amd")
+from hba_amd import ops, synth  # noqa: E402
+
+
+@pytest.fixture(scope="module")
+def dev():
+    if not torch.cuda.is_available():
+        pytest.fail("GPU tests need a visible gfx950 device")
+    return torch.device("cuda:0")
+
+
+def f(t):
+    return t.detach().float().cpu().numpy()
+
+
+def inputs(dev, dt, n, Hq, Hkv, d, m=4, seed=0, sharp=True, needles=False, **cfgkw):
+    cfg = hba_amd.HBAConfig(n_heads=Hq, n_kv=Hkv, head_dim=d, slots=m, **cfgkw)
+    x = synth.layer_inputs(1, n, Hq, Hkv, d, m=m, dtype=dt, device=dev, seed=seed, sharp=sharp, needles=needles,
+                           block=cfg.block, window=cfg.window)
+    prm = synth.Params(x["q_gain"], x["k_gain"], x["probes"], x["proj"])
+    cos, sin = hba_amd.rope_tables(n, d, cfg.rope_theta, dev)
+    return cfg, x, prm, cos, sin
+
+
+def rows_of(n):
+    return np.unique(np.concatenate([np.arange(0, 8), np.linspace(0, n - 1, 80).astype(np.int64),
+                                     np.arange(n - 16, n)]))
+
+
+# ------------------------------------------------------------ sinks > 64 ----
+@pytest.mark.parametrize("dt,S,d", [("bf16", 100, 64), ("bf16", 128, 64), ("bf16", 100, 128), ("f32", 100, 64),
+                                    ("f32", 200, 64)])
+def test_sinks_beyond_one_block_union_mask(dev, dt, S, d):
+    """S sinks with S > 64: block 1 is a candidate, and where a query picked
+    it, its keys below S count once (as sinks).  The selection is steered so
+    that block 1 is picked: its keys lean toward the queries."""
+    tdt = torch.bfloat16 if dt == "bf16" else torch.float32
+    Hq, Hkv = (14, 2) if d == 64 else (28, 4)
+    n, W, k = 2048, 512, 8
+    cfg, x, prm, cos, sin = inputs(dev, tdt, n, Hq, Hkv, d, sinks=S, window=W, k_blocks=k)
+    # turn block 1's keys toward every KV group's mean query direction
+    kk = x["k"].float()
+    for g in range(Hkv):
+        u = x["q"][0, :, g * (Hq // Hkv):(g + 1) * (Hq // Hkv)].float().mean((0, 1))
+        u = u / u.norm()
+        kk[0, 64:128, g] = kk[0, 64:128, g].norm(dim=-1, keepdim=True) * u
+    x["k"] = kk.to(tdt)
+    r = hba_amd.forward_stages(x["q"], x["k"], x["v"], cos, sin, cfg, prm, prm)
+    torch.cuda.synchronize()
+    idx, cnt = r["idx"][0].cpu().numpy(), r["cnt"][0].cpu().numpy()
+    rows = rows_of(n)
+    picked1 = sum(int((idx[g, i, :cnt[g, i]] == 1).any()) for g in range(Hkv) for i in rows)
+    assert picked1 > len(rows) // 2, picked1          # the case under test occurs
+    P = O.prepare(f(x["q"])[0], f(x["k"])[0], f(x["v"])[0], f(cos), f(sin), cfg, f(x["probes"]), f(x["proj"]),
+                  f(x["q_gain"]), f(x["k_gain"]), 1e-6, dt, S0=f(r["S0"])[0])
+    sel = lambda g, i: idx[g, i, :cnt[g, i]]
+    ref = O.dense_rows(P.qc, P.qr, P.kc, P.kr, P.v, sel, r["scale"], S, W, 64, rows)
+    err = np.abs(f(r["out"])[0][rows] - ref).max()
+    assert err <= (2e-2 if dt == "bf16" else 1e-5), err
+    # the eval drop-in gives the same rows
+    out_e = hba_amd.hba_attention_eval(x["q"], x["k"], x["v"], cos, sin, cfg, prm, prm)
+    assert torch.equal(out_e, r["out"])
+
+
+# ----------------------------------------------------------- generic path ----
+GENERIC = [
+    # the reference's test geometry (tests/test_qknorm.py:28-35), flat and hierarchical
+    dict(n=512, Hq=4, Hkv=2, d=8, block=16, window=64, sinks=4, k_blocks=8, fanout=4, beam=2, hier=False),
+    dict(n=512, Hq=4, Hkv=2, d=8, block=16, window=64, sinks=4, k_blocks=8, fanout=4, beam=2, hier=True),
+    # hierarchical off the tuned geometry: block 32, head dim 96
+    dict(n=2048, Hq=6, Hkv=2, d=96, block=32, window=128, sinks=8, k_blocks=6, fanout=8, beam=3, hier=True),
+    # beam > 16 at the tuned block size
+    dict(n=8192, Hq=14, Hkv=2, d=64, block=64, window=1024, sinks=4, k_blocks=16, fanout=4, beam=24, hier=True),
+    # k > 64 (the select-all gate sets k = n / block, gates.py:211)
+    dict(n=8192, Hq=14, Hkv=2, d=64, block=64, window=1024, sinks=4, k_blocks=128, hier=False),
+    # more than 16 query heads per KV head
+    dict(n=2048, Hq=34, Hkv=2, d=64, block=64, window=512, sinks=4, k_blocks=8, hier=False),
+]
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f32"])
+@pytest.mark.parametrize("case", GENERIC, ids=lambda c: "-".join(f"{k}{v}" for k, v in c.items()))
+def test_generic_path_vs_oracle(dev, dt, case):
+    c = dict(case)
+    hier = c.pop("hier")
+    n, Hq, Hkv, d = c.pop("n"), c.pop("Hq"), c.pop("Hkv"), c.pop("d")
+    tdt = torch.bfloat16 if dt == "bf16" else torch.float32
+    cfg, x, prm, cos, sin = inputs(dev, tdt, n, Hq, Hkv, d, needles=n >= 4096, **c)
+    assert not hba_amd.attention._tuned(x["q"], x["k"], cfg, prm, hier) or (dt == "f32" and not hier)
+    with torch.no_grad():
+        r = hba_amd.forward_stages(x["q"], x["k"], x["v"], cos, sin, cfg, prm, prm, hier=hier)
+        out_e = hba_amd.hba_attention_eval(x["q"], x["k"], x["v"], cos, sin, cfg, prm, prm, None, hier=hier)
+    torch.cuda.synchronize()
+    assert r["out"].dtype == tdt and torch.equal(out_e, r["out"])
+    # the oracle in fp32 on the same storage-rounded inputs, on the kernel's summaries
+    P = O.prepare(f(x["q"])[0], f(x["k"])[0], f(x["v"])[0], f(cos), f(sin), cfg, f(x["probes"]), f(x["proj"]),
+                  f(x["q_gain"]), f(x["k_gain"]), 1e-6, "f32", S0=f(r["S0"])[0])
+    rows = rows_of(n)
+    oi, ov, oc = O.select(P, cfg, hier=hier, pos=rows, dtype="f32")
+    kk = oi.shape[-1]
+    gi = r["idx"][0].cpu().numpy()[:, rows, :kk]
+    gc = r["cnt"][0].cpu().numpy()[:, rows]
+    assert np.array_equal(gc, oc)
+    for g in range(Hkv):
+        for j in range(len(rows)):
+            assert np.array_equal(gi[g, j, :gc[g, j]], oi[g, j, :oc[g, j]]), (g, rows[j])
+    assert int(oc.max()) > 0
+    I, C = O._scatter_rows(oi, oc, rows, n)
+    ref = O.attn_rows(P.qc, P.qr, P.kc, P.kr, P.v, I, C, r["scale"], cfg.sinks, cfg.window, cfg.block, rows)
+    err = np.abs(f(r["out"])[0][rows] - ref)
+    if dt == "f32":
+        assert err.max() <= 1e-5, err.max()
+    else:   # one bf16 rounding of the output
+        assert (err <= 2 ** -8 * np.maximum(np.abs(ref), 1e-3) + 1e-6).all(), err.max()
+        # and the oracle's bf16 emulation, within the bf16 bar
+        Pb = O.prepare(f(x["q"])[0], f(x["k"])[0], f(x["v"])[0], f(cos), f(sin), cfg, f(x["probes"]),
+                       f(x["proj"]), f(x["q_gain"]), f(x["k_gain"]), 1e-6, "bf16", S0=f(r["S0"])[0])
+        refb = O.attn_rows(Pb.qc, Pb.qr, Pb.kc, Pb.kr, Pb.v, I, C, r["scale"], cfg.sinks, cfg.window, cfg.block,
+                           rows)
+        assert np.abs(f(r["out"])[0][rows] - refb).max() <= 2e-2
+
+
+def test_generic_path_refuses_gradients(dev):
+    """The backward runs on the tuned geometry only: off it, a gradient
+    request raises before any launch."""
+    cfg, x, prm, cos, sin = inputs(dev, torch.bfloat16, 512, 4, 2, 8, block=16, window=64, k_blocks=8)
+    q = x["q"].clone().requires_grad_(True)
+    with pytest.raises(NotImplementedError, match="backward"):
+        hba_amd.hba_attention_eval(q, x["k"], x["v"], cos, sin, cfg, prm, prm)
+    cfg2, x2, prm2, cos2, sin2 = inputs(dev, torch.bfloat16, 1024, 14, 2, 64, sinks=100, window=256, k_blocks=4)
+    q2 = x2["q"].clone().requires_grad_(True)
+    with pytest.raises(NotImplementedError, match="sinks"):
+        hba_amd.hba_attention_eval(q2, x2["k"], x2["v"], cos2, sin2, cfg2, prm2, prm2)

@@ -524,9 +524,10 @@ def test_invalid_arguments_raise(dev):
     with pytest.raises(AssertionError):
         hba_amd.hba_attention_eval(x["q"][:, :1000], x["k"][:, :1000], x["v"][:, :1000], cos, sin, cfg,
                                    prm, prm, None)
-    with pytest.raises(RuntimeError):
-        cfg2 = hba_amd.HBAConfig(n_heads=14, n_kv=2, window=256, sinks=65, k_blocks=4)
-        hba_amd.hba_attention_eval(x["q"], x["k"], x["v"], cos, sin, cfg2, prm, prm, None)
+    r = hba_amd.forward_stages(x["q"], x["k"], x["v"], cos, sin, cfg, prm, prm)
+    with pytest.raises(RuntimeError):                                      # bf16 kernels: at most 128 sinks
+        ops.attn_fwd(x["q"], prm.q.gain, prm.k.gain, 1e-6, r["kc"], r["kr"], r["vt"], cos, sin, r["idx"], r["cnt"],
+                     129, cfg.window, r["scale"])
     S0 = torch.zeros(1, 2, 16, 4, 64, dtype=torch.bfloat16, device=dev)
     with pytest.raises(RuntimeError):                                      # k > 64
         ops.score_select(x["q"], x["q_gain"], 1e-6, S0, 256, 65, 1 / 64)
@@ -553,6 +554,22 @@ def test_overlapped_schedule_equals_one_stream(dev):
                            r["cnt"], cfg.sinks, cfg.window, r["scale"])
         torch.cuda.synchronize()
         assert torch.equal(r["out"], ref)
+
+
+@pytest.mark.parametrize("qknorm,G,k", [(True, 7, 16), (False, 7, 16), (True, 4, 12), (True, 8, 16)])
+def test_attention_bf16_is_deterministic(dev, qknorm, G, k):
+    """The bf16 union attention gives the same bits on repeated calls (every
+    workgroup adds its partials in a fixed order), with the fixed softmax
+    shift and with the running maximum (no QKNorm)."""
+    cfg, x, prm, cos, sin = make(dev, "bf16", n=4096, W=1024, k=k, Hq=2 * G, Hkv=2, needles=True, qknorm=qknorm,
+                                 sharp=qknorm)
+    r = hba_amd.forward_stages(x["q"], x["k"], x["v"], cos, sin, cfg, prm, prm, overlap=False)
+    qg, kg = (prm.q.gain, prm.k.gain) if qknorm else (None, None)
+    outs = [ops.attn_fwd(x["q"], qg, kg, 1e-6, r["kc"], r["kr"], r["vt"], cos, sin, r["idx"], r["cnt"], cfg.sinks,
+                         cfg.window, r["scale"]) for _ in range(3)]
+    torch.cuda.synchronize()
+    assert all(torch.equal(o, r["out"]) for o in outs)
+    assert torch.isfinite(outs[0].float()).all()
 
 
 @pytest.mark.parametrize("dt,qknorm,n", [("bf16", True, 2048), ("bf16", False, 1024), ("f32", True, 512)])
