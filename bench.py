@@ -266,9 +266,39 @@ def bench_decode(dev, iters=200, batch=None):
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) * 1000.0 / (reps * nsteps), ok and bool(torch.equal(gout, eager))
 
-    us, ok = timed_graph(DECODE_STEPS_PER_GRAPH)
+    def timed_cold(reps=40):
+        # one step per graph replay, each after 512 MB have streamed through
+        # the GPU (more than its 256 MB Infinity Cache and the L2s) and with a
+        # fresh query: the step reads its pages, summaries and page table
+        # from HBM.  The streaming runs outside the timed events; the step is
+        # timed alone (graph launch included, as in the one-step warm figure).
+        qbuf = torch.empty_like(q)
+        graph = torch.cuda.CUDAGraph()
+        qbuf.copy_(q)
+        with torch.cuda.graph(graph):
+            hba_amd.hba_decode_step(qbuf, cache, cfg, prm, cos, sin, scales=scales)
+        gq = torch.Generator(device=dev).manual_seed(5)
+        fresh = [torch.randn(q.shape, generator=gq, device=dev).to(q.dtype) for _ in range(8)]
+        flush = torch.zeros(128 << 20, dtype=torch.float32, device=dev)   # 512 MB
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        times = []
+        for r in range(reps + 3):
+            flush.add_(1.0)
+            qbuf.copy_(fresh[r % len(fresh)])
+            e0.record()
+            graph.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            if r >= 3:
+                times.append(e0.elapsed_time(e1) * 1000.0)
+        del flush
+        return sorted(times)[len(times) // 2]
+
+    us_warm, ok = timed_graph(DECODE_STEPS_PER_GRAPH)
     us1, ok1 = timed_graph(1)
     ok = ok and ok1
+    us = timed_cold()
     nbytes = decode_bytes(lens, Hkv, d, m, S, W, k, Hq)
     gbs = nbytes / (us * 1e-6) / 1e9
     pair = Bd * Hkv >= DECODE_PAIR_MIN and os.environ.get("HBA_DECODE_KERNEL") != "fused"
@@ -280,8 +310,11 @@ def bench_decode(dev, iters=200, batch=None):
            "replayed from a HIP graph")
     return dict(us_per_step=round(us, 3), algorithmic_bytes=nbytes, achieved_GBs=round(gbs, 1),
                 hbm_frac=round(gbs / PEAK_HBM_GBS, 4), graph_replay_matches_eager=ok,
-                timing=f"{DECODE_STEPS_PER_GRAPH} steps per HIP graph replay, per-step time",
-                us_per_step_one_step_graph=round(us1, 3),
+                timing="cold: median over 40 steps of one HIP-graph replay each, after 512 MB streamed "
+                       "through the GPU (caches flushed) and with a fresh query; graph launch included",
+                us_per_step_warm_10_step_graph=round(us_warm, 3),
+                warm_GBs=round(nbytes / (us_warm * 1e-6) / 1e9, 1),
+                us_per_step_warm_one_step_graph=round(us1, 3),
                 batch=Bd, context="L ~ U[16384, 32768], paged bf16, shuffled page table", kernels=kern)
 
 
