@@ -5,8 +5,10 @@
 // (hba_attention_dense src/hba/attention.py:342-356, hba_attention_eval
 //  :676-711, hba_attention_fused's LSE merge :592-603).
 //
-// bf16: hba_attn_bf16.hip (MFMA: a window kernel, then a sinks + routed
-//   kernel that merges into the window's rows by LSE).
+// bf16: hba_attn_bf16.hip (MFMA: one launch streams each query tile's
+//   window tiles, sink blocks and routed blocks in one softmax state; the
+//   split entry points below run the window and the rest as two launches
+//   merged by LSE).
 // f32: attn_f32_kernel, one thread per (query, head), sequential fp32 dot
 //   products and a two-pass softmax; the fp32 parity path.
 #include "hba_common.h"
@@ -127,10 +129,19 @@ int launch_attn_f32(const void *q, const int64_t *qs, const float *qgain, float 
 }
 }  // namespace
 
+extern "C" int hba_attn_fwd_workspace_bytes(int dtype, int64_t B, int64_t n, int64_t Hq, int64_t d,
+                                            size_t *bytes) {
+    if (!bytes || B <= 0 || n <= 0 || Hq <= 0 || d <= 0) return HBA_ERR_INVALID_ARG;
+    if (dtype != HBA_DTYPE_F32 && dtype != HBA_DTYPE_BF16) return HBA_ERR_UNSUPPORTED;
+    // bf16: the RoPE query operand of the window tiles, [B, n, Hq, d] bf16
+    *bytes = (dtype == HBA_DTYPE_BF16) ? (((size_t)B * n * Hq * d * 2 + 255) & ~(size_t)255) : 0;
+    return HBA_OK;
+}
+
 extern "C" int hba_attn_workspace_size(int dtype, int64_t B, int64_t n, int64_t Hq, size_t *bytes) {
     if (!bytes || B <= 0 || n <= 0 || Hq <= 0) return HBA_ERR_INVALID_ARG;
     if (dtype != HBA_DTYPE_F32 && dtype != HBA_DTYPE_BF16) return HBA_ERR_UNSUPPORTED;
-    // bf16: the window's LSE per (batch, head, query), fp32
+    // bf16 split launches: the window's LSE per (batch, head, query), fp32
     *bytes = (dtype == HBA_DTYPE_BF16) ? (size_t)B * Hq * n * sizeof(float) : 0;
     return HBA_OK;
 }
@@ -172,14 +183,14 @@ extern "C" int hba_attn_fwd(int dtype, const void *q, const int64_t q_strides[3]
     hipStream_t s = (hipStream_t)stream;
     if (dtype == HBA_DTYPE_BF16) {
         size_t need = 0;
-        hba_attn_workspace_size(dtype, B, n, Hq, &need);
+        hba_attn_fwd_workspace_bytes(dtype, B, n, Hq, d, &need);
         if (!workspace || ws_bytes < need || !abi::aligned16(workspace)) return HBA_ERR_INVALID_ARG;
-        float *lse = (float *)workspace;
         st = (d == 64) ? launch_attn_bf16<64>(q, q_strides, q_gain, k_gain, eps, kc, kr, vt, cos_tab, sin_tab,
-                                              idx, cnt, B, n, Hq, Hkv, S, W, k, scale, out, out_strides, lse, s)
+                                              idx, cnt, B, n, Hq, Hkv, S, W, k, scale, out, out_strides, workspace,
+                                              s)
                        : launch_attn_bf16<128>(q, q_strides, q_gain, k_gain, eps, kc, kr, vt, cos_tab, sin_tab,
-                                               idx, cnt, B, n, Hq, Hkv, S, W, k, scale, out, out_strides, lse,
-                                               s);
+                                               idx, cnt, B, n, Hq, Hkv, S, W, k, scale, out, out_strides,
+                                               workspace, s);
     } else
         st = (d == 64) ? launch_attn_f32<64>(q, q_strides, q_gain, eps, kc, kr, vt, cos_tab, sin_tab,
                                              idx, cnt, B, n, Hq, Hkv, S, W, k, scale, out, out_strides, s)

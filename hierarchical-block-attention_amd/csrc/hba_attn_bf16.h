@@ -1,5 +1,7 @@
-// Launcher of the bf16 union attention (window kernel, then sinks + routed
-// kernel merging into the window's rows).  lse: fp32 [B, Hq, n] scratch.
+// Launchers of the bf16 union attention: one launch over the whole union
+// (launch_attn_bf16; qrw: bf16 [B, n, Hq, D] scratch for the RoPE query
+// operand), or the window and the sinks + routed blocks as two launches
+// merged by the window's LSE (lse: fp32 [B, Hq, n] scratch).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -11,7 +13,7 @@ template <int D>
 int launch_attn_bf16(const void *q, const int64_t *qs, const float *qgain, const float *kgain, float eps,
                      const void *kc, const void *kr, const void *vt, const float *cosT, const float *sinT,
                      const int32_t *idx, const int32_t *cnt, int64_t B, int64_t n, int64_t Hq, int64_t Hkv,
-                     int64_t S, int64_t W, int64_t k, float scale, void *out, const int64_t *os, float *lse,
+                     int64_t S, int64_t W, int64_t k, float scale, void *out, const int64_t *os, void *qrw,
                      hipStream_t s);
 
 // The two launches separately (window; then sinks + routed, ordered after it).

@@ -95,22 +95,22 @@ __device__ __forceinline__ float colsum(bf16x8 p0, bf16x8 p1) {
 }
 
 // Query operand of one lane's column (query i, head h) for S^T = K . Q^T:
-// d = 32*ks + 8*lg + 0..7.  QKNorm in fp32 rounded to bf16 (attention.py:
-// 88-94; the sum of squares is reduced across the column's four lanes); with
-// rope, apply_rope's rotation and bf16 roundings (:40-44) at position i.  The
-// rotation partner d +- D/2 sits in the same lane at ks +- NKS/2.  Invalid
-// columns read row 0 and are zeroed (no divergence around the shuffles).
-// qscale multiplies the operand before its bf16 rounding: the fixed-shift
-// softmax passes scale*log2(e), so that S^T comes out in log2 units.
+// d = 32*ks + 8*lg + 0..7.  qrow: the row's elements this lane holds,
+// QKNorm'd in fp32 and rounded to bf16 (attention.py:88-94; the sum of
+// squares is reduced across the column's four lanes).  qpack: the NoPE
+// operand; qpack_rope: apply_rope's rotation and bf16 roundings (:40-44) at
+// position i (the rotation partner d +- D/2 sits in the same lane at ks +-
+// NKS/2).  Invalid columns read row 0 and are zeroed (no divergence around
+// the shuffles).  qscale multiplies the operand before its bf16 rounding:
+// the fixed-shift softmax passes scale*log2(e), so that S^T comes out in
+// log2 units.
 template <int D>
-__device__ __forceinline__ void qoperand(const bf16_t *q, int64_t qsb, int64_t qsn, int64_t qsh,
-                                         const float *qgain, float eps, const float *cosT,
-                                         const float *sinT, int64_t b, int64_t i, int h, bool valid,
-                                         bool rope, int lg, float qscale, bf16x8 (&qop)[D / 32]) {
+__device__ __forceinline__ void qrow(const bf16_t *q, int64_t qsb, int64_t qsn, int64_t qsh, const float *qgain,
+                                     float eps, int64_t b, int64_t i, int h, bool valid, int lg,
+                                     float (&x)[D / 32][8]) {
     constexpr int NKS = D / 32;
     const int64_t ii = valid ? i : 0;
     const bf16_t *row = q + b * qsb + ii * qsn + (int64_t)h * qsh;
-    float x[NKS][8];
     float ss = 0.0f;
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks) {
@@ -133,25 +133,76 @@ __device__ __forceinline__ void qoperand(const bf16_t *q, int64_t qsb, int64_t q
 #pragma unroll
         for (int ks = 0; ks < NKS; ++ks)
 #pragma unroll
-            for (int e = 0; e < 8; ++e) x[ks][e] = rnd_bf16((x[ks][e] / r) * gn);
+            for (int e = 0; e < 8; e += 2) {
+                x[ks][e] = (x[ks][e] / r) * gn;
+                x[ks][e + 1] = (x[ks][e + 1] / r) * gn;
+                rnd_bf16_pair(x[ks][e], x[ks][e + 1]);   // v_cvt_pk_bf16_f32: two roundings per instruction
+            }
     }
+}
+
+template <int D>
+__device__ __forceinline__ void qpack(const float (&x)[D / 32][8], bool valid, float qscale,
+                                      bf16x8 (&qop)[D / 32]) {
 #pragma unroll
-    for (int ks = 0; ks < NKS; ++ks) {
+    for (int ks = 0; ks < D / 32; ++ks) {
         float y[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            float v = x[ks][e];
-            if (rope) {
-                const int d = 32 * ks + 8 * lg + e;
-                const float rot = (ks < NKS / 2) ? -x[ks + NKS / 2][e] : x[ks - NKS / 2][e];
-                const float t1 = rnd_bf16(v * rnd_bf16(cosT[ii * D + d]));
-                const float t2 = rnd_bf16(rot * rnd_bf16(sinT[ii * D + d]));
-                v = rnd_bf16(t1 + t2);
-            }
-            y[e] = valid ? v * qscale : 0.0f;
+        for (int e = 0; e < 8; ++e) y[e] = valid ? x[ks][e] * qscale : 0.0f;
+        qop[ks] = pack8(y);
+    }
+}
+
+template <int D>
+__device__ __forceinline__ void qpack_rope(const float (&x)[D / 32][8], const float *cosT, const float *sinT,
+                                           int64_t i, bool valid, int lg, float qscale, bf16x8 (&qop)[D / 32]) {
+    constexpr int NKS = D / 32;
+    const int64_t ii = valid ? i : 0;
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+        // the lane's 8 consecutive table entries, two 16-byte loads per table
+        float ct[8], st[8];
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+            const float4 c = *reinterpret_cast<const float4 *>(cosT + ii * D + 32 * ks + 8 * lg + 4 * hf);
+            const float4 sn = *reinterpret_cast<const float4 *>(sinT + ii * D + 32 * ks + 8 * lg + 4 * hf);
+            ct[4 * hf] = c.x, ct[4 * hf + 1] = c.y, ct[4 * hf + 2] = c.z, ct[4 * hf + 3] = c.w;
+            st[4 * hf] = sn.x, st[4 * hf + 1] = sn.y, st[4 * hf + 2] = sn.z, st[4 * hf + 3] = sn.w;
+        }
+        // the roundings in pairs (v_cvt_pk_bf16_f32)
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+            rnd_bf16_pair(ct[e], ct[e + 1]);
+            rnd_bf16_pair(st[e], st[e + 1]);
+        }
+        float y[8];
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+            float t1a = x[ks][e] * ct[e], t1b = x[ks][e + 1] * ct[e + 1];
+            float t2a = ((ks < NKS / 2) ? -x[ks + NKS / 2][e] : x[ks - NKS / 2][e]) * st[e];
+            float t2b = ((ks < NKS / 2) ? -x[ks + NKS / 2][e + 1] : x[ks - NKS / 2][e + 1]) * st[e + 1];
+            rnd_bf16_pair(t1a, t1b);
+            rnd_bf16_pair(t2a, t2b);
+            float va = t1a + t2a, vb = t1b + t2b;
+            rnd_bf16_pair(va, vb);
+            y[e] = valid ? va * qscale : 0.0f;
+            y[e + 1] = valid ? vb * qscale : 0.0f;
         }
         qop[ks] = pack8(y);
     }
+}
+
+template <int D>
+__device__ __forceinline__ void qoperand(const bf16_t *q, int64_t qsb, int64_t qsn, int64_t qsh,
+                                         const float *qgain, float eps, const float *cosT,
+                                         const float *sinT, int64_t b, int64_t i, int h, bool valid,
+                                         bool rope, int lg, float qscale, bf16x8 (&qop)[D / 32]) {
+    float x[D / 32][8];
+    qrow<D>(q, qsb, qsn, qsh, qgain, eps, b, i, h, valid, lg, x);
+    if (rope)
+        qpack_rope<D>(x, cosT, sinT, i, valid, lg, qscale, qop);
+    else
+        qpack<D>(x, valid, qscale, qop);
 }
 
 // Workgroup -> (batch*KV head combo, query tile).  Workgroup i runs on XCD
@@ -640,13 +691,103 @@ __device__ __forceinline__ void rt_update(const bf16_t *Ks, const bf16_t *Vs, co
     }
 }
 
-template <int D, int PTW, bool FIXED, bool S2>
+// One staged window tile (RoPE keys) against one 16-row tile of the routed
+// layout: keys jlo..jhi (from the tile's first key) of the column's window
+// are valid, every key when full (wave-uniform).  qop is the RoPE operand.
+template <int D, bool FIXED>
+__device__ __forceinline__ void win_update(const bf16_t *Ks, const bf16_t *Vs, const bf16x8 (&qop)[D / 32],
+                                           f32x4 (&O)[D / 16], float &mrun, float &lsum, bool full, int jlo,
+                                           int jhi, float sl2, float bl2, int l16, int lg) {
+    constexpr int NKS = D / 32, NDT = D / 16;
+    // the row tiles of a wave read the same fragments: keep the compiler from
+    // holding one tile's fragments in registers for the next (the routed
+    // layout has no registers to spare for them)
+    asm volatile("" ::: "memory");
+    const float c0 = FIXED ? -bl2 : 0.0f;   // fixed shift: S^T starts at -shift, exp2 takes it directly
+    f32x4 Sa[4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+        Sa[mt] = f32x4{c0, c0, c0, c0};
+        const int r = permk(mt, l16);
+        const bf16_t *kp = Ks + r * D;
+        const int sw = swzK(r);
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) Sa[mt] = mma(ldb8(kp + 8 * ((4 * ks + lg) ^ sw)), qop[ks], Sa[mt]);
+    }
+    float p[2][8];
+    if constexpr (FIXED) {
+        if (full) {
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) p[mt >> 1][(mt & 1) * 4 + e] = ex2(Sa[mt][e]);
+        } else {
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int j = 32 * (mt >> 1) + 8 * lg + 4 * (mt & 1) + e;
+                    p[mt >> 1][(mt & 1) * 4 + e] = ex2(((j >= jlo) & (j <= jhi)) ? Sa[mt][e] : -INFINITY);
+                }
+        }
+    } else {
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int j = 32 * (mt >> 1) + 8 * lg + 4 * (mt & 1) + e;
+                tmax = fmaxf(tmax, (full | ((j >= jlo) & (j <= jhi))) ? Sa[mt][e] : -INFINITY);
+            }
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        const float mnew = fmaxf(mrun, tmax * sl2);
+        const float shift = (mnew == -INFINITY) ? 0.0f : mnew;
+        const float alpha = ex2(mrun - shift);
+        mrun = mnew;
+        lsum *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) O[dt] *= alpha;
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int j = 32 * (mt >> 1) + 8 * lg + 4 * (mt & 1) + e;
+                const float a = fmaf(Sa[mt][e], sl2, -shift);
+                p[mt >> 1][(mt & 1) * 4 + e] = ex2((full | ((j >= jlo) & (j <= jhi))) ? a : -INFINITY);
+            }
+    }
+    const bf16x8 pb0 = pack8(p[0]), pb1 = pack8(p[1]);
+    lsum += colsum(pb0, pb1);
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+        const int r = 16 * dt + l16;
+        const bf16_t *vp = Vs + r * 64;
+        const int sw = swzV(r);
+        O[dt] = mma(ldb8(vp + 8 * (lg ^ sw)), pb0, O[dt]);
+        O[dt] = mma(ldb8(vp + 8 * ((lg + 4) ^ sw)), pb1, O[dt]);
+    }
+}
+
+// P bits of a bit row starting at bit r0 (r0 > -32; bits before the row's
+// start or past its nw words read as 0).
+template <int P>
+__device__ __forceinline__ uint32_t bits_at(const uint32_t *row, int r0, int nw) {
+    const int a = r0 >> 5, sh = r0 & 31;   // arithmetic shift: word -1 for r0 < 0
+    uint32_t v = (a >= 0 && a < nw) ? row[a] >> sh : 0u;
+    if (sh != 0 && a + 1 < nw) v |= row[a + 1] << (32 - sh);
+    return v & ((1u << P) - 1u);
+}
+
+template <int D, int PTW, bool FIXED, bool S2, bool WIN>
 __device__ __forceinline__ void routed_body(
     const bf16_t *__restrict__ q, int64_t qsb, int64_t qsn, int64_t qsh, const float *__restrict__ qgain,
     float eps, const bf16_t *__restrict__ kc, const bf16_t *__restrict__ vt,
     const int32_t *__restrict__ idx, const int32_t *__restrict__ cnt, int64_t n, int Hq, int Hkv, int S,
     int kk, float sl2, float bl2, int combo, int tile, bf16_t *__restrict__ out,
-    int64_t osb, int64_t osn, int64_t osh, const float *__restrict__ lse, char *smem, int &nlist) {
+    int64_t osb, int64_t osn, int64_t osh, const float *__restrict__ lse, char *smem, int &nlist,
+    const bf16_t *__restrict__ kr, const float *__restrict__ cosT, const float *__restrict__ sinT, int W,
+    bf16_t *__restrict__ qrw) {
     using C = RtCfg<D>;
     const int G = Hq / Hkv;
     const int QPT = 16 / G;
@@ -661,6 +802,18 @@ __device__ __forceinline__ void routed_body(
     const int nbw = (int)((nb + 31) / 32);
     const bf16_t *KC = kc + bh * n * D;
     const bf16_t *VT = vt + bh * D * n;
+    // WIN: the workgroup first streams the window tiles of its queries (kr
+    // rows, RoPE operand) through the ring, then the sinks and routed blocks.
+    const int64_t dkr = WIN ? (kr - kc) : 0;   // kc row -> the same kr row, in elements
+    int wt0 = 0, nwin = 0;
+    if constexpr (WIN) {
+        const int64_t ilast = ((i0 + QT < n) ? i0 + QT : n) - 1;
+        const int64_t kfirst = ((int64_t)S > i0 - W + 1) ? (int64_t)S : i0 - W + 1;
+        if (kfirst <= ilast) {
+            wt0 = (int)(kfirst / 64);
+            nwin = (int)(ilast / 64) - wt0 + 1;
+        }
+    }
 
     // LDS: ring | sel [QT][kk] | bitmap [nbw] | pre [nbw] | list [nb] |
     //      qbits [QT][nbw] | wbits [WAVES*PTW][nbw]
@@ -693,16 +846,19 @@ __device__ __forceinline__ void routed_body(
             dstr[pp] = 64;
         }
     }
-    auto fill = [&](int blk, int slot) {
+    auto fill = [&](int blk, int slot, bool rope) {
 #pragma unroll
-        for (int pp = 0; pp < C::DPW; ++pp)
-            dma16(dsrc[pp] + (int64_t)blk * dstr[pp],
+        for (int pp = 0; pp < C::DPW; ++pp) {
+            const bool kpart = w + C::WAVES * pp < C::KPARTS;   // wave-uniform
+            dma16(dsrc[pp] + (int64_t)blk * dstr[pp] + ((WIN && rope && kpart) ? dkr : 0),
                   ring_lds + (uint32_t)(slot * C::SLOT * 2) + (uint32_t)(w + C::WAVES * pp) * 1024u);
+        }
     };
+    constexpr int NPRO = (C::NS / C::PH - 1) * C::PH;   // entries staged ahead of the first phase
     // sinks: block 0 into the last ring slot and (S > 64) block 1 into the
     // one before (both free until the first refill), landing during the set-up
-    if (S > 0) fill(0, C::NS - 1);
-    if (S2) fill(1, C::NS - 2);
+    if (S > 0) fill(0, C::NS - 1, false);
+    if (S2) fill(1, C::NS - 2, false);
 
     // ----------------------------------------------------- per-row state --
     // (first, so that the query loads overlap the selection set-up)
@@ -722,8 +878,25 @@ __device__ __forceinline__ void routed_body(
         lsum[t] = 0.0f;
 #pragma unroll
         for (int dt = 0; dt < C::NDT; ++dt) O[t][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-        qoperand<D>(q, qsb, qsn, qsh, qgain, eps, nullptr, nullptr, b, icol[t], g * G + hh, cok[t], false, lg,
-                    FIXED ? sl2 : 1.0f, qop[t]);
+        if (WIN && nwin > 0) {
+            // the RoPE operand of the window tiles, parked in the workspace
+            // ([B, n, Hq, D], the row of this column) until the routed blocks
+            // are done; its loads overlap the selection set-up
+            float x[C::NKS][8];
+            qrow<D>(q, qsb, qsn, qsh, qgain, eps, b, icol[t], g * G + hh, cok[t], lg, x);
+            qpack<D>(x, cok[t], FIXED ? sl2 : 1.0f, qop[t]);
+            bf16x8 qr[C::NKS];
+            qpack_rope<D>(x, cosT, sinT, icol[t], cok[t], lg, FIXED ? sl2 : 1.0f, qr);
+            if (cok[t]) {
+                bf16_t *dst = qrw + (((int64_t)b * n + icol[t]) * Hq + g * G + hh) * D + 8 * lg;
+#pragma unroll
+                for (int ks = 0; ks < C::NKS; ++ks)
+                    *reinterpret_cast<u32x4 *>(dst + 32 * ks) = __builtin_bit_cast(u32x4, qr[ks]);
+            }
+        } else {
+            qoperand<D>(q, qsb, qsn, qsh, qgain, eps, nullptr, nullptr, b, icol[t], g * G + hh, cok[t], false, lg,
+                        FIXED ? sl2 : 1.0f, qop[t]);
+        }
     }
 
     // ------------------------------------- selection lists and their union
@@ -785,64 +958,130 @@ __device__ __forceinline__ void routed_body(
     // evens the waves' work out before they meet again.
     constexpr int P = C::PH, NPH = C::NS / C::PH;
     static_assert(32 % P == 0, "a phase's entries lie in one bitmap word");
-    const int npro = min(ne, (NPH - 1) * P);
-    for (int e = 0; e < npro; ++e) fill(list[e], e);
-    if (S > 0) {
-        wait_vm_n(npro * C::DPW);
-        __syncthreads();   // every share of the sink blocks landed
-        for (int sb = 0; sb < (S2 ? 2 : 1); ++sb) {
-            const bf16_t *Ks = ring + (C::NS - 1 - sb) * C::SLOT;
-            const int Sb = min(S - 64 * sb, 64);            // sink keys of this block
-            const int nmt = (Sb <= 4) ? 1 : (Sb <= 32 ? 2 : 4);   // M-tiles holding keys 0..Sb-1
+    static_assert(NPRO == (NPH - 1) * P, "prologue depth");
+    {
+        const int npro = min(ne, NPRO);
+        for (int e = 0; e < npro; ++e) fill(list[e], e, false);
+        if (S > 0) {
+            wait_vm_n(npro * C::DPW);
+            __syncthreads();   // every share of the sink blocks landed
+            for (int sb = 0; sb < (S2 ? 2 : 1); ++sb) {
+                const bf16_t *Ks = ring + (C::NS - 1 - sb) * C::SLOT;
+                const int Sb = min(S - 64 * sb, 64);            // sink keys of this block
+                const int nmt = (Sb <= 4) ? 1 : (Sb <= 32 ? 2 : 4);   // M-tiles holding keys 0..Sb-1
 #pragma unroll
-            for (int tt = 0; tt < PTW; ++tt) {
-                if (i0 + (int64_t)(w * PTW + tt) * QPT >= n) break;
-                rt_update<D, FIXED>(Ks, Ks + 64 * D, qop[tt], O[tt], mrun[tt], lsum[tt], RM_SINK, icol[tt] - 64 * sb,
-                                    cok[tt], Sb, nmt, FIXED ? 1.0f : sl2, bl2, l16, lg);
+                for (int tt = 0; tt < PTW; ++tt) {
+                    if (i0 + (int64_t)(w * PTW + tt) * QPT >= n) break;
+                    rt_update<D, FIXED>(Ks, Ks + 64 * D, qop[tt], O[tt], mrun[tt], lsum[tt], RM_SINK, icol[tt] - 64 * sb,
+                                        cok[tt], Sb, nmt, FIXED ? 1.0f : sl2, bl2, l16, lg);
+                }
             }
         }
-    }
-    // with S > 64 the keys 64..S-1 are sinks: routed block 1 (union entry 0
-    // if picked) counts only its keys from S on
-    const bool b1 = S2 && ne > 0 && list[0] == 1;
-    uint32_t qw[PTW], ww[PTW];   // this lane's query's / this row tile's bits of the current word
-    for (int e0 = 0; e0 < ne; e0 += P) {
-        // this wave's shares of entries e0..e0+P-1 have landed once at most
-        // the shares of the entries issued after them are in flight
-        const int issued = min(ne, e0 + (NPH - 1) * P);
-        wait_vm_n(max(0, issued - (e0 + P)) * C::DPW);
-        __syncthreads();   // every share of this phase landed; the previous phase (and the sinks) consumed
-        const int nf = min(ne, e0 + NPH * P);
-        int nxt[P];   // the refill's block ids, read before the first DMA is issued
+        // with S > 64 the keys 64..S-1 are sinks: routed block 1 (union entry 0
+        // if picked) counts only its keys from S on
+        const bool b1 = S2 && ne > 0 && list[0] == 1;
+        uint32_t qw[PTW], ww[PTW];   // this lane's query's / this row tile's bits of the current word
+        for (int e0 = 0; e0 < ne; e0 += P) {
+            // this wave's shares of entries e0..e0+P-1 have landed once at most
+            // the shares of the entries issued after them are in flight
+            const int issued = min(ne, e0 + (NPH - 1) * P);
+            wait_vm_n(max(0, issued - (e0 + P)) * C::DPW);
+            __syncthreads();   // every share of this phase landed; the previous phase (and the sinks) consumed
+            const int nf = min(ne, e0 + NPH * P);
+            int nxt[P];   // the refill's block ids, read before the first DMA is issued
 #pragma unroll
-        for (int j = 0; j < P; ++j) nxt[j] = (issued + j < nf) ? list[issued + j] : 0;
+            for (int j = 0; j < P; ++j) nxt[j] = (issued + j < nf) ? list[issued + j] : 0;
 #pragma unroll
-        for (int j = 0; j < P; ++j)
-            if (issued + j < nf) fill(nxt[j], (issued + j) % C::NS);
-        const int sh = e0 & 31;
-        if (sh == 0) {
+            for (int j = 0; j < P; ++j)
+                if (issued + j < nf) fill(nxt[j], (issued + j) % C::NS, false);
+            const int sh = e0 & 31;
+            if (sh == 0) {
+#pragma unroll
+                for (int tt = 0; tt < PTW; ++tt) {
+                    const int rt = w * PTW + tt;
+                    qw[tt] = cok[tt] ? qbits[(rt * QPT + qs) * nbw + (e0 >> 5)] : 0u;
+                    ww[tt] = __builtin_amdgcn_readfirstlane(wbits[rt * nbw + (e0 >> 5)]);
+                }
+            }
 #pragma unroll
             for (int tt = 0; tt < PTW; ++tt) {
-                const int rt = w * PTW + tt;
-                qw[tt] = cok[tt] ? qbits[(rt * QPT + qs) * nbw + (e0 >> 5)] : 0u;
-                ww[tt] = __builtin_amdgcn_readfirstlane(wbits[rt * nbw + (e0 >> 5)]);
-            }
-        }
-#pragma unroll
-        for (int tt = 0; tt < PTW; ++tt) {
-            uint32_t hits = (ww[tt] >> sh) & ((1u << P) - 1u);   // this phase's entries the row tile needs
-            while (hits) {
-                const int j = __builtin_ctz(hits);
-                hits &= hits - 1u;
-                const int e = e0 + j;
-                const bf16_t *Ks = ring + (e % C::NS) * C::SLOT;
-                const bool hit = (qw[tt] >> (sh + j)) & 1u;
-                rt_update<D, FIXED>(Ks, Ks + 64 * D, qop[tt], O[tt], mrun[tt], lsum[tt], RM_COL, icol[tt], hit, S,
-                                    4, FIXED ? 1.0f : sl2, bl2, l16, lg, (S2 && b1 && e == 0) ? S - 64 : 0);
+                uint32_t hits = (ww[tt] >> sh) & ((1u << P) - 1u);   // this phase's entries the row tile needs
+                while (hits) {
+                    const int j = __builtin_ctz(hits);
+                    hits &= hits - 1u;
+                    const int e = e0 + j;
+                    const bf16_t *Ks = ring + (e % C::NS) * C::SLOT;
+                    const bool hit = (qw[tt] >> (sh + j)) & 1u;
+                    rt_update<D, FIXED>(Ks, Ks + 64 * D, qop[tt], O[tt], mrun[tt], lsum[tt], RM_COL, icol[tt], hit, S,
+                                        4, FIXED ? 1.0f : sl2, bl2, l16, lg, (S2 && b1 && e == 0) ? S - 64 : 0);
+                }
             }
         }
     }
 
+    if constexpr (WIN) {
+        // ---- then the window tiles (kr rows) with the RoPE operand, every
+        // row tile whose columns have keys in them
+        if (nwin > 0) {
+            __syncthreads();   // every wave is done with the ring
+            // the RoPE operand back from the workspace (this lane's own rows)
+#pragma unroll
+            for (int t = 0; t < PTW; ++t) {
+                const bf16_t *src = qrw + (((int64_t)b * n + (cok[t] ? icol[t] : 0)) * Hq + g * G + hh) * D + 8 * lg;
+#pragma unroll
+                for (int ks = 0; ks < C::NKS; ++ks) {
+                    const bf16x8 v = ldb8(src + 32 * ks);
+                    qop[t][ks] = cok[t] ? v : bf16x8{};
+                }
+            }
+            for (int e = 0; e < nwin && e < NPRO; ++e) fill(wt0 + e, e, true);
+        }
+        for (int e0 = 0; e0 < nwin; e0 += P) {
+            const int issued = min(nwin, e0 + (NPH - 1) * P);
+            wait_vm_n(max(0, issued - (e0 + P)) * C::DPW);
+            __syncthreads();   // every share of this phase landed; the previous phase consumed
+            const int nf = min(nwin, e0 + NPH * P);
+            for (int e = issued; e < nf; ++e) fill(wt0 + e, e % C::NS, true);
+            const int e1 = min(nwin, e0 + P);
+#pragma nounroll
+            for (int e = e0; e < e1; ++e) {
+                const bf16_t *Ks = ring + (e % C::NS) * C::SLOT;
+                const int64_t kb = (int64_t)(wt0 + e) * 64;
+#pragma unroll
+                for (int tt = 0; tt < PTW; ++tt) {
+                    const int64_t qa = i0 + (int64_t)(w * PTW + tt) * QPT;
+                    if (qa >= n) break;
+                    const int64_t qb = (qa + QPT - 1 < n) ? qa + QPT - 1 : n - 1;
+                    const int64_t loa = ((int64_t)S > qa - W + 1) ? (int64_t)S : qa - W + 1;
+                    const int64_t lob = ((int64_t)S > qb - W + 1) ? (int64_t)S : qb - W + 1;
+                    if (kb > qb || kb + 63 < loa) continue;   // no column has a window key here
+                    const bool full = kb >= lob && kb + 63 <= qa;
+                    const int64_t lo = ((int64_t)S > icol[tt] - W + 1) ? (int64_t)S : icol[tt] - W + 1;
+                    const int64_t jlo = lo - kb, jhi = icol[tt] - kb;
+                    win_update<D, FIXED>(Ks, Ks + 64 * D, qop[tt], O[tt], mrun[tt], lsum[tt], full,
+                                         (int)(jlo < 0 ? 0 : (jlo > 64 ? 64 : jlo)),
+                                         (int)(jhi < -1 ? -1 : (jhi > 63 ? 63 : jhi)), FIXED ? 1.0f : sl2, bl2,
+                                         l16, lg);
+                }
+            }
+        }
+        // ------------------------------------------- normalise and store
+#pragma unroll
+        for (int t = 0; t < PTW; ++t) {
+            const float l = lsum[t];   // the column's full sum in every lane
+            if (!cok[t]) continue;
+            const float inv = (l > 0.0f) ? 1.0f / l : 0.0f;
+            bf16_t *orow = out + (int64_t)b * osb + icol[t] * osn + (int64_t)(g * G + hh) * osh;
+#pragma unroll
+            for (int dt = 0; dt < C::NDT; ++dt) {
+                u32x2 u;
+                u[0] = (uint32_t)f2bf(O[t][dt][0] * inv) | ((uint32_t)f2bf(O[t][dt][1] * inv) << 16);
+                u[1] = (uint32_t)f2bf(O[t][dt][2] * inv) | ((uint32_t)f2bf(O[t][dt][3] * inv) << 16);
+                *reinterpret_cast<u32x2 *>(orow + 16 * dt + 4 * lg) = u;
+            }
+        }
+        return;
+    }
     // ------------------- merge with the window's (out, LSE), normalise, store
 #pragma unroll
     for (int t = 0; t < PTW; ++t) {
@@ -876,14 +1115,18 @@ __device__ __forceinline__ void routed_body(
 }
 
 // S2: sinks beyond the first block (64 < S <= 128), a separate instantiation
-// so that the common case carries none of its code.
-template <int D, int PTW, bool S2>
+// so that the common case carries none of its code.  WIN: the whole union in
+// one launch (window tiles from kr first, then the sinks and routed blocks,
+// one softmax state, rows normalised and stored); otherwise the sinks and
+// routed blocks merged into the window launch's rows by their LSE.
+template <int D, int PTW, bool S2, bool WIN>
 __global__ __launch_bounds__(RtCfg<D>::NTHR, RtCfg<D>::NTHR / 256) void attn_routed_kernel(
     const bf16_t *__restrict__ q, int64_t qsb, int64_t qsn, int64_t qsh, const float *__restrict__ qgain,
     const float *__restrict__ kgain, float eps, const bf16_t *__restrict__ kc, const bf16_t *__restrict__ vt,
     const int32_t *__restrict__ idx, const int32_t *__restrict__ cnt, int64_t n, int Hq, int Hkv, int S,
     int kk, float scale, int ntiles, int Cn, int xmap, bf16_t *__restrict__ out,
-    int64_t osb, int64_t osn, int64_t osh, const float *__restrict__ lse) {
+    int64_t osb, int64_t osn, int64_t osh, const float *__restrict__ lse, const bf16_t *__restrict__ kr,
+    const float *__restrict__ cosT, const float *__restrict__ sinT, int W, bf16_t *__restrict__ qrw) {
     extern __shared__ __align__(16) char smem[];
     __shared__ int nlist;
     int combo, tile;
@@ -893,11 +1136,13 @@ __global__ __launch_bounds__(RtCfg<D>::NTHR, RtCfg<D>::NTHR / 256) void attn_rou
     const float sl2 = scale * LOG2E;
     float bl2;
     if (group_bound(qgain, kgain, combo % Hkv, G, sl2, D, bl2))
-        routed_body<D, PTW, true, S2>(q, qsb, qsn, qsh, qgain, eps, kc, vt, idx, cnt, n, Hq, Hkv, S, kk, sl2, bl2,
-                                  combo, tile, out, osb, osn, osh, lse, smem, nlist);
+        routed_body<D, PTW, true, S2, WIN>(q, qsb, qsn, qsh, qgain, eps, kc, vt, idx, cnt, n, Hq, Hkv, S, kk, sl2,
+                                           bl2, combo, tile, out, osb, osn, osh, lse, smem, nlist, kr, cosT, sinT,
+                                           W, qrw);
     else
-        routed_body<D, PTW, false, S2>(q, qsb, qsn, qsh, qgain, eps, kc, vt, idx, cnt, n, Hq, Hkv, S, kk, sl2, bl2,
-                                   combo, tile, out, osb, osn, osh, lse, smem, nlist);
+        routed_body<D, PTW, false, S2, WIN>(q, qsb, qsn, qsh, qgain, eps, kc, vt, idx, cnt, n, Hq, Hkv, S, kk,
+                                            sl2, bl2, combo, tile, out, osb, osn, osh, lse, smem, nlist, kr, cosT,
+                                            sinT, W, qrw);
 }
 
 
@@ -957,11 +1202,12 @@ static size_t routed_lds(int64_t n, int64_t G, int64_t k) {
            (size_t)((nb + 1) & ~1LL) * 2 + (size_t)(QT + C::WAVES * PTW) * nbw * 4 + 16;
 }
 
-template <int D, int PTW>
+template <int D, int PTW, bool WIN>
 static int launch_routed_t(const void *q, const int64_t *qs, const float *qgain, const float *kgain, float eps,
                            const void *kc, const void *vt, const int32_t *idx, const int32_t *cnt, int64_t B,
                            int64_t n, int64_t Hq, int64_t Hkv, int64_t S, int64_t k, float scale, void *out,
-                           const int64_t *os, const float *lse, hipStream_t s) {
+                           const int64_t *os, const float *lse, const void *kr, const float *cosT,
+                           const float *sinT, int64_t W, void *qrw, hipStream_t s) {
     using C = RtCfg<D>;
     const int G = (int)(Hq / Hkv);
     const size_t lds = routed_lds<D, PTW>(n, G, k);
@@ -971,6 +1217,7 @@ static int launch_routed_t(const void *q, const int64_t *qs, const float *qgain,
     int64_t grid;
     grid_map(B * Hkv, ntiles, xmap, grid);
     if (grid > 0x7fffffff) return HBA_ERR_UNSUPPORTED;
+    const int Wc = (int)((W < n + 1) ? W : n + 1);     // a window longer than the sequence is the sequence
     auto go = [&](auto kern) -> int {
         if (hipFuncSetAttribute(reinterpret_cast<const void *>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                                 (int)lds) != hipSuccess)
@@ -978,26 +1225,27 @@ static int launch_routed_t(const void *q, const int64_t *qs, const float *qgain,
         hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(C::NTHR), lds, s, (const bf16_t *)q, qs[0], qs[1],
                            qs[2], qgain, kgain, eps, (const bf16_t *)kc, (const bf16_t *)vt, idx, cnt, n, (int)Hq,
                            (int)Hkv, (int)S, (int)k, scale, (int)ntiles, (int)(B * Hkv), xmap, (bf16_t *)out,
-                           os[0], os[1], os[2], lse);
+                           os[0], os[1], os[2], lse, (const bf16_t *)kr, cosT, sinT, Wc, (bf16_t *)qrw);
         return HBA_OK;
     };
-    return (S > 64) ? go(&attn_routed_kernel<D, PTW, true>) : go(&attn_routed_kernel<D, PTW, false>);
+    return (S > 64) ? go(&attn_routed_kernel<D, PTW, true, WIN>) : go(&attn_routed_kernel<D, PTW, false, WIN>);
 }
 
 // PTW row tiles per wave when the selection lists fit LDS beside the ring, else one
-template <int D>
+template <int D, bool WIN>
 static int launch_routed(const void *q, const int64_t *qs, const float *qgain, const float *kgain, float eps,
                          const void *kc, const void *vt, const int32_t *idx, const int32_t *cnt, int64_t B,
                          int64_t n, int64_t Hq, int64_t Hkv, int64_t S, int64_t k, float scale, void *out,
-                         const int64_t *os, const float *lse, hipStream_t s) {
+                         const int64_t *os, const float *lse, const void *kr, const float *cosT, const float *sinT,
+                         int64_t W, void *qrw, hipStream_t s) {
     constexpr size_t LDS_MAX = 160 * 1024 - 64;   // 64 bytes for the static nlist
     const int64_t G = Hq / Hkv;
     if (routed_lds<D, RtCfg<D>::PTW>(n, G, k) <= LDS_MAX)
-        return launch_routed_t<D, RtCfg<D>::PTW>(q, qs, qgain, kgain, eps, kc, vt, idx, cnt, B, n, Hq, Hkv, S, k,
-                                                  scale, out, os, lse, s);
+        return launch_routed_t<D, RtCfg<D>::PTW, WIN>(q, qs, qgain, kgain, eps, kc, vt, idx, cnt, B, n, Hq, Hkv, S,
+                                                       k, scale, out, os, lse, kr, cosT, sinT, W, qrw, s);
     if (RtCfg<D>::PTW > 1 && routed_lds<D, 1>(n, G, k) <= LDS_MAX)
-        return launch_routed_t<D, 1>(q, qs, qgain, kgain, eps, kc, vt, idx, cnt, B, n, Hq, Hkv, S, k, scale, out,
-                                     os, lse, s);
+        return launch_routed_t<D, 1, WIN>(q, qs, qgain, kgain, eps, kc, vt, idx, cnt, B, n, Hq, Hkv, S, k, scale,
+                                          out, os, lse, kr, cosT, sinT, W, qrw, s);
     return HBA_ERR_UNSUPPORTED;
 }
 
@@ -1024,21 +1272,21 @@ int launch_attn_bf16_routed(const void *q, const int64_t *qs, const float *qgain
     using namespace ab;
     const int G = (int)(Hq / Hkv);
     if (G > 16 || n / 64 >= SENT) return HBA_ERR_UNSUPPORTED;
-    return launch_routed<D>(q, qs, qgain, kgain, eps, kc, vt, idx, cnt, B, n, Hq, Hkv, S, k, scale, out, os, lse,
-                            s);
+    return launch_routed<D, false>(q, qs, qgain, kgain, eps, kc, vt, idx, cnt, B, n, Hq, Hkv, S, k, scale, out, os,
+                                   lse, nullptr, nullptr, nullptr, 1, nullptr, s);
 }
 
 template <int D>
 int launch_attn_bf16(const void *q, const int64_t *qs, const float *qgain, const float *kgain, float eps,
                      const void *kc, const void *kr, const void *vt, const float *cosT, const float *sinT,
                      const int32_t *idx, const int32_t *cnt, int64_t B, int64_t n, int64_t Hq, int64_t Hkv,
-                     int64_t S, int64_t W, int64_t k, float scale, void *out, const int64_t *os, float *lse,
+                     int64_t S, int64_t W, int64_t k, float scale, void *out, const int64_t *os, void *qrw,
                      hipStream_t s) {
-    int st = launch_attn_bf16_window<D>(q, qs, qgain, kgain, eps, kr, vt, cosT, sinT, B, n, Hq, Hkv, S, W, scale,
-                                        out, os, lse, s);
-    if (st) return st;
-    return launch_attn_bf16_routed<D>(q, qs, qgain, kgain, eps, kc, vt, idx, cnt, B, n, Hq, Hkv, S, k, scale, out,
-                                      os, lse, s);
+    using namespace ab;
+    const int G = (int)(Hq / Hkv);
+    if (G > 16 || n / 64 >= SENT) return HBA_ERR_UNSUPPORTED;
+    return launch_routed<D, true>(q, qs, qgain, kgain, eps, kc, vt, idx, cnt, B, n, Hq, Hkv, S, k, scale, out, os,
+                                  nullptr, kr, cosT, sinT, W, qrw, s);
 }
 
 #define HBA_INST_WIN(D)                                                                                       \
@@ -1055,14 +1303,12 @@ HBA_INST_WIN(128)
 #undef HBA_INST_WIN
 
 template int launch_attn_bf16<64>(const void *, const int64_t *, const float *, const float *, float,
-                                     const void *, const void *, const void *, const float *, const float *,
-                                     const int32_t *, const int32_t *, int64_t, int64_t, int64_t, int64_t,
-                                     int64_t, int64_t, int64_t, float, void *, const int64_t *, float *,
-                                     hipStream_t);
+                                  const void *, const void *, const void *, const float *, const float *,
+                                  const int32_t *, const int32_t *, int64_t, int64_t, int64_t, int64_t, int64_t,
+                                  int64_t, int64_t, float, void *, const int64_t *, void *, hipStream_t);
 template int launch_attn_bf16<128>(const void *, const int64_t *, const float *, const float *, float,
-                                      const void *, const void *, const void *, const float *, const float *,
-                                      const int32_t *, const int32_t *, int64_t, int64_t, int64_t, int64_t,
-                                      int64_t, int64_t, int64_t, float, void *, const int64_t *, float *,
-                                      hipStream_t);
+                                   const void *, const void *, const void *, const float *, const float *,
+                                   const int32_t *, const int32_t *, int64_t, int64_t, int64_t, int64_t, int64_t,
+                                   int64_t, int64_t, float, void *, const int64_t *, void *, hipStream_t);
 
 }  // namespace hba

@@ -36,6 +36,7 @@ SIGNATURES = {
     "hba_attn_fwd": [_i, _vp, _c_i64p, _vp, _vp, _f, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64,
                      _i64, _i64, _i64, _i64, _i64, _i64, _f, _vp, ctypes.c_size_t, _vp, _c_i64p, _vp],
     "hba_attn_workspace_size": [_i, _i64, _i64, _i64, ctypes.POINTER(ctypes.c_size_t)],
+    "hba_attn_fwd_workspace_bytes": [_i, _i64, _i64, _i64, _i64, ctypes.POINTER(ctypes.c_size_t)],
     "hba_attn_window_fwd": [_vp, _c_i64p, _vp, _vp, _f, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
                             _i64, _i64, _f, _vp, ctypes.c_size_t, _vp, _c_i64p, _vp],
     "hba_attn_routed_fwd": [_vp, _c_i64p, _vp, _vp, _f, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,

@@ -107,15 +107,16 @@ def _forward_generic(q, k, v, cos, sin, cfg, summ, qkn, hier, dense_route):
     return r
 
 
-def forward_stages(q, k, v, cos, sin, cfg, summ, qkn, hier=False, dense_route=False, overlap=True):
+def forward_stages(q, k, v, cos, sin, cfg, summ, qkn, hier=False, dense_route=False, overlap=False):
     """The forward path stage by stage; returns a dict with every intermediate
-    (kc, kr, vt, S0, [S1], idx, val, cnt, out) and the scales used.  In
-    bf16 with overlap=True (the default) the attention's window launch runs on
-    a second stream while the summaries and the selection run on the current
-    one (0.4-1.5 % faster at 32K); overlap=False runs every stage in sequence
-    on the current stream.  Both give the same bits.  Geometry the tuned
-    kernels do not take (_tuned) runs on the generic fp32 kernels
-    (_forward_generic)."""
+    (kc, kr, vt, S0, [S1], idx, val, cnt, out) and the scales used.  Every
+    stage runs in sequence on the current stream; the bf16 attention is one
+    launch over the whole union.  overlap=True (bf16) instead runs the
+    attention as two launches, the window on a second stream while the
+    summaries and the selection run on this one, then the sinks and routed
+    blocks merged into it by LSE (the same softmax, with the window rows
+    rounded to bf16 once before the merge).  Geometry the tuned kernels do
+    not take (_tuned) runs on the generic fp32 kernels (_forward_generic)."""
     B, n, Hq, dh = q.shape
     assert n % cfg.block == 0, (n, cfg.block)
     if not _tuned(q, k, cfg, summ, hier):

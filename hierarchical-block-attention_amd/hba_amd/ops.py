@@ -325,7 +325,8 @@ def attn_fwd(q: Tensor, q_gain: Optional[Tensor], k_gain: Optional[Tensor], eps:
     cnt = cnt.contiguous()
     out = torch.empty(B, n, Hq, d, dtype=q.dtype, device=dev)
     nbytes = ctypes.c_size_t(0)
-    check(lib().hba_attn_workspace_size(_code(q), B, n, Hq, ctypes.byref(nbytes)), "hba_attn_workspace_size")
+    check(lib().hba_attn_fwd_workspace_bytes(_code(q), B, n, Hq, d, ctypes.byref(nbytes)),
+          "hba_attn_fwd_workspace_bytes")
     ws = torch.empty(max(int(nbytes.value), 16), dtype=torch.uint8, device=dev)
     with torch.cuda.device(dev):
         st = lib().hba_attn_fwd(_code(q), _p(q), strides3(q), _p(qg), _p(kg), eps, _p(kc.contiguous()),

@@ -197,15 +197,21 @@ int hba_attn_fwd(int dtype, const void *q, const int64_t q_strides[3],
                  void *workspace, size_t ws_bytes,
                  void *out, const int64_t out_strides[3], void *stream);
 
-/* Scratch bytes hba_attn_fwd needs (bf16: the window's LSE, B*Hq*n fp32;
- * fp32: none).  workspace must be 16-byte aligned. */
+/* Scratch bytes hba_attn_fwd needs: bf16, the RoPE query operand of the
+ * window tiles, B*n*Hq*d bf16 (rounded up to 256 bytes; the one launch
+ * parks it between its routed blocks and its window tiles); fp32, none.
+ * workspace must be 16-byte aligned; no initial contents. */
+int hba_attn_fwd_workspace_bytes(int dtype, int64_t B, int64_t n, int64_t Hq, int64_t d, size_t *bytes);
+
+/* Scratch bytes of the split launches below (bf16: the window's LSE,
+ * B*Hq*n fp32; fp32: none).  workspace must be 16-byte aligned. */
 int hba_attn_workspace_size(int dtype, int64_t B, int64_t n, int64_t Hq, size_t *bytes);
 
 /*
- * The two launches of the bf16 hba_attn_fwd as separate calls, for callers
- * that run the window (which needs no selection) concurrently with
- * summarisation and selection on another stream.  Same arguments, checks
- * and workspace as hba_attn_fwd (bf16 only).
+ * The bf16 union attention as two launches, for callers that run the window
+ * (which needs no selection) concurrently with summarisation and selection
+ * on another stream.  Same arguments and checks as hba_attn_fwd (bf16 only);
+ * workspace sized by hba_attn_workspace_size.
  *   hba_attn_window_fwd: the RoPE window region
  *     (attention.py:342-356 window term); writes its normalised rows into
  *     out and their log-sum-exp into workspace.
@@ -213,7 +219,8 @@ int hba_attn_workspace_size(int dtype, int64_t B, int64_t n, int64_t Hq, size_t 
  *     union softmax), merged by LSE into out.  It must be ordered after
  *     hba_attn_window_fwd on the same out and workspace (same stream, or an
  *     event wait).
- * hba_attn_fwd is hba_attn_window_fwd then hba_attn_routed_fwd on one stream.
+ * The same softmax as hba_attn_fwd's one launch, except that the window rows
+ * are rounded to bf16 once before the merge.
  */
 int hba_attn_window_fwd(const void *q, const int64_t q_strides[3],
                         const float *q_gain, const float *k_gain, float eps,

@@ -78,7 +78,7 @@ def test_argument_checks_run_before_any_launch():
     assert st == -1                                    # n % 64 != 0
     st = L.hba_attn_fwd(1, fake, s3, None, None, 1e-6, fake, fake, fake, fake, fake, fake, fake, 1, 128, 14,
                         2, 64, 4, 1024, 64, 16, 0.1, fake, 16, fake, s3, None)
-    assert st == -1                                    # workspace smaller than B*Hq*n*4
+    assert st == -1                                    # workspace smaller than B*n*Hq*d*2
     st = L.hba_attn_window_fwd(fake, s3, None, None, 1e-6, fake, fake, fake, fake, 1, 100, 14, 2, 64, 4, 1024,
                                64, 0.1, fake, 1 << 20, fake, s3, None)
     assert st == -1                                    # n % 64 != 0
@@ -91,6 +91,11 @@ def test_argument_checks_run_before_any_launch():
     nbytes = ctypes.c_size_t(0)
     assert L.hba_attn_workspace_size(1, 2, 128, 14, ctypes.byref(nbytes)) == 0 and nbytes.value == 2 * 14 * 128 * 4
     assert L.hba_attn_workspace_size(0, 2, 128, 14, ctypes.byref(nbytes)) == 0 and nbytes.value == 0
+    assert L.hba_attn_fwd_workspace_bytes(1, 2, 128, 14, 64, ctypes.byref(nbytes)) == 0
+    assert nbytes.value == 2 * 128 * 14 * 64 * 2
+    assert L.hba_attn_fwd_workspace_bytes(1, 1, 64, 3, 1, ctypes.byref(nbytes)) == 0 and nbytes.value == 512
+    assert L.hba_attn_fwd_workspace_bytes(0, 2, 128, 14, 64, ctypes.byref(nbytes)) == 0 and nbytes.value == 0
+    assert L.hba_attn_fwd_workspace_bytes(1, 2, 128, 14, 0, ctypes.byref(nbytes)) == -1
     st = L.hba_score_select(1, fake, s3, None, 1e-6, fake, 1, 128, 14, 2, 96, 4, 64, 1024, 16, 0.1,
                             fake, fake, fake, None, None)
     assert st == -2                                    # d = 96 unsupported

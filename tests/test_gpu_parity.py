@@ -540,20 +540,37 @@ def test_invalid_arguments_raise(dev):
                                    cprm, cprm, None)
 
 
-def test_overlapped_schedule_equals_one_stream(dev):
-    """forward_stages (overlap=True, the default) runs the bf16 window launch
-    on a second stream while the selection runs; its output must be
-    bit-identical to hba_attn_fwd (both launches on one stream) on the same
-    selection, and to the one-stream schedule (overlap=False)."""
+def test_overlapped_schedule_matches_one_launch(dev):
+    """forward_stages(overlap=True) runs the bf16 attention as two launches,
+    the window on a second stream while the selection runs, then the sinks
+    and routed blocks merged by LSE; the default runs it as one launch after
+    the selection (hba_attn_fwd, bit-identical).  The two forms compute the
+    same softmax and differ only by the window rows' bf16 rounding before
+    the merge (at most 2**-6 apart on these unit-scale values, 1e-4 on
+    average), and both are within the bf16 bar of the oracle on sampled rows."""
     cfg, x, prm, cos, sin = make(dev, "bf16", n=4096, W=1024, k=16, needles=True)
-    seq = hba_amd.forward_stages(x["q"], x["k"], x["v"], cos, sin, cfg, prm, prm, overlap=False)["out"]
+    seq = hba_amd.forward_stages(x["q"], x["k"], x["v"], cos, sin, cfg, prm, prm)
+    ref = ops.attn_fwd(x["q"], prm.q.gain, prm.k.gain, 1e-6, seq["kc"], seq["kr"], seq["vt"], cos, sin, seq["idx"],
+                       seq["cnt"], cfg.sinks, cfg.window, seq["scale"])
+    torch.cuda.synchronize()
+    assert torch.equal(seq["out"], ref)
+    P = O.prepare(f(x["q"])[0], f(x["k"])[0], f(x["v"])[0], f(cos), f(sin), cfg, f(x["probes"]), f(x["proj"]),
+                  f(x["q_gain"]), f(x["k_gain"]), 1e-6, "bf16", S0=f(seq["S0"])[0])
+    rows = np.unique(np.concatenate([np.arange(0, 70), np.linspace(0, 4095, 120).astype(np.int64),
+                                     np.arange(4030, 4096)]))
+    idx, cnt = seq["idx"][0].cpu().numpy(), seq["cnt"][0].cpu().numpy()
+    dense = O.dense_rows(P.qc, P.qr, P.kc, P.kr, P.v, lambda g, i: idx[g, i, :cnt[g, i]], seq["scale"], cfg.sinks,
+                         cfg.window, 64, rows)
+    a = f(seq["out"])[0]
     for _ in range(3):   # repeated calls reuse the side stream and the allocator's blocks
         r = hba_amd.forward_stages(x["q"], x["k"], x["v"], cos, sin, cfg, prm, prm, overlap=True)
-        assert torch.equal(r["out"], seq)
-        ref = ops.attn_fwd(x["q"], prm.q.gain, prm.k.gain, 1e-6, r["kc"], r["kr"], r["vt"], cos, sin, r["idx"],
-                           r["cnt"], cfg.sinks, cfg.window, r["scale"])
         torch.cuda.synchronize()
-        assert torch.equal(r["out"], ref)
+        assert torch.equal(r["idx"], seq["idx"])
+        b = f(r["out"])[0]
+        dab = np.abs(a - b)
+        assert dab.max() <= 2 ** -6 and dab.mean() <= 1e-4, (dab.max(), dab.mean())
+        for o in (a, b):
+            assert np.abs(o[rows] - dense).max() <= 2e-2
 
 
 @pytest.mark.parametrize("qknorm,G,k", [(True, 7, 16), (False, 7, 16), (True, 4, 12), (True, 8, 16)])
