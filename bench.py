@@ -41,10 +41,10 @@ DECODE = dict(batch=32, len_lo=16384, len_hi=32768, seed=0)
 # ring in one softmax state.  Its time is taken with HIP events around the op.
 ATTN_KERNELS = "hba_attn_fwd = attn_routed_kernel<64,2,false,true> (sinks + routed blocks, then window tiles)"
 # HBM (beyond-L2) bytes per hba_attn_fwd call on this workload: rocprofv3 --pmc
-# FETCH_SIZE and WRITE_SIZE summed over the two kernels, each divided by the
-# counter's reading per byte of a plain device copy (python bench.py
-# --copy-probe 1024); profiles/hba_attn_32k_traffic.md.
-ATTN_TRAFFIC_BYTES = 769909293
+# FETCH_SIZE and WRITE_SIZE of the launch, each divided by the counter's
+# reading per byte of a plain device copy (python bench.py --copy-probe 1024);
+# profiles/hba_attn_32k_traffic.md.
+ATTN_TRAFFIC_BYTES = 542983240
 
 
 def cpu_model():
