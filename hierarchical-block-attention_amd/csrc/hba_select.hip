@@ -487,13 +487,19 @@ __host__ __device__ inline size_t sel_ksup_off(int nwp) { return (sel_pre_off(nw
 __host__ __device__ inline size_t sel_cs_off(int nwp) { return sel_ksup_off(nwp) + (size_t)64 * 16 * 2; }
 // marked_only: run only for a 64-query tile holding a query whose cnt is
 // SEL_OVERFLOW (the threshold kernel's overflow), and recompute the tile.
-template <int D, int KMAX, bool HIER, int BEAMMAX = 16>
-__global__ __launch_bounds__(256, (D == 64) ? 2 : 1) void score_select_mfma_kernel(
+// gather (HIER): 0 the block scan filtered by parent; 1 level 2 by super in
+// this kernel; 2 level 1 only: each query's kept supers (ascending, -1 past
+// them) into ks_out [B, Hkv, n, 16] and its routing query into rq_out
+// [B, Hkv, n, D], for hier_l2_kernel.  L1 (with HIER and gather 2): an
+// instantiation holding only that level-1 code, whose registers let three
+// workgroups share a CU.
+template <int D, int KMAX, bool HIER, int BEAMMAX = 16, bool L1 = false>
+__global__ __launch_bounds__(256, L1 ? 3 : ((D == 64) ? 2 : 1)) void score_select_mfma_kernel(
     const bf16_t *__restrict__ q, int64_t qsb, int64_t qsn, int64_t qsh, const float *__restrict__ qgain,
     float eps, const bf16_t *__restrict__ S0, int64_t n, int Hq, int Hkv, int64_t nb, int64_t W, int kk,
     float scale, int32_t *__restrict__ idx, float *__restrict__ val, int32_t *__restrict__ cnt,
     float *__restrict__ scores, const bf16_t *__restrict__ S1, int F, int beam, float *__restrict__ sup_scores,
-    int marked_only, int gather) {
+    int marked_only, int gather, bf16_t *__restrict__ rq_out, int16_t *__restrict__ ks_out) {
     int tile_, g_;
     int64_t b_;
     sel_deep_first((int)((n + 63) / 64), Hkv, tile_, g_, b_);
@@ -620,6 +626,29 @@ __global__ __launch_bounds__(256, (D == 64) ? 2 : 1) void score_select_mfma_kern
             if (lg == 0) pmask[qcol * nw + (p >> 5)] |= 1u << (p & 31);
         });
         __syncthreads();
+        if (L1 || gather == 2) {
+            // ---- level 1 only: the kept supers ascending and the routing query
+            const int nwu = (int)((ns + 31) / 32);
+            if (tid < 64 && i0 + tid < n) {
+                int16_t *dst = ks_out + ((b * Hkv + g) * n + i0 + tid) * 16;
+                int c = 0;
+                for (int wd = 0; wd < nwu && c < 16; ++wd) {
+                    uint32_t msk = pmask[tid * nw + wd];
+                    while (msk && c < 16) {
+                        dst[c++] = (int16_t)(wd * 32 + __ffs(msk) - 1);
+                        msk &= msk - 1u;
+                    }
+                }
+                for (; c < 16; ++c) dst[c] = -1;
+            }
+            for (int e = tid; e < 64 * (D / 8); e += 256) {   // 16-byte chunks of the 64 rows
+                const int qq = e / (D / 8), c = e % (D / 8);
+                if (i0 + qq < n)
+                    *reinterpret_cast<u32x4s *>(rq_out + ((b * Hkv + g) * n + i0 + qq) * D + 8 * c) =
+                        *reinterpret_cast<const u32x4s *>(qgs + qq * ROWQ + 8 * c);
+            }
+            return;
+        }
         if (gather) {
             // ---- level 2 by super (F = 4, 8 or 16; beff * F <= SEL_GMAXE):
             // each kept super's F children are scored against only the
@@ -924,6 +953,314 @@ __global__ __launch_bounds__(256, (D == 64) ? 2 : 1) void score_select_mfma_kern
             val[o + j] = -INFINITY;
         }
         if (lg == 0) cnt[(b * Hkv + g) * n + iq] = c;
+    }
+}
+
+// ------------------------------------- bf16 level 2 over query groups ----
+// Level 2 of the two-level descent for a group of QG queries (a multiple of
+// 64) of one KV head, after score_select_mfma_kernel (gather 2) wrote each
+// query's kept supers ks (ascending) and routing query rq.  The group's
+// (query, kept super) pairs are bucketed by super in LDS; each super's F
+// children are loaded once, as the A operand of the flat scan's MFMA tile,
+// and scored against 16 of its queries per tile: the flat scan's operands and
+// order, so its fp32 scores bit for bit.  Child c of a query's r-th kept
+// super goes to its list position r*F + c in LDS (positions no child fills
+// stay -inf); the kout best positions of each query are then ranked as in
+// score_select_mfma_kernel's level 2 (threshold, list, rank by count), and a
+// query whose list overflows is marked for the exact pass.  Against a 64-query
+// tile, a group of a few hundred queries loads each super's children once for
+// ~QG*beam/ns queries instead of ~64*beam/ns.
+namespace hl2 {
+constexpr int NT = 1024;   // 16 waves: the latency-bound phases overlap across waves
+constexpr int NW = NT / 64;
+constexpr int KSW = 16;   // kept-super slots per query in ks
+constexpr int TKW = 4 * 32 + 4 * SEL_GCAP;   // top-k scratch per wave (8-byte keys)
+// LDS layout: cs [QG][E] f32 | ksl [QG][16] i16 | lists [QG*beff] u16 |
+// cntS, offS [nsp] i32 | one region holding the group's routing queries
+// [QG][D + 8] bf16 (padded rows: a tile's 16 rows fall in distinct banks)
+// while the supers are scored, then the top-k scratch [NW][TKW] u64
+__host__ __device__ inline size_t off_ksl(int QG, int E) { return (size_t)QG * E * 4; }
+__host__ __device__ inline size_t off_list(int QG, int E) { return off_ksl(QG, E) + (size_t)QG * KSW * 2; }
+__host__ __device__ inline size_t off_cnt(int QG, int E, int beff) {
+    return (off_list(QG, E) + (size_t)QG * beff * 2 + 15) & ~(size_t)15;
+}
+__host__ __device__ inline size_t off_tk(int QG, int E, int beff, int nsp) {
+    return (off_cnt(QG, E, beff) + (size_t)nsp * 8 + 15) & ~(size_t)15;
+}
+__host__ __device__ inline size_t region(int QG, int D) {
+    const size_t rq = (size_t)QG * (D + 8) * 2, tk = (size_t)NW * TKW * 8;
+    return rq > tk ? rq : tk;
+}
+__host__ __device__ inline size_t bytes(int QG, int E, int beff, int nsp, int D) {
+    return off_tk(QG, E, beff, nsp) + region(QG, D) + 16;
+}
+}  // namespace hl2
+
+template <int D>
+__global__ __launch_bounds__(hl2::NT) void hier_l2_kernel(
+    const bf16_t *__restrict__ S0, const bf16_t *__restrict__ rq, const int16_t *__restrict__ ks, int64_t n,
+    int Hkv, int64_t nb, int64_t W, int kk, int F, int beff, int QG, int ngroups, float scale,
+    int32_t *__restrict__ idx, float *__restrict__ val, int32_t *__restrict__ cnt, float *__restrict__ scores) {
+    using namespace hl2;
+    constexpr int NKS = D / 32;
+    extern __shared__ __align__(16) char hsm[];
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, lg = lane >> 4;
+    // workgroup -> (group, KV head, batch), the deepest groups first
+    const int64_t per = (int64_t)gridDim.x / ngroups;   // Hkv * B
+    const int group = ngroups - 1 - (int)(blockIdx.x / per);
+    const int g = (int)((blockIdx.x % per) % Hkv);
+    const int64_t b = (blockIdx.x % per) / Hkv;
+    const int64_t q0 = (int64_t)group * QG;
+    const int nq = (int)((n - q0 < QG) ? n - q0 : QG);
+    const int E = beff * F;
+    const int kout = (kk < E) ? kk : E;
+    const int64_t bh = b * Hkv + g;
+    const int64_t last_bm = cand_bmax(q0 + nq - 1, 64, W);
+    const int nsp = (last_bm >= 1) ? (int)(last_bm / F) + 1 : 0;   // supers a query of the group can keep
+    float *cs = reinterpret_cast<float *>(hsm);
+    int16_t *ksl = reinterpret_cast<int16_t *>(hsm + off_ksl(QG, E));
+    uint16_t *lists = reinterpret_cast<uint16_t *>(hsm + off_list(QG, E));
+    int *cntS = reinterpret_cast<int *>(hsm + off_cnt(QG, E, beff));
+    int *offS = cntS + nsp;
+    uint64_t *tkall = reinterpret_cast<uint64_t *>(hsm + off_tk(QG, E, beff, nsp));
+    constexpr int RQS = D + 8;   // padded row of the routing queries in LDS
+    bf16_t *rqs = reinterpret_cast<bf16_t *>(tkall);   // the same region, before the top-k
+
+    // ---- the group's kept supers, the scores' -inf, zero counts
+    for (int e = tid; e < QG * 2; e += NT) {   // 2 x 16 bytes per query
+        const int qq = e >> 1;
+        u32x4s v = {0xffffffffu, 0xffffffffu, 0xffffffffu, 0xffffffffu};   // -1 pairs past the group
+        if (qq < nq) v = *reinterpret_cast<const u32x4s *>(ks + (bh * n + q0 + qq) * KSW + 8 * (e & 1));
+        *reinterpret_cast<u32x4s *>(ksl + qq * KSW + 8 * (e & 1)) = v;
+    }
+    for (int e = tid; e < QG * E; e += NT) cs[e] = -INFINITY;
+    for (int e = tid; e < QG * (D / 8); e += NT) {   // the group's routing queries, 16 bytes at a time
+        const int qq = e / (D / 8), c = e % (D / 8);
+        u32x4s v = {0u, 0u, 0u, 0u};
+        if (qq < nq) v = *reinterpret_cast<const u32x4s *>(rq + (bh * n + q0 + qq) * D + 8 * c);
+        *reinterpret_cast<u32x4s *>(rqs + qq * RQS + 8 * c) = v;
+    }
+    for (int e = tid; e < nsp; e += NT) cntS[e] = 0;
+    __syncthreads();
+    // ---- bucket the (query, kept super) pairs by super: count, offsets, fill
+    for (int qq = tid; qq < nq; qq += NT)
+        for (int r = 0; r < beff; ++r) {
+            const int sp = ksl[qq * KSW + r];
+            if (sp >= 0 && sp < nsp) atomicAdd(&cntS[sp], 1);
+        }
+    __syncthreads();
+    if (w == 0) {
+        int base = 0;
+        for (int s0 = 0; s0 < nsp; s0 += 64) {
+            const int c = (s0 + lane < nsp) ? cntS[s0 + lane] : 0;
+            int incl = c;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const int t = __shfl_up(incl, o, 64);
+                if (lane >= o) incl += t;
+            }
+            if (s0 + lane < nsp) offS[s0 + lane] = base + incl - c;
+            base += __shfl(incl, 63, 64);
+        }
+    }
+    __syncthreads();
+    for (int qq = tid; qq < nq; qq += NT)
+        for (int r = 0; r < beff; ++r) {
+            const int sp = ksl[qq * KSW + r];
+            if (sp >= 0 && sp < nsp) {
+                const int pos = atomicAdd(&offS[sp], 1);   // offS ends as the end of each bucket
+                lists[pos] = (uint16_t)((qq << 4) | r);
+            }
+        }
+    __syncthreads();
+    // ---- per super: its children once, 16 of its queries per MFMA tile.
+    // Wave w takes the non-empty supers w, w + NW, ...; the next one's
+    // children and first tile of routing queries load while this one computes.
+    const bf16_t *Sg = S0 + bh * nb * 4 * D;
+    const int NMT = F / 4;
+    auto loadA = [&](int sp, bf16x8 (&af)[4][NKS]) {
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+            if (mt >= NMT) break;   // uniform
+            int64_t blk = (int64_t)sp * F + 4 * mt + (l16 >> 2);
+            blk = (blk < nb) ? blk : nb - 1;   // rows past the last block: never stored
+            const bf16_t *src = Sg + (blk * 4 + (l16 & 3)) * D + 8 * lg;
+#pragma unroll
+            for (int ks2 = 0; ks2 < NKS; ++ks2) af[mt][ks2] = ldb8(src + 32 * ks2);
+        }
+    };
+    // tile j0 of super sp: this lane's column entry and its routing query
+    auto loadQ = [&](int sp, int j0, bf16x8 (&qv)[NKS], int &ent, bool &cv) {
+        const int c = cntS[sp];
+        cv = j0 + l16 < c;
+        ent = cv ? lists[offS[sp] - c + j0 + l16] : 0;
+        const bf16_t *row = rqs + (ent >> 4) * RQS + 8 * lg;
+#pragma unroll
+        for (int ks2 = 0; ks2 < NKS; ++ks2) qv[ks2] = ldb8(row + 32 * ks2);
+    };
+    auto tile = [&](int sp, const bf16x8 (&af)[4][NKS], const bf16x8 (&qv)[NKS], int ent, bool cv) {
+        const int qq = ent >> 4, r = ent & 15;
+        const int64_t qi = q0 + qq;
+        f32x4 acc[4];
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+            if (mt >= NMT) break;
+            acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks2 = 0; ks2 < NKS; ++ks2)
+                acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[mt][ks2], qv[ks2], acc[mt], 0, 0, 0);
+        }
+        const int64_t bm = cand_bmax(qi, 64, W);
+        float *dst = cs + qq * E + r * F;
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+            if (mt >= NMT) break;
+            const int ch = 4 * mt + lg;
+            const int64_t blk = (int64_t)sp * F + ch;
+            float best = acc[mt][0];
+            best = (acc[mt][1] > best) ? acc[mt][1] : best;
+            best = (acc[mt][2] > best) ? acc[mt][2] : best;
+            best = (acc[mt][3] > best) ? acc[mt][3] : best;
+            const float v = best * scale;
+            const bool ok = cv && blk >= 1 && blk <= bm;
+            if (cv) dst[ch] = ok ? v : -INFINITY;
+            if (ok && scores) scores[(bh * n + qi) * nb + blk] = v;
+        }
+    };
+    auto next_super = [&](int sp) {   // the wave's next non-empty super at or after sp (uniform)
+        while (sp < nsp && cntS[sp] == 0) sp += NW;
+        return sp;
+    };
+    {
+        bf16x8 afA[4][NKS], afB[4][NKS], qA[NKS], qB[NKS];
+        int eA = 0, eB = 0;
+        bool cA = false, cB = false;
+        int sp = next_super(w);
+        if (sp < nsp) {
+            loadA(sp, afA);
+            loadQ(sp, 0, qA, eA, cA);
+        }
+        while (sp < nsp) {
+            const int sn = next_super(sp + NW);
+            if (sn < nsp) {
+                loadA(sn, afB);
+                loadQ(sn, 0, qB, eB, cB);
+            }
+            tile(sp, afA, qA, eA, cA);
+            const int c = cntS[sp];
+            for (int j0 = 16; j0 < c; j0 += 16) {
+                bf16x8 qv[NKS];
+                int e;
+                bool cv;
+                loadQ(sp, j0, qv, e, cv);
+                tile(sp, afA, qv, e, cv);
+            }
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+                for (int ks2 = 0; ks2 < NKS; ++ks2) afA[mt][ks2] = afB[mt][ks2];
+#pragma unroll
+            for (int ks2 = 0; ks2 < NKS; ++ks2) qA[ks2] = qB[ks2];
+            eA = eB;
+            cA = cB;
+            sp = sn;
+        }
+    }
+    __syncthreads();
+    // ---- per query, 16 lanes: the kout best listed children (as
+    // score_select_mfma_kernel's level 2)
+    uint64_t *tk = tkall + w * TKW;
+    uint64_t *lst = tk + 4 * 32;
+    const int qq4 = lane >> 4, sl = lane & 15;
+    constexpr int EL = SEL_GMAXE / 16;   // positions per lane
+    const int j0l = sl / F, jstep = 16 / F, ch0 = sl % F;
+    for (int base = 16 * w; base < nq; base += 16 * NW) {   // 16 queries per wave and pass
+        for (int r4 = 0; r4 < 4; ++r4) {
+            const int qc = base + 4 * r4 + qq4;
+            const bool qv_ = qc < nq;
+            const int qcc = qv_ ? qc : 0;
+            const int64_t qi = q0 + qc;
+            const float *cq = cs + qcc * E;
+            const int16_t *kq = ksl + qcc * KSW;
+            float cvv[EL];
+            int kb[EL];
+#pragma unroll
+            for (int t = 0; t < EL; ++t) {
+                const int p = sl + 16 * t;
+                const int jr = j0l + t * jstep;
+                cvv[t] = (qv_ && p < E) ? cq[p] : -INFINITY;
+                kb[t] = kq[jr < 16 ? jr : 15];
+            }
+            uint64_t ky[EL];
+#pragma unroll
+            for (int t = 0; t < EL; ++t) ky[t] = (cvv[t] == -INFINITY) ? 0ull : sel_key(cvv[t], kb[t] * F + ch0);
+            uint64_t t0 = 0ull, t1 = 0ull;
+#pragma unroll
+            for (int t = 0; t < EL; ++t) {
+                const uint64_t key = ky[t];
+                t1 = (key > t0) ? t0 : ((key > t1) ? key : t1);
+                t0 = (key > t0) ? key : t0;
+            }
+            tk[qq4 * 32 + 2 * sl] = t0;
+            tk[qq4 * 32 + 2 * sl + 1] = t1;
+            wave_lds_sync();
+            int g0 = 0, g1 = 0;
+            for (int j = 0; j < 32; ++j) {
+                const uint64_t x = tk[qq4 * 32 + j];
+                g0 += (x > t0) ? 1 : 0;
+                g1 += (x > t1) ? 1 : 0;
+            }
+            uint64_t tau = ~0ull;
+            if (g0 < kout) tau = t0;
+            if (g1 < kout && t1 < tau) tau = t1;
+#pragma unroll
+            for (int o = 1; o < 16; o <<= 1) {
+                const uint64_t ot = shfl_xor_u64(tau, o);
+                tau = (ot < tau) ? ot : tau;
+            }
+            int mine = 0;
+#pragma unroll
+            for (int t = 0; t < EL; ++t) mine += (ky[t] != 0ull && ky[t] >= tau) ? 1 : 0;
+            int incl = mine;
+#pragma unroll
+            for (int o = 1; o < 16; o <<= 1) {
+                const int t = __shfl_up(incl, o, 16);
+                if (sl >= o) incl += t;
+            }
+            const int total = __shfl(incl, 15, 16);
+            if (total <= SEL_GCAP) {
+                int pos = incl - mine;
+#pragma unroll
+                for (int t = 0; t < EL; ++t)
+                    if (ky[t] != 0ull && ky[t] >= tau) lst[qq4 * SEL_GCAP + pos++] = ky[t];
+            }
+            wave_lds_sync();
+            if (qv_) {
+                const int64_t o = (bh * n + qi) * kk;
+                if (total > SEL_GCAP) {   // too many ties at tau: the exact pass recomputes the tile
+                    if (sl == 0) cnt[bh * n + qi] = SEL_OVERFLOW;
+                } else {
+                    const uint64_t *lq = lst + qq4 * SEL_GCAP;
+                    for (int j = sl; j < total; j += 16) {
+                        const uint64_t key = lq[j];
+                        int rank = 0;
+#pragma unroll 8
+                        for (int j2 = 0; j2 < total; ++j2) rank += (lq[j2] > key) ? 1 : 0;
+                        if (rank < kout) {
+                            idx[o + rank] = sel_key_block(key);
+                            val[o + rank] = sel_key_score(key);
+                        }
+                    }
+                    const int taken = (total < kout) ? total : kout;
+                    for (int j = taken + sl; j < kk; j += 16) {
+                        idx[o + j] = -1;
+                        val[o + j] = -INFINITY;
+                    }
+                    if (sl == 0) cnt[bh * n + qi] = taken;
+                }
+            }
+            wave_lds_sync();   // tk and lst are reused by the next four queries
+        }
     }
 }
 
@@ -1284,7 +1621,8 @@ void launch_flat(const void *q, const int64_t *qs, const float *qgain, float eps
                                (int)Hkv, n / 64, W, (int)k, scale, idx, val, cnt, scores, ntiles);
             hipLaunchKernelGGL((score_select_mfma_kernel<D, KMAX, false>), g1, dim3(256), 0, s,
                                (const bf16_t *)q, qs[0], qs[1], qs[2], qgain, eps, (const bf16_t *)S0, n, (int)Hq,
-                               (int)Hkv, n / 64, W, (int)k, scale, idx, val, cnt, scores, nullptr, 1, 1, nullptr, 1, 0);
+                               (int)Hkv, n / 64, W, (int)k, scale, idx, val, cnt, scores, nullptr, 1, 1, nullptr, 1, 0,
+                               nullptr, nullptr);
             return;
         }
     }
@@ -1294,11 +1632,35 @@ void launch_flat(const void *q, const int64_t *qs, const float *qgain, float eps
                        scale, idx, val, cnt, scores);
 }
 
+// Workspace of the grouped level 2 (hier_l2_kernel): the routing queries
+// [B, Hkv, n, D] bf16, then the kept supers [B, Hkv, n, 16] int16.
+inline size_t hier_ws_rq(int64_t B, int64_t n, int64_t Hkv, int64_t D) {
+    return ((size_t)B * Hkv * n * D * 2 + 255) & ~(size_t)255;
+}
+inline size_t hier_ws_bytes(int64_t B, int64_t n, int64_t Hkv, int64_t D) {
+    return hier_ws_rq(B, n, Hkv, D) + (((size_t)B * Hkv * n * hl2::KSW * 2 + 255) & ~(size_t)255);
+}
+// Queries per group: the largest multiple of 64 (up to 1024) whose lists fit LDS.
+inline int hier_qg(int E, int beff, int64_t ns, int64_t D) {
+    for (int QG = 1024; QG >= 64; QG -= 64)
+        if (hl2::bytes(QG, E, beff, (int)ns, (int)D) <= (size_t)160 * 1024 - 64) return QG;
+    return 0;
+}
+// The grouped level 2 applies: bf16, 4 slots, k <= 32, G <= 16, F in {4, 8,
+// 16}, beam * F <= 256 (and the geometry of score_select_mfma_kernel's HIER).
+inline bool hier_grouped_ok(int64_t d, int64_t m, int64_t n, int64_t Hq, int64_t Hkv, int64_t k, int64_t F,
+                            int64_t beam) {
+    const int64_t ns = (n / 64 + F - 1) / F;
+    const int64_t beff = (beam < ns) ? beam : ns;
+    return (d == 64 || d == 128) && m == 4 && k <= 32 && ns <= 32 * SEL_PMW && Hq / Hkv <= 16 && F >= 4 &&
+           16 % F == 0 && beff * F <= SEL_GMAXE && beff <= hl2::KSW && hier_qg((int)(beff * F), (int)beff, ns, d) > 0;
+}
+
 template <int DT, int D, int M, int KMAX>
 void launch_hier(const void *q, const int64_t *qs, const float *qgain, float eps, const void *S0,
                  const void *S1, int64_t B, int64_t n, int64_t Hq, int64_t Hkv, int64_t W, int64_t k,
                  int64_t F, int64_t beam, float scale, int32_t *idx, float *val, int32_t *cnt,
-                 float *scores, float *sup_scores, hipStream_t s) {
+                 float *scores, float *sup_scores, void *ws, hipStream_t s) {
     const int64_t ns = (n / 64 + F - 1) / F;
     if constexpr (DT == 1 && M == 4 && KMAX <= 32) {
         if (ns <= 32 * SEL_PMW && Hq / Hkv <= 16) {
@@ -1313,6 +1675,32 @@ void launch_hier(const void *q, const int64_t *qs, const float *qgain, float eps
             // level 1 keeps beam-sized lists per lane (insertion cost grows with the length)
             auto kfn = (beam <= 8) ? score_select_mfma_kernel<D, KMAX, true, 8>
                                    : score_select_mfma_kernel<D, KMAX, true, 16>;
+            if (ws) {
+                // level 1 per 64-query tile into the workspace, then level 2
+                // and the ranking per group of QG queries
+                const int E = (int)(beff * F);
+                const int QG = hier_qg(E, (int)beff, ns, D);
+                const int ngroups = (int)((n + QG - 1) / QG);
+                bf16_t *rq = reinterpret_cast<bf16_t *>(ws);
+                int16_t *ksp = reinterpret_cast<int16_t *>(reinterpret_cast<char *>(ws) + hier_ws_rq(B, n, Hkv, D));
+                auto k1 = (beam <= 8) ? score_select_mfma_kernel<D, KMAX, true, 8, true>
+                                      : score_select_mfma_kernel<D, KMAX, true, 16, true>;
+                hipLaunchKernelGGL(k1, grid, dim3(256), pm, s, (const bf16_t *)q, qs[0], qs[1], qs[2], qgain, eps,
+                                   (const bf16_t *)S0, n, (int)Hq, (int)Hkv, n / 64, W, (int)k, scale, idx, val,
+                                   cnt, scores, (const bf16_t *)S1, (int)F, (int)beam, sup_scores, 0, 2, rq, ksp);
+                const size_t lds = hl2::bytes(QG, E, (int)beff, (int)ns, D);
+                if (hipFuncSetAttribute(reinterpret_cast<const void *>(&hier_l2_kernel<D>),
+                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+                    return;   // the error stays as hipGetLastError's, which the entry point reports
+                hipLaunchKernelGGL((hier_l2_kernel<D>), dim3((unsigned)(ngroups * Hkv * B)), dim3(hl2::NT), lds, s,
+                                   (const bf16_t *)S0, (const bf16_t *)rq, (const int16_t *)ksp, n, (int)Hkv, n / 64,
+                                   W, (int)k, (int)F, (int)beff, QG, ngroups, scale, idx, val, cnt, scores);
+                hipLaunchKernelGGL(kfn, grid, dim3(256), pm, s, (const bf16_t *)q, qs[0], qs[1], qs[2], qgain, eps,
+                                   (const bf16_t *)S0, n, (int)Hq, (int)Hkv, n / 64, W, (int)k, scale, idx, val,
+                                   cnt, scores, (const bf16_t *)S1, (int)F, (int)beam, sup_scores, 1, 0, nullptr,
+                                   nullptr);
+                return;
+            }
             if (gather && pmg > 65536 &&
                 hipFuncSetAttribute(reinterpret_cast<const void *>(kfn), hipFuncAttributeMaxDynamicSharedMemorySize,
                                     (int)pmg) != hipSuccess)
@@ -1320,11 +1708,12 @@ void launch_hier(const void *q, const int64_t *qs, const float *qgain, float eps
             hipLaunchKernelGGL(kfn, grid, dim3(256), gather ? pmg : pm, s, (const bf16_t *)q, qs[0], qs[1], qs[2],
                                qgain, eps, (const bf16_t *)S0, n, (int)Hq, (int)Hkv, n / 64, W, (int)k, scale, idx,
                                val, cnt, scores, (const bf16_t *)S1, (int)F, (int)beam, sup_scores, 0,
-                               gather ? 1 : 0);
+                               gather ? 1 : 0, nullptr, nullptr);
             if (gather)
                 hipLaunchKernelGGL(kfn, grid, dim3(256), pm, s, (const bf16_t *)q, qs[0], qs[1], qs[2], qgain, eps,
                                    (const bf16_t *)S0, n, (int)Hq, (int)Hkv, n / 64, W, (int)k, scale, idx, val,
-                                   cnt, scores, (const bf16_t *)S1, (int)F, (int)beam, sup_scores, 1, 0);
+                                   cnt, scores, (const bf16_t *)S1, (int)F, (int)beam, sup_scores, 1, 0, nullptr,
+                                   nullptr);
             return;
         }
     }
@@ -1381,20 +1770,38 @@ extern "C" int hba_score_select(int dtype, const void *q, const int64_t q_stride
     return HBA_OK;
 }
 
+extern "C" int hba_hier_select_workspace_bytes(int dtype, int64_t B, int64_t n, int64_t Hq, int64_t Hkv,
+                                               int64_t d, int64_t m, int64_t k, int64_t fanout, int64_t beam,
+                                               size_t *bytes) {
+    if (!bytes || B <= 0 || n <= 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv != 0 || d <= 0 || m <= 0 || k < 1 ||
+        fanout < 1 || beam < 1)
+        return HBA_ERR_INVALID_ARG;
+    if (dtype != HBA_DTYPE_F32 && dtype != HBA_DTYPE_BF16) return HBA_ERR_UNSUPPORTED;
+    *bytes = (dtype == HBA_DTYPE_BF16 && hier_grouped_ok(d, m, n, Hq, Hkv, k, fanout, beam))
+                 ? hier_ws_bytes(B, n, Hkv, d)
+                 : 0;
+    return HBA_OK;
+}
+
 extern "C" int hba_hier_select(int dtype, const void *q, const int64_t q_strides[3],
                                const float *q_gain, float eps, const void *S0, const void *S1,
                                int64_t B, int64_t n, int64_t Hq, int64_t Hkv, int64_t d, int64_t m,
                                int64_t Bk, int64_t W, int64_t k, int64_t fanout, int64_t beam,
                                float scale, int32_t *idx, float *val, int32_t *cnt, float *scores,
-                               float *sup_scores, void *stream) {
+                               float *sup_scores, void *workspace, size_t ws_bytes, void *stream) {
     int st = select_checks(dtype, q, q_strides, S0, B, n, Hq, Hkv, d, m, Bk, W, k, idx, val, cnt);
     if (st) return st;
     if (!S1 || fanout < 1 || beam < 1) return HBA_ERR_INVALID_ARG;
     if (beam > 16 || fanout > 64) return HBA_ERR_UNSUPPORTED;
+    // the grouped level 2 runs where a large enough workspace comes in
+    size_t need = 0;
+    hba_hier_select_workspace_bytes(dtype, B, n, Hq, Hkv, d, m, k, fanout, beam, &need);
+    void *ws = (need > 0 && workspace && ws_bytes >= need) ? workspace : nullptr;
+    if (ws && !abi::aligned16(ws)) return HBA_ERR_INVALID_ARG;
     hipStream_t s = (hipStream_t)stream;
 #define HBA_HIER(DT, D)                                                                            \
     HBA_SEL_DISPATCH_M(launch_hier, DT, D, q, q_strides, q_gain, eps, S0, S1, B, n, Hq, Hkv, W, k,   \
-                       fanout, beam, scale, idx, val, cnt, scores, sup_scores, s)
+                       fanout, beam, scale, idx, val, cnt, scores, sup_scores, ws, s)
     HBA_DISPATCH_DT_D(dtype, d, HBA_HIER);
 #undef HBA_HIER
     HBA_LAUNCH_CHECK();

@@ -29,7 +29,9 @@ SIGNATURES = {
     "hba_score_select": [_i, _vp, _c_i64p, _vp, _f, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                          _i64, _i64, _f, _vp, _vp, _vp, _vp, _vp],
     "hba_hier_select": [_i, _vp, _c_i64p, _vp, _f, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
-                        _i64, _i64, _i64, _i64, _i64, _f, _vp, _vp, _vp, _vp, _vp, _vp],
+                        _i64, _i64, _i64, _i64, _i64, _f, _vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_size_t, _vp],
+    "hba_hier_select_workspace_bytes": [_i, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                                        ctypes.POINTER(ctypes.c_size_t)],
     "hba_route_queries": [_i, _vp, _c_i64p, _vp, _f, _i64, _i64, _i64, _i64, _i64, _vp, _vp],
     "hba_hier_select_rows": [_i, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _f,
                              _vp, _vp, _vp],

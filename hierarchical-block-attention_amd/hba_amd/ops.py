@@ -228,19 +228,31 @@ def hier_select(q: Tensor, q_gain: Optional[Tensor], eps: float, S0: Tensor, S1:
     return _hier_select(q, q_gain, eps, S0, S1, window, k, fanout, beam, scale, None, None)
 
 
-def hier_select_with_scores(q, q_gain, eps, S0, S1, window, k, fanout, beam, scale):
+def hier_select_with_scores(q, q_gain, eps, S0, S1, window, k, fanout, beam, scale, grouped=True):
     """hier_select that also returns the fp32 scores it ranked: children of the
     kept supers [B, Hkv, n, nb] and candidate-bearing supers [B, Hkv, n, ns]
     (-inf elsewhere; the super array is filled by the bf16 GEMM path only).
-    The verification form, not a torch op."""
+    The verification form, not a torch op.  grouped=False scores the second
+    level per 64-query tile (no workspace)."""
     B, n = q.shape[0], q.shape[1]
     Hkv, nb, ns = S0.shape[1], S0.shape[2], S1.shape[2]
     scores = torch.full((B, Hkv, n, nb), float("-inf"), dtype=torch.float32, device=q.device)
     sup = torch.full((B, Hkv, n, ns), float("-inf"), dtype=torch.float32, device=q.device)
-    return (*_hier_select(q, q_gain, eps, S0, S1, window, k, fanout, beam, scale, scores, sup), scores, sup)
+    return (*_hier_select(q, q_gain, eps, S0, S1, window, k, fanout, beam, scale, scores, sup, grouped),
+            scores, sup)
 
 
-def _hier_select(q, q_gain, eps, S0, S1, window, k, fanout, beam, scale, scores, sup_scores):
+def hier_workspace_bytes(q, S0, k, fanout, beam):
+    """Workspace bytes of the grouped second level (0 where it does not apply)."""
+    B, n, Hq, d = q.shape
+    Hkv, m = S0.shape[1], S0.shape[3]
+    nbytes = ctypes.c_size_t(0)
+    check(lib().hba_hier_select_workspace_bytes(_code(q), B, n, Hq, Hkv, d, m, k, fanout, beam,
+                                                ctypes.byref(nbytes)), "hba_hier_select_workspace_bytes")
+    return int(nbytes.value)
+
+
+def _hier_select(q, q_gain, eps, S0, S1, window, k, fanout, beam, scale, scores, sup_scores, grouped=True):
     dev = _dev(q)
     _rows(q, "q")
     B, n, Hq, d = q.shape
@@ -251,10 +263,12 @@ def _hier_select(q, q_gain, eps, S0, S1, window, k, fanout, beam, scale, scores,
         raise ValueError("S0/S1 do not match q and fanout")
     qg = _f32c(q_gain, dev, Hq, "q_gain")
     idx, val, cnt = _sel_out(q, Hkv, k)
+    nbytes = hier_workspace_bytes(q, S0, k, fanout, beam) if grouped else 0
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev) if nbytes else None
     with torch.cuda.device(dev):
         st = lib().hba_hier_select(_code(q), _p(q), strides3(q), _p(qg), eps, _p(S0), _p(S1), B, n, Hq,
                                    Hkv, d, m, BLOCK, window, k, fanout, beam, scale, _p(idx), _p(val),
-                                   _p(cnt), _p(scores), _p(sup_scores), _stream(dev))
+                                   _p(cnt), _p(scores), _p(sup_scores), _p(ws), nbytes, _stream(dev))
     check(st, "hba_hier_select")
     return idx, val, cnt
 

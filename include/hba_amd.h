@@ -126,14 +126,27 @@ int hba_score_select(int dtype, const void *q, const int64_t q_strides[3],
  * kernel ranked a score: sup_scores fp32 [B, Hkv, n, ns] with the score of
  * every super holding a candidate child, scores fp32 [B, Hkv, n, n/Bk] with
  * the score of every candidate child of a kept super.  sup_scores is written
- * by the MFMA path only.
+ * by the MFMA path only.  workspace (16-byte aligned, no initial contents;
+ * NULL allowed): with at least hba_hier_select_workspace_bytes bytes, the
+ * bf16 descent scores its second level per group of a few hundred queries
+ * (each super's children loaded once for the group's queries that kept it);
+ * otherwise per 64-query tile.  The same picks either way.
  */
 int hba_hier_select(int dtype, const void *q, const int64_t q_strides[3],
                     const float *q_gain, float eps, const void *S0, const void *S1,
                     int64_t B, int64_t n, int64_t Hq, int64_t Hkv, int64_t d,
                     int64_t m, int64_t Bk, int64_t W, int64_t k, int64_t fanout,
                     int64_t beam, float scale, int32_t *idx, float *val, int32_t *cnt,
-                    float *scores, float *sup_scores, void *stream);
+                    float *scores, float *sup_scores, void *workspace, size_t ws_bytes,
+                    void *stream);
+
+/* Workspace bytes hba_hier_select can use for this geometry: bf16 with m == 4,
+ * k <= 32, fanout 4, 8 or 16 and min(beam, ns) * fanout <= 256, the routing
+ * queries (B*Hkv*n*d bf16) and the kept supers (B*Hkv*n*16 int16); 0 where
+ * the grouped second level does not apply. */
+int hba_hier_select_workspace_bytes(int dtype, int64_t B, int64_t n, int64_t Hq, int64_t Hkv,
+                                    int64_t d, int64_t m, int64_t k, int64_t fanout, int64_t beam,
+                                    size_t *bytes);
 
 /*
  * Routing queries: qg [B, n, Hkv, d] (contiguous, storage dtype) = per KV

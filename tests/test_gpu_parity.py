@@ -399,6 +399,37 @@ def test_hier_select_drop_in_any_mask(dev, dt, nb, F, beam, kk):
     assert (idx[:, 4] == -1).all()
 
 
+@pytest.mark.parametrize("n,F,beam,kk,B,dump", [(8192, 8, 4, 16, 1, True), (32768, 16, 8, 16, 2, True),
+                                                  (32768, 4, 16, 32, 1, True), (24576, 16, 3, 8, 1, True),
+                                                  (131072, 16, 8, 16, 1, False)])
+def test_hier_grouped_level2_equals_per_tile(dev, n, F, beam, kk, B, dump):
+    """The bf16 descent's second level scored per group of queries (with a
+    workspace: each super's children once for the group's queries that kept
+    it) and per 64-query tile give the same picks, values and counts, and the
+    same super and child score dumps: the same MFMA operands in the same
+    order, the same ranking rule.  Cases: fanout 4 / 8 / 16, beam 3 to 16,
+    k up to 32, two batches, n not a multiple of the group, 128K (picks
+    only: the dump would be 2 GB)."""
+    g = torch.Generator().manual_seed(n + F + beam)
+    Hkv, Hq, d, m, W = 2, 14, 64, 4, 1024
+    nb = n // 64
+    q = torch.randn(B, n, Hq, d, generator=g).to(torch.bfloat16).to(dev)
+    gq = torch.full((Hq,), d ** 0.25, device=dev)
+    S0 = (torch.randn(B, Hkv, nb, m, d, generator=g) * 0.5).to(torch.bfloat16).to(dev)
+    S1 = ops.build_super(S0, F)
+    assert ops.hier_workspace_bytes(q, S0, kk, F, beam) > 0   # the grouped path applies
+    if dump:
+        a = ops.hier_select_with_scores(q, gq, 1e-6, S0, S1, W, kk, F, beam, 0.125, grouped=True)
+        t = ops.hier_select_with_scores(q, gq, 1e-6, S0, S1, W, kk, F, beam, 0.125, grouped=False)
+    else:
+        a = ops._hier_select(q, gq, 1e-6, S0, S1, W, kk, F, beam, 0.125, None, None, grouped=True)
+        t = ops._hier_select(q, gq, 1e-6, S0, S1, W, kk, F, beam, 0.125, None, None, grouped=False)
+    torch.cuda.synchronize()
+    for x, y in zip(a, t):
+        assert torch.equal(x, y)
+    assert int(a[2].max()) == min(kk, min(beam, (nb + F - 1) // F) * F)
+
+
 def test_hier_select_threshold_overflow(dev):
     """A layout on which the by-super path's threshold admits more children
     than its 64-entry list: child c < 8 of super j scores 255 - 32 c - j
