@@ -710,14 +710,17 @@ __global__ __launch_bounds__(64) void decode_d3_kernel(const float *__restrict__
 // ============================================================================
 // bf16: the step in one launch.
 //
-// Grid (Bd, Hkv, nz), DF_NT threads.  Wave w of workgroup z of (s, g) runs
-// window/sink unit 8*z + w (if there is one).  Workgroups z < nsg also score
-// chunk z of cpb = DF_NT / m candidate pages (one slot row per thread; the
-// summary loads are issued before the window's) and publish the chunk's
-// top-K; the last of them to arrive at the (s, g) score counter merges the
-// lists (and writes sel_idx / sel_cnt), then runs the K routed pages,
-// ceil(K / 8) per wave.  Workgroup z folds its window units into one partial
-// state per head (an LSE merge over its waves) in workspace slot z, the
+// Grid (Bd, Hkv, nz), DF_NT threads.  Workgroups z < nsg score chunk z of
+// cpb = DF_NT / m candidate pages (one slot row per thread) and publish the
+// chunk's top-K; the last of them to arrive at the (s, g) score counter
+// merges the lists (and writes sel_idx / sel_cnt), then runs the K routed
+// pages, ceil(K / 8) per wave.  Wave w of workgroup z >= nsg runs window /
+// sink unit 8*(z - nsg) + w (if there is one): the score workgroups load only
+// what the selection needs, so that their summaries do not queue behind the
+// window pages, and the routing workgroup has no unit of its own between its
+// merge and the routed pages.  Workgroup z folds its window units into one
+// partial state per head (an LSE merge over its waves; none for a score
+// workgroup) in workspace slot z, the
 // routing workgroup its routed pages in slot nz (a slot of their own, so
 // that the merge order does not depend on which workgroup routes: the step
 // is deterministic); the last of the nz workgroups to arrive at the (s, g)
@@ -725,7 +728,7 @@ __global__ __launch_bounds__(64) void decode_d3_kernel(const float *__restrict__
 // workgroup waits for another (the last arrival does the dependent work), so
 // any dispatch order completes.  The counters are zero on entry and the last
 // arrival leaves them zero.  At 32 sequences of 16-32K tokens, 2 KV heads and
-// m = 4 the grid is 256 workgroups, one per CU.
+// m = 4 the grid is 448 workgroups (4 score + 3 unit workgroups per pair).
 // ============================================================================
 constexpr int DF_NT = 512;
 constexpr int DF_NW = DF_NT / 64;
@@ -738,7 +741,7 @@ struct DecFGeom {
     int nsg;       // score workgroups per (s, g): max(nsc, 1)
     int cpb;       // candidate pages per chunk: DF_NT / m
     int nwp;       // window page units; unit nwp is the sinks
-    int nz;        // workgroups per (s, g): max(nsg, ceil((nwp + 1) / DF_NW))
+    int nz;        // workgroups per (s, g): nsg score workgroups, then ceil((nwp + 1) / DF_NW) unit workgroups
     int64_t bmax;  // largest candidate page of any length up to lmax
     int64_t lmax;  // longest sequence the geometry (and the RoPE tables) cover
 };
@@ -751,7 +754,7 @@ __host__ __device__ inline DecFGeom dec_fgeom(int64_t W, int64_t m, int64_t max_
     gm.nsg = gm.nsc > 0 ? gm.nsc : 1;
     gm.nwp = (int)((W + 63) / 64) + 1;
     const int uwg = (gm.nwp + 1 + DF_NW - 1) / DF_NW;
-    gm.nz = gm.nsg > uwg ? gm.nsg : uwg;
+    gm.nz = gm.nsg + uwg;
     gm.lmax = max_len;
     return gm;
 }
@@ -978,8 +981,10 @@ __global__ __launch_bounds__(DF_NT) void decode_fused_kernel(
     const float scale = scales[s];
     const int64_t bmax = (L >= 1) ? cand_bmax(L - 1, BK, W) : 0;
     const int nsc_s = (int)((bmax + CPB - 1) / CPB);   // this sequence's chunks
-    // this wave's window / sink unit
-    const int u = z * DF_NW + w;
+    // this wave's window / sink unit (unit workgroups z >= nsg only: the
+    // score workgroups load just what the selection needs, and the routing
+    // one goes from its merge straight to the routed pages)
+    const int u = scorer ? gm.nwp + 1 : (z - gm.nsg) * DF_NW + w;
     int64_t lo = 0, hi = -1, page = 0;
     const bool any = u <= gm.nwp && dec_unit_range(u, L, S, W, gm.nwp, lo, hi, page);   // wave-uniform
     const bool rope = u < gm.nwp;
