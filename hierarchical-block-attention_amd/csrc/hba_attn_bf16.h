@@ -28,4 +28,18 @@ int launch_attn_bf16_routed(const void *q, const int64_t *qs, const float *qgain
                             int64_t n, int64_t Hq, int64_t Hkv, int64_t S, int64_t k, float scale, void *out,
                             const int64_t *os, const float *lse, hipStream_t s);
 
+// The query gradient of the union attention (bf16, d = 64, G <= 16, S <= 64;
+// HBA_ERR_UNSUPPORTED otherwise): dq (raw q) and the gain gradient added into
+// dq_gain, and for the key gradients the QKNorm'd and rotated rows (qc_ws,
+// qr_ws: bf16 [B, n, Hq, D]), the LSE and D (lse_ws, dd_ws: fp32 [B, Hq, n]).
+// kct, krt: kc and kr transposed, [B, Hkv, D, n]; v, out, dout as the
+// forward's inputs and output.
+template <int D>
+int launch_attn_bf16_dq(const void *q, const float *qgain, const float *kgain, float eps, const void *kc,
+                        const void *kr, const void *kct, const void *krt, const void *v, const float *cosT,
+                        const float *sinT, const int32_t *idx, const int32_t *cnt, const void *out,
+                        const void *dout, int64_t B, int64_t n, int64_t Hq, int64_t Hkv, int64_t S, int64_t W,
+                        int64_t k, float scale, void *qc_ws, void *qr_ws, float *lse_ws, float *dd_ws, void *dq,
+                        float *dq_gain, hipStream_t s);
+
 }  // namespace hba

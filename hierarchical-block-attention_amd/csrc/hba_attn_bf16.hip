@@ -779,6 +779,73 @@ __device__ __forceinline__ uint32_t bits_at(const uint32_t *row, int r0, int nw)
     return v & ((1u << P) - 1u);
 }
 
+// The union of the picks of a tile's QT queries (from i0, kk picks each) as
+// an ascending list of routed blocks (sel: the picks, invalid ones SENT;
+// bitmap and pre: the union as bits and the entries before each word), and
+// each pick as bits over the list's entries: per query (qbits) and per row
+// tile of QPT queries (wbits, nrt rows).  Returns the entry count (also in
+// nlist).  Called by the whole workgroup of NTHR threads; ends with a barrier.
+template <int NTHR>
+__device__ __forceinline__ int union_of_picks(const int32_t *__restrict__ idx, const int32_t *__restrict__ cnt,
+                                              int64_t bh, int64_t n, int64_t i0, int QT, int QPT, int nrt, int kk,
+                                              int64_t nb, int nbw, int16_t *sel, uint32_t *bitmap, int *pre,
+                                              int16_t *list, uint32_t *qbits, uint32_t *wbits, int &nlist) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    for (int e = tid; e < nbw; e += NTHR) bitmap[e] = 0u;
+    for (int e = tid; e < (QT + nrt) * nbw; e += NTHR) qbits[e] = 0u;   // wbits follow qbits
+    __syncthreads();
+    // one thread per (query, pick); invalid picks become SENT in place
+    for (int t = tid; t < QT * kk; t += NTHR) {
+        const int qq = t / kk, r = t - qq * kk;
+        const int64_t i = i0 + qq;
+        int v = SENT;
+        if (i < n && r < min(max(cnt[bh * n + i], 0), kk)) {
+            v = idx[(bh * n + i) * kk + r];
+            if (v < 1 || v >= nb) v = SENT;                // block 0 is never routed
+            else atomicOr(&bitmap[v >> 5], 1u << (v & 31));
+        }
+        sel[t] = (int16_t)v;
+    }
+    __syncthreads();
+    if (w == 0) {
+        int base = 0;
+        for (int w0 = 0; w0 < nbw; w0 += 64) {
+            uint32_t word = (w0 + lane < nbw) ? bitmap[w0 + lane] : 0u;
+            const int pc = __popc(word);
+            int incl = pc;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const int t = __shfl_up(incl, o, 64);
+                if (lane >= o) incl += t;
+            }
+            int off = base + incl - pc;
+            if (w0 + lane < nbw) pre[w0 + lane] = off;
+            while (word) {
+                const int bit = __ffs(word) - 1;
+                list[off++] = (int16_t)((w0 + lane) * 32 + bit);
+                word &= word - 1u;
+            }
+            base += __shfl(incl, 63, 64);
+        }
+        if (lane == 0) nlist = base;
+    }
+    __syncthreads();
+    const int ne = nlist;
+    auto entry_of = [&](int v) { return pre[v >> 5] + __popc(bitmap[v >> 5] & ((1u << (v & 31)) - 1u)); };
+    // each pick as a union entry index: its query's bits, and its row tile's
+    for (int t = tid; t < QT * kk; t += NTHR) {
+        const int v = sel[t];
+        if (v == SENT) continue;
+        const int qq = t / kk;
+        const int e = entry_of(v);
+        atomicOr(&qbits[qq * nbw + (e >> 5)], 1u << (e & 31));
+        atomicOr(&wbits[(qq / QPT) * nbw + (e >> 5)], 1u << (e & 31));   // row tile qq / QPT
+    }
+    __syncthreads();
+    return ne;
+}
+
 template <int D, int PTW, bool FIXED, bool S2, bool WIN>
 __device__ __forceinline__ void routed_body(
     const bf16_t *__restrict__ q, int64_t qsb, int64_t qsn, int64_t qsh, const float *__restrict__ qgain,
@@ -900,58 +967,8 @@ __device__ __forceinline__ void routed_body(
     }
 
     // ------------------------------------- selection lists and their union
-    for (int e = tid; e < nbw; e += C::NTHR) bitmap[e] = 0u;
-    for (int e = tid; e < (QT + C::WAVES * PTW) * nbw; e += C::NTHR) qbits[e] = 0u;
-    __syncthreads();
-    // one thread per (query, pick); invalid picks become SENT in place
-    for (int t = tid; t < QT * kk; t += C::NTHR) {
-        const int qq = t / kk, r = t - qq * kk;
-        const int64_t i = i0 + qq;
-        int v = SENT;
-        if (i < n && r < min(max(cnt[bh * n + i], 0), kk)) {
-            v = idx[(bh * n + i) * kk + r];
-            if (v < 1 || v >= nb) v = SENT;                // block 0 is never routed
-            else atomicOr(&bitmap[v >> 5], 1u << (v & 31));
-        }
-        sel[t] = (int16_t)v;
-    }
-    __syncthreads();
-    if (w == 0) {
-        int base = 0;
-        for (int w0 = 0; w0 < nbw; w0 += 64) {
-            uint32_t word = (w0 + lane < nbw) ? bitmap[w0 + lane] : 0u;
-            const int pc = __popc(word);
-            int incl = pc;
-#pragma unroll
-            for (int o = 1; o < 64; o <<= 1) {
-                const int t = __shfl_up(incl, o, 64);
-                if (lane >= o) incl += t;
-            }
-            int off = base + incl - pc;
-            if (w0 + lane < nbw) pre[w0 + lane] = off;
-            while (word) {
-                const int bit = __ffs(word) - 1;
-                list[off++] = (int16_t)((w0 + lane) * 32 + bit);
-                word &= word - 1u;
-            }
-            base += __shfl(incl, 63, 64);
-        }
-        if (lane == 0) nlist = base;
-    }
-    __syncthreads();
-    const int ne = nlist;
-    auto entry_of = [&](int v) { return pre[v >> 5] + __popc(bitmap[v >> 5] & ((1u << (v & 31)) - 1u)); };
-    // each pick as a union entry index: its query's bits, and its row tile's
-    for (int t = tid; t < QT * kk; t += C::NTHR) {
-        const int v = sel[t];
-        if (v == SENT) continue;
-        const int qq = t / kk;
-        const int e = entry_of(v);
-        atomicOr(&qbits[qq * nbw + (e >> 5)], 1u << (e & 31));
-        atomicOr(&wbits[(qq / QPT) * nbw + (e >> 5)], 1u << (e & 31));   // row tile qq / QPT
-    }
-
-    __syncthreads();
+    const int ne = union_of_picks<C::NTHR>(idx, cnt, bh, n, i0, QT, QPT, C::WAVES * PTW, kk, nb, nbw, sel, bitmap, pre,
+                                           list, qbits, wbits, nlist);
 
     // The ring holds NPH phases of PH blocks, with one barrier per phase: a
     // block's hits fall on few of the waves, and a phase of several blocks
@@ -1146,6 +1163,492 @@ __global__ __launch_bounds__(RtCfg<D>::NTHR, RtCfg<D>::NTHR / 256) void attn_rou
 }
 
 
+// ========================================== query gradient (backward) ====
+// bwd_dq_union_kernel: the query gradient of the union attention for bf16
+// inputs, on the forward's layout -- workgroup = (batch, KV head, QT
+// queries), 16-row tiles of the G heads of 16/G queries, PTW tiles per wave
+// -- so that each staged block serves every query of the tile that picked
+// it.  Per column (query i, head h) over its union U_i, with p the softmax,
+// D = <dO, O> and k the key the score was taken against:
+//   dP_j = <dO, v_j>,  ds_j = p_j (dP_j - D),  dq^ += scale sum_j ds_j k_j
+// (the gradient with respect to the QKNorm'd row; window keys give it in the
+// rotated frame).  Per 64-key block: S^T = K.Q^T and dP^T = V.dO^T (K and V
+// tiles, key rows in permk order, so that both accumulators come out in the
+// B-operand layout), then dq^T += K^T.dS^T (K^T tile).  A ring slot holds
+// the three tiles.  The window tiles (kr, krt; the RoPE operand) stream
+// first; rope^T then maps the column's partial sum back to the unrotated
+// frame in registers (a row element and its rotation partner sit in the same
+// lane) and the sinks and routed blocks (kc, kct; the NoPE operand, read back
+// from the rows this workgroup wrote at set-up) follow in the same softmax
+// state.  Softmax as the forward: the QKNorm bound as a fixed shift when it
+// holds, else a running max.  Outputs: dq (rope^T and the QKNorm backward
+// applied), the gain gradient (one atomic per head per workgroup), and for
+// the key-gradient kernels the QKNorm'd and rotated rows (bf16), the LSE
+// (natural log) and D.
+template <int D, int WAVES>
+struct DqCfg {
+    static constexpr int NKS = D / 32;
+    static constexpr int NDT = D / 16;
+    static constexpr int NTHR = WAVES * 64;
+    static constexpr int TILE = 64 * D;                   // bf16 elements of a K, V or K^T tile
+    static constexpr int SLOT = 3 * TILE;
+    static constexpr int KPARTS = TILE * 2 / 1024;        // 1 KB parts of a tile
+    static constexpr int NPARTS = 3 * KPARTS;
+    static constexpr int PPW = (NPARTS + WAVES - 1) / WAVES;   // DMA parts per wave per block, at most
+};
+
+enum { DQ_ALL = 0, DQ_COL = 1, DQ_RANGE = 2 };
+
+// The MFMA operand x * f, rounded to bf16 (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ bf16x8 scale8(bf16x8 x, float f) {
+    float y[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) y[e] = (float)x[e] * f;
+    return pack8(y);
+}
+
+// One staged block (K tile Ks, V tile Vk, K^T tile KT) against one 16-row
+// tile.  MODE DQ_ALL: every key of every column; DQ_COL: every key of the
+// columns whose query picked the block (colok); DQ_RANGE: keys jlo..jhi
+// (from the block's first key) of each column.  acc accumulates
+// sum_j p~_j (dP_j - D) k_j with p~ = exp2 of the score less the shift;
+// lsum (per lane: the lane's keys only) sum_j p~_j.  The V fragments are read
+// after the scores' exponentials, so that the K and V fragments are not live
+// together.
+template <int D, bool FIXED, int MODE>
+__device__ __forceinline__ void dq_update(const bf16_t *Ks, const bf16_t *Vk, const bf16_t *KT,
+                                          const bf16x8 (&qop)[D / 32], const bf16x8 (&dop)[D / 32], float Dh,
+                                          f32x4 (&acc)[D / 16], float &mrun, float &lsum, bool colok, int jlo,
+                                          int jhi, float sl2, float bl2, int l16, int lg) {
+    constexpr int NKS = D / 32, NDT = D / 16;
+    asm volatile("" ::: "memory");   // no fragment held over from the previous row tile
+    const bool cdead = MODE == DQ_COL && !colok;
+    const float c0 = FIXED ? (cdead ? -INFINITY : -bl2) : 0.0f;
+    const int sw = swzK(permk(0, l16));   // the same for every mt
+    f32x4 Sa[4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+        Sa[mt] = f32x4{c0, c0, c0, c0};
+        const int r = permk(mt, l16);
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) Sa[mt] = mma(ldb8(Ks + r * D + 8 * ((4 * ks + lg) ^ sw)), qop[ks], Sa[mt]);
+    }
+    float p[4][4];
+    if constexpr (FIXED) {
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int j = 32 * (mt >> 1) + 8 * lg + 4 * (mt & 1) + e;
+                const bool ok = (MODE != DQ_RANGE) || ((j >= jlo) & (j <= jhi));
+                p[mt][e] = ex2(ok ? Sa[mt][e] : -INFINITY);
+            }
+    } else {
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int j = 32 * (mt >> 1) + 8 * lg + 4 * (mt & 1) + e;
+                const bool ok = (MODE == DQ_RANGE) ? ((j >= jlo) & (j <= jhi)) : !cdead;
+                tmax = fmaxf(tmax, ok ? Sa[mt][e] : -INFINITY);
+            }
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        const float mnew = fmaxf(mrun, tmax * sl2);
+        const float shift = (mnew == -INFINITY) ? 0.0f : mnew;
+        const float alpha = ex2(mrun - shift);
+        mrun = mnew;
+        lsum *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) acc[dt] *= alpha;
+        const float sh = cdead ? INFINITY : shift;   // a dead column: every argument -inf
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int j = 32 * (mt >> 1) + 8 * lg + 4 * (mt & 1) + e;
+                const bool ok = (MODE != DQ_RANGE) || ((j >= jlo) & (j <= jhi));
+                p[mt][e] = ex2(ok ? fmaf(Sa[mt][e], sl2, -sh) : -INFINITY);
+            }
+    }
+    f32x4 Pa[4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+        Pa[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        const int r = permk(mt, l16);
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) Pa[mt] = mma(ldb8(Vk + r * D + 8 * ((4 * ks + lg) ^ sw)), dop[ks], Pa[mt]);
+    }
+    float ds[2][8];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            lsum += p[mt][e];
+            ds[mt >> 1][(mt & 1) * 4 + e] = p[mt][e] * (Pa[mt][e] - Dh);
+        }
+    const bf16x8 db0 = pack8(ds[0]), db1 = pack8(ds[1]);
+    const int swt = swzV(l16);   // swzV(16 dt + l16) for every dt
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+        const bf16_t *kp = KT + (16 * dt + l16) * 64;
+        acc[dt] = mma(ldb8(kp + 8 * (lg ^ swt)), db0, acc[dt]);
+        acc[dt] = mma(ldb8(kp + 8 * ((lg + 4) ^ swt)), db1, acc[dt]);
+    }
+}
+
+template <int D, int WAVES, int PTW, int NS, int PH, bool FIXED>
+__device__ __forceinline__ void dq_body(
+    const bf16_t *__restrict__ q, const float *__restrict__ qgain, float eps, const bf16_t *__restrict__ kc,
+    const bf16_t *__restrict__ kr, const bf16_t *__restrict__ kct, const bf16_t *__restrict__ krt,
+    const bf16_t *__restrict__ v, const float *__restrict__ cosT, const float *__restrict__ sinT,
+    const int32_t *__restrict__ idx, const int32_t *__restrict__ cnt, const bf16_t *__restrict__ out,
+    const bf16_t *__restrict__ dout, int64_t n, int Hq, int Hkv, int S, int W, int kk, float scale, float sl2,
+    float bl2, int combo, int tile, bf16_t *__restrict__ qc_ws, bf16_t *__restrict__ qr_ws,
+    float *__restrict__ lse_ws, float *__restrict__ dd_ws, bf16_t *__restrict__ dq, float *__restrict__ dq_gain,
+    char *smem, int &nlist) {
+    using C = DqCfg<D, WAVES>;
+    constexpr int NKS = C::NKS, NDT = C::NDT;
+    constexpr int P = PH, NPH = NS / PH, NPRO = (NPH - 1) * PH;
+    static_assert(NS % PH == 0 && NPH >= 2, "the ring holds whole phases, one of them ahead");
+    const int G = Hq / Hkv;
+    const int QPT = 16 / G;
+    const int QT = WAVES * PTW * QPT;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, l16 = lane & 15, lg = lane >> 4;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int b = combo / Hkv, g = combo % Hkv;
+    const int64_t i0 = (int64_t)tile * QT;
+    const int64_t bh = (int64_t)b * Hkv + g;
+    const int64_t nb = n / 64;
+    const int nbw = (int)((nb + 31) / 32);
+    int wt0 = 0, nwin = 0;   // the window tiles of the workgroup's queries
+    {
+        const int64_t ilast = ((i0 + QT < n) ? i0 + QT : n) - 1;
+        const int64_t kfirst = ((int64_t)S > i0 - W + 1) ? (int64_t)S : i0 - W + 1;
+        if (kfirst <= ilast) {
+            wt0 = (int)(kfirst / 64);
+            nwin = (int)(ilast / 64) - wt0 + 1;
+        }
+    }
+
+    // LDS: ring | sel [QT][kk] | bitmap [nbw] | pre [nbw] | list [nb] |
+    //      qbits [QT][nbw] | wbits [WAVES*PTW][nbw]
+    bf16_t *ring = reinterpret_cast<bf16_t *>(smem);
+    const uint32_t ring_lds = lds_offset(ring);
+    int16_t *sel = reinterpret_cast<int16_t *>(smem + (size_t)NS * C::SLOT * 2);
+    uint32_t *bitmap = reinterpret_cast<uint32_t *>(sel + ((QT * kk + 1) & ~1));
+    int *pre = reinterpret_cast<int *>(bitmap + nbw);
+    int16_t *list = reinterpret_cast<int16_t *>(pre + nbw);
+    uint32_t *qbits = reinterpret_cast<uint32_t *>(list + ((nb + 1) & ~1LL));
+    uint32_t *wbits = qbits + QT * nbw;
+
+    // A ring slot: K tile [64][D] (swzK), V tile [64][D] (swzK), K^T tile
+    // [D][64] (swzV), in 1 KB parts; part w + WAVES*pp is this wave's.  The
+    // sources at block 0 and the stride per block are set once; a window tile
+    // reads kr / krt (the same rows of the other tensor) instead of kc / kct.
+    const bf16_t *KC = kc + bh * n * D;
+    const bf16_t *KCT = kct + bh * D * n;
+    const bf16_t *VB = v + ((int64_t)b * n * Hkv + g) * D;   // v [B, n, Hkv, D]
+    const int64_t dkr = kr - kc, dkrt = krt - kct;
+    const bf16_t *dsrc[C::PPW];
+    int64_t dstr[C::PPW], drot[C::PPW];
+#pragma unroll
+    for (int pp = 0; pp < C::PPW; ++pp) {
+        const int part = w + WAVES * pp;
+        const int tl = part / C::KPARTS;            // 0: K, 1: V, 2: K^T, 3: none
+        const int pc = (part % C::KPARTS) * 64 + lane;
+        dsrc[pp] = KC;
+        dstr[pp] = 0;
+        drot[pp] = 0;
+        if (tl == 0) {
+            const int r = pc / (D / 8), c = (pc % (D / 8)) ^ swzK(pc / (D / 8));
+            dsrc[pp] = KC + r * D + 8 * c;
+            dstr[pp] = 64 * D;
+            drot[pp] = dkr;
+        } else if (tl == 1) {
+            const int r = pc / (D / 8), c = (pc % (D / 8)) ^ swzK(pc / (D / 8));
+            dsrc[pp] = VB + (int64_t)r * Hkv * D + 8 * c;
+            dstr[pp] = 64 * (int64_t)Hkv * D;
+        } else if (tl == 2) {
+            const int r = pc >> 3, c = (pc & 7) ^ swzV(pc >> 3);
+            dsrc[pp] = KCT + (int64_t)r * n + 8 * c;
+            dstr[pp] = 64;
+            drot[pp] = dkrt;
+        }
+    }
+    const int dpw = (C::NPARTS - w + WAVES - 1) / WAVES;   // this wave's DMA instructions per block
+    auto fill = [&](int blk, int slot, bool rope) {
+#pragma unroll
+        for (int pp = 0; pp < C::PPW; ++pp)
+            if (w + WAVES * pp < C::NPARTS)   // wave-uniform
+                dma16(dsrc[pp] + (int64_t)blk * dstr[pp] + (rope ? drot[pp] : 0),
+                      ring_lds + (uint32_t)(slot * C::SLOT * 2) + (uint32_t)(w + WAVES * pp) * 1024u);
+    };
+    // the first window tiles land during the set-up
+    for (int e = 0; e < nwin && e < NPRO; ++e) fill(wt0 + e, e, true);
+
+    // ----------------------------------------------------- per-row state --
+    const int qs = l16 / G;
+    const int hh = l16 % G;
+    const int h = g * G + hh;
+    const bool colv = l16 < QPT * G;
+    bf16x8 qop[PTW][NKS], dop[PTW][NKS];
+    f32x4 acc[PTW][NDT];
+    float mrun[PTW], lsum[PTW], Dh[PTW];
+    int64_t icol[PTW];
+    bool cok[PTW];
+#pragma unroll
+    for (int t = 0; t < PTW; ++t) {
+        icol[t] = i0 + (int64_t)(w * PTW + t) * QPT + qs;
+        cok[t] = colv && icol[t] < n;
+        mrun[t] = -INFINITY;
+        lsum[t] = 0.0f;
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) acc[t][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        const int64_t row = (((int64_t)b * n + (cok[t] ? icol[t] : 0)) * Hq + h) * D + 8 * lg;
+        float x[NKS][8];
+        qrow<D>(q, n * Hq * D, (int64_t)Hq * D, D, qgain, eps, b, icol[t], h, cok[t], lg, x);
+        bf16x8 qn[NKS], qr[NKS];   // the QKNorm'd row and its rotation (bf16-exact)
+        qpack<D>(x, cok[t], 1.0f, qn);
+        qpack_rope<D>(x, cosT, sinT, icol[t], cok[t], lg, 1.0f, qr);
+        float od = 0.0f;
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) {
+            if (cok[t]) {
+                *reinterpret_cast<u32x4 *>(qc_ws + row + 32 * ks) = __builtin_bit_cast(u32x4, qn[ks]);
+                *reinterpret_cast<u32x4 *>(qr_ws + row + 32 * ks) = __builtin_bit_cast(u32x4, qr[ks]);
+            }
+            qop[t][ks] = FIXED ? scale8(qr[ks], sl2) : qr[ks];
+            const u32x4 du = *reinterpret_cast<const u32x4 *>(dout + row + 32 * ks);
+            const u32x4 uo = *reinterpret_cast<const u32x4 *>(out + row + 32 * ks);
+            dop[t][ks] = cok[t] ? __builtin_bit_cast(bf16x8, du) : bf16x8{};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                od = fmaf(__uint_as_float(du[e] << 16), __uint_as_float(uo[e] << 16), od);
+                od = fmaf(__uint_as_float(du[e] & 0xffff0000u), __uint_as_float(uo[e] & 0xffff0000u), od);
+            }
+        }
+        od += __shfl_xor(od, 16, 64);
+        od += __shfl_xor(od, 32, 64);
+        Dh[t] = cok[t] ? od : 0.0f;
+        if (cok[t] && lg == 0) dd_ws[((int64_t)b * Hq + h) * n + icol[t]] = od;
+    }
+
+    // ------------------------------------- selection lists and their union
+    const int ne = union_of_picks<C::NTHR>(idx, cnt, bh, n, i0, QT, QPT, WAVES * PTW, kk, nb, nbw, sel, bitmap, pre,
+                                           list, qbits, wbits, nlist);
+
+    // ----------------------------------------- window tiles (RoPE operand)
+    for (int e0 = 0; e0 < nwin; e0 += P) {
+        const int issued = min(nwin, e0 + NPRO);
+        wait_vm_n(max(0, issued - (e0 + P)) * dpw);
+        __syncthreads();   // every share of this phase landed; the previous phase consumed
+        const int nf = min(nwin, e0 + NPH * P);
+        for (int e = issued; e < nf; ++e) fill(wt0 + e, e % NS, true);
+        const int e1 = min(nwin, e0 + P);
+#pragma nounroll
+        for (int e = e0; e < e1; ++e) {
+            const bf16_t *Ks = ring + (e % NS) * C::SLOT;
+            const int64_t kb = (int64_t)(wt0 + e) * 64;
+#pragma unroll
+            for (int tt = 0; tt < PTW; ++tt) {
+                const int64_t qa = i0 + (int64_t)(w * PTW + tt) * QPT;
+                if (qa >= n) break;
+                const int64_t qb = (qa + QPT - 1 < n) ? qa + QPT - 1 : n - 1;
+                const int64_t loa = ((int64_t)S > qa - W + 1) ? (int64_t)S : qa - W + 1;
+                const int64_t lob = ((int64_t)S > qb - W + 1) ? (int64_t)S : qb - W + 1;
+                if (kb > qb || kb + 63 < loa) continue;   // no column has a window key here
+                const bool full = kb >= lob && kb + 63 <= qa;
+                const int64_t lo = ((int64_t)S > icol[tt] - W + 1) ? (int64_t)S : icol[tt] - W + 1;
+                const int64_t jlo = lo - kb, jhi = cok[tt] ? icol[tt] - kb : -1;
+                // a full tile as the range 0..63 (one inlined copy of the update)
+                dq_update<D, FIXED, DQ_RANGE>(Ks, Ks + C::TILE, Ks + 2 * C::TILE, qop[tt], dop[tt], Dh[tt], acc[tt],
+                                              mrun[tt], lsum[tt], true,
+                                              full ? 0 : (int)(jlo < 0 ? 0 : (jlo > 64 ? 64 : jlo)),
+                                              full ? 63 : (int)(jhi < -1 ? -1 : (jhi > 63 ? 63 : jhi)), sl2, bl2,
+                                              l16, lg);
+            }
+        }
+    }
+
+    // ------------------- back to the unrotated frame; the NoPE operand
+    __syncthreads();   // every wave is done with the ring
+    const int hs = (S > 0) ? 1 : 0;   // stream entry 0 is the sink block when there are sinks
+    const int ntot = hs + ne;
+    auto sblk = [&](int c) { return (c < hs) ? 0 : (int)list[c - hs]; };
+    for (int c = 0; c < ntot && c < NPRO; ++c) fill(sblk(c), c, false);
+#pragma unroll
+    for (int t = 0; t < PTW; ++t) {
+        const int64_t ii = cok[t] ? icol[t] : 0;
+        // rope^T(z) = z cos + rot^T(z sin), rot^T([z1, z2]) = [z2, -z1]: element
+        // d = 16 dt + 4 lg + e and its partner d ^ D/2 (dt ^ NDT/2) in this lane
+        float cs[NDT][4], sn[NDT][4];
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) {
+            const float4 c4 = *reinterpret_cast<const float4 *>(cosT + ii * D + 16 * dt + 4 * lg);
+            const float4 s4 = *reinterpret_cast<const float4 *>(sinT + ii * D + 16 * dt + 4 * lg);
+            cs[dt][0] = c4.x, cs[dt][1] = c4.y, cs[dt][2] = c4.z, cs[dt][3] = c4.w;
+            sn[dt][0] = s4.x, sn[dt][1] = s4.y, sn[dt][2] = s4.z, sn[dt][3] = s4.w;
+#pragma unroll
+            for (int e = 0; e < 4; e += 2) {
+                rnd_bf16_pair(cs[dt][e], cs[dt][e + 1]);
+                rnd_bf16_pair(sn[dt][e], sn[dt][e + 1]);
+            }
+        }
+        f32x4 y[NDT];
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int pd = dt ^ (NDT / 2);
+                const float zp = acc[t][pd][e] * sn[pd][e];
+                y[dt][e] = acc[t][dt][e] * cs[dt][e] + ((dt < NDT / 2) ? zp : -zp);
+            }
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) acc[t][dt] = y[dt];
+        const bf16_t *src = qc_ws + (((int64_t)b * n + ii) * Hq + h) * D + 8 * lg;
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) {
+            const bf16x8 qv = ldb8(src + 32 * ks);
+            qop[t][ks] = cok[t] ? (FIXED ? scale8(qv, sl2) : qv) : bf16x8{};
+        }
+    }
+
+    // ------------------------------ sinks and routed blocks (NoPE operand)
+    for (int c0 = 0; c0 < ntot; c0 += P) {
+        const int issued = min(ntot, c0 + NPRO);
+        wait_vm_n(max(0, issued - (c0 + P)) * dpw);
+        __syncthreads();
+        const int nf = min(ntot, c0 + NPH * P);
+        int nxt[P];   // the refill's block ids, read before the first DMA is issued
+#pragma unroll
+        for (int j = 0; j < P; ++j) nxt[j] = (issued + j < nf) ? sblk(issued + j) : 0;
+#pragma unroll
+        for (int j = 0; j < P; ++j)
+            if (issued + j < nf) fill(nxt[j], (issued + j) % NS, false);
+#pragma unroll
+        for (int tt = 0; tt < PTW; ++tt) {
+            const int rt = w * PTW + tt;
+            if (i0 + (int64_t)rt * QPT >= n) break;
+            uint32_t hits = __builtin_amdgcn_readfirstlane(bits_at<P>(wbits + rt * nbw, c0 - hs, nbw));
+            if (c0 < hs) hits |= 1u;   // the sink block: every row tile
+            const uint32_t qw = cok[tt] ? bits_at<P>(qbits + (rt * QPT + qs) * nbw, c0 - hs, nbw) : 0u;
+            while (hits) {
+                const int j = __builtin_ctz(hits);
+                hits &= hits - 1u;
+                const int c = c0 + j;
+                const bf16_t *Ks = ring + (c % NS) * C::SLOT;
+                if (c < hs) {   // keys j < S and j <= i
+                    const int64_t jh = (icol[tt] < (int64_t)S - 1) ? icol[tt] : (int64_t)S - 1;
+                    dq_update<D, FIXED, DQ_RANGE>(Ks, Ks + C::TILE, Ks + 2 * C::TILE, qop[tt], dop[tt], Dh[tt],
+                                                  acc[tt], mrun[tt], lsum[tt], true, 0, cok[tt] ? (int)jh : -1, sl2,
+                                                  bl2, l16, lg);
+                } else {
+                    dq_update<D, FIXED, DQ_COL>(Ks, Ks + C::TILE, Ks + 2 * C::TILE, qop[tt], dop[tt], Dh[tt],
+                                                acc[tt], mrun[tt], lsum[tt], (qw >> j) & 1u, 0, 63, sl2, bl2, l16, lg);
+                }
+            }
+        }
+    }
+
+    // ------------- LSE, dq = QKNorm backward of scale * acc / l, gain sums
+    float gq[PTW];
+#pragma unroll
+    for (int t = 0; t < PTW; ++t) {
+        float l = lsum[t];
+        l += __shfl_xor(l, 16, 64);
+        l += __shfl_xor(l, 32, 64);
+        const float sh = FIXED ? bl2 : mrun[t];
+        if (cok[t] && lg == 0)
+            lse_ws[((int64_t)b * Hq + h) * n + icol[t]] = (l > 0.0f) ? (sh + __log2f(l)) / LOG2E : INFINITY;
+        const float f = (l > 0.0f) ? scale / l : 0.0f;
+        const int64_t row = (((int64_t)b * n + (cok[t] ? icol[t] : 0)) * Hq + h) * D;
+        float xr[NDT][4], yv[NDT][4];
+        float ss = 0.0f, yx = 0.0f;
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) {
+            const u32x2 u = *reinterpret_cast<const u32x2 *>(q + row + 16 * dt + 4 * lg);
+            xr[dt][0] = __uint_as_float(u[0] << 16);
+            xr[dt][1] = __uint_as_float(u[0] & 0xffff0000u);
+            xr[dt][2] = __uint_as_float(u[1] << 16);
+            xr[dt][3] = __uint_as_float(u[1] & 0xffff0000u);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                yv[dt][e] = acc[t][dt][e] * f;
+                ss = fmaf(xr[dt][e], xr[dt][e], ss);
+                yx = fmaf(yv[dt][e], xr[dt][e], yx);
+            }
+        }
+        ss += __shfl_xor(ss, 16, 64);
+        ss += __shfl_xor(ss, 32, 64);
+        yx += __shfl_xor(yx, 16, 64);
+        yx += __shfl_xor(yx, 32, 64);
+        const float ms = ss / (float)D;
+        const float rq = sqrtf(fmaxf(ms, eps));
+        if (qgain) {
+            const float gn = qgain[h];
+            const float corr = (ms >= eps) ? gn * yx / ((float)D * rq * rq * rq) : 0.0f;
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) yv[dt][e] = (gn / rq) * yv[dt][e] - xr[dt][e] * corr;
+        }
+        gq[t] = cok[t] ? yx / rq : 0.0f;
+        if (cok[t]) {
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt) {
+                u32x2 u;
+                u[0] = (uint32_t)f2bf(yv[dt][0]) | ((uint32_t)f2bf(yv[dt][1]) << 16);
+                u[1] = (uint32_t)f2bf(yv[dt][2]) | ((uint32_t)f2bf(yv[dt][3]) << 16);
+                *reinterpret_cast<u32x2 *>(dq + row + 16 * dt + 4 * lg) = u;
+            }
+        }
+    }
+    if (qgain && dq_gain) {   // workgroup-uniform: per head over the workgroup's columns, one atomic each
+        float *gs = reinterpret_cast<float *>(smem);   // the ring, once every wave is done with it: [WAVES * PTW][16]
+        __syncthreads();
+#pragma unroll
+        for (int t = 0; t < PTW; ++t)
+            if (lg == 0) gs[(w * PTW + t) * 16 + l16] = gq[t];
+        __syncthreads();
+        if (tid < G) {
+            float sum = 0.0f;
+            for (int r = 0; r < WAVES * PTW; ++r)
+                for (int qq = 0; qq < QPT; ++qq) sum += gs[r * 16 + qq * G + tid];
+            unsafeAtomicAdd(&dq_gain[g * G + tid], sum);
+        }
+    }
+}
+
+template <int D, int WAVES, int PTW, int NS, int PH>
+__global__ __launch_bounds__(WAVES * 64, WAVES / 4) void bwd_dq_union_kernel(
+    const bf16_t *__restrict__ q, const float *__restrict__ qgain, const float *__restrict__ kgain, float eps,
+    const bf16_t *__restrict__ kc, const bf16_t *__restrict__ kr, const bf16_t *__restrict__ kct,
+    const bf16_t *__restrict__ krt, const bf16_t *__restrict__ v, const float *__restrict__ cosT,
+    const float *__restrict__ sinT, const int32_t *__restrict__ idx, const int32_t *__restrict__ cnt,
+    const bf16_t *__restrict__ out, const bf16_t *__restrict__ dout, int64_t n, int Hq, int Hkv, int S, int W,
+    int kk, float scale, int ntiles, int Cn, int xmap, bf16_t *__restrict__ qc_ws, bf16_t *__restrict__ qr_ws,
+    float *__restrict__ lse_ws, float *__restrict__ dd_ws, bf16_t *__restrict__ dq, float *__restrict__ dq_gain) {
+    extern __shared__ __align__(16) char smem[];
+    __shared__ int nlist;
+    int combo, tile;
+    xcd_map(blockIdx.x, Cn, ntiles, xmap, combo, tile);
+    if (tile >= ntiles || combo >= Cn) return;
+    const int G = Hq / Hkv;
+    const float sl2 = scale * LOG2E;
+    float bl2;
+    if (group_bound(qgain, kgain, combo % Hkv, G, sl2, D, bl2))
+        dq_body<D, WAVES, PTW, NS, PH, true>(q, qgain, eps, kc, kr, kct, krt, v, cosT, sinT, idx, cnt, out, dout, n,
+                                             Hq, Hkv, S, W, kk, scale, sl2, bl2, combo, tile, qc_ws, qr_ws, lse_ws,
+                                             dd_ws, dq, dq_gain, smem, nlist);
+    else
+        dq_body<D, WAVES, PTW, NS, PH, false>(q, qgain, eps, kc, kr, kct, krt, v, cosT, sinT, idx, cnt, out, dout,
+                                              n, Hq, Hkv, S, W, kk, scale, sl2, bl2, combo, tile, qc_ws, qr_ws,
+                                              lse_ws, dd_ws, dq, dq_gain, smem, nlist);
+}
+
 // ============================================================ launchers ====
 static void grid_map(int64_t Cn, int64_t ntiles, int &xmap, int64_t &grid) {
     if (8 % Cn == 0) {
@@ -1249,6 +1752,44 @@ static int launch_routed(const void *q, const int64_t *qs, const float *qgain, c
     return HBA_ERR_UNSUPPORTED;
 }
 
+template <int D, int WAVES, int PTW, int NS>
+static size_t dq_lds(int64_t n, int64_t G, int64_t k) {
+    using C = DqCfg<D, WAVES>;
+    const int64_t QT = (int64_t)WAVES * PTW * (16 / G);
+    const int64_t nb = n / 64;
+    const int64_t nbw = (nb + 31) / 32;
+    return (size_t)NS * C::SLOT * 2 + (size_t)((QT * k + 1) & ~1LL) * 2 + (size_t)nbw * 8 +
+           (size_t)((nb + 1) & ~1LL) * 2 + (size_t)(QT + WAVES * PTW) * nbw * 4 + 16;
+}
+
+template <int D, int WAVES, int PTW, int NS, int PH>
+static int launch_dq_t(const void *q, const float *qgain, const float *kgain, float eps, const void *kc,
+                       const void *kr, const void *kct, const void *krt, const void *v, const float *cosT,
+                       const float *sinT, const int32_t *idx, const int32_t *cnt, const void *out, const void *dout,
+                       int64_t B, int64_t n, int64_t Hq, int64_t Hkv, int64_t S, int64_t W, int64_t k, float scale,
+                       void *qc_ws, void *qr_ws, float *lse_ws, float *dd_ws, void *dq, float *dq_gain,
+                       hipStream_t s) {
+    const int64_t G = Hq / Hkv;
+    const size_t lds = dq_lds<D, WAVES, PTW, NS>(n, G, k);
+    const int64_t QT = (int64_t)WAVES * PTW * (16 / G);
+    const int64_t ntiles = (n + QT - 1) / QT;
+    int xmap;
+    int64_t grid;
+    grid_map(B * Hkv, ntiles, xmap, grid);
+    if (grid > 0x7fffffff) return HBA_ERR_UNSUPPORTED;
+    const int Wc = (int)((W < n + 1) ? W : n + 1);     // a window longer than the sequence is the sequence
+    auto kern = &bwd_dq_union_kernel<D, WAVES, PTW, NS, PH>;
+    if (hipFuncSetAttribute(reinterpret_cast<const void *>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)lds) != hipSuccess)
+        return HBA_ERR_LAUNCH;
+    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(WAVES * 64), lds, s, (const bf16_t *)q, qgain, kgain, eps,
+                       (const bf16_t *)kc, (const bf16_t *)kr, (const bf16_t *)kct, (const bf16_t *)krt,
+                       (const bf16_t *)v, cosT, sinT, idx, cnt, (const bf16_t *)out, (const bf16_t *)dout, n,
+                       (int)Hq, (int)Hkv, (int)S, Wc, (int)k, scale, (int)ntiles, (int)(B * Hkv), xmap,
+                       (bf16_t *)qc_ws, (bf16_t *)qr_ws, lse_ws, dd_ws, (bf16_t *)dq, dq_gain);
+    return HBA_OK;
+}
+
 }  // namespace ab
 
 template <int D>
@@ -1288,6 +1829,39 @@ int launch_attn_bf16(const void *q, const int64_t *qs, const float *qgain, const
     return launch_routed<D, true>(q, qs, qgain, kgain, eps, kc, vt, idx, cnt, B, n, Hq, Hkv, S, k, scale, out, os,
                                   nullptr, kr, cosT, sinT, W, qrw, s);
 }
+
+template <int D>
+int launch_attn_bf16_dq(const void *q, const float *qgain, const float *kgain, float eps, const void *kc,
+                        const void *kr, const void *kct, const void *krt, const void *v, const float *cosT,
+                        const float *sinT, const int32_t *idx, const int32_t *cnt, const void *out,
+                        const void *dout, int64_t B, int64_t n, int64_t Hq, int64_t Hkv, int64_t S, int64_t W,
+                        int64_t k, float scale, void *qc_ws, void *qr_ws, float *lse_ws, float *dd_ws, void *dq,
+                        float *dq_gain, hipStream_t s) {
+    using namespace ab;
+    const int64_t G = Hq / Hkv;
+    if (D != 64 || G > 16 || S > 64 || n % 64 || n / 64 >= SENT) return HBA_ERR_UNSUPPORTED;
+    constexpr size_t LDS_MAX = 160 * 1024 - 64;   // 64 bytes for the static nlist
+    // d = 64: 16 waves (4 per SIMD, within 128 VGPRs) of one row tile, 32
+    // queries at G = 7; a 6-slot ring (3 blocks per phase) when the selection
+    // lists fit beside it, else 4 slots.  Measured at 32K (whole backward):
+    // 16 x 1 3.74 ms, 12 waves x 2 tiles 4.11, 8 x 3 4.09 (2 waves per SIMD
+    // leave the update's LDS and MFMA latencies exposed); 16 x 1 with 2-block
+    // phases 4.00, with a 4-slot ring 3.90
+    if (dq_lds<64, 16, 1, 6>(n, G, k) <= LDS_MAX)
+        return launch_dq_t<64, 16, 1, 6, 3>(q, qgain, kgain, eps, kc, kr, kct, krt, v, cosT, sinT, idx, cnt, out,
+                                           dout, B, n, Hq, Hkv, S, W, k, scale, qc_ws, qr_ws, lse_ws, dd_ws, dq,
+                                           dq_gain, s);
+    if (dq_lds<64, 16, 1, 4>(n, G, k) <= LDS_MAX)
+        return launch_dq_t<64, 16, 1, 4, 2>(q, qgain, kgain, eps, kc, kr, kct, krt, v, cosT, sinT, idx, cnt, out,
+                                           dout, B, n, Hq, Hkv, S, W, k, scale, qc_ws, qr_ws, lse_ws, dd_ws, dq,
+                                           dq_gain, s);
+    return HBA_ERR_UNSUPPORTED;
+}
+template int launch_attn_bf16_dq<64>(const void *, const float *, const float *, float, const void *, const void *,
+                                     const void *, const void *, const void *, const float *, const float *,
+                                     const int32_t *, const int32_t *, const void *, const void *, int64_t, int64_t,
+                                     int64_t, int64_t, int64_t, int64_t, int64_t, float, void *, void *, float *,
+                                     float *, void *, float *, hipStream_t);
 
 #define HBA_INST_WIN(D)                                                                                       \
     template int launch_attn_bf16_window<D>(const void *, const int64_t *, const float *, const float *, float, \

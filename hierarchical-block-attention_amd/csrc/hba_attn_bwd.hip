@@ -35,7 +35,11 @@
 // and bwd_dkv_fin (rope^T and the QKNorm backward of the key rows); a second
 // bwd_dkv_mfma launch takes the sink keys.  The fp32 path takes the sink keys
 // in bwd_sink.  Both split the sink keys' query rows over workgroups.
+#include <cstdlib>
+#include <cstring>
+
 #include "hba_abi.h"
+#include "hba_attn_bf16.h"
 #include "hba_common.h"
 
 namespace hba {
@@ -1278,6 +1282,15 @@ __global__ __launch_bounds__(256) void bwd_dkv_fin_kernel(
 
 using namespace hba;
 
+// The bf16 query gradient: the union kernel (launch_attn_bf16_dq: 64 queries
+// per workgroup sharing each staged block) where it takes the geometry, else
+// bwd_dq_mfma.  HBA_BWD_DQ_KERNEL=pair in the environment selects
+// bwd_dq_mfma (16/G queries per wave) everywhere.
+static bool bwd_dq_union_on() {
+    const char *e = getenv("HBA_BWD_DQ_KERNEL");
+    return !(e && !strcmp(e, "pair"));
+}
+
 // Workspace of hba_attn_bwd: the query rows in the storage type (QKNorm'd,
 // rotated), LSE and D per (head, row), the fp32 sink accumulators
 // [B, Hkv, 2, 64, d]; on the bf16 path also the transposed keys kct, krt
@@ -1378,11 +1391,21 @@ extern "C" int hba_attn_bwd(int dtype, const void *q, const void *k, const void 
         if constexpr (DT == 1) {                                                                                \
             hipLaunchKernelGGL((bw::bwd_kt_kernel<D>), dim3((unsigned)g2), dim3(256), 0, s, (const bf16_t *)kc,  \
                                (const bf16_t *)kr, kct, krt, n, dkv_acc);                                        \
-            hipLaunchKernelGGL((bw::bwd_dq_mfma_kernel<D>), dim3((unsigned)g1q), dim3(256), 0, s,                \
-                               (const bf16_t *)q, (const bf16_t *)kc, (const bf16_t *)kr, kct, krt,             \
-                               (const bf16_t *)v, q_gain, eps, cos_tab, sin_tab, idx, cnt, (const bf16_t *)out,  \
-                               (const bf16_t *)dout, (int)B, n, (int)Hq, (int)Hkv, (int)S, W, (int)k_blocks,     \
-                               scale, qpw, qcb_ws, qrb_ws, lse_ws, dd_ws, sink_acc, (bf16_t *)dq, dq_gain);      \
+            int dqs = HBA_ERR_UNSUPPORTED;                                                                      \
+            if constexpr (D == 64)                                                                              \
+                if (bwd_dq_union_on())                                                                              \
+                    dqs = launch_attn_bf16_dq<D>(q, q_gain, k_gain, eps, kc, kr, kct, krt, v, cos_tab, sin_tab,  \
+                                                 idx, cnt, out, dout, B, n, Hq, Hkv, S, W, k_blocks, scale,      \
+                                                 qcb_ws, qrb_ws, lse_ws, dd_ws, dq, dq_gain, s);                 \
+            if (dqs == HBA_ERR_UNSUPPORTED)                                                                     \
+                hipLaunchKernelGGL((bw::bwd_dq_mfma_kernel<D>), dim3((unsigned)g1q), dim3(256), 0, s,            \
+                                   (const bf16_t *)q, (const bf16_t *)kc, (const bf16_t *)kr, kct, krt,         \
+                                   (const bf16_t *)v, q_gain, eps, cos_tab, sin_tab, idx, cnt,                  \
+                                   (const bf16_t *)out, (const bf16_t *)dout, (int)B, n, (int)Hq, (int)Hkv,     \
+                                   (int)S, W, (int)k_blocks, scale, qpw, qcb_ws, qrb_ws, lse_ws, dd_ws,         \
+                                   sink_acc, (bf16_t *)dq, dq_gain);                                            \
+            else if (dqs != HBA_OK)                                                                             \
+                return dqs;                                                                                     \
         } else if (Hq / Hkv <= 8)                                                                               \
             hipLaunchKernelGGL((bw::bwd_dq_kernel<DT, D, 8>), dim3((unsigned)g1), dim3(256), 0, s,               \
                                (const T *)q, (const T *)kc, (const T *)kr, (const T *)v, q_gain, eps, cos_tab,   \
