@@ -491,7 +491,8 @@ def bench_bwd32k(dev, reps=5):
                        "teacher_TFLOPs": round(teacher_flop / (aux_ms * 1e-3) / 1e12, 2),
                        "what": "hba_aux_kl: QKNorm'd queries, block scores, the teacher's block LSEs on MFMA over "
                                "every candidate key, the KL rows, d aux / d probes and d proj (median of 3)"},
-            "kernels": "bwd_kt (transposed keys) + bwd_dq_mfma (16/G queries per wave, 64-key units on MFMA) + "
+            "kernels": "bwd_kt (transposed keys) + bwd_dq_union_kernel (32 queries per workgroup, each staged "
+                       "64-key block's K, V and K^T tiles shared through an LDS ring, MFMA) + "
                        "bwd_dkv_mfma (one workgroup per KV head, 64-key block and 4096-row range, 64-pair tiles "
                        "on MFMA; a second launch for the sink keys) + bwd_dkv_fin (rope^T, QKNorm backward)"}
 
