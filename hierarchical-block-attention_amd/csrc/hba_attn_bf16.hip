@@ -237,12 +237,15 @@ template <int D>
 struct RtCfg {
     static constexpr int NKS = D / 32;
     static constexpr int NDT = D / 16;
-    // d = 64: 16 waves (4 per SIMD) of 2 row tiles each, within 128 VGPRs.
-    // d = 128: 8 waves (2 per SIMD) of 3 row tiles within 256 VGPRs, so that a
-    // workgroup covers 48 queries and each staged block serves more of them.
-    static constexpr int WAVES = (D == 64) ? 16 : 8;
+    // 16 waves (4 per SIMD) within 128 VGPRs: 2 row tiles each at d = 64, 1
+    // at d = 128 (32 queries per workgroup).  At d = 128, 8 waves (2 per SIMD)
+    // of 3 row tiles within 256 VGPRs cover 48 queries, so that each staged
+    // block serves more of them, but leave the update's LDS and MFMA
+    // latencies exposed: the 64K donor-shaped attention took 13.62 ms that
+    // way against 13.35 ms.
+    static constexpr int WAVES = 16;
     static constexpr int NTHR = WAVES * 64;
-    static constexpr int PTW = (D == 64) ? 2 : 3;      // max 16-row tiles per wave
+    static constexpr int PTW = (D == 64) ? 2 : 1;      // max 16-row tiles per wave
     static constexpr int SLOT = 2 * 64 * D;            // bf16 per ring slot (K + V^T)
     static constexpr int NS = (D == 64) ? 8 : 4;       // ring depth (blocks, 128 KB)
     static constexpr int PH = NS / 2;                  // blocks per barrier phase
