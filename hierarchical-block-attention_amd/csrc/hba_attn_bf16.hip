@@ -788,11 +788,27 @@ __device__ __forceinline__ uint32_t bits_at(const uint32_t *row, int r0, int nw)
 // each pick as bits over the list's entries: per query (qbits) and per row
 // tile of QPT queries (wbits, nrt rows).  Returns the entry count (also in
 // nlist).  Called by the whole workgroup of NTHR threads; ends with a barrier.
+// pk: this thread's first pick (t = threadIdx.x) as pick_load left it, so
+// that its loads can go out before the caller's other set-up.
+struct Pick {
+    int v, c;   // idx and cnt entries (SENT, 0 past the tile or the sequence)
+};
+__device__ __forceinline__ Pick pick_load(const int32_t *__restrict__ idx, const int32_t *__restrict__ cnt, int64_t bh,
+                                          int64_t n, int64_t i0, int QT, int kk) {
+    const int t = threadIdx.x, qq = t / kk, r = t - qq * kk;
+    const int64_t i = i0 + qq;
+    Pick pk{SENT, 0};
+    if (t < QT * kk && i < n) {   // two independent loads
+        pk.c = cnt[bh * n + i];
+        pk.v = idx[(bh * n + i) * kk + r];
+    }
+    return pk;
+}
 template <int NTHR>
 __device__ __forceinline__ int union_of_picks(const int32_t *__restrict__ idx, const int32_t *__restrict__ cnt,
                                               int64_t bh, int64_t n, int64_t i0, int QT, int QPT, int nrt, int kk,
                                               int64_t nb, int nbw, int16_t *sel, uint32_t *bitmap, int *pre,
-                                              int16_t *list, uint32_t *qbits, uint32_t *wbits, int &nlist) {
+                                              int16_t *list, uint32_t *qbits, uint32_t *wbits, int &nlist, Pick pk) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     for (int e = tid; e < nbw; e += NTHR) bitmap[e] = 0u;
@@ -802,12 +818,15 @@ __device__ __forceinline__ int union_of_picks(const int32_t *__restrict__ idx, c
     for (int t = tid; t < QT * kk; t += NTHR) {
         const int qq = t / kk, r = t - qq * kk;
         const int64_t i = i0 + qq;
-        int v = SENT;
-        if (i < n && r < min(max(cnt[bh * n + i], 0), kk)) {
-            v = idx[(bh * n + i) * kk + r];
-            if (v < 1 || v >= nb) v = SENT;                // block 0 is never routed
-            else atomicOr(&bitmap[v >> 5], 1u << (v & 31));
+        int v = pk.v, c = pk.c;
+        if (t != tid) {
+            c = (i < n) ? cnt[bh * n + i] : 0;
+            v = (i < n) ? idx[(bh * n + i) * kk + r] : SENT;
         }
+        if (i < n && r < min(max(c, 0), kk) && v >= 1 && v < nb)   // block 0 is never routed
+            atomicOr(&bitmap[v >> 5], 1u << (v & 31));
+        else
+            v = SENT;
         sel[t] = (int16_t)v;
     }
     __syncthreads();
@@ -930,6 +949,9 @@ __device__ __forceinline__ void routed_body(
     if (S > 0) fill(0, C::NS - 1, false);
     if (S2) fill(1, C::NS - 2, false);
 
+    // this thread's first pick, loaded before the query rows
+    const Pick pk = pick_load(idx, cnt, bh, n, i0, QT, kk);
+
     // ----------------------------------------------------- per-row state --
     // (first, so that the query loads overlap the selection set-up)
     const int qs = l16 / G;
@@ -971,7 +993,7 @@ __device__ __forceinline__ void routed_body(
 
     // ------------------------------------- selection lists and their union
     const int ne = union_of_picks<C::NTHR>(idx, cnt, bh, n, i0, QT, QPT, C::WAVES * PTW, kk, nb, nbw, sel, bitmap, pre,
-                                           list, qbits, wbits, nlist);
+                                           list, qbits, wbits, nlist, pk);
 
     // The ring holds NPH phases of PH blocks, with one barrier per phase: a
     // block's hits fall on few of the waves, and a phase of several blocks
@@ -1391,6 +1413,7 @@ __device__ __forceinline__ void dq_body(
     };
     // the first window tiles land during the set-up
     for (int e = 0; e < nwin && e < NPRO; ++e) fill(wt0 + e, e, true);
+    const Pick pk = pick_load(idx, cnt, bh, n, i0, QT, kk);   // this thread's first pick
 
     // ----------------------------------------------------- per-row state --
     const int qs = l16 / G;
@@ -1441,7 +1464,7 @@ __device__ __forceinline__ void dq_body(
 
     // ------------------------------------- selection lists and their union
     const int ne = union_of_picks<C::NTHR>(idx, cnt, bh, n, i0, QT, QPT, WAVES * PTW, kk, nb, nbw, sel, bitmap, pre,
-                                           list, qbits, wbits, nlist);
+                                           list, qbits, wbits, nlist, pk);
 
     // ----------------------------------------- window tiles (RoPE operand)
     for (int e0 = 0; e0 < nwin; e0 += P) {
