@@ -325,23 +325,38 @@ __device__ __forceinline__ void routing_queries_tile(const bf16_t *q, int64_t qs
     for (int j = 0; j < GMAX / 4; ++j) rr[j] = 1.0f;
     auto chains = [&](auto nj_const) {
         constexpr int NJ = decltype(nj_const)::value;
-        uint4 rw[NJ][D / 8];
-#pragma unroll
-        for (int j = 0; j < NJ; ++j) {
-            const int h = (part + 4 * j < G) ? part + 4 * j : G - 1;   // past G: a duplicate, unused
-#pragma unroll
-            for (int c = 0; c < D / 8; ++c) rw[j][c] = reinterpret_cast<const uint4 *>(row0 + (int64_t)h * qsh)[c];
-        }
         float ss[NJ];
 #pragma unroll
         for (int j = 0; j < NJ; ++j) ss[j] = 0.0f;
-#pragma unroll
-        for (int t = 0; t < D; ++t)
+        if constexpr (D <= 64) {   // every full row in flight at once
+            uint4 rw[NJ][D / 8];
 #pragma unroll
             for (int j = 0; j < NJ; ++j) {
-                const float x = unpack(rw[j][t >> 3], t & 7);
-                ss[j] = fmaf(x, x, ss[j]);
+                const int h = (part + 4 * j < G) ? part + 4 * j : G - 1;   // past G: a duplicate, unused
+#pragma unroll
+                for (int c = 0; c < D / 8; ++c) rw[j][c] = reinterpret_cast<const uint4 *>(row0 + (int64_t)h * qsh)[c];
             }
+#pragma unroll
+            for (int t = 0; t < D; ++t)
+#pragma unroll
+                for (int j = 0; j < NJ; ++j) {
+                    const float x = unpack(rw[j][t >> 3], t & 7);
+                    ss[j] = fmaf(x, x, ss[j]);
+                }
+        } else {   // one full row at a time: beside the quarter rows, two would not fit the registers
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) {
+                const int h = (part + 4 * j < G) ? part + 4 * j : G - 1;
+                uint4 rw[D / 8];
+#pragma unroll
+                for (int c = 0; c < D / 8; ++c) rw[c] = reinterpret_cast<const uint4 *>(row0 + (int64_t)h * qsh)[c];
+#pragma unroll
+                for (int t = 0; t < D; ++t) {
+                    const float x = unpack(rw[t >> 3], t & 7);
+                    ss[j] = fmaf(x, x, ss[j]);
+                }
+            }
+        }
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
             float ms = ss[j] / (float)D;
@@ -1297,7 +1312,7 @@ struct Cfg {
 
 
 template <int D, int KMAX>
-__global__ __launch_bounds__(256, (D == 64) ? 2 : 1) void score_select_thr_kernel(
+__global__ __launch_bounds__(256, 2) void score_select_thr_kernel(
     const bf16_t *__restrict__ q, int64_t qsb, int64_t qsn, int64_t qsh, const float *__restrict__ qgain,
     float eps, const bf16_t *__restrict__ S0, int64_t n, int Hq, int Hkv, int64_t nb, int64_t W, int kk,
     float scale, int32_t *__restrict__ idx, float *__restrict__ val, int32_t *__restrict__ cnt,
@@ -1347,18 +1362,24 @@ __global__ __launch_bounds__(256, (D == 64) ? 2 : 1) void score_select_thr_kerne
     // of block 1 + 16 st + 4 mt + l16 / 4 (clamped to tile_bmax: rows past it
     // are never visited); visit(ct, block, score, candidate) per lane and
     // column tile.  Stages wholly within 1 .. bmin need no candidate mask.
+    auto load_mt = [&](int st, int mt, bf16x8 (&af)[NKS]) {
+        int blk = 1 + st * CB + 4 * mt + (l16 >> 2);
+        blk = (blk <= tile_bmax) ? blk : tile_bmax;
+        const bf16_t *src = Sg + ((int64_t)blk * 4 + (l16 & 3)) * D + 8 * lg;
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) af[ks] = ldb8(src + 32 * ks);
+    };
     auto load = [&](int st, bf16x8 (&af)[4][NKS]) {
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-            int blk = 1 + st * CB + 4 * mt + (l16 >> 2);
-            blk = (blk <= tile_bmax) ? blk : tile_bmax;
-            const bf16_t *src = Sg + ((int64_t)blk * 4 + (l16 & 3)) * D + 8 * lg;
-#pragma unroll
-            for (int ks = 0; ks < NKS; ++ks) af[mt][ks] = ldb8(src + 32 * ks);
-        }
+        for (int mt = 0; mt < 4; ++mt) load_mt(st, mt, af[mt]);
     };
+    // d = 64: two stages of A fragments in flight (a0, a1).  d = 128: their
+    // 128 VGPRs do not fit beside the B operand (1 KB per lane went to
+    // scratch), so one stage's buffers roll: M-tile mt of stage st + 4 is
+    // loaded into af[mt] as soon as stage st's MFMAs have read it.
+    constexpr bool ROLL = D > 64;
     auto scan = [&](auto &&visit) {
-        auto stage = [&](int st, const bf16x8 (&af)[4][NKS], auto mask_c) {
+        auto stage = [&](int st, bf16x8 (&af)[4][NKS], auto mask_c, int nxt) {
             constexpr bool MASK = decltype(mask_c)::value;
             const int b0 = 1 + st * CB;
 #pragma unroll
@@ -1374,6 +1395,7 @@ __global__ __launch_bounds__(256, (D == 64) ? 2 : 1) void score_select_thr_kerne
 #pragma unroll
                     for (int ct = 0; ct < NCT; ++ct)
                         acc[ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[mt][ks], qb[ct][ks], acc[ct], 0, 0, 0);
+                if (ROLL && nxt >= 0) load_mt(nxt, mt, af[mt]);   // wave-uniform
 #pragma unroll
                 for (int ct = 0; ct < NCT; ++ct) {
                     // the max is exact in any order (no NaN)
@@ -1382,22 +1404,32 @@ __global__ __launch_bounds__(256, (D == 64) ? 2 : 1) void score_select_thr_kerne
                 }
             }
         };
-        auto run = [&](int st, const bf16x8 (&af)[4][NKS]) {
-            if (st * CB + CB <= bmin) stage(st, af, std::false_type());   // uniform
-            else stage(st, af, std::true_type());
+        auto run = [&](int st, bf16x8 (&af)[4][NKS], int nxt) {
+            if (st * CB + CB <= bmin) stage(st, af, std::false_type(), nxt);   // uniform
+            else stage(st, af, std::true_type(), nxt);
         };
-        bf16x8 a0[4][NKS], a1[4][NKS];
-        int st = w;
-        if (st < nst) load(st, a0);
-        if (st + 4 < nst) load(st + 4, a1);
-        while (st < nst) {
-            run(st, a0);
-            if (st + 8 < nst) load(st + 8, a0);
-            st += 4;
-            if (st >= nst) break;
-            run(st, a1);
-            if (st + 8 < nst) load(st + 8, a1);
-            st += 4;
+        if constexpr (ROLL) {
+            bf16x8 a0[4][NKS];
+            int st = w;
+            if (st < nst) load(st, a0);
+            while (st < nst) {
+                run(st, a0, (st + 4 < nst) ? st + 4 : -1);
+                st += 4;
+            }
+        } else {
+            bf16x8 a0[4][NKS], a1[4][NKS];
+            int st = w;
+            if (st < nst) load(st, a0);
+            if (st + 4 < nst) load(st + 4, a1);
+            while (st < nst) {
+                run(st, a0, -1);
+                if (st + 8 < nst) load(st + 8, a0);
+                st += 4;
+                if (st >= nst) break;
+                run(st, a1, -1);
+                if (st + 8 < nst) load(st + 8, a1);
+                st += 4;
+            }
         }
     };
 
