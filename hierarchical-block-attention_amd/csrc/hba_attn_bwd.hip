@@ -968,20 +968,27 @@ struct DkvTile {
     alignas(16) int row[DKV_TP];
 };
 
+// 512 threads: wave w takes keys 16 (w & 3) .. + 15 of the block and pairs
+// 32 (w >> 2) .. + 31 of each 64-pair tile (4 waves per SIMD at d = 64, so
+// that one wave's LDS -> MFMA -> exp -> MFMA chain overlaps the others'); the
+// two halves add their sums into the same accumulator rows.
+constexpr int DKV_NT = 512;
 template <int D>
-__global__ __launch_bounds__(256) void bwd_dkv_mfma_kernel(
+__global__ __launch_bounds__(DKV_NT, D == 64 ? 4 : 2) void bwd_dkv_mfma_kernel(
     const bf16_t *__restrict__ kc, const bf16_t *__restrict__ kr, const bf16_t *__restrict__ v,
     const int32_t *__restrict__ idx, const int32_t *__restrict__ cnt, const bf16_t *__restrict__ dout, int64_t n,
     int Hq, int Hkv, int S, int64_t W, int kk, float scale, int nsplit, const bf16_t *__restrict__ qc_ws,
     const bf16_t *__restrict__ qr_ws, const float *__restrict__ lse_ws, const float *__restrict__ dd_ws,
-    float *__restrict__ dkv_acc, int sink_rows) {
-    constexpr int NKS = D / 32, NDT = D / 16, NCH = D / 8, CPT = DKV_TP * NCH / 256;
+    const float *__restrict__ cosT, const float *__restrict__ sinT, float *__restrict__ dkv_acc, int sink_rows) {
+    constexpr int NKS = D / 32, NDT = D / 16, NCH = D / 8, CPT = DKV_TP * NCH / DKV_NT;
+    static_assert(CPT * DKV_NT == DKV_TP * NCH, "a tile's 16-byte chunks split evenly over the threads");
     using Tl = DkvTile<D>;
     constexpr int XP = Tl::XP, TP = Tl::TP;
     __shared__ Tl tl[2];
     __shared__ int rows[DKV_RL];
-    __shared__ int wcount[4];
+    __shared__ int wcount[DKV_NT / 64];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, l16 = lane & 15, lg = lane >> 4;
+    const int kg = w & 3, hw = w >> 2;   // this wave's 16 keys and 32-pair half of each tile
     const bool sinks = sink_rows > 0;
     const int64_t nb = sinks ? 1 : n / 64;
     const int split = (int)(blockIdx.x % nsplit);
@@ -992,18 +999,48 @@ __global__ __launch_bounds__(256) void bwd_dkv_mfma_kernel(
     const int64_t kb = 64 * blk;
     const int64_t rows_per = sinks ? (int64_t)sink_rows : (int64_t)DKV_ROWS;
     const int64_t r0 = (int64_t)split * rows_per, r1 = min(n, r0 + rows_per);
-    const int64_t jl = kb + 16 * w + l16;   // the key of this lane's S / dP column
+    const int64_t jl = kb + 16 * kg + l16;   // the key of this lane's S / dP column
 
-    bf16x8 kcb[NKS], krb[NKS], vb[NKS];
+    // the key operand of the current rows (kr rows for the window, kc rows
+    // for the sinks and routed rows) and the value rows
+    bf16x8 kop[NKS], vb[NKS];
+    auto load_k = [&](const bf16_t *kt) {
 #pragma unroll
-    for (int ks = 0; ks < NKS; ++ks) {
-        kcb[ks] = ld_b8(kc + (bg * n + jl) * D + 32 * ks + 8 * lg);
-        krb[ks] = ld_b8(kr + (bg * n + jl) * D + 32 * ks + 8 * lg);
-        vb[ks] = ld_b8(v + (((int64_t)b * n + jl) * Hkv + g) * D + 32 * ks + 8 * lg);
-    }
-    f32x4 gkc[NDT], gkr[NDT], gv[NDT];
+        for (int ks = 0; ks < NKS; ++ks) kop[ks] = ld_b8(kt + (bg * n + jl) * D + 32 * ks + 8 * lg);
+    };
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) gkc[dt] = gkr[dt] = gv[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int ks = 0; ks < NKS; ++ks) vb[ks] = ld_b8(v + (((int64_t)b * n + jl) * Hkv + g) * D + 32 * ks + 8 * lg);
+    // dk in the NoPE frame (the window rows' sums, taken in the rotated frame,
+    // are mapped back by rope^T before the routed rows add theirs) and dv;
+    // lane (l16, lg) holds keys kb + 16 kg + 4 lg + e, elements 16 dt + l16
+    f32x4 gk[NDT], gv[NDT];
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) gk[dt] = gv[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // rope^T(z) = z cos + rot^T(z sin) at each key's position, with the
+    // tables rounded to bf16 as apply_rope's; an element's rotation partner
+    // d ^ D/2 is element dt ^ NDT/2 of the same lane
+    auto rope_t = [&]() {
+        float cs[NDT][4], sn[NDT][4];
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int64_t j = kb + 16 * kg + 4 * lg + e;
+                cs[dt][e] = rnd_bf16(cosT[j * D + 16 * dt + l16]);
+                sn[dt][e] = rnd_bf16(sinT[j * D + 16 * dt + l16]);
+            }
+        f32x4 y[NDT];
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int pd = dt ^ (NDT / 2);
+                const float zp = gk[pd][e] * sn[pd][e];
+                y[dt][e] = gk[dt][e] * cs[dt][e] + ((dt < NDT / 2) ? zp : -zp);
+            }
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) gk[dt] = y[dt];
+    };
 
     // pairs gp = 0 .. total-1: query row row_of(gp / G), head g G + gp % G;
     // mode 0: window rows (rotated), 1: routed rows, 2: sink rows (NoPE)
@@ -1017,7 +1054,7 @@ __global__ __launch_bounds__(256) void bwd_dkv_mfma_kernel(
         auto load = [&](int64_t t) {
 #pragma unroll
             for (int r = 0; r < CPT; ++r) {
-                const int q = tid + 256 * r, p = q / NCH, c = q % NCH;
+                const int q = tid + DKV_NT * r, p = q / NCH, c = q % NCH;
                 const int64_t gp = t * DKV_TP + p;
                 plse[r] = INFINITY;
                 pdd[r] = 0.0f;
@@ -1042,7 +1079,7 @@ __global__ __launch_bounds__(256) void bwd_dkv_mfma_kernel(
         auto store = [&](Tl &T) {
 #pragma unroll
             for (int r = 0; r < CPT; ++r) {
-                const int q = tid + 256 * r, p = q / NCH, c = q % NCH;
+                const int q = tid + DKV_NT * r, p = q / NCH, c = q % NCH;
                 *reinterpret_cast<u32x4b *>(&T.xs[p * XP + 8 * c]) = xr[r];
                 *reinterpret_cast<u32x4b *>(&T.os[p * XP + 8 * c]) = orr[r];
                 // transposed rows d = 8 c + e, this pair in 8-pair group (p >> 3) ^ (c & 7)
@@ -1060,10 +1097,10 @@ __global__ __launch_bounds__(256) void bwd_dkv_mfma_kernel(
             }
         };
         auto compute = [&](const Tl &T) {
-            if (mode == 2 && 16 * w >= S) return;                  // no sink among the wave's keys
-#pragma unroll
-          for (int hp = 0; hp < DKV_TP / 32; ++hp) {
-            if (T.row[32 * hp] < 0) break;                         // the rest is padding (pairs fill in order)
+            if (mode == 2 && 16 * kg >= S) return;                 // no sink among the wave's keys
+          {
+            const int hp = hw;
+            if (T.row[32 * hp] < 0) return;                        // padding (pairs fill in order)
             f32x4 Sa[2], Pa[2];
 #pragma unroll
             for (int mt = 0; mt < 2; ++mt) {
@@ -1072,7 +1109,7 @@ __global__ __launch_bounds__(256) void bwd_dkv_mfma_kernel(
                 Sa[mt] = Pa[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int ks = 0; ks < NKS; ++ks) {
-                    Sa[mt] = mfma16(ld_b8(xa + 32 * ks), rope ? krb[ks] : kcb[ks], Sa[mt]);
+                    Sa[mt] = mfma16(ld_b8(xa + 32 * ks), kop[ks], Sa[mt]);
                     Pa[mt] = mfma16(ld_b8(oa + 32 * ks), vb[ks], Pa[mt]);
                 }
             }
@@ -1101,9 +1138,7 @@ __global__ __launch_bounds__(256) void bwd_dkv_mfma_kernel(
                 const int dr = 16 * dt + l16;                      // pairs 32 hp + 8 lg .. + 7 of row dr
                 const int to = dr * TP + ((((4 * hp + lg) ^ (dr >> 3)) & 7) << 3);
                 gv[dt] = mfma16(pa, ld_b8(&T.ot[to]), gv[dt]);
-                const bf16x8 xb = ld_b8(&T.xt[to]);
-                if (rope) gkr[dt] = mfma16(da, xb, gkr[dt]);
-                else gkc[dt] = mfma16(da, xb, gkc[dt]);
+                gk[dt] = mfma16(da, ld_b8(&T.xt[to]), gk[dt]);
             }
           }
         };
@@ -1122,6 +1157,7 @@ __global__ __launch_bounds__(256) void bwd_dkv_mfma_kernel(
     bool had_win = false, had_rt = false;
     if (sinks) {
         had_rt = true;
+        load_k(kc);
         run((r1 - r0) * G, [&](int64_t r) { return r0 + r; }, 2);
     }
     // window rows: key j >= S is in the window of queries j .. j + W - 1
@@ -1130,13 +1166,16 @@ __global__ __launch_bounds__(256) void bwd_dkv_mfma_kernel(
         const int64_t wb = min(min(n - 1, kb + 63 + W - 1), r1 - 1);
         if (wb >= wa) {
             had_win = true;
+            load_k(kr);
             run((wb - wa + 1) * G, [&](int64_t r) { return wa + r; }, 0);
+            rope_t();
         }
     }
     // routed rows: the queries of the range whose selection holds this block,
     // collected over scan chunks of 512 rows (two per thread) until the list
     // could overflow, then run as one pipelined series of tiles
     if (!sinks && blk >= 1) {
+        load_k(kc);
         // 16-byte list loads when every row's list starts 16-byte aligned
         const bool vec_idx = (kk & 3) == 0 && (reinterpret_cast<uintptr_t>(idx) & 15) == 0;
         auto picks = [&](int64_t i) -> bool {
@@ -1158,27 +1197,22 @@ __global__ __launch_bounds__(256) void bwd_dkv_mfma_kernel(
         int64_t i0 = r0;
         while (i0 < r1) {
             int tot = 0;
-            while (i0 < r1 && tot <= DKV_RL - 512) {
-                const bool pa = picks(i0 + tid), pb = picks(i0 + 256 + tid);
-                const uint64_t ba = __ballot(pa), bb = __ballot(pb);
-                if (lane == 0) wcount[w] = __popcll(ba) | (__popcll(bb) << 16);
+            while (i0 < r1 && tot <= DKV_RL - DKV_NT) {
+                const bool pa = picks(i0 + tid);
+                const uint64_t ba = __ballot(pa);
+                if (lane == 0) wcount[w] = __popcll(ba);
                 __syncthreads();
-                int basea = 0, baseb = 0, ta = 0, tb = 0;
+                int basea = 0, ta = 0;
 #pragma unroll
-                for (int u = 0; u < 4; ++u) {
+                for (int u = 0; u < DKV_NT / 64; ++u) {
                     const int wc = wcount[u];
-                    if (u < w) {
-                        basea += wc & 0xffff;
-                        baseb += wc >> 16;
-                    }
-                    ta += wc & 0xffff;
-                    tb += wc >> 16;
+                    if (u < w) basea += wc;
+                    ta += wc;
                 }
                 if (pa) rows[tot + basea + __popcll(ba & ((1ull << lane) - 1ull))] = (int)(i0 + tid);
-                if (pb) rows[tot + ta + baseb + __popcll(bb & ((1ull << lane) - 1ull))] = (int)(i0 + 256 + tid);
                 __syncthreads();                                  // rows[] complete; wcount[] reused
-                tot += ta + tb;
-                i0 += 512;
+                tot += ta;
+                i0 += DKV_NT;
             }
             if (tot > 0) {
                 had_rt = true;
@@ -1188,17 +1222,18 @@ __global__ __launch_bounds__(256) void bwd_dkv_mfma_kernel(
         }
     }
 
-    if (sinks && 16 * w >= S) return;                              // after the last barrier
-    float *acc = dkv_acc + (bg * n + kb + 16 * w + 4 * lg) * 3 * D + l16;
+    if (sinks && 16 * kg >= S) return;                             // after the last barrier
+    float *acc = dkv_acc + (bg * n + kb + 16 * kg + 4 * lg) * 3 * D + l16;
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            if (sinks && 16 * w + 4 * lg + e >= S) continue;
+            if (sinks && 16 * kg + 4 * lg + e >= S) continue;
             float *a = acc + e * 3 * D + 16 * dt;
-            if (had_rt) unsafeAtomicAdd(a, gkc[dt][e]);
-            if (had_win) unsafeAtomicAdd(a + D, gkr[dt][e]);
-            if (had_rt || had_win) unsafeAtomicAdd(a + 2 * D, gv[dt][e]);
+            if (had_rt || had_win) {   // dk in the NoPE slot; the rotated slot stays zero
+                unsafeAtomicAdd(a, gk[dt][e]);
+                unsafeAtomicAdd(a + 2 * D, gv[dt][e]);
+            }
         }
 }
 
@@ -1424,14 +1459,15 @@ extern "C" int hba_attn_bwd(int dtype, const void *q, const void *k, const void 
                                nsplit, scale, qc_ws, lse_ws, dd_ws, sink_acc);                                   \
         if constexpr (DT == 1) {                                                                                \
             if (S > 0)                                                                                          \
-                hipLaunchKernelGGL((bw::bwd_dkv_mfma_kernel<D>), dim3((unsigned)gs), dim3(256), 0, s,            \
+                hipLaunchKernelGGL((bw::bwd_dkv_mfma_kernel<D>), dim3((unsigned)gs), dim3(bw::DKV_NT), 0, s,     \
                                    (const bf16_t *)kc, (const bf16_t *)kr, (const bf16_t *)v, idx, cnt,          \
                                    (const bf16_t *)dout, n, (int)Hq, (int)Hkv, (int)S, W, (int)k_blocks, scale,  \
-                                   nsplit, qcb_ws, qrb_ws, lse_ws, dd_ws, dkv_acc, bw::SINK_ROWS);               \
-            hipLaunchKernelGGL((bw::bwd_dkv_mfma_kernel<D>), dim3((unsigned)g3), dim3(256), 0, s,                \
+                                   nsplit, qcb_ws, qrb_ws, lse_ws, dd_ws, cos_tab, sin_tab, dkv_acc,            \
+                                   bw::SINK_ROWS);                                                              \
+            hipLaunchKernelGGL((bw::bwd_dkv_mfma_kernel<D>), dim3((unsigned)g3), dim3(bw::DKV_NT), 0, s,         \
                                (const bf16_t *)kc, (const bf16_t *)kr, (const bf16_t *)v, idx, cnt,              \
                                (const bf16_t *)dout, n, (int)Hq, (int)Hkv, (int)S, W, (int)k_blocks, scale,      \
-                               nsplit_kv, qcb_ws, qrb_ws, lse_ws, dd_ws, dkv_acc, 0);                            \
+                               nsplit_kv, qcb_ws, qrb_ws, lse_ws, dd_ws, cos_tab, sin_tab, dkv_acc, 0);          \
             hipLaunchKernelGGL((bw::bwd_dkv_fin_kernel<D>), dim3((unsigned)g4), dim3(256), 0, s,                 \
                                (const bf16_t *)k, k_gain, eps, cos_tab, sin_tab, n, (int)Hkv, (int)S, dkv_acc,    \
                                (const float *)nullptr, (bf16_t *)dk, (bf16_t *)dv, dk_gain);                     \
