@@ -321,19 +321,31 @@ __device__ __forceinline__ float col_sum(float v) {
     return v + __shfl_xor(v, 32, 64);
 }
 
+// Query rows per bwd_dkv_mfma workgroup (its row range), and the routed rows
+// of each (range, key block) as bits: pbits [B, Hkv, nsplit, n / 64,
+// PB_WORDS], bit i % DKV_ROWS of range i / DKV_ROWS set when row i's
+// selection holds the block.
+constexpr int DKV_ROWS = 4096;
+constexpr int PB_WORDS = DKV_ROWS / 32;
+
 // transposed prepared keys, kct / krt [B, Hkv, d, n]: one workgroup per 64-key
 // tile; it also clears the tile's rows of the dk / dv accumulator dkv_acc
-// [B, Hkv, n, 3, d] (bwd_dkv_mfma adds into it next)
+// [B, Hkv, n, 3, d] (bwd_dkv_mfma adds into it next) and the tile's routed-row
+// bits of every range (bwd_pick_bits sets them next)
 template <int D>
 __global__ __launch_bounds__(256) void bwd_kt_kernel(const bf16_t *__restrict__ kc, const bf16_t *__restrict__ kr,
                                                      bf16_t *__restrict__ kct, bf16_t *__restrict__ krt, int64_t n,
-                                                     float *__restrict__ dkv_acc) {
+                                                     float *__restrict__ dkv_acc, uint32_t *__restrict__ pbits,
+                                                     int nsplit) {
     __shared__ bf16_t tile[64][D + 2];
     const int64_t nt = n / 64;
     const int64_t bg = blockIdx.x / nt, kb = (blockIdx.x % nt) * 64;
     {
         f32x4 *acc = reinterpret_cast<f32x4 *>(dkv_acc + (bg * n + kb) * 3 * D);
         for (int e = threadIdx.x; e < 64 * 3 * D / 4; e += 256) acc[e] = f32x4{0.f, 0.f, 0.f, 0.f};
+        const int64_t blk = blockIdx.x % nt;
+        for (int e = threadIdx.x; e < nsplit * PB_WORDS; e += 256)
+            pbits[((bg * nsplit + e / PB_WORDS) * nt + blk) * PB_WORDS + e % PB_WORDS] = 0u;
     }
     for (int pass = 0; pass < 2; ++pass) {
         const bf16_t *src = (pass ? kr : kc) + (bg * n + kb) * D;
@@ -343,6 +355,25 @@ __global__ __launch_bounds__(256) void bwd_kt_kernel(const bf16_t *__restrict__ 
         for (int e = threadIdx.x; e < 64 * D; e += 256) dst[(int64_t)(e / 64) * n + (e % 64)] = tile[e % 64][e / 64];
         __syncthreads();
     }
+}
+
+// The routed rows of every key block as bits (layout above): one thread per
+// (b, g, row, pick); atomic ORs, so the bits are the same in any order.  A
+// block picked twice by a row sets one bit, as the row attends it once.
+__global__ __launch_bounds__(256) void bwd_pick_bits_kernel(const int32_t *__restrict__ idx,
+                                                            const int32_t *__restrict__ cnt, int64_t n, int64_t nb,
+                                                            int kk, int64_t total, int nsplit,
+                                                            uint32_t *__restrict__ pbits) {
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (t >= total) return;                                       // total = B Hkv n kk
+    const int64_t row = t / kk;                                   // bg n + i
+    const int r = (int)(t - row * kk);
+    if (r >= min(max(cnt[row], 0), kk)) return;
+    const int v = idx[t];
+    if (v < 1 || v >= nb) return;                                 // block 0 is never routed
+    const int64_t bg = row / n, i = row - bg * n;
+    const int li = (int)(i % DKV_ROWS);
+    atomicOr(&pbits[((bg * nsplit + i / DKV_ROWS) * nb + v) * PB_WORDS + (li >> 5)], 1u << (li & 31));
 }
 
 template <int D>
@@ -949,8 +980,7 @@ __global__ __launch_bounds__(DkvCfg<D>::NT) void bwd_dkv_kernel(
 // per (b, g, range of sink_rows rows) against block 0, every row of the range
 // attending the keys j < S with j <= i (NoPE); waves whose 16 keys hold no
 // sink skip the products.
-constexpr int DKV_ROWS = 4096;
-constexpr int DKV_RL = 1024;   // routed rows collected before their tiles run
+constexpr int DKV_RL = 1024;   // routed rows run as one series of tiles at most
 constexpr int DKV_TP = 64;   // pairs per tile: two halves of 32, the pair count of one product
 
 __device__ __forceinline__ int pslot(int mt, int r) { return 8 * (r >> 2) + 4 * mt + (r & 3); }
@@ -979,7 +1009,8 @@ __global__ __launch_bounds__(DKV_NT, D == 64 ? 4 : 2) void bwd_dkv_mfma_kernel(
     const int32_t *__restrict__ idx, const int32_t *__restrict__ cnt, const bf16_t *__restrict__ dout, int64_t n,
     int Hq, int Hkv, int S, int64_t W, int kk, float scale, int nsplit, const bf16_t *__restrict__ qc_ws,
     const bf16_t *__restrict__ qr_ws, const float *__restrict__ lse_ws, const float *__restrict__ dd_ws,
-    const float *__restrict__ cosT, const float *__restrict__ sinT, float *__restrict__ dkv_acc, int sink_rows) {
+    const float *__restrict__ cosT, const float *__restrict__ sinT, const uint32_t *__restrict__ pbits,
+    float *__restrict__ dkv_acc, int sink_rows) {
     constexpr int NKS = D / 32, NDT = D / 16, NCH = D / 8, CPT = DKV_TP * NCH / DKV_NT;
     static_assert(CPT * DKV_NT == DKV_TP * NCH, "a tile's 16-byte chunks split evenly over the threads");
     using Tl = DkvTile<D>;
@@ -1172,53 +1203,39 @@ __global__ __launch_bounds__(DKV_NT, D == 64 ? 4 : 2) void bwd_dkv_mfma_kernel(
         }
     }
     // routed rows: the queries of the range whose selection holds this block,
-    // collected over scan chunks of 512 rows (two per thread) until the list
-    // could overflow, then run as one pipelined series of tiles
+    // read from its bits (ascending), run in series of at most DKV_RL rows
     if (!sinks && blk >= 1) {
         load_k(kc);
-        // 16-byte list loads when every row's list starts 16-byte aligned
-        const bool vec_idx = (kk & 3) == 0 && (reinterpret_cast<uintptr_t>(idx) & 15) == 0;
-        auto picks = [&](int64_t i) -> bool {
-            if (i >= r1) return false;
-            const int nc = min(max(cnt[bg * n + i], 0), kk);
-            const int32_t *sl = idx + (bg * n + i) * kk;
-            bool pk = false;
-            if (vec_idx) {
-                for (int r = 0; r < nc; r += 4) {
-                    const int4 v4 = *reinterpret_cast<const int4 *>(sl + r);
-                    pk |= (v4.x == (int32_t)blk) | ((r + 1 < nc) & (v4.y == (int32_t)blk)) |
-                          ((r + 2 < nc) & (v4.z == (int32_t)blk)) | ((r + 3 < nc) & (v4.w == (int32_t)blk));
-                }
-            } else {
-                for (int r = 0; r < nc; ++r) pk |= sl[r] == (int32_t)blk;
-            }
-            return pk;
-        };
-        int64_t i0 = r0;
-        while (i0 < r1) {
-            int tot = 0;
-            while (i0 < r1 && tot <= DKV_RL - DKV_NT) {
-                const bool pa = picks(i0 + tid);
-                const uint64_t ba = __ballot(pa);
-                if (lane == 0) wcount[w] = __popcll(ba);
-                __syncthreads();
-                int basea = 0, ta = 0;
+        const uint32_t *bits = pbits + ((bg * nsplit + split) * nb + blk) * PB_WORDS;
+        const uint32_t word = (tid < PB_WORDS) ? bits[tid] : 0u;   // rows r0 + 32 tid ..
+        const int c = __popc(word);
+        int incl = c;   // prefix over the words (threads 0 .. PB_WORDS - 1: two waves)
 #pragma unroll
-                for (int u = 0; u < DKV_NT / 64; ++u) {
-                    const int wc = wcount[u];
-                    if (u < w) basea += wc;
-                    ta += wc;
+        for (int o = 1; o < 64; o <<= 1) {
+            const int t = __shfl_up(incl, o, 64);
+            if (lane >= o) incl += t;
+        }
+        static_assert(PB_WORDS == 128, "the words' prefix spans two waves");
+        if (lane == 63 && w < 2) wcount[w] = incl;
+        __syncthreads();
+        const int pos = incl - c + ((w == 1) ? wcount[0] : 0);     // the word's first row's position
+        const int total = wcount[0] + wcount[1];
+        for (int run0 = 0; run0 < total; run0 += DKV_RL) {
+            __syncthreads();                                      // rows[] consumed (and wcount[] read)
+            if (word) {
+                uint32_t wd = word;
+                int p = pos;
+                while (wd) {
+                    const int bit = __ffs(wd) - 1;
+                    wd &= wd - 1u;
+                    if (p >= run0 && p < run0 + DKV_RL) rows[p - run0] = (int)(r0 + 32 * tid + bit);
+                    ++p;
                 }
-                if (pa) rows[tot + basea + __popcll(ba & ((1ull << lane) - 1ull))] = (int)(i0 + tid);
-                __syncthreads();                                  // rows[] complete; wcount[] reused
-                tot += ta;
-                i0 += DKV_NT;
             }
-            if (tot > 0) {
-                had_rt = true;
-                run((int64_t)tot * G, [&](int64_t r) { return (int64_t)rows[r]; }, 1);
-            }
-            __syncthreads();                                      // rows[] reused
+            __syncthreads();                                      // rows[] complete
+            had_rt = true;
+            const int tot = min(DKV_RL, total - run0);
+            run((int64_t)tot * G, [&](int64_t r) { return (int64_t)rows[r]; }, 1);
         }
     }
 
@@ -1332,7 +1349,7 @@ static bool bwd_dq_union_on() {
 // [B, Hkv, d, n] and the fp32 dk / dv accumulators [B, Hkv, n, 3, d].
 namespace {
 struct BwdWs {
-    size_t qc, qr, lse, dd, sink, kct, krt, dkv, total;
+    size_t qc, qr, lse, dd, sink, kct, krt, dkv, pbits, total;
 };
 size_t bw_align(size_t x) { return (x + 255) & ~(size_t)255; }
 BwdWs bwd_ws_layout(int dtype, int64_t B, int64_t n, int64_t Hq, int64_t Hkv, int64_t d) {
@@ -1353,6 +1370,8 @@ BwdWs bwd_ws_layout(int dtype, int64_t B, int64_t n, int64_t Hq, int64_t Hkv, in
         L.kct = take((size_t)(B * Hkv * d * n) * 2);
         L.krt = take((size_t)(B * Hkv * d * n) * 2);
         L.dkv = take((size_t)(B * Hkv * n * 3 * d) * 4);
+        const int64_t nsplit = (n + bw::DKV_ROWS - 1) / bw::DKV_ROWS;
+        L.pbits = take((size_t)(B * Hkv * nsplit * (n / 64) * bw::PB_WORDS) * 4);
     }
     L.total = o;
     return L;
@@ -1405,6 +1424,7 @@ extern "C" int hba_attn_bwd(int dtype, const void *q, const void *k, const void 
     bf16_t *kct = (bf16_t *)(wsb + L.kct);                         // [B, Hkv, d, n] (bf16 path)
     bf16_t *krt = (bf16_t *)(wsb + L.krt);
     float *dkv_acc = (float *)(wsb + L.dkv);                       // [B, Hkv, n, 3, d] (bf16 path)
+    uint32_t *pbits = (uint32_t *)(wsb + L.pbits);                 // routed-row bits (bf16 path)
     hipStream_t s = (hipStream_t)stream;
     const int64_t nwaves = B * Hkv * n;
     const int64_t g1 = (nwaves + 3) / 4;
@@ -1419,13 +1439,17 @@ extern "C" int hba_attn_bwd(int dtype, const void *q, const void *k, const void 
     const int nsplit_kv = (int)((n + bw::DKV_ROWS - 1) / bw::DKV_ROWS);
     const int64_t g3 = B * Hkv * (n / 64) * nsplit_kv;
     const int64_t g4 = B * Hkv * (n / 64);                        // bwd_dkv_fin: one workgroup per 64-key block
+    const int64_t gpb = (B * Hkv * n * k_blocks + 255) / 256;     // bwd_pick_bits: a thread per pick
+    if (gpb > 0x7fffffffLL) return HBA_ERR_UNSUPPORTED;
     if (g3 > 0x7fffffffLL) return HBA_ERR_UNSUPPORTED;
 #define HBA_BWD(DT, D)                                                                                          \
     do {                                                                                                        \
         using T = St<DT>::T;                                                                                    \
         if constexpr (DT == 1) {                                                                                \
             hipLaunchKernelGGL((bw::bwd_kt_kernel<D>), dim3((unsigned)g2), dim3(256), 0, s, (const bf16_t *)kc,  \
-                               (const bf16_t *)kr, kct, krt, n, dkv_acc);                                        \
+                               (const bf16_t *)kr, kct, krt, n, dkv_acc, pbits, nsplit_kv);                      \
+            hipLaunchKernelGGL(bw::bwd_pick_bits_kernel, dim3((unsigned)gpb), dim3(256), 0, s, idx, cnt, n,      \
+                               n / 64, (int)k_blocks, B * Hkv * n * k_blocks, nsplit_kv, pbits);                 \
             int dqs = HBA_ERR_UNSUPPORTED;                                                                      \
             if constexpr (D == 64)                                                                              \
                 if (bwd_dq_union_on())                                                                              \
@@ -1462,12 +1486,12 @@ extern "C" int hba_attn_bwd(int dtype, const void *q, const void *k, const void 
                 hipLaunchKernelGGL((bw::bwd_dkv_mfma_kernel<D>), dim3((unsigned)gs), dim3(bw::DKV_NT), 0, s,     \
                                    (const bf16_t *)kc, (const bf16_t *)kr, (const bf16_t *)v, idx, cnt,          \
                                    (const bf16_t *)dout, n, (int)Hq, (int)Hkv, (int)S, W, (int)k_blocks, scale,  \
-                                   nsplit, qcb_ws, qrb_ws, lse_ws, dd_ws, cos_tab, sin_tab, dkv_acc,            \
+                                   nsplit, qcb_ws, qrb_ws, lse_ws, dd_ws, cos_tab, sin_tab, pbits, dkv_acc,     \
                                    bw::SINK_ROWS);                                                              \
             hipLaunchKernelGGL((bw::bwd_dkv_mfma_kernel<D>), dim3((unsigned)g3), dim3(bw::DKV_NT), 0, s,         \
                                (const bf16_t *)kc, (const bf16_t *)kr, (const bf16_t *)v, idx, cnt,              \
                                (const bf16_t *)dout, n, (int)Hq, (int)Hkv, (int)S, W, (int)k_blocks, scale,      \
-                               nsplit_kv, qcb_ws, qrb_ws, lse_ws, dd_ws, cos_tab, sin_tab, dkv_acc, 0);          \
+                               nsplit_kv, qcb_ws, qrb_ws, lse_ws, dd_ws, cos_tab, sin_tab, pbits, dkv_acc, 0);   \
             hipLaunchKernelGGL((bw::bwd_dkv_fin_kernel<D>), dim3((unsigned)g4), dim3(256), 0, s,                 \
                                (const bf16_t *)k, k_gain, eps, cos_tab, sin_tab, n, (int)Hkv, (int)S, dkv_acc,    \
                                (const float *)nullptr, (bf16_t *)dk, (bf16_t *)dv, dk_gain);                     \

@@ -43,13 +43,14 @@ def test_static_queries_without_a_gpu():
 def test_backward_workspace_is_sized_by_dtype_and_kv_heads():
     """bf16 at 32K, 14/2 heads, d = 64: bf16 query rows (2 x n*Hq*d), LSE and
     D (2 x Hq*n fp32), sink accumulators (2*Hkv*64*d fp32), transposed keys
-    (2 x Hkv*d*n bf16), dk/dv accumulators (3*Hkv*n*d fp32), each rounded up
-    to 256 bytes; within the all-dtype bound of hba_attn_bwd_workspace_size."""
+    (2 x Hkv*d*n bf16), dk/dv accumulators (3*Hkv*n*d fp32), the routed-row
+    bits (Hkv * n/4096 ranges * n/64 blocks * 4096 bits), each rounded up to
+    256 bytes; within the all-dtype bound of hba_attn_bwd_workspace_size."""
     L = _lib.lib()
     B, n, Hq, Hkv, d = 1, 32768, 14, 2, 64
     r = lambda x: (x + 255) // 256 * 256
     want = (2 * r(n * Hq * d * 2) + 2 * r(Hq * n * 4) + r(Hkv * 2 * 64 * d * 4) + 2 * r(Hkv * d * n * 2)
-            + r(Hkv * n * 3 * d * 4))
+            + r(Hkv * n * 3 * d * 4) + r(Hkv * (n // 4096) * (n // 64) * 4096 // 8))
     got, bound = ctypes.c_size_t(0), ctypes.c_size_t(0)
     assert L.hba_attn_bwd_workspace_bytes(1, B, n, Hq, Hkv, d, ctypes.byref(got)) == 0
     assert got.value == want
