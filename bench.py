@@ -493,8 +493,9 @@ def bench_bwd32k(dev, reps=5):
                                "every candidate key, the KL rows, d aux / d probes and d proj (median of 3)"},
             "kernels": "bwd_kt (transposed keys) + bwd_dq_union_kernel (32 queries per workgroup, each staged "
                        "64-key block's K, V and K^T tiles shared through an LDS ring, MFMA) + "
-                       "bwd_dkv_mfma (one workgroup per KV head, 64-key block and 4096-row range, 64-pair tiles "
-                       "on MFMA; a second launch for the sink keys) + bwd_dkv_fin (rope^T, QKNorm backward)"}
+                       "bwd_pick_bits (the selection as routed-row bits per key block) + bwd_dkv_mfma (8 waves "
+                       "per KV head, 64-key block and 4096-row range, 64-pair tiles on MFMA; a second launch for "
+                       "the sink keys) + bwd_dkv_fin (rope^T, QKNorm backward)"}
 
 
 def bench_hier128k(dev):
