@@ -443,8 +443,9 @@ int hba_attn_bwd(int dtype, const void *q, const void *k, const void *v,
  * rotated query rows (2*B*n*Hq*d in the storage type), the per-row LSE and
  * <dout, out> (2*B*Hq*n fp32), the sink-key accumulators (2*B*Hkv*64*d
  * fp32); on the bf16 path also the transposed prepared keys (2*B*Hkv*n*d
- * bf16) and the dk/dv accumulators (3*B*Hkv*n*d fp32); each part rounded up
- * to 256 bytes. */
+ * bf16), the dk/dv accumulators (3*B*Hkv*n*d fp32) and the routed-row bits
+ * (B*Hkv*ceil(n/4096)*(n/64)*512 bytes: one bit per query row of each
+ * 4096-row range and key block); each part rounded up to 256 bytes. */
 int hba_attn_bwd_workspace_bytes(int dtype, int64_t B, int64_t n, int64_t Hq, int64_t Hkv,
                                  int64_t d, size_t *bytes);
 
