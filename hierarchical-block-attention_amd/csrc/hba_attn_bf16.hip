@@ -895,6 +895,7 @@ __device__ __forceinline__ void routed_body(
     // rows, RoPE operand) through the ring, then the sinks and routed blocks.
     const int64_t dkr = WIN ? (kr - kc) : 0;   // kc row -> the same kr row, in elements
     int wt0 = 0, nwin = 0;
+    int woff = 0, wpre = 0;   // WIN: the window tiles' first ring slot; how many the routed loop issued
     if constexpr (WIN) {
         const int64_t ilast = ((i0 + QT < n) ? i0 + QT : n) - 1;
         const int64_t kfirst = ((int64_t)S > i0 - W + 1) ? (int64_t)S : i0 - W + 1;
@@ -1022,6 +1023,12 @@ __device__ __forceinline__ void routed_body(
         // with S > 64 the keys 64..S-1 are sinks: routed block 1 (union entry 0
         // if picked) counts only its keys from S on
         const bool b1 = S2 && ne > 0 && list[0] == 1;
+        // WIN: the last routed phase also issues the first window tiles, into
+        // the slots after its own (those of the phase before it, consumed
+        // before its barrier), so that they land during its updates; the
+        // window tiles then run through the ring from slot woff
+        woff = 0;
+        wpre = 0;
         uint32_t qw[PTW], ww[PTW];   // this lane's query's / this row tile's bits of the current word
         for (int e0 = 0; e0 < ne; e0 += P) {
             // this wave's shares of entries e0..e0+P-1 have landed once at most
@@ -1036,6 +1043,13 @@ __device__ __forceinline__ void routed_body(
 #pragma unroll
             for (int j = 0; j < P; ++j)
                 if (issued + j < nf) fill(nxt[j], (issued + j) % C::NS, false);
+            if constexpr (WIN) {
+                if (e0 + P >= ne && nwin > 0) {   // the last phase (wave-uniform)
+                    woff = (e0 + P) % C::NS;
+                    wpre = min(nwin, NPRO);
+                    for (int e = 0; e < wpre; ++e) fill(wt0 + e, (woff + e) % C::NS, true);
+                }
+            }
             const int sh = e0 & 31;
             if (sh == 0) {
 #pragma unroll
@@ -1076,18 +1090,18 @@ __device__ __forceinline__ void routed_body(
                     qop[t][ks] = cok[t] ? v : bf16x8{};
                 }
             }
-            for (int e = 0; e < nwin && e < NPRO; ++e) fill(wt0 + e, e, true);
+            for (int e = wpre; e < nwin && e < NPRO; ++e) fill(wt0 + e, (woff + e) % C::NS, true);
         }
         for (int e0 = 0; e0 < nwin; e0 += P) {
             const int issued = min(nwin, e0 + (NPH - 1) * P);
             wait_vm_n(max(0, issued - (e0 + P)) * C::DPW);
             __syncthreads();   // every share of this phase landed; the previous phase consumed
             const int nf = min(nwin, e0 + NPH * P);
-            for (int e = issued; e < nf; ++e) fill(wt0 + e, e % C::NS, true);
+            for (int e = issued; e < nf; ++e) fill(wt0 + e, (woff + e) % C::NS, true);
             const int e1 = min(nwin, e0 + P);
 #pragma nounroll
             for (int e = e0; e < e1; ++e) {
-                const bf16_t *Ks = ring + (e % C::NS) * C::SLOT;
+                const bf16_t *Ks = ring + ((woff + e) % C::NS) * C::SLOT;
                 const int64_t kb = (int64_t)(wt0 + e) * 64;
 #pragma unroll
                 for (int tt = 0; tt < PTW; ++tt) {
