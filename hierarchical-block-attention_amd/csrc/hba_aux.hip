@@ -150,6 +150,134 @@ __global__ __launch_bounds__(256) void aux_scores_kernel(const typename St<DT>::
     }
 }
 
+// The same block scores for bf16 storage and m = 4 on MFMA: per (batch, KV
+// head, 64 queries) the GEMM C^T[summary rows x queries] = S0 . qg^T with
+// v_mfma_f32_16x16x32_bf16.  qg and S0 are bf16-exact, so every product is
+// exact in fp32 and only the order of the fp32 sums differs from the
+// sequential chain (scores within a few fp32 ulps).  A 16-row M tile is 4
+// blocks x 4 slots: lane (l16, lg) receives the 4 slot scores of one block
+// for one query, so the slot max and the tie mask come from registers.  The
+// four waves take 16-block stages w, w + 4, ... and load their A fragments
+// from L2 a stage ahead (d = 64: two stages in flight; d = 128: one stage's
+// buffers refilled M-tile by M-tile, for registers).
+typedef __bf16 abf16x8 __attribute__((ext_vector_type(8)));
+typedef float af32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int au32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ abf16x8 a_ldb8(const bf16_t *p) {
+    return __builtin_bit_cast(abf16x8, *reinterpret_cast<const au32x4 *>(p));
+}
+template <int D>
+__global__ __launch_bounds__(256, 2) void aux_scores_mfma_kernel(const bf16_t *__restrict__ qc,
+                                                                 const bf16_t *__restrict__ S0, int64_t n,
+                                                                 int64_t Hq, int64_t Hkv, int64_t W, float scale_r,
+                                                                 float *__restrict__ qg_out,
+                                                                 float *__restrict__ bsc,
+                                                                 uint8_t *__restrict__ ties) {
+    constexpr int NKS = D / 32, NCT = 4, CB = 16, ROWQ = D + 8;
+    __shared__ __align__(16) bf16_t qgs[64 * ROWQ];
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, lg = lane >> 4;
+    const int64_t i0 = (int64_t)blockIdx.x * 64, g = blockIdx.y, b = blockIdx.z;
+    const int64_t G = Hq / Hkv, nb = n / BK;
+    const int64_t bh = b * Hkv + g;
+    // the grouped queries: the head sum in head order, rounded (as aux_scores_kernel)
+    for (int e = tid; e < 64 * D; e += 256) {
+        const int qi = e / D, t = e % D;
+        const int64_t i = i0 + qi;
+        float s = 0.0f;
+        if (i < n) {
+            const bf16_t *row = qc + ((b * n + i) * Hq + g * G) * D + t;
+            s = bf2f(row[0]);
+            for (int64_t h = 1; h < G; ++h) s = s + bf2f(row[h * D]);
+            s = rnd_bf16(s);
+            qg_out[(bh * n + i) * D + t] = s;
+        }
+        qgs[qi * ROWQ + t] = f2bf(s);
+    }
+    __syncthreads();
+    abf16x8 qb[NCT][NKS];
+    int64_t bm[NCT];
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct) {
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) qb[ct][ks] = a_ldb8(qgs + (16 * ct + l16) * ROWQ + 32 * ks + 8 * lg);
+        const int64_t i = i0 + 16 * ct + l16;
+        bm[ct] = (i < n) ? cand_bmax(i, BK, W) : 0;
+    }
+    const int64_t ilast = (i0 + 63 < n) ? i0 + 63 : n - 1;
+    const int64_t tile_bmax = cand_bmax(ilast, BK, W);
+    const int nst = (tile_bmax > 0) ? (int)((tile_bmax + CB - 1) / CB) : 0;
+    const bf16_t *Sg = S0 + bh * nb * 4 * D;
+    auto load_mt = [&](int st, int mt, abf16x8 (&af)[NKS]) {
+        int64_t blk = 1 + (int64_t)st * CB + 4 * mt + (l16 >> 2);
+        blk = (blk <= tile_bmax) ? blk : tile_bmax;
+        const bf16_t *src = Sg + (blk * 4 + (l16 & 3)) * D + 8 * lg;
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) af[ks] = a_ldb8(src + 32 * ks);
+    };
+    auto stage = [&](int st, abf16x8 (&af)[4][NKS], int nxt) {
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+            af32x4 acc[NCT];
+#pragma unroll
+            for (int ct = 0; ct < NCT; ++ct) acc[ct] = af32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < NKS; ++ks)
+#pragma unroll
+                for (int ct = 0; ct < NCT; ++ct)
+                    acc[ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[mt][ks], qb[ct][ks], acc[ct], 0, 0, 0);
+            if (D > 64 && nxt >= 0) load_mt(nxt, mt, af[mt]);   // wave-uniform
+            const int64_t c = 1 + (int64_t)st * CB + 4 * mt + lg;
+#pragma unroll
+            for (int ct = 0; ct < NCT; ++ct) {
+                const int64_t i = i0 + 16 * ct + l16;
+                if (i >= n || c > bm[ct]) continue;
+                float best = -INFINITY;
+                uint32_t mask = 0;
+#pragma unroll
+                for (int sl = 0; sl < 4; ++sl) {
+                    const float v = acc[ct][sl];
+                    if (v > best) {
+                        best = v;
+                        mask = 1u << sl;
+                    } else if (v == best) {
+                        mask |= 1u << sl;
+                    }
+                }
+                const int64_t o = (bh * n + i) * nb + c;
+                bsc[o] = best * scale_r;
+                ties[o] = (uint8_t)mask;
+            }
+        }
+    };
+    auto load = [&](int st, abf16x8 (&af)[4][NKS]) {
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) load_mt(st, mt, af[mt]);
+    };
+    if constexpr (D > 64) {
+        abf16x8 a0[4][NKS];
+        int st = w;
+        if (st < nst) load(st, a0);
+        while (st < nst) {
+            stage(st, a0, (st + 4 < nst) ? st + 4 : -1);
+            st += 4;
+        }
+    } else {
+        abf16x8 a0[4][NKS], a1[4][NKS];
+        int st = w;
+        if (st < nst) load(st, a0);
+        if (st + 4 < nst) load(st + 4, a1);
+        while (st < nst) {
+            stage(st, a0, -1);
+            if (st + 8 < nst) load(st + 8, a0);
+            st += 4;
+            if (st >= nst) break;
+            stage(st, a1, -1);
+            if (st + 8 < nst) load(st + 8, a1);
+            st += 4;
+        }
+    }
+}
+
 // ------------------------------------------------------------- teacher -----
 // Each wave owns 16 columns: QPW = 16/G queries x the G heads of KV head g
 // (column c -> query i0w + c/G, head g*G + c%G; columns past QPW*G idle).
@@ -695,9 +823,14 @@ extern "C" int hba_aux_kl(int dtype, const void *q, const int64_t q_strides[3], 
         hipLaunchKernelGGL((aux::aux_qc_kernel<DT, D>), dim3((unsigned)((B * n * Hq + 255) / 256)),       \
                            dim3(256), 0, s, (const T *)q, q_strides[0], q_strides[1], q_strides[2], q_gain, \
                            eps, B, n, Hq, qc);                                                           \
-        hipLaunchKernelGGL((aux::aux_scores_kernel<DT, D>), dim3((unsigned)((n + 63) / 64), (unsigned)Hkv,  \
-                           (unsigned)B), dim3(256), 0, s, (const T *)qc, (const T *)S0, n, Hq, Hkv, (int)m, W, \
-                           scale_r, qg, bsc, ties);                                                      \
+        if (DT == 1 && m == 4)                                                                           \
+            hipLaunchKernelGGL((aux::aux_scores_mfma_kernel<D>), dim3((unsigned)((n + 63) / 64),         \
+                               (unsigned)Hkv, (unsigned)B), dim3(256), 0, s, (const bf16_t *)qc,          \
+                               (const bf16_t *)S0, n, Hq, Hkv, W, scale_r, qg, bsc, ties);                \
+        else                                                                                             \
+            hipLaunchKernelGGL((aux::aux_scores_kernel<DT, D>), dim3((unsigned)((n + 63) / 64),          \
+                               (unsigned)Hkv, (unsigned)B), dim3(256), 0, s, (const T *)qc, (const T *)S0, n, \
+                               Hq, Hkv, (int)m, W, scale_r, qg, bsc, ties);                              \
         const int64_t qpw = 16 / G;                                                                      \
         if (DT == 1)                                                                                     \
             hipLaunchKernelGGL((aux::aux_teacher_bf16_kernel<D>),                                        \
