@@ -658,6 +658,88 @@ __global__ __launch_bounds__(1024) void aux_dsum_kernel(const float *__restrict_
     }
 }
 
+// The same partials on fp32 MFMA (v_mfma_f32_16x16x4_f32): per 64-query
+// chunk, dS0 rows (block, slot) += A^T . qg with A[q][(block, slot)] = the
+// query's d bsc * scale / tie count where the slot is one of its maxima, else
+// 0.  A workgroup takes 64 / m blocks (64 rows, 4 M-tiles) and one query
+// segment, so that each staged chunk of qg serves 16 blocks; wave w takes
+// the 16-column tiles w, w + 4, ... of d.  fp32 operands: the products are
+// those of the scalar chain, the sums run in the MFMA's fixed order.
+template <int D>
+__global__ __launch_bounds__(256) void aux_dsum_mfma_kernel(const float *__restrict__ dbsc,
+                                                            const uint8_t *__restrict__ ties,
+                                                            const float *__restrict__ qg, int64_t n, int64_t Hkv,
+                                                            int m, int64_t W, float scale_r,
+                                                            float *__restrict__ pdS0) {
+    constexpr int NDT = D / 16, DTW = NDT / 4;      // 16-column tiles of d; per wave
+    __shared__ float qgs[64][D + 4];
+    __shared__ float ca[64][64 + 4];                 // [query][row = block * m + slot]
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, l16 = lane & 15, lg = lane >> 4;
+    const int bt = 64 / m;                           // blocks per workgroup
+    const int64_t c0 = (int64_t)blockIdx.x * bt, qs = blockIdx.y % QS, g = blockIdx.y / QS, b = blockIdx.z;
+    const int64_t nb = n / BK;
+    const int64_t bg = b * Hkv + g;
+    af32x4 acc[4][DTW];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int u = 0; u < DTW; ++u) acc[mt][u] = af32x4{0.f, 0.f, 0.f, 0.f};
+    // this segment's 64-query chunks of the first block's candidate queries
+    const int64_t ilo = (c0 + 1) * BK + W - 1;
+    const int64_t nch = (ilo < n) ? (n - ilo + 63) / 64 : 0;
+    const int64_t per = (nch + QS - 1) / QS;
+    const int64_t k0 = qs * per, k1 = (k0 + per < nch) ? k0 + per : nch;
+    for (int64_t kc_ = k0; kc_ < k1; ++kc_) {
+        const int64_t i0 = ilo + kc_ * 64;
+        __syncthreads();   // the previous chunk is used
+        for (int e = tid; e < 64 * D; e += 256) {
+            const int64_t i = i0 + e / D;
+            qgs[e / D][e % D] = (i < n) ? qg[(bg * n + i) * D + e % D] : 0.0f;
+        }
+        for (int e = tid; e < 64 * bt; e += 256) {
+            const int qi = e / bt, j = e % bt;
+            const int64_t i = i0 + qi, cj = c0 + j;
+            float cf = 0.0f;
+            uint32_t mk = 0;
+            if (i < n && cj < nb && cj >= 1 && cj <= cand_bmax(i, BK, W)) {
+                const int64_t o = (bg * n + i) * nb + cj;
+                mk = ties[o];
+                cf = dbsc[o] * scale_r / (float)__builtin_popcount(mk);
+            }
+            for (int sl = 0; sl < m; ++sl) ca[qi][j * m + sl] = ((mk >> sl) & 1u) ? cf : 0.0f;
+        }
+        __syncthreads();
+        // A: row l16 of M-tile mt, queries 4 ks + lg; B: query 4 ks + lg, column l16 of the d tile
+#pragma unroll 4
+        for (int ks = 0; ks < 16; ++ks) {
+            const int qk = 4 * ks + lg;
+            float a[4];
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) a[mt] = ca[qk][16 * mt + l16];
+#pragma unroll
+            for (int u = 0; u < DTW; ++u) {
+                const float bv = qgs[qk][16 * (w + 4 * u) + l16];
+#pragma unroll
+                for (int mt = 0; mt < 4; ++mt)
+                    acc[mt][u] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[mt], bv, acc[mt][u], 0, 0, 0);
+            }
+        }
+    }
+    // C row 4 lg + e of M-tile mt is dS0 row 16 mt + 4 lg + e = block * m + slot; column l16 of tile w + 4 u
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int r = 16 * mt + 4 * lg + e;
+            const int64_t c = c0 + r / m;
+            const int sl = r % m;
+            if (r / m >= bt || c >= nb) continue;
+            float *dst = pdS0 + ((qs * Hkv * gridDim.z + bg) * nb + c) * m * D + sl * D;
+#pragma unroll
+            for (int u = 0; u < DTW; ++u) dst[16 * (w + 4 * u) + l16] = acc[mt][u][e];
+        }
+}
+
 // -------------------------------------------------- summariser backward ----
 // Workgroup = (block c, g, b): recompute the block's slot attention (att) and
 // pooled rows (Sp) from its keys, then with dO = d aux / d S0[c]:
@@ -853,9 +935,14 @@ extern "C" int hba_aux_kl(int dtype, const void *q, const int64_t q_strides[3], 
 #define HBA_AUX_BWD(DT, D)                                                                               \
     do {                                                                                                 \
         typedef St<DT>::T T;                                                                             \
-        hipLaunchKernelGGL((aux::aux_dsum_kernel<D>), dim3((unsigned)((nb + 16 / m - 1) / (16 / m)),     \
-                           (unsigned)(Hkv * aux::QS), (unsigned)B), dim3(1024), 0, s, bsc, ties, qg, n, Hkv, \
-                           (int)m, W, scale_r, pdS0);                                                    \
+        if (64 % m == 0)                                                                                 \
+            hipLaunchKernelGGL((aux::aux_dsum_mfma_kernel<D>), dim3((unsigned)((nb + 64 / m - 1) / (64 / m)), \
+                               (unsigned)(Hkv * aux::QS), (unsigned)B), dim3(256), 0, s, bsc, ties, qg, n,  \
+                               Hkv, (int)m, W, scale_r, pdS0);                                           \
+        else                                                                                             \
+            hipLaunchKernelGGL((aux::aux_dsum_kernel<D>), dim3((unsigned)((nb + 16 / m - 1) / (16 / m)), \
+                               (unsigned)(Hkv * aux::QS), (unsigned)B), dim3(1024), 0, s, bsc, ties, qg, n, \
+                               Hkv, (int)m, W, scale_r, pdS0);                                           \
         hipLaunchKernelGGL(aux::aux_gsum_kernel, dim3((unsigned)((B * Hkv * nb * m * d + 255) / 256)),   \
                            dim3(256), 0, s, pdS0, (int64_t)aux::QS, B * Hkv * nb * m * d, dS0);          \
         hipLaunchKernelGGL((aux::aux_sbwd_kernel<DT, D>), dim3((unsigned)nb, (unsigned)Hkv, (unsigned)B),  \
