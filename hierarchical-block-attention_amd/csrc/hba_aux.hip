@@ -665,7 +665,8 @@ __global__ __launch_bounds__(1024) void aux_dsum_kernel(const float *__restrict_
 // segment, so that each staged chunk of qg serves 16 blocks; wave w takes
 // the 16-column tiles w, w + 4, ... of d.  fp32 operands: the products are
 // those of the scalar chain, the sums run in the MFMA's fixed order.
-template <int D>
+// CE: (d bsc, tie mask) entries per thread and chunk, 64 * (64 / m) / 256 rounded up (4 for m >= 4)
+template <int D, int CE>
 __global__ __launch_bounds__(256) void aux_dsum_mfma_kernel(const float *__restrict__ dbsc,
                                                             const uint8_t *__restrict__ ties,
                                                             const float *__restrict__ qg, int64_t n, int64_t Hkv,
@@ -689,26 +690,55 @@ __global__ __launch_bounds__(256) void aux_dsum_mfma_kernel(const float *__restr
     const int64_t nch = (ilo < n) ? (n - ilo + 63) / 64 : 0;
     const int64_t per = (nch + QS - 1) / QS;
     const int64_t k0 = qs * per, k1 = (k0 + per < nch) ? k0 + per : nch;
-    for (int64_t kc_ = k0; kc_ < k1; ++kc_) {
+    // chunk staging through registers, one chunk ahead of the products:
+    // qg rows (64 x D) and the 64 x bt (d bsc, tie mask) entries
+    constexpr int QPT = 64 * D / 256;
+    float rq[QPT];
+    float rc[CE];
+    uint32_t rm[CE];
+    auto gload = [&](int64_t kc_) {
         const int64_t i0 = ilo + kc_ * 64;
-        __syncthreads();   // the previous chunk is used
-        for (int e = tid; e < 64 * D; e += 256) {
+#pragma unroll
+        for (int r = 0; r < QPT; ++r) {
+            const int e = tid + 256 * r;
             const int64_t i = i0 + e / D;
-            qgs[e / D][e % D] = (i < n) ? qg[(bg * n + i) * D + e % D] : 0.0f;
+            rq[r] = (i < n) ? qg[(bg * n + i) * D + e % D] : 0.0f;
         }
-        for (int e = tid; e < 64 * bt; e += 256) {
+#pragma unroll
+        for (int r = 0; r < CE; ++r) {
+            const int e = tid + 256 * r;
             const int qi = e / bt, j = e % bt;
             const int64_t i = i0 + qi, cj = c0 + j;
-            float cf = 0.0f;
-            uint32_t mk = 0;
-            if (i < n && cj < nb && cj >= 1 && cj <= cand_bmax(i, BK, W)) {
+            rc[r] = 0.0f;
+            rm[r] = 0u;
+            if (e < 64 * bt && i < n && cj < nb && cj >= 1 && cj <= cand_bmax(i, BK, W)) {
                 const int64_t o = (bg * n + i) * nb + cj;
-                mk = ties[o];
-                cf = dbsc[o] * scale_r / (float)__builtin_popcount(mk);
+                rm[r] = ties[o];
+                rc[r] = dbsc[o];
             }
-            for (int sl = 0; sl < m; ++sl) ca[qi][j * m + sl] = ((mk >> sl) & 1u) ? cf : 0.0f;
         }
+    };
+    auto lstore = [&]() {
+#pragma unroll
+        for (int r = 0; r < QPT; ++r) {
+            const int e = tid + 256 * r;
+            qgs[e / D][e % D] = rq[r];
+        }
+#pragma unroll
+        for (int r = 0; r < CE; ++r) {
+            const int e = tid + 256 * r;
+            if (e >= 64 * bt) continue;
+            const int qi = e / bt, j = e % bt;
+            const float cf = rm[r] ? rc[r] * scale_r / (float)__builtin_popcount(rm[r]) : 0.0f;
+            for (int sl = 0; sl < m; ++sl) ca[qi][j * m + sl] = ((rm[r] >> sl) & 1u) ? cf : 0.0f;
+        }
+    };
+    if (k0 < k1) gload(k0);
+    for (int64_t kc_ = k0; kc_ < k1; ++kc_) {
+        __syncthreads();   // the previous chunk is used
+        lstore();
         __syncthreads();
+        if (kc_ + 1 < k1) gload(kc_ + 1);   // in flight during this chunk's products
         // A: row l16 of M-tile mt, queries 4 ks + lg; B: query 4 ks + lg, column l16 of the d tile
 #pragma unroll 4
         for (int ks = 0; ks < 16; ++ks) {
@@ -935,8 +965,12 @@ extern "C" int hba_aux_kl(int dtype, const void *q, const int64_t q_strides[3], 
 #define HBA_AUX_BWD(DT, D)                                                                               \
     do {                                                                                                 \
         typedef St<DT>::T T;                                                                             \
-        if (64 % m == 0)                                                                                 \
-            hipLaunchKernelGGL((aux::aux_dsum_mfma_kernel<D>), dim3((unsigned)((nb + 64 / m - 1) / (64 / m)), \
+        if (64 % m == 0 && m >= 4)                                                                       \
+            hipLaunchKernelGGL((aux::aux_dsum_mfma_kernel<D, 4>), dim3((unsigned)((nb + 64 / m - 1) / (64 / m)), \
+                               (unsigned)(Hkv * aux::QS), (unsigned)B), dim3(256), 0, s, bsc, ties, qg, n,  \
+                               Hkv, (int)m, W, scale_r, pdS0);                                           \
+        else if (64 % m == 0)                                                                            \
+            hipLaunchKernelGGL((aux::aux_dsum_mfma_kernel<D, 16>), dim3((unsigned)((nb + 64 / m - 1) / (64 / m)), \
                                (unsigned)(Hkv * aux::QS), (unsigned)B), dim3(256), 0, s, bsc, ties, qg, n,  \
                                Hkv, (int)m, W, scale_r, pdS0);                                           \
         else                                                                                             \

@@ -750,14 +750,18 @@ AUX_TOL = {"f32": (1e-6, 2e-5), "bf16": (1e-6, 2e-5)}
 AUX_BF16_EXACT_S0_TOL = (2e-5, 8e-2)
 
 
-@pytest.mark.parametrize("dt,d,Hq,Hkv,qknorm,B", [("f32", 64, 14, 2, True, 2), ("bf16", 64, 14, 2, True, 1),
-                                                  ("f32", 128, 28, 4, False, 1), ("bf16", 128, 28, 4, True, 1)])
-def test_aux_kl_matches_oracle(dev, dt, d, Hq, Hkv, qknorm, B):
+@pytest.mark.parametrize("dt,d,Hq,Hkv,qknorm,B,m", [("f32", 64, 14, 2, True, 2, 4), ("bf16", 64, 14, 2, True, 1, 4),
+                                                    ("f32", 128, 28, 4, False, 1, 4), ("bf16", 128, 28, 4, True, 1, 4),
+                                                    ("bf16", 64, 8, 2, True, 1, 2), ("f32", 64, 8, 2, False, 1, 8),
+                                                    ("f32", 64, 6, 2, True, 1, 3)])
+def test_aux_kl_matches_oracle(dev, dt, d, Hq, Hkv, qknorm, B, m):
     """hba_aux_kl at the kernels' geometries (G = 7, d = 64 and 128, qknorm
-    on and off, B = 2) against the oracle's float64 aux and gradients on the
-    same storage-rounded content q/k (n = 2048, W = 512: 1535 queries with
+    on and off, B = 2; 2, 3, 4 and 8 slots: the dS0 products take 16 or 4
+    staged entries per thread, or the scalar kernel where 64 % m != 0)
+    against the oracle's float64 aux and gradients on the same
+    storage-rounded content q/k (n = 2048, W = 512: 1535 queries with
     candidates, up to 23 candidate blocks)."""
-    n, W, m = 2048, 512, 4
+    n, W = 2048, 512
     rs = np.random.RandomState(7 + d + B)
     inp = dict(q=rs.standard_normal((B, n, Hq, d)).astype(np.float32),
                k=rs.standard_normal((B, n, Hkv, d)).astype(np.float32),
