@@ -76,8 +76,9 @@ def layer_setup(dev):
 
 def run_layer_overlapped(cfg, x, prm, cos, sin):
     """One layer forward as forward_stages(overlap=True) runs it in bf16: the
-    attention as two launches, the window on a second stream concurrent with
-    summarize and score_select, the sinks + routed launch after both."""
+    keys and block summaries in one launch, then the attention as two
+    launches, the window on a second stream concurrent with score_select, the
+    sinks + routed launch after both."""
     import torch
     from hba_amd import ops
     qeps = keps = 1e-6
@@ -85,7 +86,7 @@ def run_layer_overlapped(cfg, x, prm, cos, sin):
     n, Hkv, d = q.shape[1], x["k"].shape[2], q.shape[3]
     from hba_amd.config import union_scale
     scale = union_scale(cfg, d, n)
-    kc, kr, vt = ops.prep_keys(x["k"], x["v"], prm.k.gain, keps, cos, sin)
+    kc, kr, vt, S0 = ops.prep_keys_summarize(x["k"], x["v"], prm.k.gain, keps, cos, sin, prm.probes, prm.proj)
     main = torch.cuda.current_stream()
     side = ops.side_stream(q.device)
     out, ws = ops.attn_buffers(q, Hkv)
@@ -94,7 +95,6 @@ def run_layer_overlapped(cfg, x, prm, cos, sin):
         ops.attn_window_(q, prm.q.gain, prm.k.gain, qeps, kr, vt, cos, sin, cfg.sinks, cfg.window, scale, out, ws)
     for t in (out, ws, kr, vt):
         t.record_stream(side)
-    S0 = ops.summarize(kc, prm.probes, prm.proj)
     idx, val, cnt = ops.score_select(q, prm.q.gain, qeps, S0, cfg.window, cfg.k_blocks, scale)
     main.wait_stream(side)
     return ops.attn_routed_(q, prm.q.gain, prm.k.gain, qeps, kc, vt, idx, cnt, cfg.sinks, scale, out, ws)
@@ -114,11 +114,8 @@ def run_layer(cfg, x, prm, cos, sin, ev=None):
     from hba_amd.config import union_scale
     scale = union_scale(cfg, d, n)
     mark("prep", 0)
-    kc, kr, vt = ops.prep_keys(x["k"], x["v"], prm.k.gain, keps, cos, sin)
+    kc, kr, vt, S0 = ops.prep_keys_summarize(x["k"], x["v"], prm.k.gain, keps, cos, sin, prm.probes, prm.proj)
     mark("prep", 1)
-    mark("summ", 0)
-    S0 = ops.summarize(kc, prm.probes, prm.proj)
-    mark("summ", 1)
     mark("select", 0)
     idx, val, cnt = ops.score_select(x["q"], prm.q.gain, qeps, S0, cfg.window, cfg.k_blocks, scale)
     mark("select", 1)
@@ -150,7 +147,7 @@ def bench_layer(dev, steps, warmup):
     ms_split = t4.elapsed_time(t5) / steps
     # the stages in sequence, each bracketed by events: the per-stage times
     # and the attention op's own duration (roofline)
-    names = ("prep", "summ", "select", "attn")
+    names = ("prep", "select", "attn")   # prep: the keys and the block summaries, one launch
     evs = [{k: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for k in names}
            for _ in range(steps)]
     t2 = torch.cuda.Event(enable_timing=True)
@@ -577,12 +574,12 @@ def bench_donor(dev, steps=64):
     Lmax = n + 4 * steps + 3          # the tokens appended below: 1 + steps + 2 (1 + steps) + steps
     cos, sin = hba_amd.rope_tables(Lmax, d, cfg.rope_theta, dev)
     scale = union_scale(cfg, d, n)
-    t_prep, (kc, kr, vt) = _timed(lambda: ops.prep_keys(x["k"], x["v"], prm.k.gain, 1e-6, cos, sin), reps=3)
-    t_summ, S0 = _timed(lambda: ops.summarize(kc, prm.probes, prm.proj), reps=3)
+    t_prep, (kc, kr, vt, S0) = _timed(lambda: ops.prep_keys_summarize(x["k"], x["v"], prm.k.gain, 1e-6, cos, sin,
+                                                                      prm.probes, prm.proj), reps=3)
     t_sel, (idx, val, cnt) = _timed(lambda: ops.score_select(x["q"], prm.q.gain, 1e-6, S0, W, k, scale), reps=3)
     t_attn, _ = _timed(lambda: ops.attn_fwd(x["q"], prm.q.gain, prm.k.gain, 1e-6, kc, kr, vt, cos, sin, idx, cnt,
                                             S, W, scale), reps=3)
-    t_layer = t_prep + t_summ + t_sel + t_attn
+    t_layer = t_prep + t_sel + t_attn
     flop = (synth.attention_flops(B, n, Hq, d, S, W, 64, k) + synth.scoring_flops(B, n, Hkv, d, m, 64, W) +
             synth.summarizer_flops(B, n, Hkv, d, m, 64))
     # decode continuation from the prefill cache
@@ -640,7 +637,7 @@ def bench_donor(dev, steps=64):
             "config": {"workload": "hba_layer_fwd_donor_64k_d128", "batch": B, "seq_len": n, "q_heads": Hq,
                        "kv_heads": Hkv, "head_dim": d, "sinks": S, "window": W, "top_k": k, "decode_steps": steps},
             "prefill": {"tokens_per_s": round(B * n / (t_layer * 1e-3), 1), "ms": round(t_layer, 4),
-                        "stage_ms": {"prep": round(t_prep, 4), "summ": round(t_summ, 4), "select": round(t_sel, 4),
+                        "stage_ms": {"prep_and_summaries": round(t_prep, 4), "select": round(t_sel, 4),
                                      "attn": round(t_attn, 4)},
                         "mfma_frac": round(flop / (t_layer * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)},
             "decode": {"step_us_median": round(step_us[len(step_us) // 2], 2),
@@ -730,8 +727,8 @@ def main():
                      "mean_keys_per_query": round(res["mean_keys"], 1)},
         "layer_frac_of_mfma_roofline": round(total_flop / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
         "stage_ms": {k: round(v, 4) for k, v in res["stage_ms"].items()},
-        "schedule": {"step": "prep_keys, summarize, score_select, hba_attn_fwd (one launch) in sequence on "
-                             "one stream",
+        "schedule": {"step": "prep_keys_summarize (keys and block summaries, one launch), score_select, "
+                             "hba_attn_fwd (one launch) in sequence on one stream",
                      "ms_per_step_two_launch_attn_window_overlapped": round(res["ms_split"], 4),
                      "ms_per_step_with_stage_events": round(res["ms_marked"], 4)},
         "decode": dec,

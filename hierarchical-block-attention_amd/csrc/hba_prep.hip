@@ -107,21 +107,21 @@ __device__ __forceinline__ void store8(typename St<DT>::T *p, const float (&x)[8
 // rotation's partner elements (rotate-half) come from lane c ^ (D/16).  The
 // values are transposed through LDS, so that vt rows are written as 8
 // consecutive keys per lane.
+// kb (optional): the tile's kc rows as floats, row stride D + 1, for a
+// summary of the block in the same workgroup.  256 threads.
 template <int DT, int D>
-__global__ __launch_bounds__(256) void prep_keys_kernel(
+__device__ __forceinline__ void prep_tile(
     const typename St<DT>::T *__restrict__ k, int64_t ksb, int64_t ksn, int64_t ksh,
     const typename St<DT>::T *__restrict__ v, int64_t vsb, int64_t vsn, int64_t vsh,
     const float *__restrict__ kgain, float eps, const float *__restrict__ cosT,
-    const float *__restrict__ sinT, int64_t n, int64_t Hkv, int64_t ntile,
+    const float *__restrict__ sinT, int64_t n, int64_t Hkv, int64_t tile, int64_t bg,
     typename St<DT>::T *__restrict__ kc, typename St<DT>::T *__restrict__ kr,
-    typename St<DT>::T *__restrict__ vt) {
+    typename St<DT>::T *__restrict__ vt, float *__restrict__ kb) {
     using T = typename St<DT>::T;
     constexpr int TPH = D / 8;          // lanes per key row
     constexpr int RPP = 256 / TPH;      // rows per pass
     __shared__ float vs[D][65];         // the tile's values (exact in fp32), key-minor
     const int tid = threadIdx.x;
-    const int64_t tile = blockIdx.x % ntile;
-    const int64_t bg = blockIdx.x / ntile;   // b * Hkv + g
     const int64_t b = bg / Hkv, g = bg % Hkv;
     const int jl = tid % TPH, t0 = 8 * jl;
     const bool lo = t0 < D / 2;
@@ -156,6 +156,10 @@ __global__ __launch_bounds__(256) void prep_keys_kernel(
         }
         const int64_t row = (bg * n + jj) * D + t0;
         if (act) store8<DT>(kc + row, x);
+        if (kb) {
+#pragma unroll
+            for (int u = 0; u < 8; ++u) kb[r * (D + 1) + t0 + u] = x[u];
+        }
         if (kr) {
             float cs[8], sn[8], y[8];
             load8<0>(cosT + jj * D + t0, cs);
@@ -196,6 +200,18 @@ __global__ __launch_bounds__(256) void prep_keys_kernel(
                 if (jo + u < n) St<DT>::st(vrow, (int64_t)t * n + jo + u, o[u]);
         }
     }
+}
+
+template <int DT, int D>
+__global__ __launch_bounds__(256) void prep_keys_kernel(
+    const typename St<DT>::T *__restrict__ k, int64_t ksb, int64_t ksn, int64_t ksh,
+    const typename St<DT>::T *__restrict__ v, int64_t vsb, int64_t vsn, int64_t vsh,
+    const float *__restrict__ kgain, float eps, const float *__restrict__ cosT,
+    const float *__restrict__ sinT, int64_t n, int64_t Hkv, int64_t ntile,
+    typename St<DT>::T *__restrict__ kc, typename St<DT>::T *__restrict__ kr,
+    typename St<DT>::T *__restrict__ vt) {
+    prep_tile<DT, D>(k, ksb, ksn, ksh, v, vsb, vsn, vsh, kgain, eps, cosT, sinT, n, Hkv, blockIdx.x % ntile,
+                     blockIdx.x / ntile, kc, kr, vt, nullptr);
 }
 
 // LDS of one block summary: the block's 64 key rows (reused, once the pooled
@@ -355,6 +371,31 @@ __global__ __launch_bounds__(256) void summarize_kernel(
     }
     __syncthreads();
     summarize_staged<DT, D, LONE>(sm, probes + g * m * D, proj + g * D * D, m, att_scale, dst, tid);
+}
+
+// prep_keys and the slot summaries of every full block in one launch: the
+// workgroup of a 64-key tile keeps its kc rows (as the floats it stores) in
+// LDS and runs summarize_staged on them, so that S0 has the bits of
+// summarize_kernel over the stored kc, without its launch and its re-read.
+template <int DT, int D>
+__global__ __launch_bounds__(256) void prep_summ_kernel(
+    const typename St<DT>::T *__restrict__ k, int64_t ksb, int64_t ksn, int64_t ksh,
+    const typename St<DT>::T *__restrict__ v, int64_t vsb, int64_t vsn, int64_t vsh,
+    const float *__restrict__ kgain, float eps, const float *__restrict__ cosT,
+    const float *__restrict__ sinT, int64_t n, int64_t Hkv, int64_t ntile,
+    typename St<DT>::T *__restrict__ kc, typename St<DT>::T *__restrict__ kr,
+    typename St<DT>::T *__restrict__ vt, const float *__restrict__ probes, const float *__restrict__ proj,
+    int m, float att_scale, typename St<DT>::T *__restrict__ S0) {
+    __shared__ SummSmem<D, false> sm;
+    const int64_t tile = blockIdx.x % ntile, bg = blockIdx.x / ntile;
+    prep_tile<DT, D>(k, ksb, ksn, ksh, v, vsb, vsn, vsh, kgain, eps, cosT, sinT, n, Hkv, tile, bg, kc, kr, vt,
+                     &sm.kb[0][0]);
+    const int64_t nb = n / 64;
+    if (tile >= nb) return;   // a partial last tile has no summary (workgroup-uniform)
+    __syncthreads();          // every kb row is written
+    const int64_t g = bg % Hkv;
+    summarize_staged<DT, D, false>(sm, probes + g * m * D, proj + g * D * D, m, att_scale,
+                                   S0 + (bg * nb + tile) * m * D, threadIdx.x);
 }
 
 // Super-summaries: sequential child sum, rounded, divided by the child count,
@@ -603,6 +644,40 @@ extern "C" int hba_prep_keys(int dtype, const void *k, const int64_t k_strides[3
                        Hkv, ntile, (St<DT>::T *)kc, (St<DT>::T *)kr, (St<DT>::T *)vt)
     HBA_DISPATCH_DT_D(dtype, d, HBA_PREP);
 #undef HBA_PREP
+    HBA_LAUNCH_CHECK();
+    return HBA_OK;
+}
+
+extern "C" int hba_prep_keys_summarize(int dtype, const void *k, const int64_t k_strides[3], const void *v,
+                                       const int64_t v_strides[3], const float *k_gain, float eps,
+                                       const float *cos_tab, const float *sin_tab, int64_t B, int64_t n,
+                                       int64_t Hkv, int64_t d, void *kc, void *kr, void *vt, const float *probes,
+                                       const float *proj, int64_t m, void *S0, void *stream) {
+    int st = abi::check_dtype_dim(dtype, d);
+    if (st) return st;
+    if (!k || !k_strides || !kc || !probes || !proj || !S0 || B <= 0 || n <= 0 || Hkv <= 0)
+        return HBA_ERR_INVALID_ARG;
+    if (kr && (!cos_tab || !sin_tab)) return HBA_ERR_INVALID_ARG;
+    if (vt && (!v || !v_strides)) return HBA_ERR_INVALID_ARG;
+    if (m < 1 || m > 8) return HBA_ERR_UNSUPPORTED;
+    if (kr && (!abi::aligned16(cos_tab) || !abi::aligned16(sin_tab))) return HBA_ERR_UNSUPPORTED;
+    if (!abi::rows_aligned(dtype, k, k_strides) || (vt && !abi::rows_aligned(dtype, v, v_strides)) ||
+        !abi::aligned16(kc) || (kr && !abi::aligned16(kr)))
+        return HBA_ERR_UNSUPPORTED;
+    hipStream_t s = (hipStream_t)stream;
+    const int64_t ntile = (n + 63) / 64;
+    if (B * Hkv * ntile > 0x7fffffff) return HBA_ERR_UNSUPPORTED;
+    dim3 grid((unsigned)(B * Hkv * ntile));
+    const int64_t *vs = v_strides ? v_strides : k_strides;
+    const float att_scale = (float)(1.0 / __builtin_sqrt((double)d));
+#define HBA_PREP_SUMM(DT, D)                                                                       \
+    hipLaunchKernelGGL((prep_summ_kernel<DT, D>), grid, dim3(256), 0, s,                           \
+                       (const St<DT>::T *)k, k_strides[0], k_strides[1], k_strides[2],             \
+                       (const St<DT>::T *)v, vs[0], vs[1], vs[2], k_gain, eps, cos_tab, sin_tab, n, \
+                       Hkv, ntile, (St<DT>::T *)kc, (St<DT>::T *)kr, (St<DT>::T *)vt, probes, proj, \
+                       (int)m, att_scale, (St<DT>::T *)S0)
+    HBA_DISPATCH_DT_D(dtype, d, HBA_PREP_SUMM);
+#undef HBA_PREP_SUMM
     HBA_LAUNCH_CHECK();
     return HBA_OK;
 }

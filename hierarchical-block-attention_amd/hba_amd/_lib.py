@@ -24,6 +24,8 @@ SIGNATURES = {
     "hba_device_check": [],
     "hba_prep_keys": [_i, _vp, _c_i64p, _vp, _c_i64p, _vp, _f, _vp, _vp, _i64, _i64, _i64, _i64,
                       _vp, _vp, _vp, _vp],
+    "hba_prep_keys_summarize": [_i, _vp, _c_i64p, _vp, _c_i64p, _vp, _f, _vp, _vp, _i64, _i64, _i64, _i64,
+                                _vp, _vp, _vp, _vp, _vp, _i64, _vp, _vp],
     "hba_summarize": [_i, _vp, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _vp],
     "hba_build_super": [_i, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp],
     "hba_score_select": [_i, _vp, _c_i64p, _vp, _f, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64,

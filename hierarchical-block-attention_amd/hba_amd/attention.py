@@ -110,10 +110,11 @@ def _forward_generic(q, k, v, cos, sin, cfg, summ, qkn, hier, dense_route):
 def forward_stages(q, k, v, cos, sin, cfg, summ, qkn, hier=False, dense_route=False, overlap=False):
     """The forward path stage by stage; returns a dict with every intermediate
     (kc, kr, vt, S0, [S1], idx, val, cnt, out) and the scales used.  Every
-    stage runs in sequence on the current stream; the bf16 attention is one
+    stage runs in sequence on the current stream: the key preparation with
+    the block summaries (one launch), the selection, the attention; the bf16 attention is one
     launch over the whole union.  overlap=True (bf16) instead runs the
     attention as two launches, the window on a second stream while the
-    summaries and the selection run on this one, then the sinks and routed
+    selection runs on this one, then the sinks and routed
     blocks merged into it by LSE (the same softmax, with the window rows
     rounded to bf16 once before the merge).  Geometry the tuned kernels do
     not take (_tuned) runs on the generic fp32 kernels (_forward_generic)."""
@@ -125,7 +126,9 @@ def forward_stages(q, k, v, cos, sin, cfg, summ, qkn, hier=False, dense_route=Fa
     scale = union_scale(cfg, dh, n)
     sel_scale = route_scale(cfg, dh) if dense_route else scale
     r = {"scale": scale, "sel_scale": sel_scale}
-    r["kc"], r["kr"], r["vt"] = ops.prep_keys(k, v, kg, keps, cos, sin)
+    # the keys' QKNorm / RoPE / V^T and the block summaries in one launch
+    r["kc"], r["kr"], r["vt"], r["S0"] = ops.prep_keys_summarize(k, v, kg, keps, cos, sin, summ.probes,
+                                                                 summ.proj)
     kk = min(cfg.k_blocks, n // cfg.block)
     # bf16, overlap: the window launch needs no selection, so it can run on a
     # second stream while the summaries and the selection run on this one
@@ -139,7 +142,6 @@ def forward_stages(q, k, v, cos, sin, cfg, summ, qkn, hier=False, dense_route=Fa
             ops.attn_window_(q, qg, kg, qeps, r["kr"], r["vt"], cos, sin, cfg.sinks, cfg.window, scale, out, ws)
         for t in (out, ws, r["kr"], r["vt"]):
             t.record_stream(side)
-    r["S0"] = ops.summarize(r["kc"], summ.probes, summ.proj, cfg.block)
     if hier:
         r["S1"] = ops.build_super(r["S0"], cfg.fanout)
         r["idx"], r["val"], r["cnt"] = ops.hier_select(q, qg, qeps, r["S0"], r["S1"], cfg.window, kk,

@@ -108,6 +108,41 @@ def _(k, v, k_gain, eps, cos, sin):
     return kc, k.new_empty(B, Hkv, n, d), k.new_empty(B, Hkv, d, n)
 
 
+@torch.library.custom_op("hba::prep_keys_summarize", mutates_args=(), device_types="cuda")
+def prep_keys_summarize(k: Tensor, v: Tensor, k_gain: Optional[Tensor], eps: float, cos: Tensor, sin: Tensor,
+                        probes: Tensor, proj: Tensor) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
+    """prep_keys and summarize (64-key blocks) in one launch: (kc, kr, vt, S0),
+    each bit-identical to the two ops'; head dim 64 or 128 only."""
+    dev = _dev(k)
+    _rows(k, "k")
+    _rows(v, "v")
+    B, n, Hkv, d = k.shape
+    if v.shape != k.shape or v.dtype != k.dtype:
+        raise ValueError("v must match k in shape and dtype")
+    cos, sin = _tables(cos, sin, n, d, dev)
+    kg = _f32c(k_gain, dev, Hkv, "k_gain")
+    m = probes.shape[1]
+    pr = _f32c(probes, dev, Hkv * m * d, "probes")
+    pj = _f32c(proj, dev, Hkv * d * d, "proj")
+    kc = torch.empty(B, Hkv, n, d, dtype=k.dtype, device=dev)
+    kr = torch.empty_like(kc)
+    vt = torch.empty(B, Hkv, d, n, dtype=k.dtype, device=dev)
+    S0 = torch.empty(B, Hkv, n // BLOCK, m, d, dtype=k.dtype, device=dev)
+    with torch.cuda.device(dev):
+        st = lib().hba_prep_keys_summarize(_code(k), _p(k), strides3(k), _p(v), strides3(v), _p(kg), eps,
+                                           _p(cos), _p(sin), B, n, Hkv, d, _p(kc), _p(kr), _p(vt), _p(pr),
+                                           _p(pj), m, _p(S0), _stream(dev))
+    check(st, "hba_prep_keys_summarize")
+    return kc, kr, vt, S0
+
+
+@prep_keys_summarize.register_fake
+def _(k, v, k_gain, eps, cos, sin, probes, proj):
+    B, n, Hkv, d = k.shape
+    return (k.new_empty(B, Hkv, n, d), k.new_empty(B, Hkv, n, d), k.new_empty(B, Hkv, d, n),
+            k.new_empty(B, Hkv, n // BLOCK, probes.shape[1], d))
+
+
 @torch.library.custom_op("hba::summarize", mutates_args=(), device_types="cuda")
 def summarize(kc: Tensor, probes: Tensor, proj: Tensor, block: int = 64) -> Tensor:
     dev = _dev(kc)

@@ -86,6 +86,24 @@ int hba_summarize(int dtype, const void *kc, int64_t B, int64_t Hkv, int64_t n,
                   int64_t m, void *S0, void *stream);
 
 /*
+ * hba_prep_keys and hba_summarize (64-key blocks) in one launch: the
+ * workgroup of a 64-key tile summarises the kc rows it has just written, so
+ * that S0 is bit-identical to hba_summarize over that kc; tuned geometry
+ * only (bf16 or fp32, d = 64 or 128; 1 <= m <= 8).
+ *   replaces: _content_qk's key half + apply_rope  src/hba/attention.py:88-94, :40-44
+ *             SlotSummarizer.summarize            src/hba/summarizer.py:34-42
+ * Arguments as hba_prep_keys, then probes fp32 [Hkv, m, d], proj fp32
+ * [Hkv, d, d] and S0 [B, Hkv, n/64, m, d].
+ */
+int hba_prep_keys_summarize(int dtype, const void *k, const int64_t k_strides[3],
+                            const void *v, const int64_t v_strides[3],
+                            const float *k_gain, float eps,
+                            const float *cos_tab, const float *sin_tab,
+                            int64_t B, int64_t n, int64_t Hkv, int64_t d,
+                            void *kc, void *kr, void *vt, const float *probes,
+                            const float *proj, int64_t m, void *S0, void *stream);
+
+/*
  * Super-summaries: per-slot mean of `fanout` consecutive block summaries.
  *   replaces: build_super  src/hba/attention.py:202-214
  * S1 [B, Hkv, ceil(nb/fanout), m, d].

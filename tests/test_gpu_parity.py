@@ -83,6 +83,24 @@ def test_summarize_matches_oracle(dev, dt, d, m):
     assert np.abs(got - ref).max() <= tol * max(1.0, np.abs(ref).max())
 
 
+@pytest.mark.parametrize("dt,d,m,n,B,gain", [("bf16", 64, 4, 2048, 1, True), ("bf16", 64, 4, 1000, 2, False),
+                                             ("bf16", 128, 4, 1037, 2, True), ("f32", 64, 2, 512, 1, True),
+                                             ("f32", 128, 8, 640, 1, False), ("bf16", 64, 1, 64, 1, True)])
+def test_prep_keys_summarize_equals_the_two_ops(dev, dt, d, m, n, B, gain):
+    """hba_prep_keys_summarize (one launch) against hba_prep_keys then
+    hba_summarize, bit for bit on kc, kr, vt and S0: both dtypes, d = 64/128,
+    1/2/4/8 slots, with and without the key gains, B = 2, a partial last tile
+    (n % 64 != 0: no summary for it) and a sequence of one block."""
+    Hq, Hkv = (4, 2) if d == 64 else (8, 4)
+    cfg, x, prm, cos, sin = make(dev, dt, n=n, B=B, d=d, m=m, Hq=Hq, Hkv=Hkv, W=64)
+    kg = x["k_gain"] if gain else None
+    kc, kr, vt = ops.prep_keys(x["k"], x["v"], kg, 1e-6, cos, sin)
+    S0 = ops.summarize(kc, x["probes"], x["proj"])
+    got = ops.prep_keys_summarize(x["k"], x["v"], kg, 1e-6, cos, sin, x["probes"], x["proj"])
+    for name, a, b in zip(("kc", "kr", "vt", "S0"), (kc, kr, vt, S0), got):
+        assert a.shape == b.shape and torch.equal(a, b), name
+
+
 @pytest.mark.parametrize("dt", ["f32", "bf16"])
 @pytest.mark.parametrize("nb,F", [(32, 16), (37, 4), (8, 16)])
 def test_build_super_bit_exact(dev, dt, nb, F):
