@@ -44,7 +44,7 @@ ATTN_KERNELS = "hba_attn_fwd = attn_routed_kernel<64,2,false,true> (sinks + rout
 # FETCH_SIZE and WRITE_SIZE of the launch, each divided by the counter's
 # reading per byte of a plain device copy (python bench.py --copy-probe 1024);
 # profiles/hba_attn_32k_traffic.md.
-ATTN_TRAFFIC_BYTES = 543054738
+ATTN_TRAFFIC_BYTES = 500836152
 
 
 def cpu_model():
