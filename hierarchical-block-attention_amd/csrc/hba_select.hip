@@ -1011,7 +1011,9 @@ __host__ __device__ inline size_t bytes(int QG, int E, int beff, int nsp, int D)
 }
 }  // namespace hl2
 
-template <int D>
+// EL: list positions per ranking lane (16 lanes per query), at least
+// beff * F / 16: 8 at beam * fanout <= 128 (the 128K geometry), else 16.
+template <int D, int EL>
 __global__ __launch_bounds__(hl2::NT) void hier_l2_kernel(
     const bf16_t *__restrict__ S0, const bf16_t *__restrict__ rq, const int16_t *__restrict__ ks, int64_t n,
     int Hkv, int64_t nb, int64_t W, int kk, int F, int beff, int QG, int ngroups, float scale,
@@ -1187,7 +1189,7 @@ __global__ __launch_bounds__(hl2::NT) void hier_l2_kernel(
     uint64_t *tk = tkall + w * TKW;
     uint64_t *lst = tk + 4 * 32;
     const int qq4 = lane >> 4, sl = lane & 15;
-    constexpr int EL = SEL_GMAXE / 16;   // positions per lane
+    static_assert(16 * EL <= SEL_GMAXE, "positions per lane");
     const int j0l = sl / F, jstep = 16 / F, ch0 = sl % F;
     for (int base = 16 * w; base < nq; base += 16 * NW) {   // 16 queries per wave and pass
         for (int r4 = 0; r4 < 4; ++r4) {
@@ -1721,10 +1723,11 @@ void launch_hier(const void *q, const int64_t *qs, const float *qgain, float eps
                                    (const bf16_t *)S0, n, (int)Hq, (int)Hkv, n / 64, W, (int)k, scale, idx, val,
                                    cnt, scores, (const bf16_t *)S1, (int)F, (int)beam, sup_scores, 0, 2, rq, ksp);
                 const size_t lds = hl2::bytes(QG, E, (int)beff, (int)ns, D);
-                if (hipFuncSetAttribute(reinterpret_cast<const void *>(&hier_l2_kernel<D>),
+                auto l2 = (E <= 128) ? hier_l2_kernel<D, 8> : hier_l2_kernel<D, SEL_GMAXE / 16>;
+                if (hipFuncSetAttribute(reinterpret_cast<const void *>(l2),
                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
                     return;   // the error stays as hipGetLastError's, which the entry point reports
-                hipLaunchKernelGGL((hier_l2_kernel<D>), dim3((unsigned)(ngroups * Hkv * B)), dim3(hl2::NT), lds, s,
+                hipLaunchKernelGGL(l2, dim3((unsigned)(ngroups * Hkv * B)), dim3(hl2::NT), lds, s,
                                    (const bf16_t *)S0, (const bf16_t *)rq, (const int16_t *)ksp, n, (int)Hkv, n / 64,
                                    W, (int)k, (int)F, (int)beff, QG, ngroups, scale, idx, val, cnt, scores);
                 hipLaunchKernelGGL(kfn, grid, dim3(256), pm, s, (const bf16_t *)q, qs[0], qs[1], qs[2], qgain, eps,
