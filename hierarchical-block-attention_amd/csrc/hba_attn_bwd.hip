@@ -35,11 +35,13 @@
 // and bwd_dkv_fin (rope^T and the QKNorm backward of the key rows); a second
 // bwd_dkv_mfma launch takes the sink keys.  The fp32 path takes the sink keys
 // in bwd_sink.  Both split the sink keys' query rows over workgroups.
+#include <algorithm>
 #include <cstdlib>
 #include <cstring>
 
 #include "hba_abi.h"
 #include "hba_attn_bf16.h"
+#include "hba_generic.h"
 #include "hba_common.h"
 
 namespace hba {
@@ -1383,6 +1385,7 @@ extern "C" int hba_attn_bwd_workspace_bytes(int dtype, int64_t B, int64_t n, int
     if (!bytes || B <= 0 || n <= 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv || d <= 0) return HBA_ERR_INVALID_ARG;
     if (dtype != HBA_DTYPE_F32 && dtype != HBA_DTYPE_BF16) return HBA_ERR_UNSUPPORTED;
     *bytes = bwd_ws_layout(dtype, B, n, Hq, Hkv, d).total;
+    if (dtype == HBA_DTYPE_F32) *bytes = std::max(*bytes, gen_bwd_ws_bytes(B, n, Hkv, d));   // the generic path
     return HBA_OK;
 }
 
@@ -1390,6 +1393,7 @@ extern "C" int hba_attn_bwd_workspace_size(int64_t B, int64_t n, int64_t Hq, int
     if (!bytes || B <= 0 || n <= 0 || Hq <= 0 || d <= 0) return HBA_ERR_INVALID_ARG;
     // an upper bound for either dtype and any Hkv <= Hq
     *bytes = bwd_ws_layout(HBA_DTYPE_BF16, B, n, Hq, Hq, d).total + (size_t)(2 * B * n * Hq * d) * 2;
+    *bytes = std::max(*bytes, gen_bwd_ws_bytes(B, n, Hq, d));   // the fp32 generic path
     return HBA_OK;
 }
 
@@ -1399,6 +1403,25 @@ extern "C" int hba_attn_bwd(int dtype, const void *q, const void *k, const void 
                             const void *dout, int64_t B, int64_t n, int64_t Hq, int64_t Hkv, int64_t d, int64_t S,
                             int64_t W, int64_t Bk, int64_t k_blocks, float scale, void *workspace, size_t ws_bytes,
                             void *dq, void *dk, void *dv, float *dq_gain, float *dk_gain, void *stream) {
+    // fp32 off the tuned kernels' geometry (block != 64, head dim not 64 /
+    // 128, more sinks than one block, k > 64, more query heads per KV head
+    // than they take): the generic kernels
+    const bool gen_geo = !tuned_shape(d, Bk) || S > Bk || k_blocks > 64 ||
+                         (Hkv > 0 && Hq % Hkv == 0 && Hq / Hkv > bw::BW_GMAX);
+    if (dtype == HBA_DTYPE_F32 && gen_geo) {
+        if (!q || !k || !v || !kc || !kr || !cos_tab || !sin_tab || !idx || !cnt || !out || !dout || !workspace ||
+            !dq || !dk || !dv)
+            return HBA_ERR_INVALID_ARG;
+        if (B <= 0 || n <= 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv || S < 0 || W < 1 || k_blocks < 1 || Bk < 1)
+            return HBA_ERR_INVALID_ARG;
+        if (!gen_shape_ok(d, Bk)) return HBA_ERR_UNSUPPORTED;
+        if (n % Bk != 0) return HBA_ERR_INVALID_ARG;
+        if (ws_bytes < gen_bwd_ws_bytes(B, n, Hkv, d) || !abi::aligned16(workspace)) return HBA_ERR_INVALID_ARG;
+        return gen_attn_bwd((const float *)q, (const float *)k, (const float *)v, (const float *)kc,
+                            (const float *)kr, q_gain, k_gain, eps, cos_tab, sin_tab, idx, cnt, (const float *)out,
+                            (const float *)dout, B, n, Hq, Hkv, d, S, W, Bk, k_blocks, scale, (float *)workspace,
+                            (float *)dq, (float *)dk, (float *)dv, dq_gain, dk_gain, (hipStream_t)stream);
+    }
     int st = abi::check_dtype_dim(dtype, d);
     if (st) return st;
     if (!q || !k || !v || !kc || !kr || !cos_tab || !sin_tab || !idx || !cnt || !out || !dout || !workspace ||

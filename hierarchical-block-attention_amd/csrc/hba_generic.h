@@ -28,4 +28,16 @@ int gen_attn(const float *q, const int64_t *qs, const float *qgain, float eps, c
              int64_t n, int64_t Hq, int64_t Hkv, int64_t d, int64_t S, int64_t W, int64_t Bk, int64_t k, float scale,
              float *out, const int64_t *os, hipStream_t s);
 
+// the generic backward's workspace: dk (NoPE and rotated frames) and dv
+// accumulators, fp32 [B, Hkv, n, d] each
+size_t gen_bwd_ws_bytes(int64_t B, int64_t n, int64_t Hkv, int64_t d);
+// fp32 gradients of gen_attn's output: q, k, v, dq, dk, dv contiguous
+// [B, n, H, d]; kc, kr [B, Hkv, n, d]; dq_gain / dk_gain accumulated into
+// (the caller zeroes them)
+int gen_attn_bwd(const float *q, const float *k, const float *v, const float *kc, const float *kr,
+                 const float *qgain, const float *kgain, float eps, const float *cosT, const float *sinT,
+                 const int32_t *idx, const int32_t *cnt, const float *out, const float *dout, int64_t B, int64_t n,
+                 int64_t Hq, int64_t Hkv, int64_t d, int64_t S, int64_t W, int64_t Bk, int64_t kk, float scale,
+                 float *ws, float *dq, float *dk, float *dv, float *dq_gain, float *dk_gain, hipStream_t s);
+
 }  // namespace hba

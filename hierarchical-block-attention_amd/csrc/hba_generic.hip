@@ -313,6 +313,159 @@ __global__ __launch_bounds__(NT) void route_queries_kernel(const float *__restri
     for (int t = 0; t < d; ++t) dst[t] = acc[t];
 }
 
+// ------------------------------------------------------------ backward ----
+// Gradients of attn_kernel's output (the autograd of attention.py:306-356
+// with the selection held fixed, routing on detached q/k :288-303), any
+// geometry gen_shape_ok takes.  With p the union softmax of row (i, h) and
+// D = <dO, O>: ds_j = p_j (<dO, v_j> - D) * scale; the query side gains
+// ds_j y_j, key j's side ds_j x and dv_j p_j dO (x, y: the NoPE rows for the
+// sinks and routed keys, the rotated rows for the window).  Then rope^T
+// (x_u = y_u cos_u + (u < H ? y_{u+H} sin_{u+H} : -y_{u-H} sin_{u-H})) and the
+// QKNorm backward dx = g/r y - [ms >= eps] x g <y, x> / (d r^3), dg = <y, x> / r.
+//   bwd_q: one thread per (query, head): dq and dq_gain, and the key sides
+//          into fp32 accumulators by atomics (dkc, dkr: NoPE and rotated
+//          frames; dv), zeroed first by bwd_zero.
+//   bwd_k: one thread per (key row, KV head): dk, dv and dk_gain.
+__global__ __launch_bounds__(NT) void bwd_zero_kernel(float *__restrict__ p, int64_t nel) {
+    const int64_t gid = (int64_t)blockIdx.x * NT + threadIdx.x;
+    if (gid < nel) p[gid] = 0.0f;
+}
+
+__device__ __forceinline__ void rope_t_n(const float *y, float *x, int d, const float *cs, const float *sn) {
+    const int H = d / 2;
+    for (int u = 0; u < d; ++u) x[u] = y[u] * cs[u] + ((u < H) ? y[u + H] * sn[u + H] : -y[u - H] * sn[u - H]);
+}
+
+// y (the gradient with respect to the normalised row) -> the raw row's, in
+// place; returns <y, x> / r (the gain's gradient).  x is the raw row.
+__device__ __forceinline__ float qknorm_bwd_n(const float *x, float *y, int d, float gain, float eps) {
+    float ss = 0.0f, yx = 0.0f;
+    for (int t = 0; t < d; ++t) {
+        ss = fmaf(x[t], x[t], ss);
+        yx = fmaf(y[t], x[t], yx);
+    }
+    const float ms = ss / (float)d;
+    const float r = sqrtf(ms < eps ? eps : ms);
+    const float corr = (ms >= eps) ? gain * yx / ((float)d * r * r * r) : 0.0f;
+    for (int t = 0; t < d; ++t) y[t] = (gain / r) * y[t] - x[t] * corr;
+    return yx / r;
+}
+
+__global__ __launch_bounds__(64) void bwd_q_kernel(const float *__restrict__ q, const float *__restrict__ qgain,
+                                                   float eps, const float *__restrict__ kc,
+                                                   const float *__restrict__ kr, const float *__restrict__ v,
+                                                   const float *__restrict__ cosT, const float *__restrict__ sinT,
+                                                   const int32_t *__restrict__ idx, const int32_t *__restrict__ cnt,
+                                                   const float *__restrict__ out, const float *__restrict__ dout,
+                                                   int64_t n, int Hq, int Hkv, int S, int64_t W, int Bk, int kk,
+                                                   int d, float scale, float *__restrict__ dq,
+                                                   float *__restrict__ dq_gain, float *__restrict__ dkc,
+                                                   float *__restrict__ dkr, float *__restrict__ dv) {
+    const int64_t i = (int64_t)blockIdx.x * 64 + threadIdx.x;
+    const int h = blockIdx.y;
+    const int64_t b = blockIdx.z;
+    if (i >= n) return;
+    const int G = Hq / Hkv, g = h / G;
+    float x[DMAX], qc[DMAX], qr[DMAX], go[DMAX], gc[DMAX], gr[DMAX];
+    const int64_t qrow = ((b * n + i) * Hq + h) * d;   // q, out, dout, dq: [B, n, Hq, d]
+    for (int t = 0; t < d; ++t) {
+        x[t] = q[qrow + t];
+        qc[t] = x[t];
+        go[t] = dout[qrow + t];
+        gc[t] = gr[t] = 0.0f;
+    }
+    if (qgain) qknorm_n(qc, d, qgain[h], eps);
+    rope_n(qc, qr, d, cosT + i * d, sinT + i * d);
+    float D = 0.0f;
+    for (int t = 0; t < d; ++t) D = fmaf(go[t], out[qrow + t], D);
+    const int64_t bh = b * Hkv + g;
+    const float *KC = kc + bh * n * d;   // kc, kr: [B, Hkv, n, d]
+    const float *KR = kr + bh * n * d;
+    const int64_t s_end = ((int64_t)S < i + 1) ? (int64_t)S : i + 1;
+    const int64_t w_beg = ((int64_t)S > i - W + 1) ? (int64_t)S : i - W + 1;
+    const int c = min(max(cnt[bh * n + i], 0), kk);
+    const int32_t *ix = idx + (bh * n + i) * kk;
+    const int64_t nb = n / Bk;
+    // the forward's softmax statistics, in its order
+    float mx = -INFINITY;
+    for (int64_t j = 0; j < s_end; ++j) mx = fmaxf(mx, dot_n(qc, KC + j * d, d) * scale);
+    for (int64_t j = w_beg; j <= i; ++j) mx = fmaxf(mx, dot_n(qr, KR + j * d, d) * scale);
+    for (int r = 0; r < c; ++r) {
+        if (ix[r] < 1 || ix[r] >= nb) continue;
+        const int64_t j0 = (int64_t)ix[r] * Bk;
+        for (int64_t j = (j0 > S ? j0 : S); j < j0 + Bk; ++j) mx = fmaxf(mx, dot_n(qc, KC + j * d, d) * scale);
+    }
+    float l = 0.0f;
+    for (int64_t j = 0; j < s_end; ++j) l += expf(dot_n(qc, KC + j * d, d) * scale - mx);
+    for (int64_t j = w_beg; j <= i; ++j) l += expf(dot_n(qr, KR + j * d, d) * scale - mx);
+    for (int r = 0; r < c; ++r) {
+        if (ix[r] < 1 || ix[r] >= nb) continue;
+        const int64_t j0 = (int64_t)ix[r] * Bk;
+        for (int64_t j = (j0 > S ? j0 : S); j < j0 + Bk; ++j) l += expf(dot_n(qc, KC + j * d, d) * scale - mx);
+    }
+    const float inv = 1.0f / l;
+    // key j against the row xv (qc or qr): the query side into acc, the key
+    // side (frame buffer kacc) and dv by atomics
+    auto key = [&](const float *xv, const float *K, float *acc, float *kacc, int64_t j) {
+        const float *kj = K + j * d;
+        const float p = expf(dot_n(xv, kj, d) * scale - mx) * inv;
+        const int64_t vrow = ((b * n + j) * Hkv + g) * d;   // v: [B, n, Hkv, d]
+        float dp = 0.0f;
+        for (int t = 0; t < d; ++t) dp = fmaf(go[t], v[vrow + t], dp);
+        const float ds = p * (dp - D) * scale;
+        const int64_t krow = (bh * n + j) * d;
+        for (int t = 0; t < d; ++t) {
+            acc[t] = fmaf(ds, kj[t], acc[t]);
+            atomicAdd(kacc + krow + t, ds * xv[t]);
+            atomicAdd(dv + krow + t, p * go[t]);
+        }
+    };
+    for (int64_t j = 0; j < s_end; ++j) key(qc, KC, gc, dkc, j);
+    for (int64_t j = w_beg; j <= i; ++j) key(qr, KR, gr, dkr, j);
+    for (int r = 0; r < c; ++r) {
+        if (ix[r] < 1 || ix[r] >= nb) continue;
+        const int64_t j0 = (int64_t)ix[r] * Bk;
+        for (int64_t j = (j0 > S ? j0 : S); j < j0 + Bk; ++j) key(qc, KC, gc, dkc, j);
+    }
+    // d(qc) = gc + rope^T(gr) at position i, then the QKNorm backward
+    float y[DMAX];
+    rope_t_n(gr, y, d, cosT + i * d, sinT + i * d);
+    for (int t = 0; t < d; ++t) y[t] += gc[t];
+    if (qgain) {
+        const float dg = qknorm_bwd_n(x, y, d, qgain[h], eps);
+        atomicAdd(dq_gain + h, dg);
+    }
+    for (int t = 0; t < d; ++t) dq[qrow + t] = y[t];
+}
+
+__global__ __launch_bounds__(NT) void bwd_k_kernel(const float *__restrict__ k, const float *__restrict__ kgain,
+                                                   float eps, const float *__restrict__ cosT,
+                                                   const float *__restrict__ sinT, const float *__restrict__ dkc,
+                                                   const float *__restrict__ dkr, const float *__restrict__ dva,
+                                                   int64_t B, int64_t n, int Hkv, int d, float *__restrict__ dk,
+                                                   float *__restrict__ dv, float *__restrict__ dk_gain) {
+    const int64_t gid = (int64_t)blockIdx.x * NT + threadIdx.x;
+    if (gid >= B * Hkv * n) return;
+    const int64_t j = gid % n, g = (gid / n) % Hkv, b = gid / (n * Hkv);
+    const int64_t arow = ((b * Hkv + g) * n + j) * d;   // accumulators: [B, Hkv, n, d]
+    const int64_t row = ((b * n + j) * Hkv + g) * d;    // k, dk, dv: [B, n, Hkv, d]
+    float x[DMAX], y[DMAX], zr[DMAX];
+    for (int t = 0; t < d; ++t) {
+        x[t] = k[row + t];
+        zr[t] = dkr[arow + t];
+    }
+    rope_t_n(zr, y, d, cosT + j * d, sinT + j * d);
+    for (int t = 0; t < d; ++t) y[t] += dkc[arow + t];
+    if (kgain) {
+        const float dg = qknorm_bwd_n(x, y, d, kgain[g], eps);
+        atomicAdd(dk_gain + g, dg);
+    }
+    for (int t = 0; t < d; ++t) {
+        dk[row + t] = y[t];
+        dv[row + t] = dva[arow + t];
+    }
+}
+
 }  // namespace gen
 
 // ------------------------------------------------------------ launchers ----
@@ -361,6 +514,32 @@ int gen_attn(const float *q, const int64_t *qs, const float *qgain, float eps, c
     hipLaunchKernelGGL(gen::attn_kernel, dim3((unsigned)((n + 63) / 64), (unsigned)Hq, (unsigned)B), dim3(64), 0, s, q,
                        qs[0], qs[1], qs[2], qgain, eps, kc, kr, vt, cosT, sinT, idx, cnt, n, (int)Hq, (int)Hkv,
                        (int)S, W, (int)Bk, (int)k, (int)d, scale, out, os[0], os[1], os[2]);
+    HBA_LAUNCH_CHECK();
+    return HBA_OK;
+}
+
+size_t gen_bwd_ws_bytes(int64_t B, int64_t n, int64_t Hkv, int64_t d) {
+    return (size_t)3 * B * Hkv * n * d * sizeof(float);
+}
+
+int gen_attn_bwd(const float *q, const float *k, const float *v, const float *kc, const float *kr,
+                 const float *qgain, const float *kgain, float eps, const float *cosT, const float *sinT,
+                 const int32_t *idx, const int32_t *cnt, const float *out, const float *dout, int64_t B, int64_t n,
+                 int64_t Hq, int64_t Hkv, int64_t d, int64_t S, int64_t W, int64_t Bk, int64_t kk, float scale,
+                 float *ws, float *dq, float *dk, float *dv, float *dq_gain, float *dk_gain, hipStream_t s) {
+    const int64_t per = B * Hkv * n * d;   // one accumulator
+    float *dkc = ws, *dkr = ws + per, *dva = ws + 2 * per;
+    const int64_t nel = 3 * per, rows = B * Hkv * n;
+    if ((nel + gen::NT - 1) / gen::NT > 0x7fffffff || (rows + gen::NT - 1) / gen::NT > 0x7fffffff ||
+        (n + 63) / 64 > 0x7fffffff || Hq > 65535 || B > 65535)
+        return HBA_ERR_UNSUPPORTED;
+    hipLaunchKernelGGL(gen::bwd_zero_kernel, dim3((unsigned)((nel + gen::NT - 1) / gen::NT)), dim3(gen::NT), 0, s, ws,
+                       nel);
+    hipLaunchKernelGGL(gen::bwd_q_kernel, dim3((unsigned)((n + 63) / 64), (unsigned)Hq, (unsigned)B), dim3(64), 0, s,
+                       q, qgain, eps, kc, kr, v, cosT, sinT, idx, cnt, out, dout, n, (int)Hq, (int)Hkv, (int)S, W,
+                       (int)Bk, (int)kk, (int)d, scale, dq, dq_gain, dkc, dkr, dva);
+    hipLaunchKernelGGL(gen::bwd_k_kernel, dim3((unsigned)((rows + gen::NT - 1) / gen::NT)), dim3(gen::NT), 0, s, k,
+                       kgain, eps, cosT, sinT, dkc, dkr, dva, B, n, (int)Hkv, (int)d, dk, dv, dk_gain);
     HBA_LAUNCH_CHECK();
     return HBA_OK;
 }

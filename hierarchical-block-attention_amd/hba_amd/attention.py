@@ -191,15 +191,28 @@ class _UnionAttention(torch.autograd.Function):
             out, kc, kr, idx, cnt = r["out"], r["kc"], r["kr"], r["idx"], r["cnt"]
             S, W = cfg.sinks, cfg.window
         ctx.save_for_backward(q, k, v, q_gain, k_gain, cos, sin, kc, kr, idx, cnt, out)
-        ctx.meta = (S, W, union_scale(cfg, dh, n), qeps)
+        ctx.meta = (S, W, union_scale(cfg, dh, n), qeps, cfg.block if mode != "equiv" else ops.BLOCK)
         return out
 
     @staticmethod
     def backward(ctx, dout):
         q, k, v, q_gain, k_gain, cos, sin, kc, kr, idx, cnt, out = ctx.saved_tensors
-        S, W, scale, eps = ctx.meta
-        dq, dk, dv, dqg, dkg = ops.attn_bwd(q, k, v, kc, kr, q_gain, k_gain, eps, cos, sin, idx, cnt, out,
-                                            dout.contiguous(), S, W, scale)
+        S, W, scale, eps, block = ctx.meta
+        G = q.shape[2] // k.shape[2]
+        # the bf16 kernels take 64-key blocks, head dims 64 / 128, S <= 64,
+        # k <= 64 and G <= 16; elsewhere the fp32 kernels run on the widened
+        # tensors (any geometry the forward takes) and the gradients are
+        # rounded back
+        wide = q.dtype != torch.float32 and (block != ops.BLOCK or q.shape[-1] not in (64, 128) or S > ops.BLOCK
+                                             or idx.shape[3] > 64 or G > 16)
+        if wide:
+            f32 = [t.float() for t in (q, k, v, kc, kr, out, dout)]
+            dq, dk, dv, dqg, dkg = ops.attn_bwd(f32[0], f32[1], f32[2], f32[3], f32[4], q_gain, k_gain, eps, cos,
+                                                sin, idx, cnt, f32[5], f32[6].contiguous(), S, W, scale, block)
+            dq, dk, dv = dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype)
+        else:
+            dq, dk, dv, dqg, dkg = ops.attn_bwd(q, k, v, kc, kr, q_gain, k_gain, eps, cos, sin, idx, cnt, out,
+                                                dout.contiguous(), S, W, scale, block)
         gq = dqg.to(q_gain.dtype) if q_gain is not None and ctx.needs_input_grad[3] else None
         gk = dkg.to(k_gain.dtype) if k_gain is not None and ctx.needs_input_grad[4] else None
         return dq, dk, dv, gq, gk, None, None, None, None, None, None, None
@@ -213,12 +226,6 @@ def _with_grad(q, k, v, cos, sin, cfg, summ, qkn, mode):
         return None
     if qg is not None and qeps != keps:
         raise NotImplementedError("the backward takes one QKNorm eps for q and k")
-    G = q.shape[2] // k.shape[2]
-    if cfg.block != ops.BLOCK or q.shape[-1] not in (64, 128) or cfg.sinks > ops.BLOCK or G > 16:
-        raise NotImplementedError(f"the backward runs at {ops.BLOCK}-key blocks, head dims 64 / 128, at most "
-                                  f"{ops.BLOCK} sinks and 16 query heads per KV head (got block {cfg.block}, "
-                                  f"head dim {q.shape[-1]}, {cfg.sinks} sinks, {G} heads per KV head); the "
-                                  "forward takes other geometry under torch.no_grad()")
     return _UnionAttention.apply(q, k, v, qg, kg, cos, sin, cfg, summ, qeps, keps, mode)
 
 

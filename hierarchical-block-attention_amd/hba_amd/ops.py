@@ -466,11 +466,13 @@ def _(q, q_gain, k_gain, eps, kc, kr, vt, cos, sin, idx, cnt, sinks, window, sca
 @torch.library.custom_op("hba::attn_bwd", mutates_args=(), device_types="cuda")
 def attn_bwd(q: Tensor, k: Tensor, v: Tensor, kc: Tensor, kr: Tensor, q_gain: Optional[Tensor],
              k_gain: Optional[Tensor], eps: float, cos: Tensor, sin: Tensor, idx: Tensor, cnt: Tensor,
-             out: Tensor, dout: Tensor, sinks: int, window: int, scale: float
+             out: Tensor, dout: Tensor, sinks: int, window: int, scale: float, block: int = 64
              ) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
     """Gradients of the union attention output (hba_attn_bwd): dq, dk, dv in
     q's dtype and the QKNorm gain gradients dq_gain [Hq], dk_gain [Hkv] (fp32;
-    zeros without QKNorm), the selection idx/cnt held fixed."""
+    zeros without QKNorm), the selection idx/cnt held fixed.  fp32 takes any
+    block size and head dim the fp32 forward takes; bf16 64-key blocks and
+    head dims 64 / 128."""
     dev = _dev(q)
     B, n, Hq, d = q.shape
     Hkv = k.shape[2]
@@ -502,14 +504,14 @@ def attn_bwd(q: Tensor, k: Tensor, v: Tensor, kc: Tensor, kr: Tensor, q_gain: Op
     with torch.cuda.device(dev):
         st = lib().hba_attn_bwd(_code(q), _p(q), _p(k), _p(v), _p(kc), _p(kr), _p(qg), _p(kg), eps, _p(cos),
                                 _p(sin), _p(idx), _p(cnt), _p(out), _p(dout), B, n, Hq, Hkv, d, sinks, window,
-                                BLOCK, idx.shape[3], scale, _p(ws), int(nbytes.value), _p(dq), _p(dk), _p(dv),
+                                block, idx.shape[3], scale, _p(ws), int(nbytes.value), _p(dq), _p(dk), _p(dv),
                                 _p(dqg), _p(dkg), _stream(dev))
     check(st, "hba_attn_bwd")
     return dq, dk, dv, dqg, dkg
 
 
 @attn_bwd.register_fake
-def _(q, k, v, kc, kr, q_gain, k_gain, eps, cos, sin, idx, cnt, out, dout, sinks, window, scale):
+def _(q, k, v, kc, kr, q_gain, k_gain, eps, cos, sin, idx, cnt, out, dout, sinks, window, scale, block=64):
     return (q.new_empty(q.shape), k.new_empty(k.shape), v.new_empty(v.shape),
             q.new_empty(q.shape[2], dtype=torch.float32), k.new_empty(k.shape[2], dtype=torch.float32))
 

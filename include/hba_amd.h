@@ -443,8 +443,13 @@ int hba_decode_fwd_noalloc(int dtype, const void *q, const float *q_gain, float 
  * fp32 storage: fp32 VALU arithmetic.  bf16 storage: bf16 MFMA products
  * with fp32 accumulation; the probabilities and dS enter the dk/dv/dq
  * products rounded to bf16, and dk/dv are summed with fp32 atomics, so the
- * bf16 result is not bit-reproducible from run to run.  Same shape rules as
- * hba_attn_fwd; G = Hq/Hkv <= 16.
+ * bf16 result is not bit-reproducible from run to run.  bf16: 64-key
+ * blocks, d = 64 / 128, S <= 64, k <= 64, G = Hq/Hkv <= 16.  fp32 takes every
+ * geometry the fp32 forward takes (any block size Bk dividing n up to 256,
+ * even d <= 256, any S, k and G): off the tuned one, one thread per (query,
+ * head) recomputes the union softmax and the key sides are summed with fp32
+ * atomics (not bit-reproducible either); its workspace is three fp32
+ * [B, Hkv, n, d] accumulators, included in hba_attn_bwd_workspace_bytes.
  */
 int hba_attn_bwd(int dtype, const void *q, const void *k, const void *v,
                  const void *kc, const void *kr,

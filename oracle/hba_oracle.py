@@ -703,6 +703,7 @@ def union_backward(q, k, v, cos, sin, scale, q_gain, k_gain, eps, idx, cnt, dout
             nc = min(max(int(cnt[g, i]), 0), kk)
             blocks = np.array([b for b in idx[g, i, :nc] if 1 <= b < nb], dtype=np.int64)
             jr = (blocks[:, None] * Bk + ar[None, :]).reshape(-1)
+            jr = jr[jr >= S]   # the union: a routed key below S is a sink, counted once (S > Bk)
             jn = np.concatenate([js, jr]).astype(np.int64)
             hs = slice(g * G, (g + 1) * G)
             Qn, Qr = qc[i, hs], qr[i, hs]

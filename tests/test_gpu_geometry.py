@@ -13,7 +13,9 @@
                 head.  Selection bit-exact against the oracle's fp32 selection
                 on the same (storage-rounded) inputs, outputs within 1e-5 of
                 its float64 rows before the output rounding, and within the
-                bf16 bar of the oracle's bf16 emulation.
+                bf16 bar of the oracle's bf16 emulation.  The backward
+                there runs on the generic fp32 kernels (bf16 inputs
+                widened), checked against the oracle's float64 backward.
 """
 import numpy as np
 import pytest
@@ -145,14 +147,48 @@ def test_generic_path_vs_oracle(dev, dt, case):
         assert np.abs(f(r["out"])[0][rows] - refb).max() <= 2e-2
 
 
-def test_generic_path_refuses_gradients(dev):
-    """The backward runs on the tuned geometry only: off it, a gradient
-    request raises before any launch."""
-    cfg, x, prm, cos, sin = inputs(dev, torch.bfloat16, 512, 4, 2, 8, block=16, window=64, k_blocks=8)
-    q = x["q"].clone().requires_grad_(True)
-    with pytest.raises(NotImplementedError, match="backward"):
-        hba_amd.hba_attention_eval(q, x["k"], x["v"], cos, sin, cfg, prm, prm)
-    cfg2, x2, prm2, cos2, sin2 = inputs(dev, torch.bfloat16, 1024, 14, 2, 64, sinks=100, window=256, k_blocks=4)
-    q2 = x2["q"].clone().requires_grad_(True)
-    with pytest.raises(NotImplementedError, match="sinks"):
-        hba_amd.hba_attention_eval(q2, x2["k"], x2["v"], cos2, sin2, cfg2, prm2, prm2)
+# (relative max error of each gradient against the oracle's float64
+# backward: fp32 as the tuned fp32 backward's gate; bf16 inputs run the fp32
+# kernels on the widened tensors, against float64 from the same bf16 values,
+# so only the forward's bf16 operands and output separate them)
+GEN_GRAD_TOL = {"f32": 2e-3, "bf16": 1.5e-2}
+
+
+@pytest.mark.parametrize("dt,n,Hq,Hkv,d,cfgkw,hier", [
+    ("f32", 512, 4, 2, 8, dict(block=16, window=64, sinks=4, k_blocks=8), False),     # tests/test_qknorm.py:28-35
+    ("bf16", 512, 4, 2, 8, dict(block=16, window=64, sinks=4, k_blocks=8, fanout=4, beam=2), True),
+    ("bf16", 1024, 14, 2, 64, dict(block=64, window=256, sinks=100, k_blocks=4), False),  # S > 64: tuned forward
+    ("f32", 1024, 6, 2, 96, dict(block=32, window=128, sinks=8, k_blocks=6), False),
+    ("f32", 512, 18, 1, 64, dict(block=64, window=128, sinks=4, k_blocks=4), False),     # G = 18
+])
+def test_generic_backward_matches_oracle(dev, dt, n, Hq, Hkv, d, cfgkw, hier):
+    """hba_attn_bwd off the tuned backward's geometry (the fp32 generic
+    kernels; bf16 inputs widened) through autograd of hba_attention_eval:
+    dq, dk, dv and the QKNorm gain gradients against the oracle's float64
+    backward on the forward's own selection -- the reference's block-16 /
+    head-dim-8 test geometry (its naive-vs-fused gradient test runs there,
+    tests/test_qknorm.py:181-187), hierarchical selection at that geometry,
+    100 sinks, d = 96 with 32-key blocks, 18 query heads per KV head."""
+    T = torch.float32 if dt == "f32" else torch.bfloat16
+    cfg, x, prm, cos, sin = inputs(dev, T, n, Hq, Hkv, d, aux_w=0.0, **cfgkw)
+    q, k, v = (x[t].clone().requires_grad_(True) for t in ("q", "k", "v"))
+    gq = x["q_gain"].clone().requires_grad_(True)
+    gk = x["k_gain"].clone().requires_grad_(True)
+    qkn = synth.Params(gq, gk, x["probes"], x["proj"])
+    out = hba_amd.hba_attention_eval(q, k, v, cos, sin, cfg, qkn, qkn, None, hier=hier)
+    dout = torch.randn(out.shape, generator=torch.Generator().manual_seed(11)).to(out.dtype).to(dev)
+    out.backward(dout)
+    torch.cuda.synchronize()
+    with torch.no_grad():
+        r = hba_amd.forward_stages(x["q"], x["k"], x["v"], cos, sin, cfg, qkn, qkn, hier=hier)
+        assert torch.equal(r["out"], out.detach())          # the same forward, the same selection
+    idx, cnt = r["idx"][0].cpu().numpy(), r["cnt"][0].cpu().numpy()
+    scale = hba_amd.union_scale(cfg, d, n)
+    ref = O.union_backward(f(x["q"])[0], f(x["k"])[0], f(x["v"])[0], f(cos), f(sin), scale, f(x["q_gain"]),
+                           f(x["k_gain"]), 1e-6, idx, cnt, f(dout)[0], cfg.sinks, cfg.window, cfg.block, True)
+    got = [f(q.grad)[0], f(k.grad)[0], f(v.grad)[0], f(gq.grad), f(gk.grad)]
+    rel = {nm: np.abs(a - b).max() / max(np.abs(b).max(), 1e-6)
+           for nm, a, b in zip(["dq", "dk", "dv", "dq_gain", "dk_gain"], got, ref)}
+    print(dt, n, Hq, Hkv, d, cfgkw, {kk: f"{e:.2e}" for kk, e in rel.items()})
+    for nm, e in rel.items():
+        assert e < GEN_GRAD_TOL[dt], (nm, e)

@@ -437,14 +437,15 @@ def _torch_union_forward(q, k, v, cos, sin, scale, gq, gk, eps, idx, cnt, S, W, 
     return torch.stack(outs, 1)
 
 
-@pytest.mark.parametrize("qknorm", [True, False])
-def test_union_backward_matches_torch_autograd(qknorm):
+@pytest.mark.parametrize("qknorm,S", [(True, 2), (False, 2), (True, 20)])
+def test_union_backward_matches_torch_autograd(qknorm, S):
     """The oracle backward against torch autograd (float64) of the masked
     dense union softmax through QKNorm and RoPE, on a selection with routed
-    blocks, sinks and a window."""
+    blocks, sinks and a window; S = 20 > Bk: routed block 1 holds sink keys,
+    which the union counts once."""
     import torch
     rs = RS(21)
-    n, Hq, Hkv, d, Bk, S, W, kk = 128, 4, 2, 8, 16, 2, 32, 3
+    n, Hq, Hkv, d, Bk, W, kk = 128, 4, 2, 8, 16, 32, 3
     q = rs.standard_normal((n, Hq, d)) * 1.5
     k = rs.standard_normal((n, Hkv, d)) * 1.5
     v = rs.standard_normal((n, Hkv, d))
