@@ -366,8 +366,9 @@ def test_fp32_generic_geometry_vs_oracle(dev, Bk, d, Hq, Hkv, n, W, S, k, m):
     rounding of the float64 restatement, the flat selection bit-exact against
     the oracle's declared order on the kernel's own summaries, and the union
     softmax within 1e-5 of the oracle's float64 rows; the eval drop-in gives
-    the same output; off the tuned geometry a gradient request refuses with a
-    clear error, and bf16 runs on the same kernels (inputs widened)."""
+    the same output; off the tuned geometry a gradient request runs the
+    generic backward (its values: test_gpu_geometry.py against the oracle's
+    backward), and bf16 runs on the same kernels (inputs widened)."""
     cfg = hba_amd.HBAConfig(n_heads=Hq, n_kv=Hkv, head_dim=d, window=W, sinks=S, k_blocks=k, slots=m, block=Bk)
     x = synth.layer_inputs(1, n, Hq, Hkv, d, m=m, dtype=torch.float32, device=dev, seed=1, sharp=True)
     prm = synth.Params(x["q_gain"], x["k_gain"], x["probes"], x["proj"])
@@ -393,10 +394,12 @@ def test_fp32_generic_geometry_vs_oracle(dev, Bk, d, Hq, Hkv, n, W, S, k, m):
     ref = O.attn_rows(P.qc, P.qr, P.kc, P.kr, P.v, o_idx, o_cnt, r["scale"], S, W, Bk, rows)
     assert np.abs(f(r["out"])[0][rows] - ref).max() <= 1e-5
     assert torch.equal(out_e, r["out"])
-    if Bk != 64 or d not in (64, 128):
+    if Bk != 64 or d not in (64, 128):   # a gradient request runs the generic fp32 backward
         q = x["q"].clone().requires_grad_(True)
-        with pytest.raises(NotImplementedError, match="backward"):
-            hba_amd.hba_attention_eval(q, x["k"], x["v"], cos, sin, cfg, prm, prm)
+        out_g = hba_amd.hba_attention_eval(q, x["k"], x["v"], cos, sin, cfg, prm, prm)
+        assert torch.equal(out_g.detach(), r["out"])
+        out_g.sum().backward()
+        assert q.grad is not None and bool(torch.isfinite(q.grad).all()) and q.grad.abs().max().item() > 0
     if Bk != 64:   # bf16 off the tuned geometry: the generic kernels on the widened inputs
         xb = {t: x[t].bfloat16() for t in ("q", "k", "v")}
         with torch.no_grad():
