@@ -31,6 +31,7 @@
 // Every reduction runs in a fixed order: the results are deterministic.
 #include "hba_common.h"
 #include "hba_abi.h"
+#include "hba_generic.h"
 
 namespace hba {
 namespace aux {
@@ -880,8 +881,22 @@ __global__ void aux_zero_kernel(float *__restrict__ p, int64_t len) {
 
 using namespace hba;
 
+// fp32 off the tuned kernels' geometry (64-key blocks, d = 64 / 128, m <= 8,
+// G <= 16): the generic kernels (hba_generic.hip)
+static bool aux_generic(int dtype, int64_t Hq, int64_t Hkv, int64_t d, int64_t m, int64_t Bk) {
+    return dtype == HBA_DTYPE_F32 && Hkv > 0 && Hq % Hkv == 0 &&
+           !(Bk == aux::BK && (d == 64 || d == 128) && m <= 8 && Hq / Hkv <= 16);
+}
+
 extern "C" int hba_aux_kl_workspace_size(int dtype, int64_t B, int64_t n, int64_t Hq, int64_t Hkv, int64_t d,
                                          int64_t m, int64_t Bk, size_t *bytes) {
+    if (aux_generic(dtype, Hq, Hkv, d, m, Bk)) {
+        if (!bytes || B <= 0 || n <= 0 || Hq <= 0 || m <= 0 || Bk <= 0) return HBA_ERR_INVALID_ARG;
+        if (!gen_aux_ok(d, Bk, m, Hq / Hkv)) return HBA_ERR_UNSUPPORTED;
+        if (n % Bk) return HBA_ERR_UNSUPPORTED;
+        *bytes = gen_aux_ws_bytes(B, n, Hq, Hkv, d, m, Bk);
+        return HBA_OK;
+    }
     int st = abi::check_dtype_dim(dtype, d);
     if (st) return st;
     if (!bytes || B <= 0 || n <= 0 || Hq <= 0 || Hkv <= 0 || m <= 0) return HBA_ERR_INVALID_ARG;
@@ -904,6 +919,10 @@ extern "C" int hba_aux_kl(int dtype, const void *q, const int64_t q_strides[3], 
         return HBA_ERR_INVALID_ARG;
     if (ws_bytes < need) return HBA_ERR_INVALID_ARG;
     if (!abi::aligned16(ws) || !abi::aligned16(kc)) return HBA_ERR_UNSUPPORTED;
+    if (aux_generic(dtype, Hq, Hkv, d, m, Bk))
+        return gen_aux_kl((const float *)q, q_strides, q_gain, eps, (const float *)kc, (const float *)S0, probes, proj,
+                          B, n, Hq, Hkv, d, m, Bk, W, scale_u, scale_r, ws, aux, dprobes, dproj,
+                          (hipStream_t)stream);
     if (n / aux::BK > 0x7fffffff || Hkv > 65535 || B > 65535) return HBA_ERR_UNSUPPORTED;
     const aux::Ws L = aux::layout(dtype, B, n, Hq, Hkv, d, m);
     char *w = (char *)ws;

@@ -40,4 +40,16 @@ int gen_attn_bwd(const float *q, const float *k, const float *v, const float *kc
                  int64_t Hq, int64_t Hkv, int64_t d, int64_t S, int64_t W, int64_t Bk, int64_t kk, float scale,
                  float *ws, float *dq, float *dk, float *dv, float *dq_gain, float *dk_gain, hipStream_t s);
 
+// the generic aux-KL (fp32): even d <= 256, Bk 1..256, m <= 32 slots,
+// G <= 64 query heads per KV head
+bool gen_aux_ok(int64_t d, int64_t Bk, int64_t m, int64_t G);
+size_t gen_aux_ws_bytes(int64_t B, int64_t n, int64_t Hq, int64_t Hkv, int64_t d, int64_t m, int64_t Bk);
+// aux (1 float) and, if dprobes is set, dprobes [Hkv, m, d] and dproj
+// [Hkv, d, d]; q raw with strides qs, kc [B, Hkv, n, d] content keys, S0
+// [B, Hkv, n/Bk, m, d] summaries
+int gen_aux_kl(const float *q, const int64_t *qs, const float *qgain, float eps, const float *kc, const float *S0,
+               const float *probes, const float *proj, int64_t B, int64_t n, int64_t Hq, int64_t Hkv, int64_t d,
+               int64_t m, int64_t Bk, int64_t W, float scale_u, float scale_r, void *ws, float *aux, float *dprobes,
+               float *dproj, hipStream_t s);
+
 }  // namespace hba

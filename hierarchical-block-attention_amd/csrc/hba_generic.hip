@@ -466,6 +466,246 @@ __global__ __launch_bounds__(NT) void bwd_k_kernel(const float *__restrict__ k, 
     }
 }
 
+// --------------------------------------------------------------- aux-KL ----
+// The summarizer's auxiliary loss (attention.py:366-389) and its gradient
+// into probes and proj at any geometry gen_shape_ok takes, in the oracle's
+// arithmetic: the teacher's block LSEs per (query, head), then per (query, KV
+// head) p* (each head's softmax over the candidate blocks' LSEs, averaged
+// over the G heads and renormalised), the block scores bsc = slot max x
+// scale_r with their tie masks, the row's KL term and d aux / d bsc = (softmax
+// (bsc) sum p* - p*) / N; dS0 from the tie-shared d bsc, the summariser's
+// backward per block, and sums in fixed orders.
+constexpr int AUX_GMAX = 64;   // query heads per KV head
+constexpr int AUX_MMAX = 32;   // slots (the tie mask is a 32-bit word)
+
+__global__ __launch_bounds__(64) void aux_teacher_kernel(const float *__restrict__ q, int64_t qsb, int64_t qsn,
+                                                         int64_t qsh, const float *__restrict__ qgain,
+                                                         float eps, const float *__restrict__ kc, int64_t n, int Hq,
+                                                         int Hkv, int Bk, int d, int64_t W, float scale_u,
+                                                         float *__restrict__ L) {
+    const int64_t i = (int64_t)blockIdx.x * 64 + threadIdx.x;
+    const int h = blockIdx.y;
+    const int64_t b = blockIdx.z;
+    if (i >= n) return;
+    const int G = Hq / Hkv, g = h / G, hh = h % G;
+    const int64_t bm = cand_bmax(i, Bk, W), nb = n / Bk;
+    if (bm < 1) return;
+    float qc[DMAX];
+    const float *row = q + b * qsb + i * qsn + (int64_t)h * qsh;
+    for (int t = 0; t < d; ++t) qc[t] = row[t];
+    if (qgain) qknorm_n(qc, d, qgain[h], eps);
+    const float *K = kc + (b * Hkv + g) * n * d;
+    float *dst = L + (((b * Hkv + g) * n + i) * G + hh) * nb;
+    for (int64_t c = 1; c <= bm; ++c) {
+        float mx = -INFINITY;
+        for (int64_t j = c * Bk; j < (c + 1) * Bk; ++j) mx = fmaxf(mx, dot_n(qc, K + j * d, d) * scale_u);
+        float z = 0.0f;
+        for (int64_t j = c * Bk; j < (c + 1) * Bk; ++j) z += expf(dot_n(qc, K + j * d, d) * scale_u - mx);
+        dst[c] = mx + logf(z);
+    }
+}
+
+// One thread per (b, g, i): p*, bsc and its tie mask, the KL term (rowt) and
+// d aux / d bsc (written over bsc).
+__global__ __launch_bounds__(NT) void aux_rows_kernel(const float *__restrict__ L, const float *__restrict__ qg,
+                                                      const float *__restrict__ S0, int64_t B, int64_t n, int Hkv,
+                                                      int G, int Bk, int m, int d, int64_t W, float scale_r,
+                                                      float invN, float *__restrict__ bsc,
+                                                      uint32_t *__restrict__ ties, float *__restrict__ rowt) {
+    const int64_t r = (int64_t)blockIdx.x * NT + threadIdx.x;
+    if (r >= B * Hkv * n) return;
+    const int64_t i = r % n, g = (r / n) % Hkv, b = r / (n * Hkv);
+    const int64_t bm = cand_bmax(i, Bk, W), nb = n / Bk;
+    if (bm < 1) {
+        rowt[r] = 0.0f;
+        return;
+    }
+    const float *Lr = L + r * G * nb;   // r = (b Hkv + g) n + i
+    float M[AUX_GMAX], Z[AUX_GMAX];
+    for (int h = 0; h < G; ++h) {
+        float mx = -INFINITY;
+        for (int64_t c = 1; c <= bm; ++c) mx = fmaxf(mx, Lr[h * nb + c]);
+        float z = 0.0f;
+        for (int64_t c = 1; c <= bm; ++c) z += expf(Lr[h * nb + c] - mx);
+        M[h] = mx;
+        Z[h] = z;
+    }
+    auto pstar_raw = [&](int64_t c) {
+        float a = 0.0f;
+        for (int h = 0; h < G; ++h) a += expf(Lr[h * nb + c] - M[h]) / Z[h];
+        return a / (float)G;
+    };
+    float ptot = 0.0f;
+    for (int64_t c = 1; c <= bm; ++c) ptot += pstar_raw(c);
+    const float pnorm = 1.0f / fmaxf(ptot, 1e-9f);
+    // block scores: slot max of qg . S0 times scale_r, and the slots at the max
+    const float *qv = qg + ((b * n + i) * Hkv + g) * d;   // qg: [B, n, Hkv, d]
+    float *br = bsc + r * nb;
+    uint32_t *tr = ties + r * nb;
+    float bmx = -INFINITY;
+    for (int64_t c = 1; c <= bm; ++c) {
+        const float *Sc = S0 + ((b * Hkv + g) * nb + c) * m * d;
+        float best = -INFINITY;
+        uint32_t mask = 0u;
+        for (int sl = 0; sl < m; ++sl) {
+            const float v = dot_n(qv, Sc + sl * d, d);
+            if (v > best) {
+                best = v;
+                mask = 1u << sl;
+            } else if (v == best) {
+                mask |= 1u << sl;
+            }
+        }
+        br[c] = best * scale_r;
+        tr[c] = mask;
+        bmx = fmaxf(bmx, br[c]);
+    }
+    float zb = 0.0f;
+    for (int64_t c = 1; c <= bm; ++c) zb += expf(br[c] - bmx);
+    const float lse = bmx + logf(zb);
+    float term = 0.0f, P = 0.0f;
+    for (int64_t c = 1; c <= bm; ++c) {
+        const float ps = pstar_raw(c) * pnorm;
+        if (ps > 0.0f) {
+            term += ps * (br[c] - lse);
+            P += ps;
+        }
+    }
+    for (int64_t c = 1; c <= bm; ++c) {
+        const float ps = pstar_raw(c) * pnorm;
+        const float soft = expf(br[c] - lse);
+        br[c] = (soft * P - (ps > 0.0f ? ps : 0.0f)) * invN;
+    }
+    rowt[r] = term;
+}
+
+// aux = -(sum of the row terms) / N, one workgroup, a fixed order.
+__global__ __launch_bounds__(NT) void aux_sum_kernel(const float *__restrict__ rowt, int64_t rows, float invN,
+                                                     float *__restrict__ aux) {
+    __shared__ double part[NT];
+    double a = 0.0;
+    for (int64_t e = threadIdx.x; e < rows; e += NT) a += (double)rowt[e];
+    part[threadIdx.x] = a;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double t = 0.0;
+        for (int e = 0; e < NT; ++e) t += part[e];
+        aux[0] = (float)(-t * (double)invN);
+    }
+}
+
+// dS0 [b, g, c, slot, t] = sum over the queries with block c as a candidate,
+// ascending, of d bsc x scale_r / (tie count) x qg[t] where the slot is at
+// the max.
+__global__ __launch_bounds__(NT) void aux_dS0_kernel(const float *__restrict__ dbsc, const uint32_t *__restrict__ ties,
+                                                     const float *__restrict__ qg, int64_t B, int64_t n, int Hkv,
+                                                     int Bk, int m, int d, int64_t W, float scale_r,
+                                                     float *__restrict__ dS0) {
+    const int64_t nb = n / Bk;
+    const int64_t gid = (int64_t)blockIdx.x * NT + threadIdx.x;
+    if (gid >= B * Hkv * nb * m * d) return;
+    const int t = (int)(gid % d), sl = (int)((gid / d) % m);
+    const int64_t c = (gid / ((int64_t)d * m)) % nb, bg = gid / ((int64_t)d * m * nb);
+    const int64_t b = bg / Hkv, g = bg % Hkv;
+    float acc = 0.0f;
+    if (c >= 1) {
+        for (int64_t i = 0; i < n; ++i) {
+            if (cand_bmax(i, Bk, W) < c) continue;
+            const int64_t o = (bg * n + i) * nb + c;
+            const uint32_t mk = ties[o];
+            if ((mk >> sl) & 1u)
+                acc = fmaf(dbsc[o] * scale_r / (float)__popc(mk), qg[((b * n + i) * Hkv + g) * d + t], acc);
+        }
+    }
+    dS0[gid] = acc;
+}
+
+// One thread per (b, g, block c, slot): the summariser's forward for the
+// slot (att over the block's keys, pooled row Sp) and its backward given
+// dS0: Sp (for d proj) and the slot's d probes partial.
+__global__ __launch_bounds__(64) void aux_sbwd_kernel(const float *__restrict__ kc, const float *__restrict__ probes,
+                                                      const float *__restrict__ proj, const float *__restrict__ dS0,
+                                                      int64_t B, int64_t n, int Hkv, int Bk, int m, int d,
+                                                      float *__restrict__ Sp_out, float *__restrict__ pprb) {
+    const int64_t nb = n / Bk;
+    const int64_t gid = (int64_t)blockIdx.x * 64 + threadIdx.x;
+    if (gid >= B * Hkv * nb * m) return;
+    const int sl = (int)(gid % m);
+    const int64_t c = (gid / m) % nb, bg = gid / (m * nb);
+    const int64_t g = bg % Hkv;
+    const float *K = kc + (bg * n + c * Bk) * d;   // the block's keys
+    const float *pr = probes + (g * m + sl) * d;
+    const float *pj = proj + g * d * d;
+    const float isd = 1.0f / sqrtf((float)d);
+    float att[256], sp[DMAX], dsp[DMAX];
+    float mx = -INFINITY;
+    for (int k = 0; k < Bk; ++k) {
+        att[k] = dot_n(pr, K + k * d, d) * isd;
+        mx = fmaxf(mx, att[k]);
+    }
+    float z = 0.0f;
+    for (int k = 0; k < Bk; ++k) {
+        att[k] = expf(att[k] - mx);
+        z += att[k];
+    }
+    for (int k = 0; k < Bk; ++k) att[k] /= z;
+    for (int t = 0; t < d; ++t) {
+        float a = 0.0f;
+        for (int k = 0; k < Bk; ++k) a = fmaf(att[k], K[k * d + t], a);
+        sp[t] = a;
+    }
+    const float *dS = dS0 + gid * d;   // gid = ((bg nb + c) m + sl)
+    for (int t = 0; t < d; ++t) {
+        float a = 0.0f;
+        for (int e = 0; e < d; ++e) a = fmaf(dS[e], pj[t * d + e], a);
+        dsp[t] = a;
+    }
+    float dat[256];
+    float sad = 0.0f;   // sum over the keys of att * datt
+    for (int k = 0; k < Bk; ++k) {
+        dat[k] = dot_n(dsp, K + k * d, d);
+        sad = fmaf(att[k], dat[k], sad);
+    }
+    float *dp = pprb + gid * d;
+    for (int t = 0; t < d; ++t) dp[t] = 0.0f;
+    for (int k = 0; k < Bk; ++k) {
+        const float dl = att[k] * (dat[k] - sad) * isd;   // d logit, times the logit's scale
+        for (int t = 0; t < d; ++t) dp[t] = fmaf(dl, K[k * d + t], dp[t]);
+    }
+    float *so = Sp_out + gid * d;
+    for (int t = 0; t < d; ++t) so[t] = sp[t];
+}
+
+// d probes [g, slot, t] = sum over (b, c) of the partials; d proj [g, t, e] =
+// sum over (b, c, slot) of Sp[t] dS0[e]; fixed orders.
+__global__ __launch_bounds__(NT) void aux_grad_kernel(const float *__restrict__ pprb, const float *__restrict__ Sp,
+                                                      const float *__restrict__ dS0, int64_t B, int64_t nb, int Hkv,
+                                                      int m, int d, float *__restrict__ dprobes,
+                                                      float *__restrict__ dproj) {
+    const int64_t gid = (int64_t)blockIdx.x * NT + threadIdx.x;
+    const int64_t np = (int64_t)Hkv * m * d, nj = (int64_t)Hkv * d * d;
+    if (gid < np) {
+        const int t = (int)(gid % d), sl = (int)((gid / d) % m);
+        const int64_t g = gid / ((int64_t)d * m);
+        float a = 0.0f;
+        for (int64_t b = 0; b < B; ++b)
+            for (int64_t c = 0; c < nb; ++c) a += pprb[(((b * Hkv + g) * nb + c) * m + sl) * d + t];
+        dprobes[gid] = a;
+    } else if (gid < np + nj) {
+        const int64_t e2 = gid - np;
+        const int e = (int)(e2 % d), t = (int)((e2 / d) % d);
+        const int64_t g = e2 / ((int64_t)d * d);
+        float a = 0.0f;
+        for (int64_t b = 0; b < B; ++b)
+            for (int64_t c = 0; c < nb; ++c)
+                for (int sl = 0; sl < m; ++sl) {
+                    const int64_t o = (((b * Hkv + g) * nb + c) * m + sl) * d;
+                    a = fmaf(Sp[o + t], dS0[o + e], a);
+                }
+        dproj[e2] = a;
+    }
+}
+
 }  // namespace gen
 
 // ------------------------------------------------------------ launchers ----
@@ -514,6 +754,88 @@ int gen_attn(const float *q, const int64_t *qs, const float *qgain, float eps, c
     hipLaunchKernelGGL(gen::attn_kernel, dim3((unsigned)((n + 63) / 64), (unsigned)Hq, (unsigned)B), dim3(64), 0, s, q,
                        qs[0], qs[1], qs[2], qgain, eps, kc, kr, vt, cosT, sinT, idx, cnt, n, (int)Hq, (int)Hkv,
                        (int)S, W, (int)Bk, (int)k, (int)d, scale, out, os[0], os[1], os[2]);
+    HBA_LAUNCH_CHECK();
+    return HBA_OK;
+}
+
+// the generic aux-KL's workspace: qg [B, n, Hkv, d], L [B, Hkv, n, G, nb],
+// bsc and ties [B, Hkv, n, nb], row terms [B, Hkv, n], dS0, Sp and the d
+// probes partials [B, Hkv, nb, m, d]
+struct GenAuxWs {
+    size_t qg, L, bsc, ties, rowt, dS0, Sp, pprb, total;
+};
+static GenAuxWs gen_aux_layout(int64_t B, int64_t n, int64_t Hq, int64_t Hkv, int64_t d, int64_t m, int64_t Bk) {
+    auto up = [](size_t x) { return (x + 255) & ~(size_t)255; };
+    const int64_t nb = n / Bk, G = Hq / Hkv;
+    GenAuxWs w;
+    size_t o = 0;
+    w.qg = o;   o += up((size_t)B * n * Hkv * d * 4);
+    w.L = o;    o += up((size_t)B * Hkv * n * G * nb * 4);
+    w.bsc = o;  o += up((size_t)B * Hkv * n * nb * 4);
+    w.ties = o; o += up((size_t)B * Hkv * n * nb * 4);
+    w.rowt = o; o += up((size_t)B * Hkv * n * 4);
+    w.dS0 = o;  o += up((size_t)B * Hkv * nb * m * d * 4);
+    w.Sp = o;   o += up((size_t)B * Hkv * nb * m * d * 4);
+    w.pprb = o; o += up((size_t)B * Hkv * nb * m * d * 4);
+    w.total = o;
+    return w;
+}
+
+bool gen_aux_ok(int64_t d, int64_t Bk, int64_t m, int64_t G) {
+    return gen_shape_ok(d, Bk) && m >= 1 && m <= gen::AUX_MMAX && G >= 1 && G <= gen::AUX_GMAX;
+}
+
+size_t gen_aux_ws_bytes(int64_t B, int64_t n, int64_t Hq, int64_t Hkv, int64_t d, int64_t m, int64_t Bk) {
+    return gen_aux_layout(B, n, Hq, Hkv, d, m, Bk).total;
+}
+
+int gen_aux_kl(const float *q, const int64_t *qs, const float *qgain, float eps, const float *kc, const float *S0,
+               const float *probes, const float *proj, int64_t B, int64_t n, int64_t Hq, int64_t Hkv, int64_t d,
+               int64_t m, int64_t Bk, int64_t W, float scale_u, float scale_r, void *ws, float *aux, float *dprobes,
+               float *dproj, hipStream_t s) {
+    const GenAuxWs L = gen_aux_layout(B, n, Hq, Hkv, d, m, Bk);
+    char *w = (char *)ws;
+    float *qg = (float *)(w + L.qg), *Lb = (float *)(w + L.L), *bsc = (float *)(w + L.bsc);
+    uint32_t *ties = (uint32_t *)(w + L.ties);
+    float *rowt = (float *)(w + L.rowt), *dS0 = (float *)(w + L.dS0), *Sp = (float *)(w + L.Sp);
+    float *pprb = (float *)(w + L.pprb);
+    const int64_t nb = n / Bk, G = Hq / Hkv, rows = B * Hkv * n;
+    // queries with a candidate block: cand_bmax(i) >= 1 <=> i >= 2 Bk + W - 1
+    const int64_t f0 = 2 * Bk + W - 1;
+    const int64_t N = B * Hkv * (n > f0 ? n - f0 : 0);
+    const float invN = N ? (float)(1.0 / (double)N) : 0.0f;
+    const int64_t ng = Hkv * m * d + Hkv * d * d;
+    if ((rows + gen::NT - 1) / gen::NT > 0x7fffffff || (B * Hkv * nb * m * d + gen::NT - 1) / gen::NT > 0x7fffffff ||
+        Hq > 65535 || B > 65535)
+        return HBA_ERR_UNSUPPORTED;
+    if (N == 0) {   // no query has a candidate block: aux and its gradients are zero
+        hipLaunchKernelGGL(gen::bwd_zero_kernel, dim3(1), dim3(gen::NT), 0, s, aux, (int64_t)1);
+        if (dprobes) {
+            hipLaunchKernelGGL(gen::bwd_zero_kernel, dim3((unsigned)((Hkv * m * d + gen::NT - 1) / gen::NT)),
+                               dim3(gen::NT), 0, s, dprobes, Hkv * m * d);
+            hipLaunchKernelGGL(gen::bwd_zero_kernel, dim3((unsigned)((Hkv * d * d + gen::NT - 1) / gen::NT)),
+                               dim3(gen::NT), 0, s, dproj, Hkv * d * d);
+        }
+        HBA_LAUNCH_CHECK();
+        return HBA_OK;
+    }
+    int st = gen_route_queries(q, qs, qgain, eps, B, n, Hq, Hkv, d, qg, s);
+    if (st) return st;
+    hipLaunchKernelGGL(gen::aux_teacher_kernel, dim3((unsigned)((n + 63) / 64), (unsigned)Hq, (unsigned)B), dim3(64), 0,
+                       s, q, qs[0], qs[1], qs[2], qgain, eps, kc, n, (int)Hq, (int)Hkv, (int)Bk, (int)d, W, scale_u,
+                       Lb);
+    hipLaunchKernelGGL(gen::aux_rows_kernel, dim3((unsigned)((rows + gen::NT - 1) / gen::NT)), dim3(gen::NT), 0, s,
+                       Lb, qg, S0, B, n, (int)Hkv, (int)G, (int)Bk, (int)m, (int)d, W, scale_r, invN, bsc, ties, rowt);
+    hipLaunchKernelGGL(gen::aux_sum_kernel, dim3(1), dim3(gen::NT), 0, s, rowt, rows, invN, aux);
+    if (dprobes) {
+        const int64_t nd = B * Hkv * nb * m * d, ns = B * Hkv * nb * m;
+        hipLaunchKernelGGL(gen::aux_dS0_kernel, dim3((unsigned)((nd + gen::NT - 1) / gen::NT)), dim3(gen::NT), 0, s,
+                           bsc, ties, qg, B, n, (int)Hkv, (int)Bk, (int)m, (int)d, W, scale_r, dS0);
+        hipLaunchKernelGGL(gen::aux_sbwd_kernel, dim3((unsigned)((ns + 63) / 64)), dim3(64), 0, s, kc, probes, proj,
+                           dS0, B, n, (int)Hkv, (int)Bk, (int)m, (int)d, Sp, pprb);
+        hipLaunchKernelGGL(gen::aux_grad_kernel, dim3((unsigned)((ng + gen::NT - 1) / gen::NT)), dim3(gen::NT), 0, s,
+                           pprb, Sp, dS0, B, nb, (int)Hkv, (int)m, (int)d, dprobes, dproj);
+    }
     HBA_LAUNCH_CHECK();
     return HBA_OK;
 }

@@ -273,10 +273,17 @@ class _AuxKL(torch.autograd.Function):
     @staticmethod
     def forward(ctx, probes, proj, q, k, v, q_gain, k_gain, cos, sin, cfg, qeps, keps, want):
         B, n, Hq, dh = q.shape
+        # the bf16 kernels take 64-key blocks, head dims 64 / 128, at most 8
+        # slots and 16 query heads per KV head; elsewhere the fp32 kernels run
+        # on the widened inputs
+        tuned = (cfg.block == ops.BLOCK and dh in (64, 128) and probes.shape[1] <= 8
+                 and Hq // k.shape[2] <= 16)
+        if q.dtype != torch.float32 and not tuned:
+            q, k, v = q.float(), k.float(), v.float()
         kc, _, _ = ops.prep_keys(k, v, k_gain, keps, cos, sin)
-        S0 = ops.summarize(kc, probes.detach(), proj.detach())
+        S0 = ops.summarize(kc, probes.detach(), proj.detach(), cfg.block)
         aux, dpr, dpj = ops.aux_kl(q, q_gain, k_gain, qeps, kc, S0, probes.detach(), proj.detach(), cfg.window,
-                                   union_scale(cfg, dh, n), route_scale(cfg, dh), want)
+                                   union_scale(cfg, dh, n), route_scale(cfg, dh), want, cfg.block)
         ctx.save_for_backward(dpr, dpj)
         ctx.dtypes = (probes.dtype, proj.dtype)
         return aux
@@ -294,9 +301,6 @@ def aux_kl(q, k, v, cos, sin, cfg, summ, qkn):
     teacher p* (group-averaged content mass of the candidate blocks) against
     log softmax of the summarizer's block scores, a 0-d fp32 tensor whose
     gradient reaches only summ.probes and summ.proj."""
-    if cfg.block != ops.BLOCK:
-        raise NotImplementedError(f"the aux-KL runs at {ops.BLOCK}-key blocks (got block {cfg.block}); set "
-                                  "cfg.aux_w = 0 to run the forward at other block sizes")
     qg, kg, qeps, keps = _qk(cfg, qkn)
     qg = None if qg is None else qg.detach()
     kg = None if kg is None else kg.detach()

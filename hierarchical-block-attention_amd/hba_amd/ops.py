@@ -606,23 +606,25 @@ def summarize_filled(kc_pages: Tensor, page_table: Tensor, seq_lens: Tensor, pro
     check(st, "hba_summarize_filled")
 
 
-def aux_kl(q, q_gain, k_gain, eps, kc, S0, probes, proj, window, scale_u, scale_r, want_grad):
+def aux_kl(q, q_gain, k_gain, eps, kc, S0, probes, proj, window, scale_u, scale_r, want_grad, block=BLOCK):
     """The summarizer auxiliary loss (hba_aux_kl): returns (aux as a 0-d fp32
     tensor, d aux / d probes, d aux / d proj), the gradients None unless
-    want_grad.  q [B, n, Hq, d] raw, kc [B, Hkv, n, d], S0 [B, Hkv, nb, m, d]."""
+    want_grad.  q [B, n, Hq, d] raw, kc [B, Hkv, n, d], S0 [B, Hkv, n/block,
+    m, d].  fp32 takes any block size and head dim the fp32 forward takes;
+    bf16 64-key blocks and head dims 64 / 128."""
     dev = _dev(q)
     _rows(q, "q")
     B, n, Hq, d = q.shape
     Hkv, m = S0.shape[1], S0.shape[3]
     kc, S0 = kc.contiguous(), S0.contiguous()
-    if kc.shape != (B, Hkv, n, d) or kc.dtype != q.dtype or S0.dtype != q.dtype or S0.shape[2] != n // BLOCK:
+    if kc.shape != (B, Hkv, n, d) or kc.dtype != q.dtype or S0.dtype != q.dtype or S0.shape[2] != n // block:
         raise ValueError(f"kc {tuple(kc.shape)} / S0 {tuple(S0.shape)} do not match q {tuple(q.shape)}")
     qg = _f32c(q_gain, dev, Hq, "q_gain")
     kg = _f32c(k_gain, dev, Hkv, "k_gain")
     pr = _f32c(probes, dev, Hkv * m * d, "probes")
     pj = _f32c(proj, dev, Hkv * d * d, "proj")
     nbytes = ctypes.c_size_t(0)
-    check(lib().hba_aux_kl_workspace_size(_code(q), B, n, Hq, Hkv, d, m, BLOCK, ctypes.byref(nbytes)),
+    check(lib().hba_aux_kl_workspace_size(_code(q), B, n, Hq, Hkv, d, m, block, ctypes.byref(nbytes)),
           "hba_aux_kl_workspace_size")
     ws = torch.empty(max(int(nbytes.value), 1), dtype=torch.uint8, device=dev)
     aux = torch.empty(1, dtype=torch.float32, device=dev)
@@ -630,7 +632,7 @@ def aux_kl(q, q_gain, k_gain, eps, kc, S0, probes, proj, window, scale_u, scale_
     dpj = torch.empty(Hkv, d, d, dtype=torch.float32, device=dev) if want_grad else None
     with torch.cuda.device(dev):
         st = lib().hba_aux_kl(_code(q), _p(q), strides3(q), _p(qg), _p(kg), eps, _p(kc), _p(S0), _p(pr), _p(pj), B,
-                              n, Hq, Hkv, d, m, BLOCK, window, scale_u, scale_r, _p(ws), ws.numel(), _p(aux),
+                              n, Hq, Hkv, d, m, block, window, scale_u, scale_r, _p(ws), ws.numel(), _p(aux),
                               _p(dpr), _p(dpj), _stream(dev))
     check(st, "hba_aux_kl")
     return aux[0], dpr, dpj

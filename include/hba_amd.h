@@ -365,8 +365,10 @@ int hba_summarize_filled(int dtype, const void *kc_pages, const int32_t *page_ta
  *           query has a candidate.
  * Work is O(n^2 d) (the teacher scores every candidate key).  ws: at least
  * hba_aux_kl_workspace_size bytes, 16-byte aligned, no initial contents.
- * Every reduction runs in a fixed order (deterministic).  Bk = 64, m <= 8,
- * Hq / Hkv <= 16.
+ * Every reduction runs in a fixed order (deterministic).  bf16: Bk = 64,
+ * d = 64 / 128, m <= 8, Hq / Hkv <= 16.  fp32 also takes any block size
+ * 1..256 dividing n, even d <= 256, m <= 32 and Hq / Hkv <= 64 (scalar
+ * kernels in the oracle's arithmetic, one thread per query row).
  */
 int hba_aux_kl_workspace_size(int dtype, int64_t B, int64_t n, int64_t Hq, int64_t Hkv, int64_t d,
                               int64_t m, int64_t Bk, size_t *bytes);

@@ -192,3 +192,48 @@ def test_generic_backward_matches_oracle(dev, dt, n, Hq, Hkv, d, cfgkw, hier):
     print(dt, n, Hq, Hkv, d, cfgkw, {kk: f"{e:.2e}" for kk, e in rel.items()})
     for nm, e in rel.items():
         assert e < GEN_GRAD_TOL[dt], (nm, e)
+
+
+# ------------------------------------------------------ aux-KL, generic ----
+@pytest.mark.parametrize("dt,n,Hq,Hkv,d,m,cfgkw", [
+    ("f32", 512, 4, 2, 8, 2, dict(block=16, window=64, sinks=2, k_blocks=4)),   # tests/test_qknorm.py:28-35
+    ("bf16", 512, 4, 2, 8, 2, dict(block=16, window=64, sinks=2, k_blocks=4)),
+    ("f32", 1024, 6, 2, 96, 3, dict(block=32, window=128, sinks=8, k_blocks=6)),
+    ("f32", 1024, 18, 1, 64, 4, dict(block=64, window=256, sinks=4, k_blocks=4)),   # G = 18
+])
+def test_generic_aux_kl_matches_oracle(dev, dt, n, Hq, Hkv, d, m, cfgkw):
+    """hba_aux_kl off the tuned geometry (the generic fp32 kernels; bf16
+    inputs widened, so compared with the fp32 oracle on the same bf16 values):
+    the aux and its gradients into probes and proj against the oracle's
+    float64 aux_kl scoring the blocks with the kernels' own summaries -- the
+    reference's block-16 / head-dim-8 test geometry with two slots (its tiny
+    model trains there with aux_w = 1, tests/test_qknorm.py:28-35, 181-187),
+    head dim 96 with 32-key blocks and three slots, 18 query heads per KV
+    head; and the dense drop-in returns the same aux with gradients reaching
+    only the summarizer."""
+    T = torch.float32 if dt == "f32" else torch.bfloat16
+    cfg, x, prm, cos, sin = inputs(dev, T, n, Hq, Hkv, d, m=m, native_ctx=1024, **cfgkw)
+    summ = hba_amd.SlotSummarizer(cfg).to(dev)
+    with torch.no_grad():
+        summ.probes.copy_(x["probes"])
+        summ.proj.copy_(x["proj"])
+    aux = hba_amd.aux_kl(x["q"], x["k"], x["v"], cos, sin, cfg, summ, prm)
+    aux.backward()
+    torch.cuda.synchronize()
+    ocfg = O.Cfg(n_heads=Hq, n_kv=Hkv, head_dim=d, slots=m, qknorm=True, native_ctx=1024, **cfgkw)
+    qc, kc, su = O.content_qk(f(x["q"]), f(x["k"]), ocfg, f(x["q_gain"]), f(x["k_gain"]), 1e-6, n, "f32")
+    kch, _, _ = ops.prep_keys(x["k"].float(), x["v"].float(), x["k_gain"], 1e-6, cos, sin)
+    S0k = f(ops.summarize(kch, summ.probes.detach(), summ.proj.detach(), cfg.block))
+    ref, dpr, dpj, _ = O.aux_kl(qc, kc, f(x["probes"]), f(x["proj"]), Hkv, su, O.route_scale(ocfg, d), cfg.block,
+                                cfg.window, S0_scores=S0k, dtype="f32")
+    errs = (abs(aux.item() - ref) / abs(ref), np.abs(f(summ.probes.grad) - dpr).max() / np.abs(dpr).max(),
+            np.abs(f(summ.proj.grad) - dpj).max() / np.abs(dpj).max())
+    print(dt, n, Hq, Hkv, d, m, cfgkw, [f"{e:.2e}" for e in errs])
+    assert ref > 0 and errs[0] <= 1e-5 and errs[1] <= 1e-4 and errs[2] <= 1e-4, errs
+    # the dense drop-in: the same aux, gradients only into the summarizer
+    summ.zero_grad(set_to_none=True)
+    q = x["q"].clone().requires_grad_(True)
+    out, aux2 = hba_amd.hba_attention_dense(q, x["k"], x["v"], cos, sin, cfg, summ, prm)
+    assert abs(aux2.item() - aux.item()) <= 1e-6 * abs(aux.item())
+    aux2.backward()
+    assert q.grad is None and summ.probes.grad is not None and summ.proj.grad is not None

@@ -1,5 +1,5 @@
 """Host-side config helpers and checks without a GPU: yarn_theta
-(attention.py:47-53), the aux-KL's block-size guard."""
+(attention.py:47-53), the generic geometry's workspace sizes."""
 import math
 
 import pytest
@@ -28,18 +28,30 @@ def test_yarn_theta_stretches_the_lowest_frequency_by_the_context_ratio(d):
         assert torch.allclose(sin[:, d // 2 - 1], torch.sin(torch.arange(8.0) * low(th)), atol=1e-7)
 
 
-def test_aux_kl_refuses_other_block_sizes():
-    """The aux-KL kernel scores 64-key blocks: at the reference's block-16
-    test geometry it raises instead of training the summarizer on 64-key
-    blocks (checked before any tensor is touched, so CPU tensors do)."""
-    from hba_amd import attention as A
-    cfg = hba_amd.HBAConfig(block=16, head_dim=64, n_heads=4, n_kv=2, window=32, k_blocks=2)
-    q = torch.zeros(1, 64, 4, 64)
-    k = torch.zeros(1, 64, 2, 64)
-
-    class Summ:
-        probes = torch.zeros(2, 4, 64, requires_grad=True)
-        proj = torch.zeros(2, 64, 64, requires_grad=True)
-
-    with pytest.raises(NotImplementedError, match="64-key blocks"):
-        A.aux_kl(q, k, k, None, None, cfg, Summ(), None)
+def test_generic_geometry_workspaces_are_sized_on_the_host():
+    """The aux-KL and the backward take the reference's block-16 / head-dim-8
+    test geometry in fp32 (the generic kernels): their workspace queries
+    (host functions, no GPU) accept it and return the sizes of the generic
+    layouts -- the aux-KL's qg, teacher LSEs, scores, ties, row terms, dS0,
+    pooled rows and d probes partials; the backward's three key-side
+    accumulators -- and bf16 at that geometry is refused (the Python side
+    widens it to fp32 first)."""
+    import ctypes
+    from hba_amd import _lib
+    L = ctypes.CDLL(_lib.LIB_PATH)
+    F32, BF16 = 0, 1
+    B, n, Hq, Hkv, d, m, Bk = 2, 512, 4, 2, 8, 2, 16
+    nb, G = n // Bk, Hq // Hkv
+    up = lambda x: (x + 255) // 256 * 256
+    want = (up(B * n * Hkv * d * 4) + up(B * Hkv * n * G * nb * 4) + 2 * up(B * Hkv * n * nb * 4)
+            + up(B * Hkv * n * 4) + 3 * up(B * Hkv * nb * m * d * 4))
+    got = ctypes.c_size_t(0)
+    fn = L.hba_aux_kl_workspace_size
+    fn.argtypes = [ctypes.c_int] + [ctypes.c_int64] * 7 + [ctypes.POINTER(ctypes.c_size_t)]
+    assert fn(F32, B, n, Hq, Hkv, d, m, Bk, ctypes.byref(got)) == 0
+    assert got.value == want
+    assert fn(BF16, B, n, Hq, Hkv, d, m, Bk, ctypes.byref(got)) != 0
+    bw = L.hba_attn_bwd_workspace_bytes
+    bw.argtypes = [ctypes.c_int] + [ctypes.c_int64] * 5 + [ctypes.POINTER(ctypes.c_size_t)]
+    assert bw(F32, B, n, Hq, Hkv, d, ctypes.byref(got)) == 0
+    assert got.value >= 3 * B * Hkv * n * d * 4
