@@ -1430,8 +1430,9 @@ extern "C" int hba_attn_bwd(int dtype, const void *q, const void *k, const void 
     if (B <= 0 || n <= 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv || S < 0 || W < 1 || k_blocks < 1)
         return HBA_ERR_INVALID_ARG;
     if (Bk != 64) return HBA_ERR_UNSUPPORTED;
-    if (n % Bk != 0 || S > Bk) return HBA_ERR_INVALID_ARG;
-    if (Hq / Hkv > bw::BW_GMAX) return HBA_ERR_UNSUPPORTED;
+    if (n % Bk != 0) return HBA_ERR_INVALID_ARG;
+    // (bf16 reaches here with these; fp32 took the generic path above)
+    if (S > Bk || k_blocks > 64 || Hq / Hkv > bw::BW_GMAX) return HBA_ERR_UNSUPPORTED;
     if (B * Hkv * n > 0x7fffffffLL * 4 || B * Hkv * (n / 64) > 0x7fffffffLL || n > 0x7fffffffLL)
         return HBA_ERR_UNSUPPORTED;
     const BwdWs L = bwd_ws_layout(dtype, B, n, Hq, Hkv, d);
