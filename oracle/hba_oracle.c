@@ -3,7 +3,7 @@
  *
  * TEST INFRASTRUCTURE ONLY.  Nothing in the product path links, loads or
  * calls this file; only tests/, __graft_entry__.smoke() and bench.py's
- * cpu_baseline leg use it, as the checker.
+ * cpu_baseline leg use it, to check the kernels' results.
  *
  * It restates, in plain C with an explicitly declared fp32 operation order,
  * the parts of the reference whose results must be bit-exact between the

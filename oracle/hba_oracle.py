@@ -1,8 +1,8 @@
 """CPU oracle for the HBA attention forward path.
 
 TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and bench.py's
-cpu_baseline leg import this module, and only as the checker (or, for the
-baseline, as the timed CPU restatement).  The product path
+cpu_baseline leg import this module, and only to check the kernels' results
+(or, for the baseline, as the timed CPU restatement).  The product path
 (hierarchical-block-attention_amd/hba_amd) never imports it and has no CPU
 fallback.
 

@@ -1,5 +1,5 @@
-"""Write golden vectors from the reference implementation (run in the build
-container only; the reference never travels to the GPU box).
+"""Write golden vectors from the reference implementation (run where the
+reference checkout is present; the tests read only the vectors it writes).
 
 It imports the reference's attention/summarizer functions from
 /root/reference/src and records, on seeded inputs, the outputs of the functions

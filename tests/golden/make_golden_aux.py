@@ -1,5 +1,5 @@
-"""Write golden vectors of the reference's summarizer auxiliary loss (run in
-the build container only; the reference never travels to the GPU box).
+"""Write golden vectors of the reference's summarizer auxiliary loss (run
+where the reference checkout is present; the tests read only the vectors).
 
 For the input cases of make_golden.py it runs, in fp32 on the CPU:
 
