@@ -1012,7 +1012,8 @@ __host__ __device__ inline size_t bytes(int QG, int E, int beff, int nsp, int D)
 }  // namespace hl2
 
 // EL: list positions per ranking lane (16 lanes per query), at least
-// beff * F / 16: 8 at beam * fanout <= 128 (the 128K geometry), else 16.
+// beff * F / 16: 4 at beam * fanout <= 64 (beam 4 of fanout 16), 8 at <= 128
+// (the 128K geometry), else 16.
 template <int D, int EL>
 __global__ __launch_bounds__(hl2::NT) void hier_l2_kernel(
     const bf16_t *__restrict__ S0, const bf16_t *__restrict__ rq, const int16_t *__restrict__ ks, int64_t n,
@@ -1723,7 +1724,9 @@ void launch_hier(const void *q, const int64_t *qs, const float *qgain, float eps
                                    (const bf16_t *)S0, n, (int)Hq, (int)Hkv, n / 64, W, (int)k, scale, idx, val,
                                    cnt, scores, (const bf16_t *)S1, (int)F, (int)beam, sup_scores, 0, 2, rq, ksp);
                 const size_t lds = hl2::bytes(QG, E, (int)beff, (int)ns, D);
-                auto l2 = (E <= 128) ? hier_l2_kernel<D, 8> : hier_l2_kernel<D, SEL_GMAXE / 16>;
+                auto l2 = (E <= 64)    ? hier_l2_kernel<D, 4>
+                          : (E <= 128) ? hier_l2_kernel<D, 8>
+                                       : hier_l2_kernel<D, SEL_GMAXE / 16>;
                 if (hipFuncSetAttribute(reinterpret_cast<const void *>(l2),
                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
                     return;   // the error stays as hipGetLastError's, which the entry point reports
