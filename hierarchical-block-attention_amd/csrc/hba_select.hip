@@ -1718,8 +1718,9 @@ void launch_hier(const void *q, const int64_t *qs, const float *qgain, float eps
                 const int ngroups = (int)((n + QG - 1) / QG);
                 bf16_t *rq = reinterpret_cast<bf16_t *>(ws);
                 int16_t *ksp = reinterpret_cast<int16_t *>(reinterpret_cast<char *>(ws) + hier_ws_rq(B, n, Hkv, D));
-                auto k1 = (beam <= 8) ? score_select_mfma_kernel<D, KMAX, true, 8, true>
-                                      : score_select_mfma_kernel<D, KMAX, true, 16, true>;
+                auto k1 = (beam <= 4)   ? score_select_mfma_kernel<D, KMAX, true, 4, true>
+                          : (beam <= 8) ? score_select_mfma_kernel<D, KMAX, true, 8, true>
+                                        : score_select_mfma_kernel<D, KMAX, true, 16, true>;
                 hipLaunchKernelGGL(k1, grid, dim3(256), pm, s, (const bf16_t *)q, qs[0], qs[1], qs[2], qgain, eps,
                                    (const bf16_t *)S0, n, (int)Hq, (int)Hkv, n / 64, W, (int)k, scale, idx, val,
                                    cnt, scores, (const bf16_t *)S1, (int)F, (int)beam, sup_scores, 0, 2, rq, ksp);
